@@ -1,0 +1,398 @@
+"""Benchmark of the MI355X Tensor elementwise / broadcast / reduction path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+
+Metric: achieved HBM GB/s (% of MI355X peak) per op, and the
+speedup over the host-CPU reference path.  A "step" is one pass of the
+configuration's ops, forward and backward, over inputs already resident in
+HBM.  Each op is timed with HIP events recorded on the library stream (the
+stream every kernel is launched on); a 512 MiB fill runs between ops (outside
+the timed region) so no op starts with its inputs in L2 / Infinity Cache.
+
+Bytes are ALGORITHMIC: every distinct input read once (broadcast operands at
+their real size), every output written once, read + write for every gradient
+accumulated with "+=".  pow's backward recomputes pow(a, b) instead of
+reading the saved output, so its bytes are the recompute figure.
+
+The default workload is config 2: A[8192,8192]
+with r[1,8192] and c[8192,1]; A+r, A*c, A/r, A->pow(c), forward and backward.
+``value`` is the step's total algorithmic bytes over its total kernel time.
+Other configs (--config c1/c3/c4/c5) print the same line for that workload.
+
+The CPU baseline is the reference's own core/tensor.cpp (oracle/_ref, built
+with the reference's flags) -- or, where that is not built, the oracle's
+restatement compiled with the same flags -- timed single-threaded on one host
+core over a row slice of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from whitematter_amd import _lib as W  # noqa: E402
+from whitematter_amd import synth  # noqa: E402
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "achieved HBM GB/s (% of MI355X peak) per op; speedup vs host-CPU ref"
+F32 = 4
+
+
+class Op:
+    def __init__(self, name, launch, nbytes, kernel, elems):
+        self.name, self.launch, self.bytes, self.kernel, self.elems = name, launch, nbytes, kernel, elems
+        self.ms = []
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def shape_arg(s):
+    return W.shape_arg(s)
+
+
+def c2_ops(rows=8192, cols=8192):
+    A, c, r, G = synth.config2(rows, cols)
+    dA, dc, dr, dG = (W.DeviceArray.from_host(x) for x in (A, c, r, G))
+    out = W.DeviceArray((rows, cols))
+    gA = W.DeviceArray((rows, cols)); gA.fill(0.0)
+    gc = W.DeviceArray((rows, 1)); gc.fill(0.0)
+    gr = W.DeviceArray((1, cols)); gr.fill(0.0)
+    N = rows * cols
+    big = N * F32
+    ops = []
+    for name, code, other, gother, vec in (("A+r", W.ADD, dr, gr, cols), ("A*c", W.MUL, dc, gc, rows),
+                                           ("A/r", W.DIV, dr, gr, cols), ("A^c", W.POW, dc, gc, rows)):
+        sa, na = shape_arg(dA.shape)
+        sb, nb = shape_arg(other.shape)
+
+        def fwd(code=code, other=other, sa=sa, na=na, sb=sb, nb=nb):
+            W.call("wm_binary", code, out.vp, dA.vp, sa, na, other.vp, sb, nb)
+
+        def bwd(code=code, other=other, gother=gother, sa=sa, na=na, sb=sb, nb=nb):
+            W.call("wm_binary_bwd", code, dG.vp, dA.vp, sa, na, other.vp, sb, nb, W.nullp(),
+                   gA.vp, 1, gother.vp, 1)
+
+        vb = vec * F32
+        fwd_bytes = big + vb + big                     # A, vector, out
+        if code == W.ADD:
+            bwd_bytes = big + 2 * big + 2 * vb         # G; A.grad RMW; r.grad RMW
+        else:
+            bwd_bytes = big + big + vb + 2 * big + 2 * vb  # G, A, vector; grads RMW
+        kf = "binary_rows_kernel"
+        kb = "bwd_colsum_kernel" if other is dr else "bwd_rowsum_kernel"
+        ops.append(Op(name + " fwd", fwd, fwd_bytes, kf, N))
+        ops.append(Op(name + " bwd", bwd, bwd_bytes, kb, N))
+    keep = [dA, dc, dr, dG, out, gA, gc, gr]
+    workload = {"workload": "c2: A[%d,%d] fp32 with r[1,%d], c[%d,1]; A+r, A*c, A/r, A->pow(c), fwd+bwd "
+                            "(grads accumulated, all inputs require grad)" % (rows, cols, cols, rows),
+                "elements": N}
+    return ops, keep, workload
+
+
+def c1_ops():
+    a, b = synth.config1()
+    rows, cols = a.shape
+    da, db = W.DeviceArray.from_host(a), W.DeviceArray.from_host(b)
+    t = W.DeviceArray((rows, cols)); rl = W.DeviceArray((rows, cols))
+    s1 = W.DeviceArray((rows, 1)); y = W.DeviceArray((1, 1))
+    dy = W.DeviceArray.from_host(np.ones((1, 1), np.float32))
+    ds1 = W.DeviceArray((rows, 1)); dr = W.DeviceArray((rows, cols)); dt = W.DeviceArray((rows, cols))
+    ga = W.DeviceArray((rows, cols)); ga.fill(0.0)
+    gb = W.DeviceArray((cols,)); gb.fill(0.0)
+    sa, na = shape_arg((rows, cols))
+    sb, nb = shape_arg((cols,))
+    N = rows * cols
+    big = N * F32
+    ops = [
+        Op("add fwd", lambda: W.call("wm_binary", W.ADD, t.vp, da.vp, sa, na, db.vp, sb, nb),
+           2 * big + cols * F32, "binary_rows_kernel", N),
+        Op("relu fwd", lambda: W.call("wm_unary", W.RELU, rl.vp, t.vp, N, 0.0, 0.0), 2 * big,
+           "unary_fwd_kernel", N),
+        Op("sum(1) fwd", lambda: W.call("wm_reduce", W.R_SUM, rl.vp, rows, cols, 1, s1.vp, W.nullp()),
+           big + rows * F32, "reduce_rows_kernel", N),
+        Op("sum() fwd", lambda: W.call("wm_reduce", W.R_SUM, s1.vp, 1, rows, 1, y.vp, W.nullp()),
+           rows * F32 + F32, "reduce_rows_kernel", rows),
+        Op("sum() bwd", lambda: W.call("wm_reduce_bwd", W.R_SUM, dy.vp, W.nullp(), 1, rows, 1, ds1.vp, 0),
+           F32 + rows * F32, "reduce_bwd_sum", rows),
+        Op("sum(1) bwd", lambda: W.call("wm_reduce_bwd", W.R_SUM, ds1.vp, W.nullp(), rows, cols, 1, dr.vp, 0),
+           rows * F32 + big, "reduce_bwd_sum_vec_kernel", N),
+        Op("relu bwd", lambda: W.call("wm_unary_bwd", W.RELU, dr.vp, t.vp, W.nullp(), dt.vp, 0, N, 0.0, 0.0),
+           3 * big, "unary_bwd_kernel", N),
+        Op("add bwd", lambda: W.call("wm_binary_bwd", W.ADD, dt.vp, da.vp, sa, na, db.vp, sb, nb, W.nullp(),
+                                     ga.vp, 1, gb.vp, 1),
+           big + 2 * big + 2 * cols * F32, "bwd_colsum_kernel", N),
+    ]
+    keep = [da, db, t, rl, s1, y, dy, ds1, dr, dt, ga, gb]
+    return ops, keep, {"workload": "c1: y = relu(a[1024,1024] + b[1024]).sum(1).sum(), fwd+bwd "
+                                   "(L2-resident, launch-bound; not a roofline case)", "elements": N}
+
+
+def c3_ops(rows=16384, cols=4096):
+    X = synth.config3(rows, cols)
+    dX = W.DeviceArray.from_host(X)
+    N = rows * cols
+    big = N * F32
+    ops, keep = [], [dX]
+    for dim, (outer, n, inner) in ((0, (1, rows, cols)), (1, (rows, cols, 1))):
+        nout = outer * inner
+        for name, code in (("sum", W.R_SUM), ("mean", W.R_MEAN), ("max", W.R_MAX), ("min", W.R_MIN),
+                           ("argmax", W.R_ARGMAX), ("argmin", W.R_ARGMIN)):
+            val = W.DeviceArray((nout,))
+            idx = W.DeviceArray((nout,), np.int64) if code in (W.R_MAX, W.R_MIN) else None
+            keep += [val] + ([idx] if idx is not None else [])
+            nbytes = big + nout * F32 + (nout * 8 if idx is not None else 0)
+            kern = "reduce_cols_kernel" if inner > 1 else "reduce_rows_kernel"
+            ops.append(Op(f"{name} dim{dim}",
+                          (lambda code=code, val=val, idx=idx, o=outer, n=n, i=inner:
+                           W.call("wm_reduce", code, dX.vp, o, n, i, val.vp, W.ptr(idx))),
+                          nbytes, kern, N))
+    full = W.DeviceArray((1,))
+    keep.append(full)
+    ops.append(Op("sum full", lambda: W.call("wm_reduce", W.R_SUM, dX.vp, 1, N, 1, full.vp, W.nullp()),
+                  big + F32, "reduce_rows_kernel", N))
+    # max backward (scatter to the first winner), dim 0 and dim 1
+    gX = W.DeviceArray((rows, cols)); gX.fill(0.0)
+    keep.append(gX)
+    for dim, (outer, n, inner) in ((0, (1, rows, cols)), (1, (rows, cols, 1))):
+        nout = outer * inner
+        idx = W.DeviceArray((nout,), np.int64)
+        W.call("wm_reduce", W.R_MAX, dX.vp, outer, n, inner, W.nullp(), idx.vp)
+        g = W.DeviceArray.from_host(synth.normal((nout,), synth.seed_for(3, 5 + dim)))
+        keep += [idx, g]
+        ops.append(Op(f"max dim{dim} bwd",
+                      (lambda g=g, idx=idx, o=outer, n=n, i=inner:
+                       W.call("wm_reduce_bwd", W.R_MAX, g.vp, idx.vp, o, n, i, gX.vp, 1)),
+                      nout * (F32 + 8 + 2 * F32), "reduce_bwd_scatter_kernel", nout))
+    return ops, keep, {"workload": "c3: X[%d,%d] fp32 quantised to 1/64; sum/mean/max/min/argmax/argmin "
+                                   "over dim 0 and dim 1 (+ full sum), max backward" % (rows, cols),
+                       "elements": N}
+
+
+def c4_ops(rows=8192, cols=32000):
+    L, G = synth.config4(rows, cols)
+    dL, dG = W.DeviceArray.from_host(L), W.DeviceArray.from_host(G)
+    y = W.DeviceArray((rows, cols)); ly = W.DeviceArray((rows, cols))
+    gx = W.DeviceArray((rows, cols)); gx.fill(0.0)
+    N = rows * cols
+    big = N * F32
+    ops = [
+        Op("softmax fwd", lambda: W.call("wm_softmax_fwd", y.vp, dL.vp, rows, cols), 2 * big,
+           "softmax_fwd_kernel", N),
+        Op("log_softmax fwd", lambda: W.call("wm_log_softmax_fwd", ly.vp, dL.vp, rows, cols), 2 * big,
+           "softmax_fwd_kernel", N),
+        Op("softmax bwd", lambda: W.call("wm_softmax_bwd", dG.vp, y.vp, gx.vp, 1, rows, cols), 4 * big,
+           "softmax_bwd_kernel", N),
+        Op("log_softmax bwd", lambda: W.call("wm_log_softmax_bwd", dG.vp, ly.vp, gx.vp, 1, rows, cols), 4 * big,
+           "softmax_bwd_kernel", N),
+    ]
+    return ops, [dL, dG, y, ly, gx], {"workload": "c4: logits[%d,%d] fp32 ~N(0,3) with 1%% +20 spikes; "
+                                                 "softmax and log_softmax fwd+bwd (dx accumulated)" % (rows, cols),
+                                      "elements": N}
+
+
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (reference core/tensor.cpp through oracle/_ref, 1 core)
+# ---------------------------------------------------------------------------
+
+def cpu_baseline_c2(sample_rows=1024, cols=8192, reps=3):
+    sys.path.insert(0, ROOT)
+    import oracle
+    A, c, r, G = synth.config2(8192, cols)
+    A, c, G = A[:sample_rows], c[:sample_rows], G[:sample_rows]
+    ref = oracle.reference()
+    kind = "reference" if ref is not None else "port"
+    N = sample_rows * cols
+    big = N * F32
+    total_bytes = 0
+    times = {}
+    cpu0 = os.sched_getaffinity(0)
+    core = min(cpu0)
+    os.sched_setaffinity(0, {core})
+    try:
+        for name, op, other in (("A+r", "add", r), ("A*c", "mul", c), ("A/r", "div", r), ("A^c", "pow", c)):
+            vb = other.size * F32
+            fb = 2 * big + vb
+            bb = 3 * big + 2 * vb if op == "add" else 4 * big + 3 * vb
+            tf, tb = [], []
+            for rep in range(reps + 1):
+                if kind == "reference":
+                    ta, to = ref.tensor(A, True), ref.tensor(other, True)
+                    t0 = time.perf_counter()
+                    y = ref.binary(op, ta, to)
+                    t1 = time.perf_counter()
+                    y.set_grad(G)
+                    t2 = time.perf_counter()
+                    y.call_grad_fn()
+                    t3 = time.perf_counter()
+                    del y, ta, to
+                else:
+                    o = oracle.get("port")
+                    t0 = time.perf_counter()
+                    out = o.binary(op, A, other)
+                    t1 = time.perf_counter()
+                    t2 = time.perf_counter()
+                    o.binary_bwd(op, G, A, other, out)
+                    t3 = time.perf_counter()
+                if rep > 0:
+                    tf.append(t1 - t0)
+                    tb.append(t3 - t2)
+            times[name + " fwd"] = (statistics.median(tf), fb)
+            times[name + " bwd"] = (statistics.median(tb), bb)
+            total_bytes += fb + bb
+    finally:
+        os.sched_setaffinity(0, cpu0)
+    total_t = sum(t for t, _ in times.values())
+    value = total_bytes / total_t / 1e9
+    return {"value": round(value, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"A[{sample_rows},{cols}] row slice of config 2 (1/{8192 // sample_rows} of A), same ops "
+                      f"fwd+bwd, median of {reps} after 1 warm-up, single-threaded on 1 of "
+                      f"{len(cpu0)} host cores",
+            "per_op_ms": {k: round(t * 1e3, 3) for k, (t, _) in times.items()},
+            "per_op_GBps": {k: round(b / t / 1e9, 4) for k, (t, b) in times.items()}}
+
+
+# ---------------------------------------------------------------------------
+
+def traffic_for(kernel: str, config: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        d = json.load(open(path))
+        return d.get(config, {}).get(kernel)
+    except Exception:
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--flush-mib", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=1024)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU; multi-GPU runs are not part of it "
+              "(value is the single-GPU throughput).", file=sys.stderr)
+        sys.exit(2)
+
+    W.call("wm_init", 0)
+    cus = W.device_cus()
+    ops, keep, workload = CONFIGS[args.config]()
+    flush = W.DeviceArray((args.flush_mib * (1 << 20) // 4,))
+
+    def run_op(op, timed):
+        flush.fill(1.0)
+        if timed:
+            W.call("wm_timer_start")
+        op.launch()
+        if timed:
+            ms = W.C.c_float()
+            W.call("wm_timer_stop", W.C.byref(ms))
+            op.ms.append(ms.value)
+
+    for _ in range(args.warmup):
+        for op in ops:
+            run_op(op, False)
+    W.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for op in ops:
+            run_op(op, True)
+    W.sync()
+    wall = time.perf_counter() - t0
+
+    per_op = {}
+    step_ms = 0.0
+    step_bytes = 0
+    for op in ops:
+        ms = statistics.mean(op.ms)
+        step_ms += ms
+        step_bytes += op.bytes
+        gbps = op.bytes / (ms * 1e-3) / 1e9
+        per_op[op.name] = {"ms": round(ms, 4), "ms_median": round(statistics.median(op.ms), 4),
+                           "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
+                           "Gelem_per_s": round(op.elems / (ms * 1e-3) / 1e9, 2), "bytes": op.bytes}
+    value = step_bytes / (step_ms * 1e-3) / 1e9
+    dom = max(ops, key=lambda o: statistics.mean(o.ms))
+    dom_ms = statistics.mean(dom.ms)
+    dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.kernel, args.config),
+                "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes,
+                "avg_ms": round(dom_ms, 4)}
+
+    # calibration copy kernel (its own launches, after the timed region)
+    n_copy = 1 << 28  # 1 GiB
+    src = W.DeviceArray((n_copy,)); dst = W.DeviceArray((n_copy,))
+    src.fill(2.0)
+    cms = []
+    for _ in range(3):
+        flush.fill(1.0)
+        W.call("wm_timer_start")
+        W.call("wm_copy_kernel", dst.vp, src.vp, n_copy)
+        ms = W.C.c_float()
+        W.call("wm_timer_stop", W.C.byref(ms))
+        cms.append(ms.value)
+    copy_gbps = 2 * n_copy * F32 / (statistics.median(cms) * 1e-3) / 1e9
+    src.free(); dst.free()
+
+    cpu = None
+    if not args.no_cpu and args.config == "c2":
+        try:
+            cpu = cpu_baseline_c2(args.cpu_rows)
+        except Exception as e:  # the baseline is reported, never the target
+            cpu = {"value": None, "error": str(e)}
+    if cpu and cpu.get("value"):
+        for name, d in per_op.items():
+            t = cpu.get("per_op_ms", {}).get(name)
+            if t:
+                # CPU ms scaled from the row sample to the full workload
+                scale = 8192 / args.cpu_rows
+                d["speedup_vs_cpu"] = round(t * scale / d["ms"], 1)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64 -> Box-Muller fp64 -> fp32, BASELINE config recipe)",
+        "config": dict(workload, pct_of_peak=round(100 * value / PEAK_GBPS, 1), cus=cus,
+                       timing="HIP events on the library stream per op; 512 MiB flush between ops "
+                              "(untimed); ms_per_step = sum of op kernel times",
+                       wall_s_timed_loop=round(wall, 3)),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "ops": per_op,
+        "copy_kernel_GBps": round(copy_gbps, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,346 @@
+"""TEST INFRASTRUCTURE ONLY: numpy front end of the CPU oracle.
+
+Loads the three builds of oracle/wm_oracle.c (strict fp32, fp64, and the
+fp64 "sum of |terms|" magnitude build) and, when present, oracle/_ref's build
+of the reference's own core/tensor.cpp.  Only tests/, __graft_entry__.smoke()
+and bench.py's cpu_baseline leg import this package; the product
+(whitematter_amd/) never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KINDS = {"f32": ("liboracle_f32.so", np.float32), "f64": ("liboracle_f64.so", np.float64),
+         "abs": ("liboracle_abs.so", np.float64), "port": ("liboracle_port.so", np.float32)}
+REF_PATH = os.path.join(HERE, "_ref", "libwmref.so")
+
+BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "pow": 4, "max": 5, "min": 6}
+UNARY = {"relu": 0, "sigmoid": 1, "tanh": 2, "log": 3, "exp": 4, "pows": 5, "sqrt": 6,
+         "abs": 7, "clamp": 8, "scale": 9}
+REDUCE = {"sum": 0, "mean": 1, "max": 2, "min": 3, "argmax": 4, "argmin": 5}
+
+_libs = {}
+
+
+def _fp(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else C.c_void_p(0)
+
+
+def _shape(s):
+    return (C.c_int64 * max(1, len(s)))(*[int(v) for v in s]), len(s)
+
+
+class Oracle:
+    """One build of wm_oracle.c; outputs are numpy arrays of its REAL type."""
+
+    def __init__(self, kind: str):
+        name, dtype = KINDS[kind]
+        path = os.path.join(HERE, name)
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle)")
+        self.L = C.CDLL(path)
+        self.dtype = np.dtype(dtype)
+        self.kind = kind
+        for fn in ("or_broadcast_shape", "or_binary", "or_binary_bwd", "or_unary", "or_unary_bwd",
+                   "or_reduce", "or_reduce_bwd", "or_softmax", "or_log_softmax", "or_softmax_bwd",
+                   "or_log_softmax_bwd", "or_f32_to_f16", "or_f16_to_f32"):
+            getattr(self.L, fn).restype = C.c_int
+
+    def broadcast_shape(self, a_shape, b_shape):
+        sa, na = _shape(a_shape)
+        sb, nb = _shape(b_shape)
+        out = (C.c_int64 * 8)()
+        nd = C.c_int()
+        if self.L.or_broadcast_shape(sa, na, sb, nb, out, C.byref(nd)) != 0:
+            raise ValueError("Shapes are not broadcastable")
+        return tuple(out[i] for i in range(nd.value))
+
+    def binary(self, op, a, b):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        oshape = self.broadcast_shape(a.shape, b.shape)
+        out = np.empty(oshape, self.dtype)
+        sa, na = _shape(a.shape)
+        sb, nb = _shape(b.shape)
+        rc = self.L.or_binary(BINARY[op], _fp(out), _fp(a), sa, na, _fp(b), sb, nb)
+        assert rc == 0
+        return out
+
+    def binary_bwd(self, op, g, a, b, out=None, need_a=True, need_b=True):
+        g = np.ascontiguousarray(g, np.float32)
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        ga = np.zeros(a.shape, self.dtype) if need_a else None
+        gb = np.zeros(b.shape, self.dtype) if need_b else None
+        o = np.ascontiguousarray(out, np.float32) if out is not None else None
+        sa, na = _shape(a.shape)
+        sb, nb = _shape(b.shape)
+        rc = self.L.or_binary_bwd(BINARY[op], _fp(g), _fp(a), sa, na, _fp(b), sb, nb, _fp(o), _fp(ga), _fp(gb))
+        assert rc == 0
+        return ga, gb
+
+    def unary(self, op, x, p0=0.0, p1=0.0):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, self.dtype)
+        self.L.or_unary(UNARY[op], _fp(out), _fp(x), C.c_int64(x.size), C.c_float(p0), C.c_float(p1))
+        return out
+
+    def unary_bwd(self, op, g, x, out, p0=0.0, p1=0.0):
+        g = np.ascontiguousarray(g, np.float32)
+        x = np.ascontiguousarray(x, np.float32) if x is not None else None
+        o = np.ascontiguousarray(out, np.float32) if out is not None else None
+        gx = np.zeros(g.shape, self.dtype)
+        self.L.or_unary_bwd(UNARY[op], _fp(g), _fp(x), _fp(o), _fp(gx), C.c_int64(g.size),
+                            C.c_float(p0), C.c_float(p1))
+        return gx
+
+    def reduce(self, op, x, outer, n, inner):
+        x = np.ascontiguousarray(x, np.float32)
+        val = np.empty((outer, inner), self.dtype)
+        idx = np.empty((outer, inner), np.int64)
+        rc = self.L.or_reduce(REDUCE[op], _fp(x), C.c_int64(outer), C.c_int64(n), C.c_int64(inner),
+                              _fp(val), _fp(idx))
+        assert rc == 0
+        return val, idx
+
+    def reduce_bwd(self, op, g, idx, outer, n, inner):
+        g = np.ascontiguousarray(g, np.float32)
+        gx = np.zeros((outer, n, inner), self.dtype)
+        i = np.ascontiguousarray(idx, np.int64) if idx is not None else None
+        rc = self.L.or_reduce_bwd(REDUCE[op], _fp(g), _fp(i), C.c_int64(outer), C.c_int64(n), C.c_int64(inner),
+                                  _fp(gx))
+        assert rc == 0
+        return gx
+
+    def softmax(self, x, log=False):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, self.dtype)
+        fn = self.L.or_log_softmax if log else self.L.or_softmax
+        fn(_fp(out), _fp(x), C.c_int64(x.shape[0]), C.c_int64(x.shape[1]))
+        return out
+
+    def softmax_bwd(self, g, out, log=False):
+        g = np.ascontiguousarray(g, np.float32)
+        o = np.ascontiguousarray(out, np.float32)
+        gx = np.zeros(g.shape, self.dtype)
+        fn = self.L.or_log_softmax_bwd if log else self.L.or_softmax_bwd
+        fn(_fp(g), _fp(o), _fp(gx), C.c_int64(g.shape[0]), C.c_int64(g.shape[1]))
+        return gx
+
+    def f32_to_f16(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.L.or_f32_to_f16(_fp(out), _fp(x), C.c_int64(x.size))
+        return out
+
+    def f16_to_f32(self, h):
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty(h.shape, np.float32)
+        self.L.or_f16_to_f32(_fp(out), _fp(h), C.c_int64(h.size))
+        return out
+
+
+def get(kind: str) -> Oracle:
+    if kind not in _libs:
+        _libs[kind] = Oracle(kind)
+    return _libs[kind]
+
+
+# ---- the reference itself (oracle/_ref, built from /root/reference) --------
+
+class RefTensor:
+    """A reference Tensor (core/tensor.h) behind oracle/_ref/libwmref.so."""
+
+    def __init__(self, L, h):
+        self.L, self.h = L, h
+
+    @property
+    def shape(self):
+        nd = self.L.wmref_ndim(self.h)
+        s = (C.c_int64 * max(1, nd))()
+        self.L.wmref_shape(self.h, s)
+        return tuple(s[i] for i in range(nd))
+
+    def data(self):
+        out = np.empty(self.L.wmref_numel(self.h), np.float32)
+        self.L.wmref_get_data(self.h, _fp(out))
+        return out.reshape(self.shape)
+
+    def grad(self):
+        out = np.empty(self.L.wmref_numel(self.h), np.float32)
+        if not self.L.wmref_get_grad(self.h, _fp(out)):
+            return None
+        return out.reshape(self.shape)
+
+    def run_grad_fn(self, g):
+        g = np.ascontiguousarray(g, np.float32)
+        return self.L.wmref_run_grad_fn(self.h, _fp(g))
+
+    def set_grad(self, g):
+        g = np.ascontiguousarray(g, np.float32)
+        return self.L.wmref_set_grad(self.h, _fp(g))
+
+    def call_grad_fn(self):
+        self.L.wmref_call_grad_fn(self.h)
+
+    def backward(self):
+        self.L.wmref_backward(self.h)
+
+    def __del__(self):
+        try:
+            self.L.wmref_free(self.h)
+        except Exception:
+            pass
+
+
+class Reference:
+    def __init__(self, path: str = REF_PATH):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} not built (make -C oracle with /root/reference present)")
+        L = C.CDLL(path)
+        for fn in ("wmref_new", "wmref_binary", "wmref_unary", "wmref_reduce", "wmref_softmax", "wmref_reshape"):
+            getattr(L, fn).restype = C.c_void_p
+        L.wmref_new.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        L.wmref_binary.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
+        L.wmref_unary.argtypes = [C.c_int, C.c_void_p, C.c_float, C.c_float]
+        L.wmref_reduce.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int]
+        L.wmref_softmax.argtypes = [C.c_int, C.c_void_p, C.c_int]
+        L.wmref_reshape.argtypes = [C.c_void_p, C.c_void_p, C.c_int]
+        for fn in ("wmref_free", "wmref_backward", "wmref_zero_grad"):
+            getattr(L, fn).argtypes = [C.c_void_p]
+            getattr(L, fn).restype = None
+        L.wmref_ndim.argtypes = [C.c_void_p]
+        L.wmref_ndim.restype = C.c_int
+        L.wmref_shape.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_shape.restype = None
+        L.wmref_numel.argtypes = [C.c_void_p]
+        L.wmref_numel.restype = C.c_int64
+        L.wmref_get_data.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_get_data.restype = None
+        L.wmref_get_grad.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_get_grad.restype = C.c_int
+        L.wmref_run_grad_fn.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_run_grad_fn.restype = C.c_int
+        L.wmref_set_grad.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_set_grad.restype = C.c_int
+        L.wmref_call_grad_fn.argtypes = [C.c_void_p]
+        L.wmref_call_grad_fn.restype = None
+        L.wmref_set_grad_enabled.argtypes = [C.c_int]
+        L.wmref_set_grad_enabled.restype = None
+        L.wmref_f32_to_f16.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.wmref_f32_to_f16.restype = None
+        L.wmref_f16_to_f32.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
+        L.wmref_f16_to_f32.restype = None
+        self.L = L
+
+    def tensor(self, data, requires_grad=False, shape: Optional[Sequence[int]] = None) -> RefTensor:
+        data = np.ascontiguousarray(data, np.float32)
+        s = tuple(shape) if shape is not None else data.shape
+        sa, nd = _shape(s)
+        return RefTensor(self.L, self.L.wmref_new(_fp(data), sa, nd, int(requires_grad)))
+
+    def binary(self, op, a: RefTensor, b: RefTensor) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_binary(BINARY[op], a.h, b.h))
+
+    # 0 relu .. 8 clamp as in UNARY; 9 mul(s), 10 div(s), 11 neg
+    def unary(self, op, x: RefTensor, p0=0.0, p1=0.0) -> RefTensor:
+        code = {"mul": 9, "divs": 10, "neg": 11}.get(op, UNARY.get(op))
+        return RefTensor(self.L, self.L.wmref_unary(code, x.h, p0, p1))
+
+    def reduce(self, op, x: RefTensor, dim: int, keepdim: bool) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_reduce(REDUCE[op], x.h, dim, int(keepdim)))
+
+    def softmax(self, x: RefTensor, log=False, dim=-1) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_softmax(int(log), x.h, dim))
+
+    def reshape(self, x: RefTensor, shape) -> RefTensor:
+        sa, nd = _shape(shape)
+        return RefTensor(self.L, self.L.wmref_reshape(x.h, sa, nd))
+
+    def f32_to_f16(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.L.wmref_f32_to_f16(_fp(x), _fp(out), x.size)
+        return out
+
+    def f16_to_f32(self, h):
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty(h.shape, np.float32)
+        self.L.wmref_f16_to_f32(_fp(h), _fp(out), h.size)
+        return out
+
+
+_ref = None
+
+
+def reference() -> Optional[Reference]:
+    """The compiled reference, or None when oracle/_ref is not built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        _ref = Reference()
+    return _ref
+
+
+# ---- comparison helpers ------------------------------------------------------
+
+def ulp_distance(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """Distance in fp32 ulps between fp32 arrays (NaN pairs count 0)."""
+    xi = np.ascontiguousarray(x, np.float32).view(np.int32).astype(np.int64)
+    yi = np.ascontiguousarray(y, np.float32).view(np.int32).astype(np.int64)
+    # Map to a monotone integer line.
+    xi = np.where(xi < 0, -(xi & 0x7FFFFFFF), xi)
+    yi = np.where(yi < 0, -(yi & 0x7FFFFFFF), yi)
+    d = np.abs(xi - yi)
+    both_nan = np.isnan(x) & np.isnan(y)
+    return np.where(both_nan, 0, d)
+
+
+def ulp_vs_f64(x32: np.ndarray, ref64: np.ndarray) -> np.ndarray:
+    """|x32 - ref64| in units of the fp32 ulp at ref64 (NaN/inf handled)."""
+    x = np.asarray(x32, np.float64)
+    r = np.asarray(ref64, np.float64)
+    # Exact values beyond fp32's range round to +-inf (round-to-nearest
+    # overflows at FLT_MAX + half an ulp = 2^128 - 2^103).
+    r = np.where(np.abs(r) >= 2.0 ** 128 - 2.0 ** 103, np.copysign(np.inf, r), r)
+    fin = np.isfinite(r)
+    ar = np.where(fin, np.abs(r), 1.0).astype(np.float32)
+    # fp32 ulp at |r|: spacing of the float nearest below/at |r|.
+    ulp = np.spacing(ar).astype(np.float64)
+    ulp = np.maximum(ulp, np.float64(np.float32(2.0 ** -149)))
+    d = np.abs(x - r) / ulp
+    same_special = (~fin) & ((np.isnan(r) & np.isnan(x)) | (r == x))
+    d = np.where(fin, d, np.where(same_special, 0.0, np.inf))
+    return d
+
+
+def bit_equal(x: np.ndarray, y: np.ndarray) -> bool:
+    """Bitwise equality, except that any NaN matches any NaN."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.ascontiguousarray(y, np.float32)
+    if x.shape != y.shape:
+        return False
+    xn, yn = np.isnan(x), np.isnan(y)
+    if not np.array_equal(xn, yn):
+        return False
+    return bool(np.array_equal(x.view(np.uint32)[~xn], y.view(np.uint32)[~yn]))
+
+
+def close_scaled(x, ref64, scale64, rtol=1e-5, atol=0.0):
+    """|x - ref| <= rtol * max(|ref|, scale) + atol elementwise, NaN == NaN.
+    Returns (ok, worst ratio)."""
+    x = np.asarray(x, np.float64)
+    r = np.asarray(ref64, np.float64)
+    s = np.maximum(np.abs(r), np.abs(np.asarray(scale64, np.float64)))
+    nan_ok = np.array_equal(np.isnan(x), np.isnan(r))
+    fin = np.isfinite(r) & np.isfinite(x)
+    inf_ok = np.array_equal(np.where(np.isinf(r), r, 0), np.where(np.isinf(x), x, 0))
+    err = np.abs(x - r)
+    lim = rtol * s + atol
+    ratio = np.where(fin, err / np.maximum(lim, 1e-300), 0.0)
+    worst = float(ratio.max()) if ratio.size else 0.0
+    return bool(nan_ok and inf_ok and worst <= 1.0), worst

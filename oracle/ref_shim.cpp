@@ -1,0 +1,152 @@
+// ref_shim.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// A C entry layer over the reference's own Tensor class (core/tensor.h), so
+// that tests and bench.py's cpu_baseline leg can drive the unmodified
+// reference CPU path through ctypes.  Built by oracle/Makefile together with
+// the reference's core/tensor.cpp (compiled where it lies, with the
+// reference's Makefile flags) into oracle/_ref/libwmref.so.
+//
+// Handles are heap-allocated TensorPtr (std::shared_ptr<Tensor>).
+// amp.h uses std::memcpy without including <cstring> itself.
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "tensor.h"
+#include "amp.h"
+
+namespace {
+
+TensorPtr& T(void* h) { return *static_cast<TensorPtr*>(h); }
+void* box(TensorPtr t) { return new TensorPtr(std::move(t)); }
+
+}  // namespace
+
+extern "C" {
+
+void* wmref_new(const float* data, const int64_t* shape, int nd, int requires_grad) {
+    std::vector<size_t> s(shape, shape + nd);
+    size_t n = 1;
+    for (auto d : s) n *= d;
+    std::vector<float> v(data, data + n);
+    return box(Tensor::create(v, s, requires_grad != 0));
+}
+
+void wmref_free(void* h) { delete static_cast<TensorPtr*>(h); }
+
+int wmref_ndim(void* h) { return (int)T(h)->shape.size(); }
+
+void wmref_shape(void* h, int64_t* out) {
+    for (size_t i = 0; i < T(h)->shape.size(); ++i) out[i] = (int64_t)T(h)->shape[i];
+}
+
+int64_t wmref_numel(void* h) { return (int64_t)T(h)->data.size(); }
+
+int wmref_requires_grad(void* h) { return T(h)->requires_grad ? 1 : 0; }
+
+void wmref_get_data(void* h, float* out) {
+    std::memcpy(out, T(h)->data.data(), T(h)->data.size() * sizeof(float));
+}
+
+// Returns 0 (and writes nothing) when the tensor has no grad buffer.
+int wmref_get_grad(void* h, float* out) {
+    if (T(h)->grad.empty()) return 0;
+    std::memcpy(out, T(h)->grad.data(), T(h)->grad.size() * sizeof(float));
+    return 1;
+}
+
+// Binary: 0 add, 1 sub, 2 mul, 3 div, 4 pow, 5 max, 6 min (core/tensor.h:73-97).
+void* wmref_binary(int op, void* a, void* b) {
+    const TensorPtr& x = T(a);
+    const TensorPtr& y = T(b);
+    switch (op) {
+        case 0: return box(x->add(y));
+        case 1: return box(x->sub(y));
+        case 2: return box(x->mul(y));
+        case 3: return box(x->div(y));
+        case 4: return box(x->pow(y));
+        case 5: return box(x->max(y));
+        default: return box(x->min(y));
+    }
+}
+
+// Unary: 0 relu, 1 sigmoid, 2 tanh_, 3 log_, 4 exp_, 5 pow(p0), 6 sqrt,
+// 7 abs, 8 clamp(p0, p1), 9 mul(p0), 10 div(p0), 11 neg.
+void* wmref_unary(int op, void* h, float p0, float p1) {
+    const TensorPtr& x = T(h);
+    switch (op) {
+        case 0: return box(x->relu());
+        case 1: return box(x->sigmoid());
+        case 2: return box(x->tanh_());
+        case 3: return box(x->log_());
+        case 4: return box(x->exp_());
+        case 5: return box(x->pow(p0));
+        case 6: return box(x->sqrt());
+        case 7: return box(x->abs());
+        case 8: return box(x->clamp(p0, p1));
+        case 9: return box(x->mul(p0));
+        case 10: return box(x->div(p0));
+        default: return box(x->neg());
+    }
+}
+
+// Reductions through the reference API: 0 sum, 1 mean, 2 max, 3 min,
+// 4 argmax, 5 argmin (core/tensor.h:92-99).
+void* wmref_reduce(int op, void* h, int dim, int keepdim) {
+    const TensorPtr& x = T(h);
+    bool k = keepdim != 0;
+    switch (op) {
+        case 0: return box(x->sum(dim, k));
+        case 1: return box(x->mean(dim, k));
+        case 2: return box(x->max(dim, k));
+        case 3: return box(x->min(dim, k));
+        case 4: return box(x->argmax(dim, k));
+        default: return box(x->argmin(dim, k));
+    }
+}
+
+void* wmref_softmax(int log, void* h, int dim) {
+    return box(log ? T(h)->log_softmax(dim) : T(h)->softmax(dim));
+}
+
+void* wmref_reshape(void* h, const int64_t* shape, int nd) {
+    std::vector<size_t> s(shape, shape + nd);
+    return box(T(h)->reshape(s));
+}
+
+// Inject an upstream gradient and run this node's closure only:
+// y->grad = g; y->grad_fn().  Returns 0 when the node has no closure.
+int wmref_run_grad_fn(void* h, const float* g) {
+    TensorPtr& y = T(h);
+    if (!y->grad_fn) return 0;
+    y->grad.assign(g, g + y->data.size());
+    y->grad_fn();
+    return 1;
+}
+
+// The same in two steps, so a timer can bracket the closure alone.
+int wmref_set_grad(void* h, const float* g) {
+    TensorPtr& y = T(h);
+    y->grad.assign(g, g + y->data.size());
+    return y->grad_fn ? 1 : 0;
+}
+
+void wmref_call_grad_fn(void* h) { T(h)->grad_fn(); }
+
+// Full reverse pass from a scalar root (core/tensor.cpp:763-781).
+void wmref_backward(void* h) { T(h)->backward(); }
+
+void wmref_zero_grad(void* h) { T(h)->zero_grad(); }
+
+void wmref_set_grad_enabled(int on) { GradMode::set_enabled(on != 0); }
+
+// fp16 storage conversions of core/amp.h:15-72.
+void wmref_f32_to_f16(const float* x, uint16_t* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = float_to_half(x[i]);
+}
+
+void wmref_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = half_to_float(x[i]);
+}
+
+}  // extern "C"

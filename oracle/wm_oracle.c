@@ -1,0 +1,428 @@
+/*
+ * wm_oracle.c -- TEST INFRASTRUCTURE ONLY (the checker, never the product).
+ *
+ * A CPU restatement of whitematter's Tensor elementwise / broadcast /
+ * reduction / softmax hot path (reference core/tensor.cpp, core/amp.h), used
+ * only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+ * Nothing under whitematter_amd/ links, loads or calls it.
+ *
+ * Each function follows the reference loop it cites: same visiting order,
+ * same accumulation order, same strict comparisons.  The file is compiled
+ * three times (oracle/Makefile):
+ *   liboracle_f32.so  REAL=float, IEEE, no contraction: the bit-exact oracle
+ *                     for add/sub/mul/div/neg/relu/abs/clamp/max/min/arg*;
+ *   liboracle_f64.so  REAL=double: the fp64 oracle for the tolerance
+ *                     contracts (transcendentals, sums, softmax, gradients);
+ *   liboracle_abs.so  REAL=double with OR_ABS: every accumulation adds |term|
+ *                     and the two subtractions of independently rounded
+ *                     quantities (log_softmax's x - log_sum and g - e*sum(g))
+ *                     add magnitudes, giving the "sum of |terms|" scale of
+ *                     each result, so a tolerance can be stated relative to
+ *                     the terms that cancel.
+ * Inputs are always fp32 arrays (what the reference stores); outputs and
+ * gradient accumulators are REAL.  Backward functions read the forward output
+ * as fp32 -- the value the reference closure reads from result->data.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifndef REAL
+#define REAL double
+#endif
+
+#ifdef OR_ABS
+#define MAG(x) fabs((double)(x))
+#define ACC(dst, term) ((dst) += MAG(term))
+#define MINUS(x, y) (MAG(x) + MAG(y))
+#else
+#define MAG(x) (x)
+#define ACC(dst, term) ((dst) += (term))
+#define MINUS(x, y) ((x) - (y))
+#endif
+
+#define OR_MAX_DIMS 8
+
+enum { OR_ADD, OR_SUB, OR_MUL, OR_DIV, OR_POW, OR_MAX, OR_MIN };
+enum { OR_RELU, OR_SIGMOID, OR_TANH, OR_LOG, OR_EXP, OR_POWS, OR_SQRT, OR_ABSOP, OR_CLAMP, OR_SCALE };
+enum { OR_R_SUM, OR_R_MEAN, OR_R_MAX, OR_R_MIN, OR_R_ARGMAX, OR_R_ARGMIN };
+
+/* ---- broadcasting: core/tensor.cpp:338-398 ------------------------------ */
+
+/* broadcast_shape, :338-358 (right-aligned; equal, or one side 1). */
+int or_broadcast_shape(const int64_t* as, int an, const int64_t* bs, int bn, int64_t* os, int* on) {
+    int nd = an > bn ? an : bn;
+    for (int i = 0; i < nd; i++) {
+        int64_t da = (i < nd - an) ? 1 : as[i - (nd - an)];
+        int64_t db = (i < nd - bn) ? 1 : bs[i - (nd - bn)];
+        if (da == db) os[i] = da;
+        else if (da == 1) os[i] = db;
+        else if (db == 1) os[i] = da;
+        else return -1;
+    }
+    *on = nd;
+    return 0;
+}
+
+/* compute_strides, :390-398. */
+static void strides_of(const int64_t* shape, int nd, int64_t* st) {
+    if (nd == 0) return;
+    st[nd - 1] = 1;
+    for (int i = nd - 2; i >= 0; i--) st[i] = st[i + 1] * shape[i + 1];
+}
+
+/* broadcast_index, :375-387: source offset of output multi-index idx. */
+static int64_t bindex(const int64_t* idx, const int64_t* src_shape, const int64_t* src_st, int src_nd, int nd) {
+    int64_t lin = 0;
+    for (int i = 0; i < src_nd; i++) {
+        int d = nd - src_nd + i;
+        int64_t si = (src_shape[i] == 1) ? 0 : idx[d];
+        lin += si * src_st[i];
+    }
+    return lin;
+}
+
+/* Odometer increment, :942-946. */
+static void bump(int64_t* idx, const int64_t* os, int nd) {
+    for (int d = nd - 1; d >= 0; d--) {
+        idx[d]++;
+        if (idx[d] < os[d]) break;
+        idx[d] = 0;
+    }
+}
+
+static int64_t numel_of(const int64_t* s, int nd) {
+    int64_t n = 1;
+    for (int i = 0; i < nd; i++) n *= s[i];
+    return n;
+}
+
+/* ---- binary ops --------------------------------------------------------- */
+
+/* One output element.  std::max/std::min expressions of :1910 / :1997. */
+static REAL bin_fwd(int op, float a, float b) {
+    switch (op) {
+        case OR_ADD: return (REAL)a + (REAL)b;
+        case OR_SUB: return (REAL)a - (REAL)b;
+        case OR_MUL: return (REAL)a * (REAL)b;
+        case OR_DIV: return (REAL)a / (REAL)b;
+        case OR_POW: return (REAL)pow((REAL)a, (REAL)b);
+        case OR_MAX: return (a < b) ? (REAL)b : (REAL)a;
+        default: return (b < a) ? (REAL)b : (REAL)a;
+    }
+}
+
+/* add :897-979, sub :981-1061, mul :1063-1145, div :1147-1235,
+ * pow(Tensor) :1385-1475, max(Tensor) :1901-1984, min(Tensor) :1986-2073.
+ * Same-shape fast path and broadcast path visit outputs in the same order. */
+int or_binary(int op, REAL* out, const float* a, const int64_t* as, int an, const float* b, const int64_t* bs,
+              int bn) {
+    int64_t os[OR_MAX_DIMS], ast[OR_MAX_DIMS], bst[OR_MAX_DIMS], idx[OR_MAX_DIMS] = {0};
+    int nd;
+    if (or_broadcast_shape(as, an, bs, bn, os, &nd)) return -1;
+    strides_of(as, an, ast);
+    strides_of(bs, bn, bst);
+    int64_t n = numel_of(os, nd);
+    for (int64_t i = 0; i < n; i++) {
+        out[i] = bin_fwd(op, a[bindex(idx, as, ast, an, nd)], b[bindex(idx, bs, bst, bn, nd)]);
+        bump(idx, os, nd);
+    }
+    return 0;
+}
+
+/* Backward closures, output row-major order, accumulating into ga / gb
+ * (either may be NULL = that input does not require grad).  out is the
+ * forward output as stored (fp32), read only by pow's d/db.
+ *   add  :956-976   ga += g;           gb += g
+ *   sub  :1039-1058 ga += g;           gb -= g
+ *   mul  :1122-1142 ga += g*b;         gb += g*a
+ *   div  :1209-1232 ga += g/b;         gb -= g*a/(b*b)
+ *   pow  :1448-1472 ga += g*b*pow(a,b-1); gb += g*out*log(a)
+ *   max  :1962-1984 a >= b ? ga += g : gb += g
+ *   min  :2049-2071 a <= b ? ga += g : gb += g                      */
+int or_binary_bwd(int op, const float* g, const float* a, const int64_t* as, int an, const float* b,
+                  const int64_t* bs, int bn, const float* out, REAL* ga, REAL* gb) {
+    int64_t os[OR_MAX_DIMS], ast[OR_MAX_DIMS], bst[OR_MAX_DIMS], idx[OR_MAX_DIMS] = {0};
+    int nd;
+    if (or_broadcast_shape(as, an, bs, bn, os, &nd)) return -1;
+    strides_of(as, an, ast);
+    strides_of(bs, bn, bst);
+    int64_t n = numel_of(os, nd);
+    for (int64_t i = 0; i < n; i++) {
+        int64_t ia = bindex(idx, as, ast, an, nd), ib = bindex(idx, bs, bst, bn, nd);
+        REAL gg = g[i], va = a[ia], vb = b[ib];
+        switch (op) {
+            case OR_ADD:
+                if (ga) ACC(ga[ia], gg);
+                if (gb) ACC(gb[ib], gg);
+                break;
+            case OR_SUB:
+                if (ga) ACC(ga[ia], gg);
+                if (gb) ACC(gb[ib], -gg);
+                break;
+            case OR_MUL:
+                if (ga) ACC(ga[ia], gg * vb);
+                if (gb) ACC(gb[ib], gg * va);
+                break;
+            case OR_DIV:
+                if (ga) ACC(ga[ia], gg / vb);
+                if (gb) ACC(gb[ib], -(gg * va / (vb * vb)));
+                break;
+            case OR_POW:
+                if (ga) ACC(ga[ia], gg * vb * (REAL)pow(va, vb - (REAL)1.0f));
+                if (gb) ACC(gb[ib], gg * (REAL)out[i] * (REAL)log(va));
+                break;
+            case OR_MAX:
+                if (a[ia] >= b[ib]) { if (ga) ACC(ga[ia], gg); }
+                else if (gb) ACC(gb[ib], gg);
+                break;
+            default:
+                if (a[ia] <= b[ib]) { if (ga) ACC(ga[ia], gg); }
+                else if (gb) ACC(gb[ib], gg);
+                break;
+        }
+        bump(idx, os, nd);
+    }
+    return 0;
+}
+
+/* ---- unary ops ---------------------------------------------------------- */
+
+/* relu :1263-1279 (simd_relu :139-158: x > 0 ? x : 0), sigmoid :1281-1300,
+ * tanh_ :1302-1321, log_ :1323-1341 (log(x + 1e-8f); the +1e-8f is the
+ * reference's fp32 add and stays fp32 here), exp_ :1343-1361, pow(float)
+ * :1363-1383, sqrt :1477-1496, abs :1498-1522, clamp :1524-1546
+ * (std::max(lo, std::min(hi, x))), mul(float) :1237-1253. */
+int or_unary(int op, REAL* out, const float* x, int64_t n, float p0, float p1) {
+    for (int64_t i = 0; i < n; i++) {
+        float v = x[i];
+        REAL r;
+        switch (op) {
+            case OR_RELU: r = v > 0 ? (REAL)v : (REAL)0; break;
+            case OR_SIGMOID: r = (REAL)1 / ((REAL)1 + (REAL)exp(-(REAL)v)); break;
+            case OR_TANH: r = (REAL)tanh((REAL)v); break;
+            case OR_LOG: { float t = v + 1e-8f; r = (REAL)log((REAL)t); break; }
+            case OR_EXP: r = (REAL)exp((REAL)v); break;
+            case OR_POWS: r = (REAL)pow((REAL)v, (REAL)p0); break;
+            case OR_SQRT: r = (REAL)sqrt((REAL)v); break;
+            case OR_ABSOP: r = (REAL)fabsf(v); break;
+            case OR_CLAMP: { float m = (v < p1) ? v : p1; r = (REAL)((p0 < m) ? m : p0); break; }
+            default: r = (REAL)v * (REAL)p0; break;
+        }
+        out[i] = r;
+    }
+    return 0;
+}
+
+/* Closures: relu :1272-1276, sigmoid :1293-1298 (reads out), tanh :1314-1319
+ * (reads out), log :1334-1339, exp :1354-1359 (reads out), pow(float)
+ * :1374-1380, sqrt :1489-1494 (reads out), abs :1508-1519, clamp
+ * :1533-1544, mul(float) :1246-1251.  gx accumulates. */
+int or_unary_bwd(int op, const float* g, const float* x, const float* out, REAL* gx, int64_t n, float p0, float p1) {
+    for (int64_t i = 0; i < n; i++) {
+        REAL gg = g[i];
+        switch (op) {
+            case OR_RELU: ACC(gx[i], gg * (x[i] > 0 ? (REAL)1 : (REAL)0)); break;
+            case OR_SIGMOID: { REAL s = out[i]; ACC(gx[i], gg * s * ((REAL)1 - s)); break; }
+            case OR_TANH: { REAL t = out[i]; ACC(gx[i], gg * ((REAL)1 - t * t)); break; }
+            case OR_LOG: { float t = x[i] + 1e-8f; ACC(gx[i], gg / (REAL)t); break; }
+            case OR_EXP: ACC(gx[i], gg * (REAL)out[i]); break;
+            case OR_POWS: ACC(gx[i], gg * (REAL)p0 * (REAL)pow((REAL)x[i], (REAL)p0 - (REAL)1)); break;
+            case OR_SQRT: ACC(gx[i], gg / ((REAL)2 * (REAL)out[i])); break;
+            case OR_ABSOP:
+                if (x[i] > 0) ACC(gx[i], gg);
+                else if (x[i] < 0) ACC(gx[i], -gg);
+                break;
+            case OR_CLAMP:
+                if (x[i] > p0 && x[i] < p1) ACC(gx[i], gg);
+                break;
+            default: ACC(gx[i], gg * (REAL)p0); break;
+        }
+    }
+    return 0;
+}
+
+/* ---- reductions --------------------------------------------------------- */
+
+/* x viewed as [outer, n, inner], reduced over n, each output slot scanned in
+ * increasing position order:
+ *   sum full :1638-1645, dim 0 :1662-1671, dim 1 :1684-1693
+ *   mean :1709-1721 (sum, then divide by n)
+ *   max/min full :1727-1738 / :1816-1827, dim 0 :1755-1768 / :1844-1857,
+ *   dim 1 :1783-1796 / :1872-1885 (start at the first element, replace only
+ *   on strictly greater / smaller)
+ *   argmax/argmin N-d :2096-2142 / :2170-2216 (same scan; index as fp32)
+ * val: REAL values (or fp32-representable indices for arg*); idx: positions. */
+int or_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner, REAL* val, int64_t* idx) {
+    if (n == 0 && op > OR_R_MEAN) return -1;
+    for (int64_t o = 0; o < outer; o++) {
+        for (int64_t i = 0; i < inner; i++) {
+            const float* p = x + o * n * inner + i;
+            int64_t slot = o * inner + i;
+            if (op == OR_R_SUM || op == OR_R_MEAN) {
+                REAL s = 0;
+                for (int64_t k = 0; k < n; k++) ACC(s, (REAL)p[k * inner]);
+                if (op == OR_R_MEAN) s = s / (REAL)(float)n;
+                val[slot] = s;
+            } else {
+                int want_max = (op == OR_R_MAX || op == OR_R_ARGMAX);
+                float best = p[0];
+                int64_t bi = 0;
+                for (int64_t k = 1; k < n; k++) {
+                    float v = p[k * inner];
+                    if (want_max ? (v > best) : (v < best)) { best = v; bi = k; }
+                }
+                if (val) val[slot] = (op == OR_R_MAX || op == OR_R_MIN) ? (REAL)best : (REAL)(float)bi;
+                if (idx) idx[slot] = bi;
+            }
+        }
+    }
+    return 0;
+}
+
+/* Closures: sum/mean gx[o,k,i] += g[o,i] (:1649-1653, :1675-1681,
+ * :1697-1703; mean reuses them, so no 1/n); max/min gx[o, idx, i] += g
+ * (:1743-1745, :1774-1778, :1802-1806 and the min twins). */
+int or_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int64_t n, int64_t inner, REAL* gx) {
+    for (int64_t o = 0; o < outer; o++) {
+        for (int64_t i = 0; i < inner; i++) {
+            int64_t slot = o * inner + i;
+            if (op == OR_R_SUM || op == OR_R_MEAN) {
+                for (int64_t k = 0; k < n; k++) ACC(gx[(o * n + k) * inner + i], (REAL)g[slot]);
+            } else if (op == OR_R_MAX || op == OR_R_MIN) {
+                ACC(gx[(o * n + idx[slot]) * inner + i], (REAL)g[slot]);
+            } else {
+                return -1;
+            }
+        }
+    }
+    return 0;
+}
+
+/* ---- softmax ------------------------------------------------------------ */
+
+/* softmax :1556-1572: row max (std::max scan), out = exp(x - max), sum,
+ * multiply by 1/sum. */
+int or_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* xr = x + r * cols;
+        REAL* orow = out + r * cols;
+        float m = xr[0];
+        for (int64_t j = 1; j < cols; j++) m = (m < xr[j]) ? xr[j] : m;
+        REAL s = 0;
+        for (int64_t j = 0; j < cols; j++) {
+            orow[j] = (REAL)exp((REAL)xr[j] - (REAL)m);
+            s += orow[j];
+        }
+        REAL inv = (REAL)1 / s;
+        for (int64_t j = 0; j < cols; j++) orow[j] *= inv;
+    }
+    return 0;
+}
+
+/* log_softmax :1601-1616: out = x - (max + log(sum exp(x - max))). */
+int or_log_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* xr = x + r * cols;
+        float m = xr[0];
+        for (int64_t j = 1; j < cols; j++) m = (m < xr[j]) ? xr[j] : m;
+        REAL s = 0;
+        for (int64_t j = 0; j < cols; j++) s += (REAL)exp((REAL)xr[j] - (REAL)m);
+        REAL log_sum = (REAL)m + (REAL)log(s);
+        for (int64_t j = 0; j < cols; j++) out[r * cols + j] = MINUS((REAL)xr[j], log_sum);
+    }
+    return 0;
+}
+
+/* softmax closure :1577-1588, the explicit Jacobian:
+ *   gx[j] += sum_k g[k] * (j == k ? s_j (1 - s_j) : -s_j s_k)
+ * with s = the stored fp32 output. */
+int or_softmax_bwd(const float* g, const float* out, REAL* gx, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* yr = out + r * cols;
+        const float* gr = g + r * cols;
+        for (int64_t j = 0; j < cols; j++) {
+            REAL sj = yr[j];
+            for (int64_t k = 0; k < cols; k++) {
+                REAL sk = yr[k];
+                REAL d = (j == k) ? sj * ((REAL)1 - sj) : -sj * sk;
+                ACC(gx[r * cols + j], (REAL)gr[k] * d);
+            }
+        }
+    }
+    return 0;
+}
+
+/* log_softmax closure :1621-1632: gx[j] += g[j] - exp(out[j]) * sum_k g[k]. */
+int or_log_softmax_bwd(const float* g, const float* out, REAL* gx, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float* gr = g + r * cols;
+        const float* yr = out + r * cols;
+        REAL gs = 0;
+        for (int64_t j = 0; j < cols; j++) ACC(gs, (REAL)gr[j]);
+        for (int64_t j = 0; j < cols; j++) {
+            REAL sm = (REAL)exp((REAL)yr[j]);
+            ACC(gx[r * cols + j], MINUS((REAL)gr[j], sm * gs));
+        }
+    }
+    return 0;
+}
+
+/* ---- fp16 storage: core/amp.h:15-72 ------------------------------------- */
+
+/* float_to_half :15-38 (truncating). */
+static uint16_t f2h(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t e = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
+    uint32_t m = x & 0x7FFFFFu;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        m = (m | 0x800000u) >> (1 - e);
+        return (uint16_t)(sign | (m >> 13));
+    } else if (e == 0xFF - 127 + 15) {
+        if (m == 0) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7C00u | (m >> 13));
+    } else if (e > 30) {
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
+}
+
+/* half_to_float :40-72 (normalising loop for subnormals). */
+static float h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu;
+    uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    float f;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+            memcpy(&f, &bits, 4);
+            return f;
+        }
+        while ((m & 0x400u) == 0) { m <<= 1; e--; }
+        e++;
+        m &= ~0x400u;
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+        memcpy(&f, &bits, 4);
+        return f;
+    }
+    bits = sign | ((e + 127 - 15) << 23) | (m << 13);
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+int or_f32_to_f16(uint16_t* out, const float* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = f2h(x[i]);
+    return 0;
+}
+
+int or_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = h2f(x[i]);
+    return 0;
+}

@@ -1,0 +1,479 @@
+// Backward of the broadcast binary ops, including the reduction of each
+// broadcast operand's gradient over the dims it was repeated along.
+//
+// The reference closures (core/tensor.cpp:956-976 and the same loop in
+// sub/mul/div/pow/max/min) walk the output in row-major order and scatter
+// "grad[src_idx] += contribution" one element at a time.  Here the output is
+// folded to the fewest dims (as in the forward) and three layouts get their
+// own kernels:
+//   flat    both operands have the output's shape: one fused elementwise pass;
+//   colsum  one operand is full [R,C], the other a row vector [1,C]: column
+//           tiles x row chunks, per-column partial sums in registers, then a
+//           fixed-order second pass (c1 bias grad, c2 r.grad, c5 g.grad);
+//   rowsum  one operand is full, the other a column vector [R,1] (or a
+//           scalar): one wave per (row, column chunk), DPP wave reduction,
+//           then a fixed-order second pass when a row is split (c2 c.grad).
+// Everything else goes through a generic kernel: one thread per operand
+// element, summing its contributions in the reference's row-major order.
+// Every path is deterministic: no atomics, fixed partition, fixed order.
+#include "wm_ops.hpp"
+
+#include <algorithm>
+
+namespace wm {
+
+int make_bcast_layout_public(const int64_t* as, int an, const int64_t* bs, int bn, int& nd, int64_t* size,
+                             int64_t* sa, int64_t* sb, int64_t& numel);
+
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------------------
+// flat: same shape
+// ---------------------------------------------------------------------------
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float4* __restrict__ g, const float4* __restrict__ a,
+                                                           const float4* __restrict__ b, const float4* __restrict__ o,
+                                                           float4* __restrict__ ga, int acc_a, float4* __restrict__ gb,
+                                                           int acc_b, int64_t n4) {
+    const bool need_a = (ga && da_reads_a<OP>()) || (gb && db_reads_a<OP>());
+    const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
+    const bool need_o = gb && db_reads_out<OP>() && o;
+    const bool recompute_o = gb && db_reads_out<OP>() && !o;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        float4 vg = g[i];
+        float4 va = need_a ? a[i] : z;
+        float4 vb = need_b ? b[i] : z;
+        float4 vo = need_o ? o[i] : z;
+        if (recompute_o) {
+            vo.x = binary_fwd<OP>(va.x, vb.x); vo.y = binary_fwd<OP>(va.y, vb.y);
+            vo.z = binary_fwd<OP>(va.z, vb.z); vo.w = binary_fwd<OP>(va.w, vb.w);
+        }
+        if (ga) {
+            float4 r;
+            r.x = binary_da<OP>(vg.x, va.x, vb.x);
+            r.y = binary_da<OP>(vg.y, va.y, vb.y);
+            r.z = binary_da<OP>(vg.z, va.z, vb.z);
+            r.w = binary_da<OP>(vg.w, va.w, vb.w);
+            if (acc_a) {
+                float4 old = ga[i];
+                r.x += old.x; r.y += old.y; r.z += old.z; r.w += old.w;
+            }
+            ga[i] = r;
+        }
+        if (gb) {
+            float4 r;
+            r.x = binary_db<OP>(vg.x, va.x, vb.x, vo.x);
+            r.y = binary_db<OP>(vg.y, va.y, vb.y, vo.y);
+            r.z = binary_db<OP>(vg.z, va.z, vb.z, vo.z);
+            r.w = binary_db<OP>(vg.w, va.w, vb.w, vo.w);
+            if (acc_b) {
+                float4 old = gb[i];
+                r.x += old.x; r.y += old.y; r.z += old.z; r.w += old.w;
+            }
+            gb[i] = r;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// colsum: F full [R,C], V row vector [1,C]; C % 4 == 0, 16-byte aligned
+// ---------------------------------------------------------------------------
+
+// One thread owns 4 adjacent columns of one column tile and walks the rows of
+// one row chunk.  VB: the vector operand is b (else a).
+template <int OP, bool VB>
+__global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restrict__ g, const float* __restrict__ F,
+                                                             const float* __restrict__ V, const float* __restrict__ o,
+                                                             float* __restrict__ gF, int accF, float* __restrict__ part,
+                                                             int64_t R, int64_t C, int64_t rows_per_chunk) {
+    const int64_t c = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 4;
+    if (c >= C) return;
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
+    const int64_t r1 = min(R, r0 + rows_per_chunk);
+    const bool want_v = part != nullptr;
+    // Which tensors the contributions read.
+    const bool gF_reads_F = VB ? da_reads_a<OP>() : db_reads_b<OP>();
+    const bool gF_reads_V = VB ? da_reads_b<OP>() : db_reads_a<OP>();
+    const bool gV_reads_F = VB ? db_reads_a<OP>() : da_reads_b<OP>();
+    const bool gV_reads_V = VB ? db_reads_b<OP>() : da_reads_a<OP>();
+    const bool want_o = VB ? (want_v && db_reads_out<OP>()) : (gF && db_reads_out<OP>());
+    const bool need_o = want_o && o;
+    const bool need_F = (gF && gF_reads_F) || (want_v && gV_reads_F) || (want_o && !o);
+    const bool need_V = (gF && gF_reads_V) || (want_v && gV_reads_V) || (want_o && !o);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 vv = need_V ? *reinterpret_cast<const float4*>(V + c) : z;
+    float4 s = z;
+    for (int64_t r = r0; r < r1; ++r) {
+        const int64_t off = r * C + c;
+        float4 vg = *reinterpret_cast<const float4*>(g + off);
+        float4 vf = need_F ? *reinterpret_cast<const float4*>(F + off) : z;
+        float4 vo = need_o ? *reinterpret_cast<const float4*>(o + off) : z;
+        float4 av = VB ? vf : vv, bv = VB ? vv : vf;
+        if (want_o && !o) {
+            vo.x = binary_fwd<OP>(av.x, bv.x); vo.y = binary_fwd<OP>(av.y, bv.y);
+            vo.z = binary_fwd<OP>(av.z, bv.z); vo.w = binary_fwd<OP>(av.w, bv.w);
+        }
+        if (gF) {
+            float4 d;
+            if constexpr (VB) {
+                d.x = binary_da<OP>(vg.x, av.x, bv.x); d.y = binary_da<OP>(vg.y, av.y, bv.y);
+                d.z = binary_da<OP>(vg.z, av.z, bv.z); d.w = binary_da<OP>(vg.w, av.w, bv.w);
+            } else {
+                d.x = binary_db<OP>(vg.x, av.x, bv.x, vo.x); d.y = binary_db<OP>(vg.y, av.y, bv.y, vo.y);
+                d.z = binary_db<OP>(vg.z, av.z, bv.z, vo.z); d.w = binary_db<OP>(vg.w, av.w, bv.w, vo.w);
+            }
+            float4* p = reinterpret_cast<float4*>(gF + off);
+            if (accF) {
+                float4 old = *p;
+                d.x += old.x; d.y += old.y; d.z += old.z; d.w += old.w;
+            }
+            *p = d;
+        }
+        if (want_v) {
+            if constexpr (VB) {
+                s.x += binary_db<OP>(vg.x, av.x, bv.x, vo.x); s.y += binary_db<OP>(vg.y, av.y, bv.y, vo.y);
+                s.z += binary_db<OP>(vg.z, av.z, bv.z, vo.z); s.w += binary_db<OP>(vg.w, av.w, bv.w, vo.w);
+            } else {
+                s.x += binary_da<OP>(vg.x, av.x, bv.x); s.y += binary_da<OP>(vg.y, av.y, bv.y);
+                s.z += binary_da<OP>(vg.z, av.z, bv.z); s.w += binary_da<OP>(vg.w, av.w, bv.w);
+            }
+        }
+    }
+    if (want_v) *reinterpret_cast<float4*>(part + (int64_t)blockIdx.y * C + c) = s;
+}
+
+// out[c] (+)= sum_k part[k, c], k in 0..K-1, with 8 interleaved accumulators
+// combined pairwise (fixed order).
+__global__ void __launch_bounds__(kBlock) colsum_finalize_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                                  int acc, int64_t K, int64_t C) {
+    for (int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x; c < C; c += (int64_t)gridDim.x * kBlock) {
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int64_t k = 0;
+        for (; k + 8 <= K; k += 8) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s[j] += part[(k + j) * C + c];
+        }
+        for (int j = 0; k < K; ++k, ++j) s[j] += part[k * C + c];
+        float t = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+        out[c] = acc ? out[c] + t : t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// rowsum: F full [R,C], V column vector [R,1] (R = 1 covers a scalar operand)
+// ---------------------------------------------------------------------------
+
+// One wave per (row, chunk) item; lanes walk the chunk 4 columns at a time.
+// VEC: C % 4 == 0 and 16-byte aligned bases.
+template <int OP, bool VB, bool VEC>
+__global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restrict__ g, const float* __restrict__ F,
+                                                             const float* __restrict__ V, const float* __restrict__ o,
+                                                             float* __restrict__ gF, int accF, float* __restrict__ gV,
+                                                             int accV, float* __restrict__ part, int64_t R, int64_t C,
+                                                             int64_t chunk, int64_t K) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
+    const bool want_v = gV != nullptr;
+    const bool gF_reads_F = VB ? da_reads_a<OP>() : db_reads_b<OP>();
+    const bool gF_reads_V = VB ? da_reads_b<OP>() : db_reads_a<OP>();
+    const bool gV_reads_F = VB ? db_reads_a<OP>() : da_reads_b<OP>();
+    const bool gV_reads_V = VB ? db_reads_b<OP>() : da_reads_a<OP>();
+    const bool want_o = VB ? (want_v && db_reads_out<OP>()) : (gF && db_reads_out<OP>());
+    const bool need_o = want_o && o;
+    const bool need_F = (gF && gF_reads_F) || (want_v && gV_reads_F) || (want_o && !o);
+    const bool need_V = (gF && gF_reads_V) || (want_v && gV_reads_V) || (want_o && !o);
+    for (int64_t item = wave; item < R * K; item += nwaves) {
+        const int64_t r = item / K;
+        const int64_t k = item - r * K;
+        const int64_t c0 = k * chunk;
+        const int64_t c1 = min(C, c0 + chunk);
+        const float v = need_V ? V[r] : 0.f;
+        const float* gr = g + r * C;
+        const float* fr = F + r * C;
+        const float* orow = o + r * C;
+        float* gfr = gF ? gF + r * C : nullptr;
+        float s = 0.f;
+        if constexpr (VEC) {
+            float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int64_t c = c0 + lane * 4; c < c1; c += 256) {
+                float4 vg = *reinterpret_cast<const float4*>(gr + c);
+                float4 vf = need_F ? *reinterpret_cast<const float4*>(fr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 vo = need_o ? *reinterpret_cast<const float4*>(orow + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float e[4] = {vf.x, vf.y, vf.z, vf.w}, gg[4] = {vg.x, vg.y, vg.z, vg.w},
+                      oo[4] = {vo.x, vo.y, vo.z, vo.w}, d[4], sv[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float av = VB ? e[j] : v, bv = VB ? v : e[j];
+                    if (want_o && !o) oo[j] = binary_fwd<OP>(av, bv);
+                    if constexpr (VB) { d[j] = binary_da<OP>(gg[j], av, bv); sv[j] = binary_db<OP>(gg[j], av, bv, oo[j]); }
+                    else { d[j] = binary_db<OP>(gg[j], av, bv, oo[j]); sv[j] = binary_da<OP>(gg[j], av, bv); }
+                }
+                if (gfr) {
+                    float4* p = reinterpret_cast<float4*>(gfr + c);
+                    float4 nd = make_float4(d[0], d[1], d[2], d[3]);
+                    if (accF) {
+                        float4 old = *p;
+                        nd.x += old.x; nd.y += old.y; nd.z += old.z; nd.w += old.w;
+                    }
+                    *p = nd;
+                }
+                s4.x += sv[0]; s4.y += sv[1]; s4.z += sv[2]; s4.w += sv[3];
+            }
+            s = (s4.x + s4.y) + (s4.z + s4.w);
+        } else {
+            for (int64_t c = c0 + lane; c < c1; c += 64) {
+                float vg = gr[c];
+                float vf = need_F ? fr[c] : 0.f;
+                float av = VB ? vf : v, bv = VB ? v : vf;
+                float vo = need_o ? orow[c] : ((want_o && !o) ? binary_fwd<OP>(av, bv) : 0.f);
+                float d, sv;
+                if constexpr (VB) { d = binary_da<OP>(vg, av, bv); sv = binary_db<OP>(vg, av, bv, vo); }
+                else { d = binary_db<OP>(vg, av, bv, vo); sv = binary_da<OP>(vg, av, bv); }
+                if (gfr) gfr[c] = accF ? gfr[c] + d : d;
+                s += sv;
+            }
+        }
+        if (want_v) {
+            s = wave_sum(s);
+            if (lane == 0) {
+                if (K == 1) gV[r] = accV ? gV[r] + s : s;
+                else part[r * K + k] = s;
+            }
+        }
+    }
+}
+
+// gV[r] (+)= sum_k part[r, k]: one block per row, fixed-order tree.
+__global__ void __launch_bounds__(kBlock) rowsum_finalize_kernel(const float* __restrict__ part, float* __restrict__ gV,
+                                                                  int acc, int64_t R, int64_t K) {
+    __shared__ float lds[kBlock / 64];
+    for (int64_t r = blockIdx.x; r < R; r += gridDim.x) {
+        float s = 0.f;
+        for (int64_t k = threadIdx.x; k < K; k += kBlock) s += part[r * K + k];
+        s = block_sum<kBlock>(s, lds);
+        if (threadIdx.x == 0) gV[r] = acc ? gV[r] + s : s;
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// generic: one thread per operand element
+// ---------------------------------------------------------------------------
+
+struct GenDims {
+    int nd;
+    int64_t size[WM_MAX_DIMS];
+    int64_t sa[WM_MAX_DIMS];
+    int64_t sb[WM_MAX_DIMS];
+    int64_t so[WM_MAX_DIMS];  // output strides
+};
+
+// WB: the gradient being produced is b's (else a's).  The thread for operand
+// element e visits every output element that reads e in row-major order and
+// sums the contributions (the reference's order, core/tensor.cpp:958-975).
+template <int OP, bool WB>
+__global__ void __launch_bounds__(kBlock) bwd_generic_kernel(const float* __restrict__ g, const float* __restrict__ a,
+                                                              const float* __restrict__ b, const float* __restrict__ o,
+                                                              float* __restrict__ gx, int acc, int64_t nx, GenDims d) {
+    for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < nx; e += (int64_t)gridDim.x * kBlock) {
+        // Output base index from the kept dims of this operand.
+        int64_t base = 0;
+        int64_t idx[WM_MAX_DIMS];
+        int64_t red_total = 1;
+        for (int k = 0; k < d.nd; ++k) {
+            int64_t s = WB ? d.sb[k] : d.sa[k];
+            if (s != 0) {
+                int64_t ik = (e / s) % d.size[k];
+                base += ik * d.so[k];
+                idx[k] = ik;
+            } else {
+                idx[k] = 0;
+                red_total *= d.size[k];
+            }
+        }
+        float acc_v = 0.f;
+        for (int64_t j = 0; j < red_total; ++j) {
+            int64_t i = base, oa = 0, ob = 0;
+            for (int k = 0; k < d.nd; ++k) {
+                i += ((WB ? d.sb[k] : d.sa[k]) == 0 ? idx[k] * d.so[k] : 0);
+                oa += idx[k] * d.sa[k];
+                ob += idx[k] * d.sb[k];
+            }
+            float vg = g[i], va = a[oa], vb = b[ob];
+            if constexpr (WB) acc_v += binary_db<OP>(vg, va, vb, db_reads_out<OP>() ? fwd_out_or<OP>(o, i, va, vb) : 0.f);
+            else acc_v += binary_da<OP>(vg, va, vb);
+            // Odometer over the reduced dims, last dim fastest.
+            for (int k = d.nd - 1; k >= 0; --k) {
+                if ((WB ? d.sb[k] : d.sa[k]) != 0) continue;
+                if (++idx[k] < d.size[k]) break;
+                idx[k] = 0;
+            }
+        }
+        gx[e] = acc ? gx[e] + acc_v : acc_v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+
+template <int OP>
+int launch_binary_bwd(const float* g, const float* a, const float* b, const float* o, float* ga, int acc_a, float* gb,
+                      int acc_b, int nd, const int64_t* size, const int64_t* sa, const int64_t* sb, int64_t numel,
+                      int64_t na, int64_t nb) {
+    hipStream_t st = stream();
+    auto contiguous_full = [&](const int64_t* s) {
+        int64_t expect = 1;
+        for (int k = nd - 1; k >= 0; --k) {
+            if (s[k] != expect) return false;
+            expect *= size[k];
+        }
+        return true;
+    };
+    const bool a_full = contiguous_full(sa), b_full = contiguous_full(sb);
+    bool aligned = aligned16(g) && aligned16(a) && aligned16(b) && (!o || aligned16(o)) && (!ga || aligned16(ga)) &&
+                   (!gb || aligned16(gb));
+
+    // flat
+    if (a_full && b_full) {
+        if (numel % 4 == 0 && aligned) {
+            int64_t n4 = numel / 4;
+            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock, 16)), dim3(kBlock), 0, st,
+                               reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(a),
+                               reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(o),
+                               reinterpret_cast<float4*>(ga), acc_a, reinterpret_cast<float4*>(gb), acc_b, n4);
+            return check_launch("wm_binary_bwd(flat)");
+        }
+    }
+
+    // 2-D layouts: [R, C] with one full operand.
+    if ((a_full || b_full) && !(a_full && b_full) && (nd == 2 || nd == 1)) {
+        const bool vb = a_full;  // the vector operand is b
+        const int64_t* sv = vb ? sb : sa;
+        const int64_t R = nd == 2 ? size[0] : 1;
+        const int64_t C = size[nd - 1];
+        const float* F = vb ? a : b;
+        const float* V = vb ? b : a;
+        float* gF = vb ? ga : gb;
+        float* gV = vb ? gb : ga;
+        const int accF = vb ? acc_a : acc_b, accV = vb ? acc_b : acc_a;
+        const bool rowvec = nd == 2 && sv[0] == 0 && sv[1] == 1;
+        const bool colvec = (nd == 2 && sv[0] == 1 && sv[1] == 0) || (nd == 1 && sv[0] == 0);
+        if (rowvec && C % 4 == 0 && aligned) {
+            const int64_t col_tiles = (C + kBlock * 4 - 1) / (kBlock * 4);
+            int64_t K = std::min<int64_t>((2048 + col_tiles - 1) / col_tiles, (R + 15) / 16);
+            K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
+            const int64_t rpc = (R + K - 1) / K;
+            K = (R + rpc - 1) / rpc;
+            Workspace ws(gV ? (size_t)(K * C) * sizeof(float) : 0);
+            if (gV && !ws.p) return set_error(WM_ERR_NOMEM, "wm_binary_bwd: workspace");
+            dim3 grid((unsigned)col_tiles, (unsigned)K);
+            if (vb)
+                hipLaunchKernelGGL((bwd_colsum_kernel<OP, true>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
+                                   ws.as<float>(), R, C, rpc);
+            else
+                hipLaunchKernelGGL((bwd_colsum_kernel<OP, false>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
+                                   ws.as<float>(), R, C, rpc);
+            WM_TRY(check_launch("wm_binary_bwd(colsum)"));
+            if (gV) {
+                hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid_for(C, kBlock, 4)), dim3(kBlock), 0, st,
+                                   ws.as<float>(), gV, accV, K, C);
+                WM_TRY(check_launch("wm_binary_bwd(colsum finalize)"));
+            }
+            return WM_OK;
+        }
+        if (colvec) {
+            // Split rows into chunks only when there are too few rows to fill the chip.
+            const int64_t target_waves = (int64_t)num_cus() * 32;
+            int64_t K = 1;
+            if (R < target_waves) K = std::min<int64_t>((target_waves + R - 1) / R, (C + 1023) / 1024);
+            K = std::max<int64_t>(K, 1);
+            int64_t chunk = (C + K - 1) / K;
+            chunk = (chunk + 255) / 256 * 256;
+            K = (C + chunk - 1) / chunk;
+            if (K < 1) K = 1;
+            Workspace ws(gV && K > 1 ? (size_t)(R * K) * sizeof(float) : 0);
+            if (gV && K > 1 && !ws.p) return set_error(WM_ERR_NOMEM, "wm_binary_bwd: workspace");
+            const bool vec = C % 4 == 0 && aligned;
+            dim3 grid(grid_for(R * K, kBlock / 64, 32));
+#define WM_RS(VBv, VECv)                                                                                          \
+    hipLaunchKernelGGL((bwd_rowsum_kernel<OP, VBv, VECv>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF, gV, accV, \
+                       ws.as<float>(), R, C, chunk, K)
+            if (vb) { if (vec) WM_RS(true, true); else WM_RS(true, false); }
+            else { if (vec) WM_RS(false, true); else WM_RS(false, false); }
+#undef WM_RS
+            WM_TRY(check_launch("wm_binary_bwd(rowsum)"));
+            if (gV && K > 1) {
+                hipLaunchKernelGGL(rowsum_finalize_kernel, dim3(grid_for(R, 1, 8)), dim3(kBlock), 0, st,
+                                   ws.as<float>(), gV, accV, R, K);
+                WM_TRY(check_launch("wm_binary_bwd(rowsum finalize)"));
+            }
+            return WM_OK;
+        }
+    }
+
+    // generic
+    GenDims d;
+    d.nd = nd;
+    int64_t so = 1;
+    for (int k = nd - 1; k >= 0; --k) {
+        d.size[k] = size[k]; d.sa[k] = sa[k]; d.sb[k] = sb[k]; d.so[k] = so;
+        so *= size[k];
+    }
+    if (ga) {
+        hipLaunchKernelGGL((bwd_generic_kernel<OP, false>), dim3(grid_for(na, kBlock)), dim3(kBlock), 0, st, g, a, b,
+                           o, ga, acc_a, na, d);
+        WM_TRY(check_launch("wm_binary_bwd(generic a)"));
+    }
+    if (gb) {
+        hipLaunchKernelGGL((bwd_generic_kernel<OP, true>), dim3(grid_for(nb, kBlock)), dim3(kBlock), 0, st, g, a, b,
+                           o, gb, acc_b, nb, d);
+        WM_TRY(check_launch("wm_binary_bwd(generic b)"));
+    }
+    return WM_OK;
+}
+
+int check_shape(const int64_t* shape, int nd, const char* what);
+int64_t shape_numel(const int64_t* shape, int nd);
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" int wm_binary_bwd(int op, const float* g, const float* a, const int64_t* a_shape, int a_ndim,
+                             const float* b, const int64_t* b_shape, int b_ndim, const float* out, float* ga,
+                             int ga_accumulate, float* gb, int gb_accumulate) {
+    WM_TRY(check_shape(a_shape, a_ndim, "wm_binary_bwd(a)"));
+    WM_TRY(check_shape(b_shape, b_ndim, "wm_binary_bwd(b)"));
+    int nd = 0;
+    int64_t size[WM_MAX_DIMS], sa[WM_MAX_DIMS], sb[WM_MAX_DIMS], numel = 0;
+    WM_TRY(make_bcast_layout_public(a_shape, a_ndim, b_shape, b_ndim, nd, size, sa, sb, numel));
+    if (!ga && !gb) return WM_OK;
+    const int64_t na = shape_numel(a_shape, a_ndim), nb = shape_numel(b_shape, b_ndim);
+    if (numel == 0) {
+        // Nothing flows back; an overwrite request still has to leave zeros.
+        WM_CHECK_INIT();
+        if (ga && !ga_accumulate) WM_TRY(wm_fill(ga, 0.f, na));
+        if (gb && !gb_accumulate) WM_TRY(wm_fill(gb, 0.f, nb));
+        return WM_OK;
+    }
+    if (!g || !a || !b) return set_error(WM_ERR_INVALID, "wm_binary_bwd: null pointer");
+    WM_CHECK_INIT();
+    switch (op) {
+#define WM_CASE(OPC) \
+    case OPC: return launch_binary_bwd<OPC>(g, a, b, out, ga, ga_accumulate, gb, gb_accumulate, nd, size, sa, sb, numel, na, nb)
+        WM_CASE(WM_ADD);
+        WM_CASE(WM_SUB);
+        WM_CASE(WM_MUL);
+        WM_CASE(WM_DIV);
+        WM_CASE(WM_POW);
+        WM_CASE(WM_MAX);
+        WM_CASE(WM_MIN);
+#undef WM_CASE
+        default: return set_error(WM_ERR_INVALID, "wm_binary_bwd: unknown op");
+    }
+}

@@ -1,0 +1,118 @@
+// Shared host/device helpers for libwm_hip (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <cmath>
+#include <string>
+
+#include "../../include/wm_hip.h"
+
+namespace wm {
+
+// ---------------------------------------------------------------------------
+// Host-side runtime state (defined in wm_runtime.hip)
+// ---------------------------------------------------------------------------
+
+// Record a failure message for wm_last_error() and return the status code.
+int set_error(int status, const std::string& msg);
+// Initialise device 0 if nothing is initialised yet.  Returns WM_OK or error.
+int ensure_init();
+hipStream_t stream();
+int num_cus();
+
+// Stream-ordered workspace from the caching allocator.  Freed blocks go back
+// to the pool immediately: every kernel runs on the one library stream, so a
+// later allocation can only be used by work enqueued after the earlier work.
+void* ws_alloc(size_t bytes);
+void ws_free(void* p);
+
+struct Workspace {
+    void* p = nullptr;
+    explicit Workspace(size_t bytes) : p(bytes ? ws_alloc(bytes) : nullptr) {}
+    ~Workspace() { if (p) ws_free(p); }
+    Workspace(const Workspace&) = delete;
+    Workspace& operator=(const Workspace&) = delete;
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+// Check the launch that was just enqueued.
+int check_launch(const char* what);
+
+#define WM_TRY(expr)                 \
+    do {                             \
+        int wm_rc_ = (expr);         \
+        if (wm_rc_ != WM_OK) return wm_rc_; \
+    } while (0)
+
+#define WM_CHECK_INIT() WM_TRY(::wm::ensure_init())
+
+// Number of workgroups for a grid-stride launch over `items` work items of
+// `per_block` items each: enough to fill every CU several times over, never
+// more than the work needs.
+inline unsigned grid_for(int64_t items, int64_t per_block, int waves_per_cu = 8) {
+    if (items <= 0) return 1;
+    int64_t need = (items + per_block - 1) / per_block;
+    int64_t cap = (int64_t)num_cus() * waves_per_cu;
+    if (cap < 1) cap = 1;
+    return (unsigned)(need < cap ? need : cap);
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+// DPP lane moves inside a 16-lane row (deterministic, no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the total.  Fixed
+// combination order, so the result is deterministic.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x124>(v);  // row_ror:4
+    v += dpp_mov<0x128>(v);  // row_ror:8
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x124>(v));
+    v = fmaxf(v, dpp_mov<0x128>(v));
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64).  `lds` must hold
+// NT/64 floats.  Every thread gets the total; order is fixed.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+    constexpr int NW = NT / 64;
+    v = wave_sum(v);
+    if (NW == 1) return v;
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += lds[i];
+    return t;
+}
+
+}  // namespace wm

@@ -1,0 +1,646 @@
+// Elementwise kernels: fill, copy, fp16 conversion, broadcast binary forward
+// and unary forward/backward.
+//
+// Layout: every tensor is contiguous row-major fp32, as in the reference
+// (core/tensor.h:35).  Broadcasting follows NumPy's right-aligned rule
+// (core/tensor.cpp:338-372); instead of the reference's per-element
+// multi-index odometer (:375-387, :936-947) the host folds the output shape
+// into as few dims as possible, the kernels give each broadcast operand a
+// stride of 0 on the dims it repeats along, and the innermost dim is walked
+// with 128-bit loads/stores in grid-stride loops.
+#include "wm_ops.hpp"
+
+#include <algorithm>
+
+namespace wm {
+
+constexpr int kBlock = 256;   // 4 waves
+constexpr int kUnroll = 2;    // float4 loads in flight per thread per step
+
+// ---------------------------------------------------------------------------
+// Broadcast layout (host)
+// ---------------------------------------------------------------------------
+
+struct BcastLayout {
+    int nd = 0;                 // collapsed rank (>= 1)
+    int64_t size[WM_MAX_DIMS];  // collapsed output sizes
+    int64_t sa[WM_MAX_DIMS];    // element strides of a (0 = broadcast)
+    int64_t sb[WM_MAX_DIMS];
+    int64_t numel = 0;
+};
+
+// Reference semantics: right-align, each pair equal or one of them 1
+// (core/tensor.cpp:338-358).
+int broadcast_shape_impl(const int64_t* as, int an, const int64_t* bs, int bn,
+                         int64_t* os, int* on) {
+    if (an < 0 || bn < 0 || an > WM_MAX_DIMS || bn > WM_MAX_DIMS)
+        return set_error(WM_ERR_INVALID, "broadcast: rank out of range (max 8)");
+    int nd = std::max(an, bn);
+    for (int i = 0; i < nd; ++i) {
+        int64_t da = (i < nd - an) ? 1 : as[i - (nd - an)];
+        int64_t db = (i < nd - bn) ? 1 : bs[i - (nd - bn)];
+        if (da < 0 || db < 0) return set_error(WM_ERR_INVALID, "broadcast: negative dim");
+        if (da == db) os[i] = da;
+        else if (da == 1) os[i] = db;
+        else if (db == 1) os[i] = da;
+        else return set_error(WM_ERR_INVALID, "Shapes are not broadcastable");
+    }
+    *on = nd;
+    return WM_OK;
+}
+
+// Per-output-dim strides of an operand (0 where it is broadcast), then merge
+// dims that both operands walk contiguously (or both repeat).
+int make_bcast_layout(const int64_t* as, int an, const int64_t* bs, int bn, BcastLayout& L) {
+    int64_t os[WM_MAX_DIMS];
+    int nd = 0;
+    WM_TRY(broadcast_shape_impl(as, an, bs, bn, os, &nd));
+    int64_t sa[WM_MAX_DIMS], sb[WM_MAX_DIMS];
+    int64_t ra = 1, rb = 1;
+    L.numel = 1;
+    for (int i = nd - 1; i >= 0; --i) {
+        int ia = i - (nd - an), ib = i - (nd - bn);
+        int64_t da = ia >= 0 ? as[ia] : 1, db = ib >= 0 ? bs[ib] : 1;
+        sa[i] = (da == 1) ? 0 : ra;
+        sb[i] = (db == 1) ? 0 : rb;
+        ra *= da;
+        rb *= db;
+        L.numel *= os[i];
+    }
+    // Drop size-1 dims, then merge neighbours.
+    int k = 0;
+    int64_t cs[WM_MAX_DIMS], ca[WM_MAX_DIMS], cb[WM_MAX_DIMS];
+    for (int i = 0; i < nd; ++i) {
+        if (os[i] == 1) continue;
+        if (k > 0 && ca[k - 1] == sa[i] * os[i] && cb[k - 1] == sb[i] * os[i]) {
+            cs[k - 1] *= os[i];
+            ca[k - 1] = sa[i];
+            cb[k - 1] = sb[i];
+        } else {
+            cs[k] = os[i]; ca[k] = sa[i]; cb[k] = sb[i];
+            ++k;
+        }
+    }
+    if (k == 0) { cs[0] = 1; ca[0] = 0; cb[0] = 0; k = 1; }
+    L.nd = k;
+    for (int i = 0; i < k; ++i) { L.size[i] = cs[i]; L.sa[i] = ca[i]; L.sb[i] = cb[i]; }
+    return WM_OK;
+}
+
+int make_bcast_layout_public(const int64_t* as, int an, const int64_t* bs, int bn, int& nd, int64_t* size,
+                             int64_t* sa, int64_t* sb, int64_t& numel) {
+    BcastLayout L;
+    WM_TRY(make_bcast_layout(as, an, bs, bn, L));
+    nd = L.nd;
+    numel = L.numel;
+    for (int i = 0; i < L.nd; ++i) { size[i] = L.size[i]; sa[i] = L.sa[i]; sb[i] = L.sb[i]; }
+    return WM_OK;
+}
+
+// Outer (row) dims of a collapsed layout, passed by value to kernels.
+struct RowDims {
+    int nd;                          // number of outer dims (0..7)
+    int64_t size[WM_MAX_DIMS - 1];
+    int64_t sa[WM_MAX_DIMS - 1];
+    int64_t sb[WM_MAX_DIMS - 1];
+};
+
+__device__ __forceinline__ void row_offsets(const RowDims& d, int64_t row, int64_t& oa, int64_t& ob) {
+    oa = 0; ob = 0;
+    for (int i = d.nd - 1; i >= 0; --i) {
+        int64_t s = d.size[i];
+        int64_t q = row / s;
+        int64_t r = row - q * s;
+        oa += r * d.sa[i];
+        ob += r * d.sb[i];
+        row = q;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kBlock) fill_vec_kernel(float4* __restrict__ out, float v, int64_t n4) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    float4 f = make_float4(v, v, v, v);
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) out[i] = f;
+}
+
+__global__ void __launch_bounds__(kBlock) fill_scalar_kernel(float* __restrict__ out, float v, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = v;
+}
+
+__global__ void __launch_bounds__(kBlock) copy_vec_kernel(float4* __restrict__ dst, const float4* __restrict__ src, int64_t n4) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) v[u] = src[i];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) dst[i] = v[u];
+        }
+    }
+}
+
+// float_to_half of core/amp.h:15-38: truncating (round-toward-zero) fp32 ->
+// fp16, overflow to Inf, float denormals and tiny values to signed zero.
+__device__ __forceinline__ uint16_t f32_to_f16_rtz(float f) {
+    uint32_t x = __float_as_uint(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    int32_t exponent = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
+    uint32_t mantissa = x & 0x7FFFFFu;
+    if (exponent <= 0) {
+        if (exponent < -10) return (uint16_t)sign;
+        mantissa = (mantissa | 0x800000u) >> (1 - exponent);
+        return (uint16_t)(sign | (mantissa >> 13));
+    } else if (exponent == 0xFF - 127 + 15) {
+        if (mantissa == 0) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7C00u | (mantissa >> 13));
+    } else if (exponent > 30) {
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    return (uint16_t)(sign | ((uint32_t)exponent << 10) | (mantissa >> 13));
+}
+
+// half_to_float of core/amp.h:40-72 (exact widening).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exponent = (h >> 10) & 0x1Fu;
+    uint32_t mantissa = h & 0x3FFu;
+    if (exponent == 0) {
+        if (mantissa == 0) return __uint_as_float(sign);
+        // Subnormal half: value = mantissa * 2^-24, exact in fp32.
+        int lz = __clz(mantissa) - 21;          // shifts to bring bit 10 up
+        mantissa = (mantissa << lz) & 0x3FFu;
+        uint32_t e = (uint32_t)(1 - lz + 127 - 15);
+        return __uint_as_float(sign | (e << 23) | (mantissa << 13));
+    } else if (exponent == 31) {
+        return __uint_as_float(sign | 0x7F800000u | (mantissa << 13));
+    }
+    return __uint_as_float(sign | ((exponent + 127 - 15) << 23) | (mantissa << 13));
+}
+
+__global__ void __launch_bounds__(kBlock) f32_to_f16_kernel(uint16_t* __restrict__ out, const float* __restrict__ x, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t n4 = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        float4 v = reinterpret_cast<const float4*>(x)[i];
+        uint2 o;
+        o.x = (uint32_t)f32_to_f16_rtz(v.x) | ((uint32_t)f32_to_f16_rtz(v.y) << 16);
+        o.y = (uint32_t)f32_to_f16_rtz(v.z) | ((uint32_t)f32_to_f16_rtz(v.w) << 16);
+        reinterpret_cast<uint2*>(out)[i] = o;
+    }
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        out[i] = f32_to_f16_rtz(x[i]);
+}
+
+__global__ void __launch_bounds__(kBlock) f16_to_f32_kernel(float* __restrict__ out, const uint16_t* __restrict__ x, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    const int64_t n4 = n / 4;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        uint2 v = reinterpret_cast<const uint2*>(x)[i];
+        float4 o = make_float4(f16_to_f32((uint16_t)(v.x & 0xFFFFu)), f16_to_f32((uint16_t)(v.x >> 16)),
+                               f16_to_f32((uint16_t)(v.y & 0xFFFFu)), f16_to_f32((uint16_t)(v.y >> 16)));
+        reinterpret_cast<float4*>(out)[i] = o;
+    }
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+        out[i] = f16_to_f32(x[i]);
+}
+
+// Same-shape binary op over float4s (the reference fast path, shape == other->shape).
+template <int OP>
+__global__ void __launch_bounds__(kBlock) binary_flat_kernel(float4* __restrict__ out, const float4* __restrict__ a,
+                                                              const float4* __restrict__ b, int64_t n4) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
+        float4 va[kUnroll], vb[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) { va[u] = a[i]; vb[u] = b[i]; }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) {
+                float4 r;
+                r.x = binary_fwd<OP>(va[u].x, vb[u].x);
+                r.y = binary_fwd<OP>(va[u].y, vb[u].y);
+                r.z = binary_fwd<OP>(va[u].z, vb[u].z);
+                r.w = binary_fwd<OP>(va[u].w, vb[u].w);
+                out[i] = r;
+            }
+        }
+    }
+}
+
+// Broadcast binary op over [rows, inner]: each tile is one row segment of
+// kBlock*4*kUnroll elements; the row's operand offsets come from the outer
+// dims once per tile.  AI/BI: stride of a/b along inner (1 = contiguous,
+// 0 = one value per row).  VEC: inner % 4 == 0 and 16-byte aligned bases.
+template <int OP, int AI, int BI, bool VEC>
+__global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a,
+                                                              const float* __restrict__ b, int64_t rows, int64_t inner,
+                                                              RowDims d) {
+    constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * kUnroll;
+    const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
+    const int64_t tiles = rows * tiles_per_row;
+    for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+        const int64_t row = t / tiles_per_row;
+        const int64_t c0 = (t - row * tiles_per_row) * kTile;
+        int64_t oa, ob;
+        row_offsets(d, row, oa, ob);
+        const float* ar = a + oa;
+        const float* br = b + ob;
+        float* orow = out + row * inner;
+        if constexpr (VEC) {
+            float4 va[kUnroll], vb[kUnroll];
+            float sa0 = AI ? 0.f : ar[0];
+            float sb0 = BI ? 0.f : br[0];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                if (c < inner) {
+                    va[u] = AI ? *reinterpret_cast<const float4*>(ar + c) : make_float4(sa0, sa0, sa0, sa0);
+                    vb[u] = BI ? *reinterpret_cast<const float4*>(br + c) : make_float4(sb0, sb0, sb0, sb0);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                if (c < inner) {
+                    float4 r;
+                    r.x = binary_fwd<OP>(va[u].x, vb[u].x);
+                    r.y = binary_fwd<OP>(va[u].y, vb[u].y);
+                    r.z = binary_fwd<OP>(va[u].z, vb[u].z);
+                    r.w = binary_fwd<OP>(va[u].w, vb[u].w);
+                    *reinterpret_cast<float4*>(orow + c) = r;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                int64_t c = c0 + (int64_t)u * kBlock + threadIdx.x;
+                if (c < inner) orow[c] = binary_fwd<OP>(ar[AI ? c : 0], br[BI ? c : 0]);
+            }
+        }
+    }
+}
+
+// Fallback for any collapsed layout: per-element index math over all dims.
+struct FullDims {
+    int nd;
+    int64_t size[WM_MAX_DIMS];
+    int64_t sa[WM_MAX_DIMS];
+    int64_t sb[WM_MAX_DIMS];
+};
+
+__device__ __forceinline__ void full_offsets(const FullDims& d, int64_t i, int64_t& oa, int64_t& ob) {
+    oa = 0; ob = 0;
+    for (int k = d.nd - 1; k >= 0; --k) {
+        int64_t s = d.size[k];
+        int64_t q = i / s;
+        int64_t r = i - q * s;
+        oa += r * d.sa[k];
+        ob += r * d.sb[k];
+        i = q;
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock) binary_generic_kernel(float* __restrict__ out, const float* __restrict__ a,
+                                                                 const float* __restrict__ b, int64_t n, FullDims d) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t oa, ob;
+        full_offsets(d, i, oa, ob);
+        out[i] = binary_fwd<OP>(a[oa], b[ob]);
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                            int64_t n, float p0, float p1) {
+    const int64_t n4 = n / 4;
+    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4* o4 = reinterpret_cast<float4*>(out);
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
+        float4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) v[u] = x4[i];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) {
+                float4 r;
+                r.x = unary_fwd<OP>(v[u].x, p0, p1);
+                r.y = unary_fwd<OP>(v[u].y, p0, p1);
+                r.z = unary_fwd<OP>(v[u].z, p0, p1);
+                r.w = unary_fwd<OP>(v[u].w, p0, p1);
+                o4[i] = r;
+            }
+        }
+    }
+    // Scalar tail (n % 4 elements).
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+        out[i] = unary_fwd<OP>(x[i], p0, p1);
+}
+
+template <int OP>
+__global__ void __launch_bounds__(kBlock) unary_fwd_scalar_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                                   int64_t n, float p0, float p1) {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+        out[i] = unary_fwd<OP>(x[i], p0, p1);
+}
+
+template <int OP, bool ACC>
+__device__ __forceinline__ float ubwd1(float g, float x, float o, float gx, float p0, float p1) {
+    float c = unary_bwd<OP>(g, x, o, p0, p1);
+    return ACC ? gx + c : c;
+}
+
+template <int OP, bool ACC>
+__global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
+                                                            const float* __restrict__ o, float* __restrict__ gx,
+                                                            int64_t n, float p0, float p1) {
+    constexpr bool RX = unary_bwd_reads_x<OP>();
+    constexpr bool RO = unary_bwd_reads_out<OP>();
+    const int64_t n4 = n / 4;
+    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
+        float4 vg[kUnroll], vx[kUnroll], vo[kUnroll], vgx[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) {
+                vg[u] = reinterpret_cast<const float4*>(g)[i];
+                vx[u] = RX ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                vo[u] = RO ? reinterpret_cast<const float4*>(o)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                vgx[u] = ACC ? reinterpret_cast<const float4*>(gx)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < n4) {
+                float4 r;
+                r.x = ubwd1<OP, ACC>(vg[u].x, vx[u].x, vo[u].x, vgx[u].x, p0, p1);
+                r.y = ubwd1<OP, ACC>(vg[u].y, vx[u].y, vo[u].y, vgx[u].y, p0, p1);
+                r.z = ubwd1<OP, ACC>(vg[u].z, vx[u].z, vo[u].z, vgx[u].z, p0, p1);
+                r.w = ubwd1<OP, ACC>(vg[u].w, vx[u].w, vo[u].w, vgx[u].w, p0, p1);
+                reinterpret_cast<float4*>(gx)[i] = r;
+            }
+        }
+    }
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+        gx[i] = ubwd1<OP, ACC>(g[i], RX ? x[i] : 0.f, RO ? o[i] : 0.f, ACC ? gx[i] : 0.f, p0, p1);
+}
+
+template <int OP, bool ACC>
+__global__ void __launch_bounds__(kBlock) unary_bwd_scalar_kernel(const float* __restrict__ g, const float* __restrict__ x,
+                                                                   const float* __restrict__ o, float* __restrict__ gx,
+                                                                   int64_t n, float p0, float p1) {
+    constexpr bool RX = unary_bwd_reads_x<OP>();
+    constexpr bool RO = unary_bwd_reads_out<OP>();
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
+        gx[i] = ubwd1<OP, ACC>(g[i], RX ? x[i] : 0.f, RO ? o[i] : 0.f, ACC ? gx[i] : 0.f, p0, p1);
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+
+template <int OP>
+int launch_binary(float* out, const float* a, const float* b, const BcastLayout& L) {
+    hipStream_t s = stream();
+    const int nd = L.nd;
+    const int64_t inner = L.size[nd - 1];
+    const int64_t ia = L.sa[nd - 1], ib = L.sb[nd - 1];
+    // Same shape (or both fully contiguous after folding): flat float4 walk.
+    if (nd == 1 && ia == 1 && ib == 1 && (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
+        int64_t n4 = inner / 4;
+        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * kUnroll)), dim3(kBlock), 0, s,
+                           reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(a),
+                           reinterpret_cast<const float4*>(b), n4);
+        return check_launch("wm_binary(flat)");
+    }
+    if (inner >= 64 && (ia == 0 || ia == 1) && (ib == 0 || ib == 1)) {
+        RowDims d;
+        d.nd = nd - 1;
+        int64_t rows = 1;
+        for (int i = 0; i < nd - 1; ++i) {
+            d.size[i] = L.size[i]; d.sa[i] = L.sa[i]; d.sb[i] = L.sb[i];
+            rows *= L.size[i];
+        }
+        // float4 path: every row start is a multiple of 4 floats when inner is.
+        bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
+        int64_t tile = (vec ? 4 : 1) * kBlock * kUnroll;
+        int64_t tiles = rows * ((inner + tile - 1) / tile);
+        dim3 grid(grid_for(tiles, 1, 16));
+#define WM_ROWS(AI, BI, V) \
+    hipLaunchKernelGGL((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d)
+        if (vec) {
+            if (ia && ib) WM_ROWS(1, 1, true);
+            else if (ia) WM_ROWS(1, 0, true);
+            else if (ib) WM_ROWS(0, 1, true);
+            else WM_ROWS(0, 0, true);
+        } else {
+            if (ia && ib) WM_ROWS(1, 1, false);
+            else if (ia) WM_ROWS(1, 0, false);
+            else if (ib) WM_ROWS(0, 1, false);
+            else WM_ROWS(0, 0, false);
+        }
+#undef WM_ROWS
+        return check_launch("wm_binary(rows)");
+    }
+    FullDims d;
+    d.nd = nd;
+    for (int i = 0; i < nd; ++i) { d.size[i] = L.size[i]; d.sa[i] = L.sa[i]; d.sb[i] = L.sb[i]; }
+    hipLaunchKernelGGL(binary_generic_kernel<OP>, dim3(grid_for(L.numel, kBlock)), dim3(kBlock), 0, s, out, a, b,
+                       L.numel, d);
+    return check_launch("wm_binary(generic)");
+}
+
+template <int OP>
+int launch_unary(float* out, const float* x, int64_t n, float p0, float p1) {
+    hipStream_t s = stream();
+    if (aligned16(out) && aligned16(x)) {
+        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * kUnroll)), dim3(kBlock), 0, s,
+                           out, x, n, p0, p1);
+    } else {
+        hipLaunchKernelGGL(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
+                           p0, p1);
+    }
+    return check_launch("wm_unary");
+}
+
+template <int OP>
+int launch_unary_bwd(const float* g, const float* x, const float* o, float* gx, int acc, int64_t n, float p0,
+                     float p1) {
+    hipStream_t s = stream();
+    constexpr bool RX = unary_bwd_reads_x<OP>();
+    constexpr bool RO = unary_bwd_reads_out<OP>();
+    if (RX && !x) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward input x");
+    if (RO && !o) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward output");
+    bool vec = aligned16(g) && aligned16(gx) && (!RX || aligned16(x)) && (!RO || aligned16(o));
+    dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll)), grid_s(grid_for(n, kBlock));
+    if (vec) {
+        if (acc) hipLaunchKernelGGL((unary_bwd_kernel<OP, true>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        else hipLaunchKernelGGL((unary_bwd_kernel<OP, false>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+    } else {
+        if (acc) hipLaunchKernelGGL((unary_bwd_scalar_kernel<OP, true>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        else hipLaunchKernelGGL((unary_bwd_scalar_kernel<OP, false>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+    }
+    return check_launch("wm_unary_bwd");
+}
+
+int check_shape(const int64_t* shape, int nd, const char* what) {
+    if (nd < 0 || nd > WM_MAX_DIMS) return set_error(WM_ERR_INVALID, std::string(what) + ": rank out of range (max 8)");
+    if (nd > 0 && !shape) return set_error(WM_ERR_INVALID, std::string(what) + ": null shape");
+    for (int i = 0; i < nd; ++i)
+        if (shape[i] < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative dim");
+    return WM_OK;
+}
+
+int64_t shape_numel(const int64_t* shape, int nd) {
+    int64_t n = 1;
+    for (int i = 0; i < nd; ++i) n *= shape[i];
+    return n;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+int wm_fill(float* out, float value, int64_t n) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_fill: negative size");
+    if (n == 0) return WM_OK;
+    if (!out) return set_error(WM_ERR_INVALID, "wm_fill: null pointer");
+    WM_CHECK_INIT();
+    if (aligned16(out) && n % 4 == 0) {
+        hipLaunchKernelGGL(fill_vec_kernel, dim3(grid_for(n / 4, kBlock)), dim3(kBlock), 0, stream(),
+                           reinterpret_cast<float4*>(out), value, n / 4);
+    } else {
+        hipLaunchKernelGGL(fill_scalar_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, stream(), out, value, n);
+    }
+    return check_launch("wm_fill");
+}
+
+int wm_copy_kernel(float* dst, const float* src, int64_t n) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_copy_kernel: negative size");
+    if (n == 0) return WM_OK;
+    if (!dst || !src) return set_error(WM_ERR_INVALID, "wm_copy_kernel: null pointer");
+    if (n % 4 || !aligned16(dst) || !aligned16(src))
+        return set_error(WM_ERR_INVALID, "wm_copy_kernel: needs 16-byte aligned buffers and n % 4 == 0");
+    WM_CHECK_INIT();
+    hipLaunchKernelGGL(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll)), dim3(kBlock), 0, stream(),
+                       reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), n / 4);
+    return check_launch("wm_copy_kernel");
+}
+
+int wm_f32_to_f16_rtz(uint16_t* out, const float* x, int64_t n) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_f32_to_f16_rtz: negative size");
+    if (n == 0) return WM_OK;
+    if (!out || !x) return set_error(WM_ERR_INVALID, "wm_f32_to_f16_rtz: null pointer");
+    if (!aligned16(x) || ((uintptr_t)out & 7u))
+        return set_error(WM_ERR_INVALID, "wm_f32_to_f16_rtz: x must be 16-byte and out 8-byte aligned");
+    WM_CHECK_INIT();
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    return check_launch("wm_f32_to_f16_rtz");
+}
+
+int wm_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_f16_to_f32: negative size");
+    if (n == 0) return WM_OK;
+    if (!out || !x) return set_error(WM_ERR_INVALID, "wm_f16_to_f32: null pointer");
+    if (!aligned16(out) || ((uintptr_t)x & 7u))
+        return set_error(WM_ERR_INVALID, "wm_f16_to_f32: out must be 16-byte and x 8-byte aligned");
+    WM_CHECK_INIT();
+    hipLaunchKernelGGL(f16_to_f32_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    return check_launch("wm_f16_to_f32");
+}
+
+int wm_broadcast_shape(const int64_t* a_shape, int a_ndim, const int64_t* b_shape, int b_ndim, int64_t* out_shape,
+                       int* out_ndim) {
+    WM_TRY(check_shape(a_shape, a_ndim, "wm_broadcast_shape(a)"));
+    WM_TRY(check_shape(b_shape, b_ndim, "wm_broadcast_shape(b)"));
+    if (!out_shape || !out_ndim) return set_error(WM_ERR_INVALID, "wm_broadcast_shape: null output");
+    return broadcast_shape_impl(a_shape, a_ndim, b_shape, b_ndim, out_shape, out_ndim);
+}
+
+int wm_binary(int op, float* out, const float* a, const int64_t* a_shape, int a_ndim, const float* b,
+              const int64_t* b_shape, int b_ndim) {
+    WM_TRY(check_shape(a_shape, a_ndim, "wm_binary(a)"));
+    WM_TRY(check_shape(b_shape, b_ndim, "wm_binary(b)"));
+    BcastLayout L;
+    WM_TRY(make_bcast_layout(a_shape, a_ndim, b_shape, b_ndim, L));
+    if (L.numel == 0) return WM_OK;
+    if (!out || !a || !b) return set_error(WM_ERR_INVALID, "wm_binary: null pointer");
+    WM_CHECK_INIT();
+    switch (op) {
+        case WM_ADD: return launch_binary<WM_ADD>(out, a, b, L);
+        case WM_SUB: return launch_binary<WM_SUB>(out, a, b, L);
+        case WM_MUL: return launch_binary<WM_MUL>(out, a, b, L);
+        case WM_DIV: return launch_binary<WM_DIV>(out, a, b, L);
+        case WM_POW: return launch_binary<WM_POW>(out, a, b, L);
+        case WM_MAX: return launch_binary<WM_MAX>(out, a, b, L);
+        case WM_MIN: return launch_binary<WM_MIN>(out, a, b, L);
+        default: return set_error(WM_ERR_INVALID, "wm_binary: unknown op");
+    }
+}
+
+int wm_unary(int op, float* out, const float* x, int64_t n, float p0, float p1) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_unary: negative size");
+    if (n == 0) return WM_OK;
+    if (!out || !x) return set_error(WM_ERR_INVALID, "wm_unary: null pointer");
+    WM_CHECK_INIT();
+    switch (op) {
+        case WM_RELU: return launch_unary<WM_RELU>(out, x, n, p0, p1);
+        case WM_SIGMOID: return launch_unary<WM_SIGMOID>(out, x, n, p0, p1);
+        case WM_TANH: return launch_unary<WM_TANH>(out, x, n, p0, p1);
+        case WM_LOG: return launch_unary<WM_LOG>(out, x, n, p0, p1);
+        case WM_EXP: return launch_unary<WM_EXP>(out, x, n, p0, p1);
+        case WM_POWS: return launch_unary<WM_POWS>(out, x, n, p0, p1);
+        case WM_SQRT: return launch_unary<WM_SQRT>(out, x, n, p0, p1);
+        case WM_ABS: return launch_unary<WM_ABS>(out, x, n, p0, p1);
+        case WM_CLAMP: return launch_unary<WM_CLAMP>(out, x, n, p0, p1);
+        case WM_SCALE: return launch_unary<WM_SCALE>(out, x, n, p0, p1);
+        default: return set_error(WM_ERR_INVALID, "wm_unary: unknown op");
+    }
+}
+
+int wm_unary_bwd(int op, const float* g, const float* x, const float* out, float* gx, int accumulate, int64_t n,
+                 float p0, float p1) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_unary_bwd: negative size");
+    if (n == 0) return WM_OK;
+    if (!g || !gx) return set_error(WM_ERR_INVALID, "wm_unary_bwd: null pointer");
+    WM_CHECK_INIT();
+    switch (op) {
+        case WM_RELU: return launch_unary_bwd<WM_RELU>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_SIGMOID: return launch_unary_bwd<WM_SIGMOID>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_TANH: return launch_unary_bwd<WM_TANH>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_LOG: return launch_unary_bwd<WM_LOG>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_EXP: return launch_unary_bwd<WM_EXP>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_POWS: return launch_unary_bwd<WM_POWS>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_SQRT: return launch_unary_bwd<WM_SQRT>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_ABS: return launch_unary_bwd<WM_ABS>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_CLAMP: return launch_unary_bwd<WM_CLAMP>(g, x, out, gx, accumulate, n, p0, p1);
+        case WM_SCALE: return launch_unary_bwd<WM_SCALE>(g, x, out, gx, accumulate, n, p0, p1);
+        default: return set_error(WM_ERR_INVALID, "wm_unary_bwd: unknown op");
+    }
+}
+
+}  // extern "C"

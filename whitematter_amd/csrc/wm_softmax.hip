@@ -1,0 +1,315 @@
+// Row softmax / log_softmax forward and backward, one row per workgroup.
+//
+// Reference: softmax core/tensor.cpp:1548-1591, log_softmax :1593-1635.  Both
+// take a 2-D tensor and always work along the last axis (the dim argument is
+// normalised and then ignored).  The reference walks each row three times
+// (max; exp + sum into the output; scale by 1/sum) and its softmax backward is
+// the explicit O(C^2) Jacobian loop (:1577-1588).  Here a row is loaded once
+// into registers (up to 1024 threads x ITEMS float4), the max and the sum of
+// exp(x - max) are combined across the workgroup through LDS, and the row is
+// written once; the backward uses the closed form
+//   dx_j += y_j * (g_j - sum_k g_k y_k)
+// which is that Jacobian contracted with g.  Rows longer than the register
+// tile stream through three passes instead.
+#include "wm_common.hpp"
+
+#include <algorithm>
+
+namespace wm {
+
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float* lds) {
+    constexpr int NW = NT / 64;
+    v = wave_max(v);
+    if (NW == 1) return v;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = lds[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) m = fmaxf(m, lds[i]);
+    return m;
+}
+
+// Registers of one thread: ITEMS float4 slots.  Element e of slot t lives at
+// column (t * NT + tid) * 4 + e (VEC) or t * NT * 4 + e * NT + tid (scalar),
+// so each load instruction of a wave is contiguous either way.
+template <int NT, int ITEMS, bool VEC>
+struct RowTile {
+    float v[ITEMS][4];
+
+    __device__ __forceinline__ static int64_t col(int t, int e) {
+        return VEC ? ((int64_t)(t * NT + (int)threadIdx.x) * 4 + e) : ((int64_t)t * NT * 4 + (int64_t)e * NT + threadIdx.x);
+    }
+
+    __device__ __forceinline__ void load(const float* row, int64_t cols, float fill) {
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t) {
+            if constexpr (VEC) {
+                int64_t c = col(t, 0);
+                if (c < cols) {
+                    float4 q = *reinterpret_cast<const float4*>(row + c);
+                    v[t][0] = q.x; v[t][1] = q.y; v[t][2] = q.z; v[t][3] = q.w;
+                } else {
+                    v[t][0] = v[t][1] = v[t][2] = v[t][3] = fill;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int64_t c = col(t, e);
+                    v[t][e] = c < cols ? row[c] : fill;
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float* row, int64_t cols) const {
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t) {
+            if constexpr (VEC) {
+                int64_t c = col(t, 0);
+                if (c < cols) *reinterpret_cast<float4*>(row + c) = make_float4(v[t][0], v[t][1], v[t][2], v[t][3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    int64_t c = col(t, e);
+                    if (c < cols) row[c] = v[t][e];
+                }
+            }
+        }
+    }
+};
+
+// LOG = false: softmax, true: log_softmax.
+template <int NT, int ITEMS, bool VEC, bool LOG>
+__global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                          int64_t rows, int64_t cols) {
+    __shared__ float lds[NT / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        RowTile<NT, ITEMS, VEC> tile;
+        tile.load(x + r * cols, cols, -INFINITY);
+        float m = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m = fmaxf(m, tile.v[t][e]);
+        m = block_max<NT>(m, lds);
+        float s = 0.f;
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // Padding slots hold -inf: exp(-inf - m) = 0 (NaN if m is -inf,
+                // which only happens when the whole row is -inf; then every
+                // real element is NaN too, as in the reference).
+                float ex = (tile.col(t, e) < cols) ? expf(tile.v[t][e] - m) : 0.f;
+                s += ex;
+                if (!LOG) tile.v[t][e] = ex;
+            }
+        s = block_sum<NT>(s, lds);
+        if (LOG) {
+            const float log_sum = m + logf(s);
+#pragma unroll
+            for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tile.v[t][e] = tile.v[t][e] - log_sum;
+        } else {
+            const float inv = 1.0f / s;
+#pragma unroll
+            for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tile.v[t][e] *= inv;
+        }
+        tile.store(out + r * cols, cols);
+    }
+}
+
+// softmax:     gx (+)= y * (g - sum(g*y)),  y = out
+// log_softmax: gx (+)= g - exp(out) * sum(g)
+template <int NT, int ITEMS, bool VEC, bool LOG>
+__global__ void __launch_bounds__(NT) softmax_bwd_kernel(const float* __restrict__ g, const float* __restrict__ out,
+                                                          float* __restrict__ gx, int acc, int64_t rows, int64_t cols) {
+    __shared__ float lds[NT / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        RowTile<NT, ITEMS, VEC> tg, ty;
+        tg.load(g + r * cols, cols, 0.f);
+        ty.load(out + r * cols, cols, 0.f);
+        float s = 0.f;
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s += LOG ? tg.v[t][e] : tg.v[t][e] * ty.v[t][e];
+        s = block_sum<NT>(s, lds);
+#pragma unroll
+        for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (LOG) tg.v[t][e] = tg.v[t][e] - expf(ty.v[t][e]) * s;
+                else tg.v[t][e] = ty.v[t][e] * (tg.v[t][e] - s);
+            }
+        if (acc) {
+            RowTile<NT, ITEMS, VEC> old;
+            old.load(gx + r * cols, cols, 0.f);
+#pragma unroll
+            for (int t = 0; t < ITEMS; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tg.v[t][e] = old.v[t][e] + tg.v[t][e];
+        }
+        tg.store(gx + r * cols, cols);
+    }
+}
+
+// Rows too long for the register tile: three streaming passes per row.
+template <bool LOG>
+__global__ void __launch_bounds__(1024) softmax_fwd_long_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                                 int64_t rows, int64_t cols) {
+    __shared__ float lds[16];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = x + r * cols;
+        float* orow = out + r * cols;
+        float m = -INFINITY;
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) m = fmaxf(m, xr[c]);
+        m = block_max<1024>(m, lds);
+        float s = 0.f;
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) s += expf(xr[c] - m);
+        s = block_sum<1024>(s, lds);
+        if (LOG) {
+            const float log_sum = m + logf(s);
+            for (int64_t c = threadIdx.x; c < cols; c += 1024) orow[c] = xr[c] - log_sum;
+        } else {
+            const float inv = 1.0f / s;
+            for (int64_t c = threadIdx.x; c < cols; c += 1024) orow[c] = expf(xr[c] - m) * inv;
+        }
+        __syncthreads();
+    }
+}
+
+template <bool LOG>
+__global__ void __launch_bounds__(1024) softmax_bwd_long_kernel(const float* __restrict__ g,
+                                                                 const float* __restrict__ out, float* __restrict__ gx,
+                                                                 int acc, int64_t rows, int64_t cols) {
+    __shared__ float lds[16];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* gr = g + r * cols;
+        const float* yr = out + r * cols;
+        float* dr = gx + r * cols;
+        float s = 0.f;
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) s += LOG ? gr[c] : gr[c] * yr[c];
+        s = block_sum<1024>(s, lds);
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) {
+            float d = LOG ? gr[c] - expf(yr[c]) * s : yr[c] * (gr[c] - s);
+            dr[c] = acc ? dr[c] + d : d;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host
+// ---------------------------------------------------------------------------
+
+// Pick the register tile: NT = 64 for rows up to 2048 columns, else 1024;
+// ITEMS the smallest power of two (<= 8) covering the row.
+struct TileChoice {
+    int nt = 0, items = 0;  // nt == 0: long-row path
+};
+
+static TileChoice choose_tile(int64_t cols) {
+    TileChoice t;
+    const int nts[2] = {64, 1024};
+    for (int nt : nts) {
+        for (int items = 1; items <= 8; items *= 2) {
+            if (cols <= (int64_t)nt * 4 * items) { t.nt = nt; t.items = items; return t; }
+        }
+    }
+    return t;
+}
+
+template <bool LOG>
+int launch_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
+    hipStream_t st = stream();
+    TileChoice tc = choose_tile(cols);
+    const bool vec = cols % 4 == 0 && aligned16(out) && aligned16(x);
+    // Several rows per CU in flight; the grid-stride loop covers the rest.
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    if (tc.nt == 0) {
+        hipLaunchKernelGGL(softmax_fwd_long_kernel<LOG>, grid, dim3(1024), 0, st, out, x, rows, cols);
+        return check_launch("wm_softmax_fwd(long)");
+    }
+#define WM_SF(NTv, IT)                                                                                        \
+    if (tc.nt == NTv && tc.items == IT) {                                                                     \
+        if (vec) hipLaunchKernelGGL((softmax_fwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
+        else hipLaunchKernelGGL((softmax_fwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
+        return check_launch("wm_softmax_fwd");                                                                \
+    }
+    WM_SF(64, 1) WM_SF(64, 2) WM_SF(64, 4) WM_SF(64, 8)
+    WM_SF(1024, 1) WM_SF(1024, 2) WM_SF(1024, 4) WM_SF(1024, 8)
+#undef WM_SF
+    return set_error(WM_ERR_INVALID, "wm_softmax_fwd: no tile");
+}
+
+template <bool LOG>
+int launch_softmax_bwd(const float* g, const float* out, float* gx, int acc, int64_t rows, int64_t cols) {
+    hipStream_t st = stream();
+    TileChoice tc = choose_tile(cols);
+    const bool vec = cols % 4 == 0 && aligned16(g) && aligned16(out) && aligned16(gx);
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    if (tc.nt == 0) {
+        hipLaunchKernelGGL(softmax_bwd_long_kernel<LOG>, grid, dim3(1024), 0, st, g, out, gx, acc, rows, cols);
+        return check_launch("wm_softmax_bwd(long)");
+    }
+#define WM_SB(NTv, IT)                                                                                              \
+    if (tc.nt == NTv && tc.items == IT) {                                                                           \
+        if (vec) hipLaunchKernelGGL((softmax_bwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
+        else hipLaunchKernelGGL((softmax_bwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
+        return check_launch("wm_softmax_bwd");                                                                      \
+    }
+    WM_SB(64, 1) WM_SB(64, 2) WM_SB(64, 4) WM_SB(64, 8)
+    WM_SB(1024, 1) WM_SB(1024, 2) WM_SB(1024, 4) WM_SB(1024, 8)
+#undef WM_SB
+    return set_error(WM_ERR_INVALID, "wm_softmax_bwd: no tile");
+}
+
+static int check_rc(int64_t rows, int64_t cols, const void* a, const void* b, const char* what) {
+    if (rows < 0 || cols < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative extent");
+    if (rows > 0 && cols > 0 && (!a || !b)) return set_error(WM_ERR_INVALID, std::string(what) + ": null pointer");
+    return WM_OK;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+int wm_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
+    WM_TRY(check_rc(rows, cols, out, x, "wm_softmax_fwd"));
+    if (rows == 0 || cols == 0) return WM_OK;
+    WM_CHECK_INIT();
+    return launch_softmax_fwd<false>(out, x, rows, cols);
+}
+
+int wm_log_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
+    WM_TRY(check_rc(rows, cols, out, x, "wm_log_softmax_fwd"));
+    if (rows == 0 || cols == 0) return WM_OK;
+    WM_CHECK_INIT();
+    return launch_softmax_fwd<true>(out, x, rows, cols);
+}
+
+int wm_softmax_bwd(const float* g, const float* out, float* gx, int accumulate, int64_t rows, int64_t cols) {
+    WM_TRY(check_rc(rows, cols, g, out, "wm_softmax_bwd"));
+    if (rows == 0 || cols == 0) return WM_OK;
+    if (!gx) return set_error(WM_ERR_INVALID, "wm_softmax_bwd: null gx");
+    WM_CHECK_INIT();
+    return launch_softmax_bwd<false>(g, out, gx, accumulate, rows, cols);
+}
+
+int wm_log_softmax_bwd(const float* g, const float* out, float* gx, int accumulate, int64_t rows, int64_t cols) {
+    WM_TRY(check_rc(rows, cols, g, out, "wm_log_softmax_bwd"));
+    if (rows == 0 || cols == 0) return WM_OK;
+    if (!gx) return set_error(WM_ERR_INVALID, "wm_log_softmax_bwd: null gx");
+    WM_CHECK_INIT();
+    return launch_softmax_bwd<true>(g, out, gx, accumulate, rows, cols);
+}
+
+}  // extern "C"
