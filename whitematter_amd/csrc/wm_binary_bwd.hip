@@ -32,9 +32,9 @@ constexpr int kBlock = 256;
 // ---------------------------------------------------------------------------
 
 template <int OP>
-__global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float4* __restrict__ g, const float4* __restrict__ a,
-                                                           const float4* __restrict__ b, const float4* __restrict__ o,
-                                                           float4* __restrict__ ga, int acc_a, float4* __restrict__ gb,
+__global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restrict__ g, const float* __restrict__ a,
+                                                           const float* __restrict__ b, const float* __restrict__ o,
+                                                           float* __restrict__ ga, int acc_a, float* __restrict__ gb,
                                                            int acc_b, int64_t n4) {
     const bool need_a = (ga && da_reads_a<OP>()) || (gb && db_reads_a<OP>());
     const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
@@ -43,10 +43,13 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float4* __restri
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
-        float4 vg = g[i];
-        float4 va = need_a ? a[i] : z;
-        float4 vb = need_b ? b[i] : z;
-        float4 vo = need_o ? o[i] : z;
+        const int64_t e = 4 * i;
+        float4 vg = ld_stream(g + e);
+        float4 va = need_a ? ld_stream(a + e) : z;
+        float4 vb = need_b ? ld_stream(b + e) : z;
+        float4 vo = need_o ? ld_stream(o + e) : z;
+        float4 oa = (ga && acc_a) ? ld_stream(ga + e) : z;
+        float4 ob = (gb && acc_b) ? ld_stream(gb + e) : z;
         if (recompute_o) {
             vo.x = binary_fwd<OP>(va.x, vb.x); vo.y = binary_fwd<OP>(va.y, vb.y);
             vo.z = binary_fwd<OP>(va.z, vb.z); vo.w = binary_fwd<OP>(va.w, vb.w);
@@ -57,11 +60,8 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float4* __restri
             r.y = binary_da<OP>(vg.y, va.y, vb.y);
             r.z = binary_da<OP>(vg.z, va.z, vb.z);
             r.w = binary_da<OP>(vg.w, va.w, vb.w);
-            if (acc_a) {
-                float4 old = ga[i];
-                r.x += old.x; r.y += old.y; r.z += old.z; r.w += old.w;
-            }
-            ga[i] = r;
+            if (acc_a) { r.x += oa.x; r.y += oa.y; r.z += oa.z; r.w += oa.w; }
+            st_stream(ga + e, r);
         }
         if (gb) {
             float4 r;
@@ -69,11 +69,8 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float4* __restri
             r.y = binary_db<OP>(vg.y, va.y, vb.y, vo.y);
             r.z = binary_db<OP>(vg.z, va.z, vb.z, vo.z);
             r.w = binary_db<OP>(vg.w, va.w, vb.w, vo.w);
-            if (acc_b) {
-                float4 old = gb[i];
-                r.x += old.x; r.y += old.y; r.z += old.z; r.w += old.w;
-            }
-            gb[i] = r;
+            if (acc_b) { r.x += ob.x; r.y += ob.y; r.z += ob.z; r.w += ob.w; }
+            st_stream(gb + e, r);
         }
     }
 }
@@ -106,11 +103,13 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 vv = need_V ? *reinterpret_cast<const float4*>(V + c) : z;
     float4 s = z;
+#pragma unroll 4
     for (int64_t r = r0; r < r1; ++r) {
         const int64_t off = r * C + c;
-        float4 vg = *reinterpret_cast<const float4*>(g + off);
-        float4 vf = need_F ? *reinterpret_cast<const float4*>(F + off) : z;
-        float4 vo = need_o ? *reinterpret_cast<const float4*>(o + off) : z;
+        float4 vg = ld_stream(g + off);
+        float4 vf = need_F ? ld_stream(F + off) : z;
+        float4 vo = need_o ? ld_stream(o + off) : z;
+        float4 old = (gF && accF) ? ld_stream(gF + off) : z;
         float4 av = VB ? vf : vv, bv = VB ? vv : vf;
         if (want_o && !o) {
             vo.x = binary_fwd<OP>(av.x, bv.x); vo.y = binary_fwd<OP>(av.y, bv.y);
@@ -125,12 +124,8 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
                 d.x = binary_db<OP>(vg.x, av.x, bv.x, vo.x); d.y = binary_db<OP>(vg.y, av.y, bv.y, vo.y);
                 d.z = binary_db<OP>(vg.z, av.z, bv.z, vo.z); d.w = binary_db<OP>(vg.w, av.w, bv.w, vo.w);
             }
-            float4* p = reinterpret_cast<float4*>(gF + off);
-            if (accF) {
-                float4 old = *p;
-                d.x += old.x; d.y += old.y; d.z += old.z; d.w += old.w;
-            }
-            *p = d;
+            if (accF) { d.x += old.x; d.y += old.y; d.z += old.z; d.w += old.w; }
+            st_stream(gF + off, d);
         }
         if (want_v) {
             if constexpr (VB) {
@@ -145,20 +140,31 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
     if (want_v) *reinterpret_cast<float4*>(part + (int64_t)blockIdx.y * C + c) = s;
 }
 
-// out[c] (+)= sum_k part[k, c], k in 0..K-1, with 8 interleaved accumulators
-// combined pairwise (fixed order).
+// out[c] (+)= sum_k part[k, c], k in 0..K-1.  A workgroup owns 64 adjacent
+// columns; its 4 waves take k = w, w+4, w+8, ... (8 interleaved accumulators
+// each), and the 4 wave sums are added in wave order through LDS.
 __global__ void __launch_bounds__(kBlock) colsum_finalize_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                                   int acc, int64_t K, int64_t C) {
-    for (int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x; c < C; c += (int64_t)gridDim.x * kBlock) {
+    __shared__ float lds[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int64_t c0 = (int64_t)blockIdx.x * 64; c0 < C; c0 += (int64_t)gridDim.x * 64) {
+        const int64_t c = c0 + lane;
         float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        int64_t k = 0;
-        for (; k + 8 <= K; k += 8) {
+        if (c < C) {
+            int64_t k = w;
+            for (; k + 28 < K; k += 32) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s[j] += part[(k + j) * C + c];
+                for (int j = 0; j < 8; ++j) s[j] += part[(k + 4 * j) * C + c];
+            }
+            for (int j = 0; k < K; k += 4, ++j) s[j & 7] += part[k * C + c];
         }
-        for (int j = 0; k < K; ++k, ++j) s[j] += part[k * C + c];
-        float t = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
-        out[c] = acc ? out[c] + t : t;
+        lds[w][lane] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+        __syncthreads();
+        if (w == 0 && c < C) {
+            float t = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+            out[c] = acc ? out[c] + t : t;
+        }
+        __syncthreads();
     }
 }
 
@@ -199,10 +205,13 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
         float s = 0.f;
         if constexpr (VEC) {
             float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
             for (int64_t c = c0 + lane * 4; c < c1; c += 256) {
-                float4 vg = *reinterpret_cast<const float4*>(gr + c);
-                float4 vf = need_F ? *reinterpret_cast<const float4*>(fr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-                float4 vo = need_o ? *reinterpret_cast<const float4*>(orow + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 vg = ld_stream(gr + c);
+                float4 vf = need_F ? ld_stream(fr + c) : z4;
+                float4 vo = need_o ? ld_stream(orow + c) : z4;
+                float4 old = (gfr && accF) ? ld_stream(gfr + c) : z4;
                 float e[4] = {vf.x, vf.y, vf.z, vf.w}, gg[4] = {vg.x, vg.y, vg.z, vg.w},
                       oo[4] = {vo.x, vo.y, vo.z, vo.w}, d[4], sv[4];
 #pragma unroll
@@ -213,13 +222,9 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
                     else { d[j] = binary_db<OP>(gg[j], av, bv, oo[j]); sv[j] = binary_da<OP>(gg[j], av, bv); }
                 }
                 if (gfr) {
-                    float4* p = reinterpret_cast<float4*>(gfr + c);
                     float4 nd = make_float4(d[0], d[1], d[2], d[3]);
-                    if (accF) {
-                        float4 old = *p;
-                        nd.x += old.x; nd.y += old.y; nd.z += old.z; nd.w += old.w;
-                    }
-                    *p = nd;
+                    if (accF) { nd.x += old.x; nd.y += old.y; nd.z += old.z; nd.w += old.w; }
+                    st_stream(gfr + c, nd);
                 }
                 s4.x += sv[0]; s4.y += sv[1]; s4.z += sv[2]; s4.w += sv[3];
             }
@@ -342,10 +347,8 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
     if (a_full && b_full) {
         if (numel % 4 == 0 && aligned) {
             int64_t n4 = numel / 4;
-            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock, 16)), dim3(kBlock), 0, st,
-                               reinterpret_cast<const float4*>(g), reinterpret_cast<const float4*>(a),
-                               reinterpret_cast<const float4*>(b), reinterpret_cast<const float4*>(o),
-                               reinterpret_cast<float4*>(ga), acc_a, reinterpret_cast<float4*>(gb), acc_b, n4);
+            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock, 32)), dim3(kBlock), 0, st, g, a, b, o,
+                               ga, acc_a, gb, acc_b, n4);
             return check_launch("wm_binary_bwd(flat)");
         }
     }
@@ -380,7 +383,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
                                    ws.as<float>(), R, C, rpc);
             WM_TRY(check_launch("wm_binary_bwd(colsum)"));
             if (gV) {
-                hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid_for(C, kBlock, 4)), dim3(kBlock), 0, st,
+                hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st,
                                    ws.as<float>(), gV, accV, K, C);
                 WM_TRY(check_launch("wm_binary_bwd(colsum finalize)"));
             }

@@ -65,6 +65,27 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // Device helpers
 // ---------------------------------------------------------------------------
 
+// Streaming (non-temporal) 128-bit and 32-bit global accesses for data that is
+// touched once per kernel: inputs read once, outputs written once, gradient
+// read-modify-writes.  Measured on MI355X: a read-only sweep reaches ~6.8 TB/s
+// with non-temporal loads against ~4.4 TB/s with cached loads when the
+// caches hold dirty lines from earlier work.  Data that is reused across
+// threads (broadcast vectors, partial sums) keeps ordinary cached loads.
+typedef float wm_v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 ld_stream(const float* p) {
+    wm_v4f v = __builtin_nontemporal_load(reinterpret_cast<const wm_v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void st_stream(float* p, float4 v) {
+    wm_v4f w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<wm_v4f*>(p));
+}
+
+__device__ __forceinline__ float ld_stream1(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_stream1(float* p, float v) { __builtin_nontemporal_store(v, p); }
+
 // DPP lane moves inside a 16-lane row (deterministic, no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {

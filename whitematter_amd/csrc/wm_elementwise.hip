@@ -15,7 +15,7 @@
 namespace wm {
 
 constexpr int kBlock = 256;   // 4 waves
-constexpr int kUnroll = 2;    // float4 loads in flight per thread per step
+constexpr int kUnroll = 4;    // float4 loads in flight per thread per step
 
 // ---------------------------------------------------------------------------
 // Broadcast layout (host)
@@ -121,10 +121,10 @@ __device__ __forceinline__ void row_offsets(const RowDims& d, int64_t row, int64
 // Kernels
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(kBlock) fill_vec_kernel(float4* __restrict__ out, float v, int64_t n4) {
+__global__ void __launch_bounds__(kBlock) fill_vec_kernel(float* __restrict__ out, float v, int64_t n4) {
     const int64_t stride = (int64_t)gridDim.x * kBlock;
-    float4 f = make_float4(v, v, v, v);
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) out[i] = f;
+    const float4 f = make_float4(v, v, v, v);
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) st_stream(out + 4 * i, f);
 }
 
 __global__ void __launch_bounds__(kBlock) fill_scalar_kernel(float* __restrict__ out, float v, int64_t n) {
@@ -132,19 +132,20 @@ __global__ void __launch_bounds__(kBlock) fill_scalar_kernel(float* __restrict__
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = v;
 }
 
-__global__ void __launch_bounds__(kBlock) copy_vec_kernel(float4* __restrict__ dst, const float4* __restrict__ src, int64_t n4) {
+__global__ void __launch_bounds__(kBlock) copy_vec_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                           int64_t n4) {
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
         float4 v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) v[u] = src[i];
+            if (i < n4) v[u] = ld_stream(src + 4 * i);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) dst[i] = v[u];
+            if (i < n4) st_stream(dst + 4 * i, v[u]);
         }
     }
 }
@@ -216,15 +217,15 @@ __global__ void __launch_bounds__(kBlock) f16_to_f32_kernel(float* __restrict__ 
 
 // Same-shape binary op over float4s (the reference fast path, shape == other->shape).
 template <int OP>
-__global__ void __launch_bounds__(kBlock) binary_flat_kernel(float4* __restrict__ out, const float4* __restrict__ a,
-                                                              const float4* __restrict__ b, int64_t n4) {
+__global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__ out, const float* __restrict__ a,
+                                                              const float* __restrict__ b, int64_t n4) {
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
         float4 va[kUnroll], vb[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) { va[u] = a[i]; vb[u] = b[i]; }
+            if (i < n4) { va[u] = ld_stream(a + 4 * i); vb[u] = ld_stream(b + 4 * i); }
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -235,7 +236,7 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float4* __restrict_
                 r.y = binary_fwd<OP>(va[u].y, vb[u].y);
                 r.z = binary_fwd<OP>(va[u].z, vb[u].z);
                 r.w = binary_fwd<OP>(va[u].w, vb[u].w);
-                out[i] = r;
+                st_stream(out + 4 * i, r);
             }
         }
     }
@@ -245,10 +246,12 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float4* __restrict_
 // kBlock*4*kUnroll elements; the row's operand offsets come from the outer
 // dims once per tile.  AI/BI: stride of a/b along inner (1 = contiguous,
 // 0 = one value per row).  VEC: inner % 4 == 0 and 16-byte aligned bases.
+// SA/SB: the operand is streamed (read once: it has a row stride), else it
+// is a row vector reused by every row and stays on cached loads.
 template <int OP, int AI, int BI, bool VEC>
 __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a,
                                                               const float* __restrict__ b, int64_t rows, int64_t inner,
-                                                              RowDims d) {
+                                                              RowDims d, int stream_a, int stream_b) {
     constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * kUnroll;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
     const int64_t tiles = rows * tiles_per_row;
@@ -268,8 +271,10 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
                 if (c < inner) {
-                    va[u] = AI ? *reinterpret_cast<const float4*>(ar + c) : make_float4(sa0, sa0, sa0, sa0);
-                    vb[u] = BI ? *reinterpret_cast<const float4*>(br + c) : make_float4(sb0, sb0, sb0, sb0);
+                    va[u] = AI ? (stream_a ? ld_stream(ar + c) : *reinterpret_cast<const float4*>(ar + c))
+                               : make_float4(sa0, sa0, sa0, sa0);
+                    vb[u] = BI ? (stream_b ? ld_stream(br + c) : *reinterpret_cast<const float4*>(br + c))
+                               : make_float4(sb0, sb0, sb0, sb0);
                 }
             }
 #pragma unroll
@@ -281,7 +286,7 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
                     r.y = binary_fwd<OP>(va[u].y, vb[u].y);
                     r.z = binary_fwd<OP>(va[u].z, vb[u].z);
                     r.w = binary_fwd<OP>(va[u].w, vb[u].w);
-                    *reinterpret_cast<float4*>(orow + c) = r;
+                    st_stream(orow + c, r);
                 }
             }
         } else {
@@ -330,14 +335,12 @@ __global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ o
                                                             int64_t n, float p0, float p1) {
     const int64_t n4 = n / 4;
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    float4* o4 = reinterpret_cast<float4*>(out);
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
         float4 v[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) v[u] = x4[i];
+            if (i < n4) v[u] = ld_stream(x + 4 * i);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
@@ -348,7 +351,7 @@ __global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ o
                 r.y = unary_fwd<OP>(v[u].y, p0, p1);
                 r.z = unary_fwd<OP>(v[u].z, p0, p1);
                 r.w = unary_fwd<OP>(v[u].w, p0, p1);
-                o4[i] = r;
+                st_stream(out + 4 * i, r);
             }
         }
     }
@@ -384,10 +387,10 @@ __global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restri
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
             if (i < n4) {
-                vg[u] = reinterpret_cast<const float4*>(g)[i];
-                vx[u] = RX ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                vo[u] = RO ? reinterpret_cast<const float4*>(o)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                vgx[u] = ACC ? reinterpret_cast<const float4*>(gx)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                vg[u] = ld_stream(g + 4 * i);
+                vx[u] = RX ? ld_stream(x + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vo[u] = RO ? ld_stream(o + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vgx[u] = ACC ? ld_stream(gx + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
 #pragma unroll
@@ -399,7 +402,7 @@ __global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restri
                 r.y = ubwd1<OP, ACC>(vg[u].y, vx[u].y, vo[u].y, vgx[u].y, p0, p1);
                 r.z = ubwd1<OP, ACC>(vg[u].z, vx[u].z, vo[u].z, vgx[u].z, p0, p1);
                 r.w = ubwd1<OP, ACC>(vg[u].w, vx[u].w, vo[u].w, vgx[u].w, p0, p1);
-                reinterpret_cast<float4*>(gx)[i] = r;
+                st_stream(gx + 4 * i, r);
             }
         }
     }
@@ -430,9 +433,8 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     // Same shape (or both fully contiguous after folding): flat float4 walk.
     if (nd == 1 && ia == 1 && ib == 1 && (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         int64_t n4 = inner / 4;
-        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * kUnroll)), dim3(kBlock), 0, s,
-                           reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(a),
-                           reinterpret_cast<const float4*>(b), n4);
+        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * kUnroll, 32)), dim3(kBlock), 0, s,
+                           out, a, b, n4);
         return check_launch("wm_binary(flat)");
     }
     if (inner >= 64 && (ia == 0 || ia == 1) && (ib == 0 || ib == 1)) {
@@ -447,9 +449,17 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
         int64_t tile = (vec ? 4 : 1) * kBlock * kUnroll;
         int64_t tiles = rows * ((inner + tile - 1) / tile);
-        dim3 grid(grid_for(tiles, 1, 16));
+        dim3 grid(grid_for(tiles, 1, 32));
+        // An operand with a row stride is read once; a row vector is re-read by every row.
+        int stream_a = 0, stream_b = 0;
+        for (int i = 0; i < nd - 1; ++i) {
+            if (L.sa[i] != 0) stream_a = 1;
+            if (L.sb[i] != 0) stream_b = 1;
+        }
+        if (nd == 1) stream_a = stream_b = 1;
 #define WM_ROWS(AI, BI, V) \
-    hipLaunchKernelGGL((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d)
+    hipLaunchKernelGGL((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
+                       stream_a, stream_b)
         if (vec) {
             if (ia && ib) WM_ROWS(1, 1, true);
             else if (ia) WM_ROWS(1, 0, true);
@@ -476,7 +486,7 @@ template <int OP>
 int launch_unary(float* out, const float* x, int64_t n, float p0, float p1) {
     hipStream_t s = stream();
     if (aligned16(out) && aligned16(x)) {
-        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * kUnroll)), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * kUnroll, 32)), dim3(kBlock), 0, s,
                            out, x, n, p0, p1);
     } else {
         hipLaunchKernelGGL(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
@@ -494,7 +504,7 @@ int launch_unary_bwd(const float* g, const float* x, const float* o, float* gx, 
     if (RX && !x) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward input x");
     if (RO && !o) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward output");
     bool vec = aligned16(g) && aligned16(gx) && (!RX || aligned16(x)) && (!RO || aligned16(o));
-    dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll)), grid_s(grid_for(n, kBlock));
+    dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll, 32)), grid_s(grid_for(n, kBlock));
     if (vec) {
         if (acc) hipLaunchKernelGGL((unary_bwd_kernel<OP, true>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
         else hipLaunchKernelGGL((unary_bwd_kernel<OP, false>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
@@ -531,8 +541,8 @@ int wm_fill(float* out, float value, int64_t n) {
     if (!out) return set_error(WM_ERR_INVALID, "wm_fill: null pointer");
     WM_CHECK_INIT();
     if (aligned16(out) && n % 4 == 0) {
-        hipLaunchKernelGGL(fill_vec_kernel, dim3(grid_for(n / 4, kBlock)), dim3(kBlock), 0, stream(),
-                           reinterpret_cast<float4*>(out), value, n / 4);
+        hipLaunchKernelGGL(fill_vec_kernel, dim3(grid_for(n / 4, kBlock, 64)), dim3(kBlock), 0, stream(), out,
+                           value, n / 4);
     } else {
         hipLaunchKernelGGL(fill_scalar_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, stream(), out, value, n);
     }
@@ -546,8 +556,8 @@ int wm_copy_kernel(float* dst, const float* src, int64_t n) {
     if (n % 4 || !aligned16(dst) || !aligned16(src))
         return set_error(WM_ERR_INVALID, "wm_copy_kernel: needs 16-byte aligned buffers and n % 4 == 0");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll)), dim3(kBlock), 0, stream(),
-                       reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), n / 4);
+    hipLaunchKernelGGL(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll, 32)), dim3(kBlock), 0, stream(), dst,
+                       src, n / 4);
     return check_launch("wm_copy_kernel");
 }
 

@@ -37,13 +37,13 @@ __device__ __forceinline__ bool strictly_better(float x, float v) {
 
 // Fold element x at position k into (v, i); positions arrive in increasing
 // order within one thread.
+// Branch-free: an empty state takes any non-NaN element (or a NaN at
+// position 0); a non-empty one only a strictly better element.
 template <bool MAXOP>
 __device__ __forceinline__ void scan_push(float& v, int64_t& i, float x, int64_t k) {
-    if (i == kEmpty) {
-        if (!__builtin_isnan(x) || k == 0) { v = x; i = k; }
-    } else if (strictly_better<MAXOP>(x, v)) {
-        v = x; i = k;
-    }
+    const bool take = strictly_better<MAXOP>(x, v) || (i == kEmpty && (!__builtin_isnan(x) || k == 0));
+    v = take ? x : v;
+    i = take ? k : i;
 }
 
 // Combine two states over disjoint position sets (any order).
@@ -91,7 +91,8 @@ __device__ __forceinline__ void write_result(float* val, int64_t* idx, int64_t s
 // ---------------------------------------------------------------------------
 
 // One wave per (row, chunk).  Partials (value, position) go to pv/pi when the
-// row is split (K > 1), else the result is written directly.
+// row is split (K > 1), else the result is written directly.  Each lane keeps
+// four 128-bit loads in flight and folds them in increasing position order.
 template <int OP, bool VEC>
 __global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __restrict__ x, int64_t rows, int64_t n,
                                                               int64_t chunk, int64_t K, float* __restrict__ val,
@@ -107,58 +108,48 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __rest
         const int64_t c0 = k * chunk;
         const int64_t c1 = min(n, c0 + chunk);
         const float* xr = x + r * n;
-        float v;
+        float v = 0.f;
         int64_t pos = kEmpty;
-        if constexpr (KIND == 0) {
-            float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-            if constexpr (VEC) {
-                int64_t c = c0 + lane * 4;
-                for (; c + 3 * 256 < c1; c += 4 * 256) {
-                    float4 a0 = *reinterpret_cast<const float4*>(xr + c);
-                    float4 a1 = *reinterpret_cast<const float4*>(xr + c + 256);
-                    float4 a2 = *reinterpret_cast<const float4*>(xr + c + 512);
-                    float4 a3 = *reinterpret_cast<const float4*>(xr + c + 768);
-                    s.x += (a0.x + a1.x) + (a2.x + a3.x);
-                    s.y += (a0.y + a1.y) + (a2.y + a3.y);
-                    s.z += (a0.z + a1.z) + (a2.z + a3.z);
-                    s.w += (a0.w + a1.w) + (a2.w + a3.w);
+        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (VEC) {
+            int64_t c = c0 + lane * 4;
+            for (; c + 3 * 256 < c1; c += 4 * 256) {
+                float4 a[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) a[u] = ld_stream(xr + c + u * 256);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if constexpr (KIND == 0) {
+                        s.x += a[u].x; s.y += a[u].y; s.z += a[u].z; s.w += a[u].w;
+                    } else {
+                        const int64_t p = c + u * 256;
+                        scan_push<KIND == 1>(v, pos, a[u].x, p);
+                        scan_push<KIND == 1>(v, pos, a[u].y, p + 1);
+                        scan_push<KIND == 1>(v, pos, a[u].z, p + 2);
+                        scan_push<KIND == 1>(v, pos, a[u].w, p + 3);
+                    }
                 }
-                for (; c < c1; c += 256) {
-                    float4 a0 = *reinterpret_cast<const float4*>(xr + c);
+            }
+            for (; c < c1; c += 256) {
+                float4 a0 = ld_stream(xr + c);
+                if constexpr (KIND == 0) {
                     s.x += a0.x; s.y += a0.y; s.z += a0.z; s.w += a0.w;
+                } else {
+                    scan_push<KIND == 1>(v, pos, a0.x, c);
+                    scan_push<KIND == 1>(v, pos, a0.y, c + 1);
+                    scan_push<KIND == 1>(v, pos, a0.z, c + 2);
+                    scan_push<KIND == 1>(v, pos, a0.w, c + 3);
                 }
-            } else {
-                for (int64_t c = c0 + lane; c < c1; c += 64) s.x += xr[c];
             }
-            v = wave_sum((s.x + s.y) + (s.z + s.w));
         } else {
-            v = 0.f;
-            if constexpr (VEC) {
-                int64_t c = c0 + lane * 4;
-                for (; c + 256 < c1; c += 2 * 256) {
-                    float4 a0 = *reinterpret_cast<const float4*>(xr + c);
-                    float4 a1 = *reinterpret_cast<const float4*>(xr + c + 256);
-                    scan_push<KIND == 1>(v, pos, a0.x, c);
-                    scan_push<KIND == 1>(v, pos, a0.y, c + 1);
-                    scan_push<KIND == 1>(v, pos, a0.z, c + 2);
-                    scan_push<KIND == 1>(v, pos, a0.w, c + 3);
-                    scan_push<KIND == 1>(v, pos, a1.x, c + 256);
-                    scan_push<KIND == 1>(v, pos, a1.y, c + 257);
-                    scan_push<KIND == 1>(v, pos, a1.z, c + 258);
-                    scan_push<KIND == 1>(v, pos, a1.w, c + 259);
-                }
-                for (; c < c1; c += 256) {
-                    float4 a0 = *reinterpret_cast<const float4*>(xr + c);
-                    scan_push<KIND == 1>(v, pos, a0.x, c);
-                    scan_push<KIND == 1>(v, pos, a0.y, c + 1);
-                    scan_push<KIND == 1>(v, pos, a0.z, c + 2);
-                    scan_push<KIND == 1>(v, pos, a0.w, c + 3);
-                }
-            } else {
-                for (int64_t c = c0 + lane; c < c1; c += 64) scan_push<KIND == 1>(v, pos, xr[c], c);
+            for (int64_t c = c0 + lane; c < c1; c += 64) {
+                float a0 = ld_stream1(xr + c);
+                if constexpr (KIND == 0) s.x += a0;
+                else scan_push<KIND == 1>(v, pos, a0, c);
             }
-            wave_combine<KIND == 1>(v, pos);
         }
+        if constexpr (KIND == 0) v = wave_sum((s.x + s.y) + (s.z + s.w));
+        else wave_combine<KIND == 1>(v, pos);
         if (lane == 0) {
             if (K == 1) write_result<OP>(val, idx, r, v, pos, n);
             else {
@@ -181,14 +172,29 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
     __shared__ int64_t li[kBlock / 64];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         if constexpr (KIND == 0) {
-            float s = 0.f;
-            for (int64_t k = threadIdx.x; k < K; k += kBlock) s += pv[r * K + k];
+            float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            int64_t k = threadIdx.x;
+            for (; k + 7 * kBlock < K; k += 8 * kBlock) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a[j] += pv[r * K + k + j * kBlock];
+            }
+            for (int j = 0; k < K; k += kBlock, ++j) a[j & 7] += pv[r * K + k];
+            float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
             s = block_sum<kBlock>(s, lv);
             if (threadIdx.x == 0) write_result<OP>(val, idx, r, s, 0, n);
         } else {
             float v = 0.f;
             int64_t pos = kEmpty;
-            for (int64_t k = threadIdx.x; k < K; k += kBlock) combine<KIND == 1>(v, pos, pv[r * K + k], pi[r * K + k]);
+            int64_t k = threadIdx.x;
+            for (; k + 7 * kBlock < K; k += 8 * kBlock) {
+                float bv[8];
+                int64_t bi[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) { bv[j] = pv[r * K + k + j * kBlock]; bi[j] = pi[r * K + k + j * kBlock]; }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) combine<KIND == 1>(v, pos, bv[j], bi[j]);
+            }
+            for (; k < K; k += kBlock) combine<KIND == 1>(v, pos, pv[r * K + k], pi[r * K + k]);
             wave_combine<KIND == 1>(v, pos);
             if ((threadIdx.x & 63) == 0) { lv[threadIdx.x >> 6] = v; li[threadIdx.x >> 6] = pos; }
             __syncthreads();
@@ -207,9 +213,11 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
 // inner > 1: columns
 // ---------------------------------------------------------------------------
 
-// Thread t of the launch owns inner positions [i0, i0+W) (W = 4 when VEC) of
-// output row o, and walks positions [k0, k1) of n.  Items are
-// (o, chunk, inner tile) triples, tile fastest.
+// Thread t of a workgroup owns W adjacent inner positions (W = 4 with
+// 128-bit loads) of output row o, so the workgroup reads 256*W contiguous
+// floats per position of n, and walks positions [k0, k1) of n in increasing
+// order with four loads in flight.  Items are (o, chunk, inner tile)
+// triples, tile fastest.
 template <int OP, bool VEC>
 __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __restrict__ x, int64_t outer, int64_t n,
                                                               int64_t inner, int64_t chunk, int64_t K,
@@ -234,34 +242,32 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 #pragma unroll
         for (int j = 0; j < W; ++j) { v[j] = 0.f; pos[j] = kEmpty; }
         int64_t p = k0;
-        // Two rows per step keeps two 128-bit loads in flight per thread.
-        for (; p + 1 < k1; p += 2) {
-            float a[W], b[W];
-            if constexpr (VEC) {
-                float4 a4 = *reinterpret_cast<const float4*>(xp + p * inner);
-                float4 b4 = *reinterpret_cast<const float4*>(xp + (p + 1) * inner);
-                a[0] = a4.x; a[1] = a4.y; a[2] = a4.z; a[3] = a4.w;
-                b[0] = b4.x; b[1] = b4.y; b[2] = b4.z; b[3] = b4.w;
-            } else {
-                a[0] = xp[p * inner];
-                b[0] = xp[(p + 1) * inner];
-            }
+        for (; p + 3 < k1; p += 4) {
+            float a[4][W];
 #pragma unroll
-            for (int j = 0; j < W; ++j) {
-                if constexpr (KIND == 0) v[j] += a[j] + b[j];
-                else {
-                    scan_push<KIND == 1>(v[j], pos[j], a[j], p);
-                    scan_push<KIND == 1>(v[j], pos[j], b[j], p + 1);
+            for (int u = 0; u < 4; ++u) {
+                if constexpr (VEC) {
+                    float4 q = ld_stream(xp + (p + u) * inner);
+                    a[u][0] = q.x; a[u][1] = q.y; a[u][2] = q.z; a[u][3] = q.w;
+                } else {
+                    a[u][0] = ld_stream1(xp + (p + u) * inner);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int j = 0; j < W; ++j) {
+                    if constexpr (KIND == 0) v[j] += a[u][j];
+                    else scan_push<KIND == 1>(v[j], pos[j], a[u][j], p + u);
+                }
         }
-        if (p < k1) {
+        for (; p < k1; ++p) {
             float a[W];
             if constexpr (VEC) {
-                float4 a4 = *reinterpret_cast<const float4*>(xp + p * inner);
-                a[0] = a4.x; a[1] = a4.y; a[2] = a4.z; a[3] = a4.w;
+                float4 q = ld_stream(xp + p * inner);
+                a[0] = q.x; a[1] = q.y; a[2] = q.z; a[3] = q.w;
             } else {
-                a[0] = xp[p * inner];
+                a[0] = ld_stream1(xp + p * inner);
             }
 #pragma unroll
             for (int j = 0; j < W; ++j) {
@@ -272,6 +278,7 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 #pragma unroll
         for (int j = 0; j < W; ++j) {
             const int64_t i = i0 + j;
+            if (i >= inner) break;
             if (K == 1) write_result<OP>(val, idx, o * inner + i, v[j], pos[j], n);
             else {
                 pv[(o * K + k) * inner + i] = v[j];
@@ -281,8 +288,9 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
     }
 }
 
-// Second pass for split columns: thread per (o, i), chunks combined with
-// 8 interleaved accumulators (sum) or the ordered combine.
+// Second pass for split columns.  A workgroup owns 64 adjacent output slots;
+// its 4 waves take chunks k = w, w+4, ... and the wave results are combined
+// in wave order through LDS.
 template <int OP>
 __global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const float* __restrict__ pv,
                                                                        const int64_t* __restrict__ pi, int64_t outer,
@@ -290,27 +298,57 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const floa
                                                                        float* __restrict__ val,
                                                                        int64_t* __restrict__ idx) {
     constexpr int KIND = kind_of(OP);
+    __shared__ float lv[4][64];
+    __shared__ int64_t li[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t total = outer * inner;
-    for (int64_t s = (int64_t)blockIdx.x * kBlock + threadIdx.x; s < total; s += (int64_t)gridDim.x * kBlock) {
-        const int64_t o = s / inner, i = s - o * inner;
-        const float* pvs = pv + o * K * inner + i;
-        if constexpr (KIND == 0) {
-            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            int64_t k = 0;
-            for (; k + 8 <= K; k += 8) {
+    for (int64_t s0 = (int64_t)blockIdx.x * 64; s0 < total; s0 += (int64_t)gridDim.x * 64) {
+        const int64_t s = s0 + lane;
+        float rv = 0.f;
+        int64_t ri = kEmpty;
+        if (s < total) {
+            const int64_t o = s / inner, i = s - o * inner;
+            const float* pvs = pv + o * K * inner + i;
+            if constexpr (KIND == 0) {
+                float acc[4] = {0.f, 0.f, 0.f, 0.f};
+                int64_t k = w;
+                for (; k + 12 < K; k += 16) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc[j] += pvs[(k + j) * inner];
+                    for (int j = 0; j < 4; ++j) acc[j] += pvs[(k + 4 * j) * inner];
+                }
+                for (int j = 0; k < K; k += 4, ++j) acc[j & 3] += pvs[k * inner];
+                rv = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            } else {
+                const int64_t* pis = pi + o * K * inner + i;
+                int64_t k = w;
+                for (; k + 28 < K; k += 32) {
+                    float bv[8];
+                    int64_t bi[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) { bv[j] = pvs[(k + 4 * j) * inner]; bi[j] = pis[(k + 4 * j) * inner]; }
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) combine<KIND == 1>(rv, ri, bv[j], bi[j]);
+                }
+                for (; k < K; k += 4) combine<KIND == 1>(rv, ri, pvs[k * inner], pis[k * inner]);
             }
-            for (int j = 0; k < K; ++k, ++j) acc[j] += pvs[k * inner];
-            float t = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-            write_result<OP>(val, idx, s, t, 0, n);
-        } else {
-            const int64_t* pis = pi + o * K * inner + i;
-            float v = 0.f;
-            int64_t pos = kEmpty;
-            for (int64_t k = 0; k < K; ++k) combine<KIND == 1>(v, pos, pvs[k * inner], pis[k * inner]);
-            write_result<OP>(val, idx, s, v, pos, n);
         }
+        lv[w][lane] = rv;
+        li[w][lane] = ri;
+        __syncthreads();
+        if (w == 0 && s < total) {
+            float tv;
+            int64_t ti = kEmpty;
+            if constexpr (KIND == 0) {
+                tv = (lv[0][lane] + lv[1][lane]) + (lv[2][lane] + lv[3][lane]);
+            } else {
+                tv = lv[0][lane]; ti = li[0][lane];
+                combine<KIND == 1>(tv, ti, lv[1][lane], li[1][lane]);
+                combine<KIND == 1>(tv, ti, lv[2][lane], li[2][lane]);
+                combine<KIND == 1>(tv, ti, lv[3][lane], li[3][lane]);
+            }
+            write_result<OP>(val, idx, s, tv, ti, n);
+        }
+        __syncthreads();
     }
 }
 
@@ -384,7 +422,7 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
     const int64_t target_waves = (int64_t)num_cus() * 32;
     if (inner == 1) {
         int64_t K = 1;
-        if (outer < target_waves) K = std::min<int64_t>((target_waves + outer - 1) / outer, (n + 1023) / 1024);
+        if (outer < target_waves) K = std::min<int64_t>((target_waves + outer - 1) / outer, (n + 4095) / 4096);
         K = std::max<int64_t>(K, 1);
         int64_t chunk = (n + K - 1) / K;
         chunk = (chunk + 255) / 256 * 256;
@@ -411,18 +449,18 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
     const bool vec = (inner % 4 == 0) && aligned16(x);
     const int64_t tile = (int64_t)kBlock * (vec ? 4 : 1);
     const int64_t tiles = (inner + tile - 1) / tile;
-    // Aim for ~16 workgroups per CU; each chunk keeps >= 16 positions.
-    const int64_t target_blocks = (int64_t)num_cus() * 16;
+    // ~4 workgroups per CU, each thread walking at least 32 positions of n.
+    const int64_t target_blocks = (int64_t)num_cus() * 4;
     int64_t K = 1;
     if (outer * tiles < target_blocks)
-        K = std::min<int64_t>((target_blocks + outer * tiles - 1) / (outer * tiles), (n + 15) / 16);
-    K = std::max<int64_t>(K, 1);
+        K = std::min<int64_t>((target_blocks + outer * tiles - 1) / (outer * tiles), (n + 31) / 32);
+    K = std::max<int64_t>(std::min<int64_t>(K, 4096), 1);
     const int64_t chunk = (n + K - 1) / K;
     K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
     Workspace wv(K > 1 ? (size_t)(outer * K * inner) * sizeof(float) : 0);
     Workspace wi(K > 1 && KIND != 0 ? (size_t)(outer * K * inner) * sizeof(int64_t) : 0);
     if (K > 1 && (!wv.p || (KIND != 0 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
-    dim3 grid(grid_for(outer * K * tiles, 1, 16));
+    dim3 grid(grid_for(outer * K * tiles, 1, 32));
     if (vec)
         hipLaunchKernelGGL((reduce_cols_kernel<OP, true>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val,
                            idx, wv.as<float>(), wi.as<int64_t>());
@@ -431,7 +469,7 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
                            val, idx, wv.as<float>(), wi.as<int64_t>());
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
-        hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, kBlock, 8)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 64, 8)), dim3(kBlock), 0,
                            st, wv.as<float>(), wi.as<int64_t>(), outer, K, inner, n, val, idx);
         WM_TRY(check_launch("wm_reduce(cols finalize)"));
     }

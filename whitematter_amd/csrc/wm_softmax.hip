@@ -48,7 +48,7 @@ struct RowTile {
             if constexpr (VEC) {
                 int64_t c = col(t, 0);
                 if (c < cols) {
-                    float4 q = *reinterpret_cast<const float4*>(row + c);
+                    float4 q = ld_stream(row + c);
                     v[t][0] = q.x; v[t][1] = q.y; v[t][2] = q.z; v[t][3] = q.w;
                 } else {
                     v[t][0] = v[t][1] = v[t][2] = v[t][3] = fill;
@@ -57,7 +57,7 @@ struct RowTile {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     int64_t c = col(t, e);
-                    v[t][e] = c < cols ? row[c] : fill;
+                    v[t][e] = c < cols ? ld_stream1(row + c) : fill;
                 }
             }
         }
@@ -68,12 +68,12 @@ struct RowTile {
         for (int t = 0; t < ITEMS; ++t) {
             if constexpr (VEC) {
                 int64_t c = col(t, 0);
-                if (c < cols) *reinterpret_cast<float4*>(row + c) = make_float4(v[t][0], v[t][1], v[t][2], v[t][3]);
+                if (c < cols) st_stream(row + c, make_float4(v[t][0], v[t][1], v[t][2], v[t][3]));
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     int64_t c = col(t, e);
-                    if (c < cols) row[c] = v[t][e];
+                    if (c < cols) st_stream1(row + c, v[t][e]);
                 }
             }
         }
@@ -126,6 +126,16 @@ __global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out
 
 // softmax:     gx (+)= y * (g - sum(g*y)),  y = out
 // log_softmax: gx (+)= g - exp(out) * sum(g)
+// For softmax the dot product is split into the dominant element (y > 0.5;
+// at most one per row) and the rest: for the dominant j,
+//   g_j - sum(g*y) = g_j * (1 - y_j) - sum_{k != j} g_k y_k,
+// which avoids the cancellation of g_j - g_j y_j when y_j is close to 1 (a
+// spike in the logits), matching what the reference's explicit Jacobian
+// (y_j (1 - y_j) on the diagonal) computes.
+__device__ __forceinline__ float softmax_dx(float g, float y, float s_dom, float s_rest) {
+    return y > 0.5f ? y * (g * (1.0f - y) - s_rest) : y * (g - (s_dom + s_rest));
+}
+
 template <int NT, int ITEMS, bool VEC, bool LOG>
 __global__ void __launch_bounds__(NT) softmax_bwd_kernel(const float* __restrict__ g, const float* __restrict__ out,
                                                           float* __restrict__ gx, int acc, int64_t rows, int64_t cols) {
@@ -134,18 +144,26 @@ __global__ void __launch_bounds__(NT) softmax_bwd_kernel(const float* __restrict
         RowTile<NT, ITEMS, VEC> tg, ty;
         tg.load(g + r * cols, cols, 0.f);
         ty.load(out + r * cols, cols, 0.f);
-        float s = 0.f;
+        float s = 0.f, sd = 0.f;
 #pragma unroll
         for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s += LOG ? tg.v[t][e] : tg.v[t][e] * ty.v[t][e];
+            for (int e = 0; e < 4; ++e) {
+                if (LOG) s += tg.v[t][e];
+                else {
+                    const float p = tg.v[t][e] * ty.v[t][e];
+                    if (ty.v[t][e] > 0.5f) sd += p;
+                    else s += p;
+                }
+            }
         s = block_sum<NT>(s, lds);
+        if (!LOG) sd = block_sum<NT>(sd, lds);
 #pragma unroll
         for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (LOG) tg.v[t][e] = tg.v[t][e] - expf(ty.v[t][e]) * s;
-                else tg.v[t][e] = ty.v[t][e] * (tg.v[t][e] - s);
+                else tg.v[t][e] = softmax_dx(tg.v[t][e], ty.v[t][e], sd, s);
             }
         if (acc) {
             RowTile<NT, ITEMS, VEC> old;
@@ -193,11 +211,16 @@ __global__ void __launch_bounds__(1024) softmax_bwd_long_kernel(const float* __r
         const float* gr = g + r * cols;
         const float* yr = out + r * cols;
         float* dr = gx + r * cols;
-        float s = 0.f;
-        for (int64_t c = threadIdx.x; c < cols; c += 1024) s += LOG ? gr[c] : gr[c] * yr[c];
-        s = block_sum<1024>(s, lds);
+        float s = 0.f, sd = 0.f;
         for (int64_t c = threadIdx.x; c < cols; c += 1024) {
-            float d = LOG ? gr[c] - expf(yr[c]) * s : yr[c] * (gr[c] - s);
+            if (LOG) s += gr[c];
+            else if (yr[c] > 0.5f) sd += gr[c] * yr[c];
+            else s += gr[c] * yr[c];
+        }
+        s = block_sum<1024>(s, lds);
+        if (!LOG) sd = block_sum<1024>(sd, lds);
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) {
+            float d = LOG ? gr[c] - expf(yr[c]) * s : softmax_dx(gr[c], yr[c], sd, s);
             dr[c] = acc ? dr[c] + d : d;
         }
         __syncthreads();
