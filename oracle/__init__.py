@@ -330,6 +330,15 @@ def bit_equal(x: np.ndarray, y: np.ndarray) -> bool:
     return bool(np.array_equal(x.view(np.uint32)[~xn], y.view(np.uint32)[~yn]))
 
 
+def equal_modulo_zero_sign(x: np.ndarray, y: np.ndarray) -> bool:
+    """bit_equal, except that -0.0 and +0.0 match.  The reference's own build
+    uses -ffast-math (which includes -fno-signed-zeros), so the sign of a zero
+    returned by its max/min is not defined by the source semantics."""
+    x = np.where(np.asarray(x, np.float32) == 0, np.float32(0), x)
+    y = np.where(np.asarray(y, np.float32) == 0, np.float32(0), y)
+    return bit_equal(x, y)
+
+
 def close_scaled(x, ref64, scale64, rtol=1e-5, atol=0.0):
     """|x - ref| <= rtol * max(|ref|, scale) + atol elementwise, NaN == NaN.
     Returns (ok, worst ratio)."""

@@ -1,0 +1,136 @@
+// bindings.cpp -- Python view of the C++ Tensor (whitematter_amd/_tensor).
+//
+// Used by the parity tests to drive the drop-in Tensor API the way the
+// reference's own C++ tests do (tests/test_tensor.cpp, test_autograd.cpp):
+// build tensors, call ops, run backward(), read data and grad.  data/grad are
+// copied to and from numpy; everything else stays on the device.
+#include <cstring>
+
+#include <pybind11/functional.h>
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include "tensor.h"
+#include "wm_hip.h"
+
+namespace py = pybind11;
+
+namespace {
+
+py::array_t<float> to_numpy(const wm::DeviceVector& v, const std::vector<size_t>& shape) {
+    std::vector<py::ssize_t> s(shape.begin(), shape.end());
+    size_t n = 1;
+    for (auto d : shape) n *= d;
+    if (n != v.size()) s = {(py::ssize_t)v.size()};
+    py::array_t<float> out(s);
+    if (v.size()) std::memcpy(out.mutable_data(), v.data(), v.size() * sizeof(float));
+    return out;
+}
+
+std::vector<float> from_numpy(py::array_t<float, py::array::c_style | py::array::forcecast> a) {
+    return std::vector<float>(a.data(), a.data() + a.size());
+}
+
+std::vector<size_t> shape_of(py::array_t<float, py::array::c_style | py::array::forcecast> a) {
+    std::vector<size_t> s;
+    for (py::ssize_t i = 0; i < a.ndim(); ++i) s.push_back((size_t)a.shape(i));
+    return s;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_tensor, m) {
+    m.doc() = "whitematter Tensor with device-resident storage on MI355X";
+    m.def("init", [](int device) {
+        if (wm_init(device) != WM_OK) throw std::runtime_error(wm_last_error());
+    });
+
+    py::class_<GradMode>(m, "GradMode")
+        .def_static("is_enabled", &GradMode::is_enabled)
+        .def_static("set_enabled", &GradMode::set_enabled);
+
+    py::class_<Tensor, TensorPtr>(m, "Tensor")
+        .def_static("create", [](const std::vector<size_t>& shape, bool rg) { return Tensor::create(shape, rg); },
+                    py::arg("shape"), py::arg("requires_grad") = false)
+        .def_static("from_array",
+                    [](py::array_t<float, py::array::c_style | py::array::forcecast> a, py::object shape, bool rg) {
+                        std::vector<size_t> s = shape.is_none() ? shape_of(a) : shape.cast<std::vector<size_t>>();
+                        return Tensor::create(from_numpy(a), s, rg);
+                    },
+                    py::arg("data"), py::arg("shape") = py::none(), py::arg("requires_grad") = false)
+        .def_static("zeros", &Tensor::zeros, py::arg("shape"), py::arg("requires_grad") = false)
+        .def_static("ones", &Tensor::ones, py::arg("shape"), py::arg("requires_grad") = false)
+        .def_static("randn", &Tensor::randn, py::arg("shape"), py::arg("requires_grad") = false)
+        .def_readwrite("shape", &Tensor::shape)
+        .def_readwrite("requires_grad", &Tensor::requires_grad)
+        .def_property(
+            "data", [](const Tensor& t) { return to_numpy(t.data, t.shape); },
+            [](Tensor& t, py::array_t<float, py::array::c_style | py::array::forcecast> a) { t.data = from_numpy(a); })
+        .def_property(
+            "grad",
+            [](const Tensor& t) -> py::object {
+                if (t.grad.empty()) return py::none();
+                return to_numpy(t.grad, t.shape);
+            },
+            [](Tensor& t, py::array_t<float, py::array::c_style | py::array::forcecast> a) { t.grad = from_numpy(a); })
+        .def_property_readonly("grad_known_zero", [](const Tensor& t) { return t.grad.known_zero(); })
+        .def_property_readonly("has_grad_fn", [](const Tensor& t) { return (bool)t.grad_fn; })
+        .def_property_readonly("num_parents", [](const Tensor& t) { return t.parents.size(); })
+        .def("size", &Tensor::size)
+        .def("ndim", &Tensor::ndim)
+        .def("item", &Tensor::item)
+        .def("zero_grad", &Tensor::zero_grad)
+        .def("backward", &Tensor::backward)
+        // Inject an upstream gradient and run this node's closure only.
+        .def("run_grad_fn",
+             [](Tensor& t, py::array_t<float, py::array::c_style | py::array::forcecast> g) {
+                 t.grad = from_numpy(g);
+                 if (t.grad_fn) t.grad_fn();
+             })
+        .def("add", &Tensor::add)
+        .def("sub", &Tensor::sub)
+        .def("mul", py::overload_cast<const TensorPtr&>(&Tensor::mul, py::const_))
+        .def("mul", py::overload_cast<float>(&Tensor::mul, py::const_))
+        .def("div", py::overload_cast<const TensorPtr&>(&Tensor::div, py::const_))
+        .def("div", py::overload_cast<float>(&Tensor::div, py::const_))
+        .def("neg", &Tensor::neg)
+        .def("relu", &Tensor::relu)
+        .def("sigmoid", &Tensor::sigmoid)
+        .def("tanh_", &Tensor::tanh_)
+        .def("log_", &Tensor::log_)
+        .def("exp_", &Tensor::exp_)
+        .def("pow", py::overload_cast<const TensorPtr&>(&Tensor::pow, py::const_))
+        .def("pow", py::overload_cast<float>(&Tensor::pow, py::const_))
+        .def("sqrt", &Tensor::sqrt)
+        .def("abs", &Tensor::abs)
+        .def("clamp", &Tensor::clamp)
+        .def("softmax", &Tensor::softmax, py::arg("dim") = -1)
+        .def("log_softmax", &Tensor::log_softmax, py::arg("dim") = -1)
+        .def("sum", &Tensor::sum, py::arg("dim") = -1, py::arg("keepdim") = false)
+        .def("mean", &Tensor::mean, py::arg("dim") = -1, py::arg("keepdim") = false)
+        .def("max", py::overload_cast<int, bool>(&Tensor::max, py::const_), py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("min", py::overload_cast<int, bool>(&Tensor::min, py::const_), py::arg("dim"),
+             py::arg("keepdim") = false)
+        .def("maximum", py::overload_cast<const TensorPtr&>(&Tensor::max, py::const_))
+        .def("minimum", py::overload_cast<const TensorPtr&>(&Tensor::min, py::const_))
+        .def("argmax", &Tensor::argmax, py::arg("dim") = -1, py::arg("keepdim") = false)
+        .def("argmin", &Tensor::argmin, py::arg("dim") = -1, py::arg("keepdim") = false)
+        .def("reshape", &Tensor::reshape)
+        .def("flatten", &Tensor::flatten, py::arg("start_dim") = 1)
+        .def("squeeze", &Tensor::squeeze, py::arg("dim") = -1)
+        .def("unsqueeze", &Tensor::unsqueeze)
+        .def("matmul", &Tensor::matmul)
+        .def("transpose", &Tensor::transpose)
+        .def("__add__", [](const TensorPtr& a, const TensorPtr& b) { return *a + b; })
+        .def("__sub__", [](const TensorPtr& a, const TensorPtr& b) { return *a - b; })
+        .def("__mul__", [](const TensorPtr& a, const TensorPtr& b) { return *a * b; })
+        .def("__mul__", [](const TensorPtr& a, float s) { return *a * s; })
+        .def("__rmul__", [](const TensorPtr& a, float s) { return s * a; })
+        .def("__truediv__", [](const TensorPtr& a, const TensorPtr& b) { return *a / b; })
+        .def("__truediv__", [](const TensorPtr& a, float s) { return *a / s; })
+        .def("__neg__", [](const TensorPtr& a) { return -(*a); });
+
+    m.def("set_grad_enabled", &GradMode::set_enabled);
+}

@@ -1,0 +1,269 @@
+// device_vector.cpp -- see device_vector.h.
+#include "device_vector.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "wm_hip.h"
+
+namespace wm {
+
+namespace {
+
+void ck(int rc, const char* what) {
+    if (rc != WM_OK) throw std::runtime_error(std::string(what) + ": " + wm_last_error());
+}
+
+}  // namespace
+
+DeviceVector::DeviceVector(size_type n, float value) : n_(n) {
+    if (n_ == 0) return;
+    if (value == 0.0f && !std::signbit(value)) set_zero();
+    else fill(value);
+}
+
+DeviceVector::DeviceVector(const std::vector<float>& v) : n_(v.size()), h_(v) {
+    host_valid_ = true;
+    dev_valid_ = false;
+}
+
+DeviceVector::DeviceVector(std::initializer_list<float> v) : DeviceVector(std::vector<float>(v)) {}
+
+DeviceVector::DeviceVector(const DeviceVector& o) : n_(o.n_) {
+    if (n_ == 0) return;
+    if (o.zero_) {
+        set_zero();
+    } else if (o.dev_valid_) {
+        ensure_dev_alloc();
+        ck(wm_d2d(d_, o.d_, n_ * sizeof(float)), "DeviceVector copy");
+        dev_valid_ = true;
+        host_valid_ = false;
+    } else {
+        h_ = o.h_;
+        host_valid_ = true;
+        dev_valid_ = false;
+    }
+}
+
+DeviceVector::DeviceVector(DeviceVector&& o) noexcept
+    : n_(o.n_), d_(o.d_), h_(std::move(o.h_)), host_valid_(o.host_valid_), dev_valid_(o.dev_valid_), zero_(o.zero_) {
+    o.n_ = 0;
+    o.d_ = nullptr;
+    o.host_valid_ = o.dev_valid_ = true;
+    o.zero_ = false;
+}
+
+DeviceVector::~DeviceVector() { release(); }
+
+DeviceVector& DeviceVector::operator=(const DeviceVector& o) {
+    if (this == &o) return *this;
+    DeviceVector tmp(o);
+    *this = std::move(tmp);
+    return *this;
+}
+
+DeviceVector& DeviceVector::operator=(DeviceVector&& o) noexcept {
+    if (this == &o) return *this;
+    release();
+    n_ = o.n_;
+    d_ = o.d_;
+    h_ = std::move(o.h_);
+    host_valid_ = o.host_valid_;
+    dev_valid_ = o.dev_valid_;
+    zero_ = o.zero_;
+    o.n_ = 0;
+    o.d_ = nullptr;
+    o.host_valid_ = o.dev_valid_ = true;
+    o.zero_ = false;
+    return *this;
+}
+
+DeviceVector& DeviceVector::operator=(const std::vector<float>& v) {
+    release();
+    n_ = v.size();
+    h_ = v;
+    host_valid_ = true;
+    dev_valid_ = false;
+    zero_ = false;
+    return *this;
+}
+
+DeviceVector& DeviceVector::operator=(std::initializer_list<float> v) { return *this = std::vector<float>(v); }
+
+void DeviceVector::release() {
+    if (d_) {
+        wm_free(d_);
+        d_ = nullptr;
+    }
+}
+
+void DeviceVector::ensure_dev_alloc() const {
+    if (d_ || n_ == 0) return;
+    void* p = nullptr;
+    ck(wm_alloc(&p, n_ * sizeof(float)), "DeviceVector allocation");
+    d_ = static_cast<float*>(p);
+}
+
+void DeviceVector::sync_host() const {
+    if (n_ == 0) return;
+    if (host_valid_) return;
+    if (zero_) {
+        h_.assign(n_, 0.0f);
+    } else {
+        h_.resize(n_);
+        ck(wm_d2h(h_.data(), d_, n_ * sizeof(float)), "DeviceVector device->host");
+    }
+    host_valid_ = true;
+}
+
+const float* DeviceVector::data() const {
+    if (n_ == 0) return h_.data();
+    sync_host();
+    return h_.data();
+}
+
+float* DeviceVector::data() {
+    if (n_ == 0) return h_.data();
+    sync_host();
+    // The caller may write through the pointer: the host copy becomes the
+    // only valid one.
+    zero_ = false;
+    dev_valid_ = false;
+    return h_.data();
+}
+
+float& DeviceVector::at(size_type i) {
+    if (i >= n_) throw std::out_of_range("DeviceVector::at");
+    return data()[i];
+}
+
+const float& DeviceVector::at(size_type i) const {
+    if (i >= n_) throw std::out_of_range("DeviceVector::at");
+    return data()[i];
+}
+
+const float* DeviceVector::dev() const {
+    if (n_ == 0) return nullptr;
+    ensure_dev_alloc();
+    if (!dev_valid_) {
+        if (zero_) {
+            ck(wm_fill(d_, 0.0f, (int64_t)n_), "DeviceVector zero fill");
+        } else {
+            ck(wm_h2d(d_, h_.data(), n_ * sizeof(float)), "DeviceVector host->device");
+        }
+        dev_valid_ = true;
+    }
+    return d_;
+}
+
+float* DeviceVector::dev_write() {
+    if (n_ == 0) return nullptr;
+    ensure_dev_alloc();
+    zero_ = false;
+    dev_valid_ = true;
+    host_valid_ = false;
+    return d_;
+}
+
+float* DeviceVector::dev_rw() {
+    if (n_ == 0) return nullptr;
+    dev();
+    zero_ = false;
+    host_valid_ = false;
+    return d_;
+}
+
+float* DeviceVector::dev_accum(int* accumulate) {
+    if (zero_) {
+        *accumulate = 0;
+        return dev_write();
+    }
+    *accumulate = 1;
+    return dev_rw();
+}
+
+void DeviceVector::set_zero() {
+    zero_ = n_ > 0;
+    host_valid_ = n_ == 0;
+    dev_valid_ = n_ == 0;
+}
+
+void DeviceVector::fill(float value) {
+    if (n_ == 0) return;
+    if (value == 0.0f && !std::signbit(value)) {
+        set_zero();
+        return;
+    }
+    ensure_dev_alloc();
+    ck(wm_fill(d_, value, (int64_t)n_), "DeviceVector fill");
+    zero_ = false;
+    dev_valid_ = true;
+    host_valid_ = false;
+}
+
+void DeviceVector::resize(size_type n, float value) {
+    if (n == n_) return;
+    if (n_ == 0 || (zero_ && value == 0.0f && !std::signbit(value))) {
+        release();
+        h_.clear();
+        n_ = n;
+        if (value == 0.0f && !std::signbit(value)) set_zero();
+        else fill(value);
+        return;
+    }
+    sync_host();
+    h_.resize(n, value);
+    release();
+    n_ = n;
+    zero_ = false;
+    host_valid_ = true;
+    dev_valid_ = false;
+}
+
+void DeviceVector::assign(size_type n, float value) {
+    release();
+    h_.clear();
+    n_ = n;
+    zero_ = false;
+    host_valid_ = dev_valid_ = true;
+    if (n_ == 0) return;
+    if (value == 0.0f && !std::signbit(value)) set_zero();
+    else fill(value);
+}
+
+void DeviceVector::clear() {
+    release();
+    h_.clear();
+    n_ = 0;
+    zero_ = false;
+    host_valid_ = dev_valid_ = true;
+}
+
+void DeviceVector::push_back(float v) {
+    sync_host();
+    h_.push_back(v);
+    release();
+    ++n_;
+    zero_ = false;
+    host_valid_ = true;
+    dev_valid_ = false;
+}
+
+DeviceVector::operator std::vector<float>() const {
+    sync_host();
+    return std::vector<float>(h_.begin(), h_.begin() + (std::ptrdiff_t)n_);
+}
+
+bool DeviceVector::operator==(const DeviceVector& o) const {
+    if (n_ != o.n_) return false;
+    if (n_ == 0) return true;
+    // Element-wise ==, as std::vector<float> compares (NaN != NaN, -0 == +0).
+    const float* a = data();
+    const float* b = o.data();
+    return std::equal(a, a + n_, b);
+}
+
+}  // namespace wm

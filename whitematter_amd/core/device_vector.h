@@ -1,0 +1,110 @@
+// device_vector.h -- host/device-coherent fp32 storage with std::vector's API.
+//
+// The reference keeps Tensor::data and Tensor::grad as std::vector<float>
+// (core/tensor.h:35-36) and its callers touch them directly: size(), data(),
+// begin()/end(), operator[], resize(), empty(), whole-vector assignment from
+// std::vector<float> or an initializer list, range-for.  DeviceVector keeps
+// that surface so callers compile unchanged, while the authoritative copy of
+// the values lives in device memory (libwm_hip's pool):
+//
+//   host access   const access copies device -> host if the host mirror is
+//                 stale; non-const access (which may write) also marks the
+//                 device copy stale, so the next kernel re-uploads it;
+//   device access dev() uploads a stale device copy; dev_write() hands out the
+//                 buffer for a full overwrite (no upload) and marks the host
+//                 mirror stale; dev_rw() does both;
+//   known zero    a fresh zero-filled vector (a new gradient, zero_grad) is
+//                 only a flag: nothing is allocated or filled until someone
+//                 needs the values, and the first backward contribution can
+//                 overwrite instead of read-modify-write (dev_accum()).
+//
+// Not thread-safe, like the reference Tensor.
+#pragma once
+
+#include <cstddef>
+#include <initializer_list>
+#include <vector>
+
+namespace wm {
+
+class DeviceVector {
+public:
+    using value_type = float;
+    using size_type = std::size_t;
+    using iterator = float*;
+    using const_iterator = const float*;
+    using reference = float&;
+    using const_reference = const float&;
+
+    DeviceVector() = default;
+    explicit DeviceVector(size_type n, float value = 0.0f);
+    DeviceVector(const std::vector<float>& v);  // NOLINT: implicit, like a vector copy
+    DeviceVector(std::initializer_list<float> v);
+    template <class It>
+    DeviceVector(It first, It last) : DeviceVector(std::vector<float>(first, last)) {}
+    DeviceVector(const DeviceVector& o);
+    DeviceVector(DeviceVector&& o) noexcept;
+    ~DeviceVector();
+
+    DeviceVector& operator=(const DeviceVector& o);
+    DeviceVector& operator=(DeviceVector&& o) noexcept;
+    DeviceVector& operator=(const std::vector<float>& v);
+    DeviceVector& operator=(std::initializer_list<float> v);
+
+    // ---- std::vector surface (host side, coherent) ------------------------
+    size_type size() const { return n_; }
+    bool empty() const { return n_ == 0; }
+    float* data();
+    const float* data() const;
+    float& operator[](size_type i) { return data()[i]; }
+    const float& operator[](size_type i) const { return data()[i]; }
+    float& at(size_type i);
+    const float& at(size_type i) const;
+    float& front() { return data()[0]; }
+    float& back() { return data()[n_ - 1]; }
+    iterator begin() { return data(); }
+    iterator end() { return data() + n_; }
+    const_iterator begin() const { return data(); }
+    const_iterator end() const { return data() + n_; }
+    const_iterator cbegin() const { return data(); }
+    const_iterator cend() const { return data() + n_; }
+    void resize(size_type n, float value = 0.0f);
+    void assign(size_type n, float value);
+    template <class It>
+    void assign(It first, It last) { *this = std::vector<float>(first, last); }
+    void clear();
+    void push_back(float v);
+    operator std::vector<float>() const;  // NOLINT: implicit, copies to the host
+    bool operator==(const DeviceVector& o) const;
+    bool operator!=(const DeviceVector& o) const { return !(*this == o); }
+
+    // ---- device side -------------------------------------------------------
+    // Device pointer to current values (uploads / zero-fills as needed).
+    const float* dev() const;
+    // Device pointer for a full overwrite: no upload, host mirror goes stale.
+    float* dev_write();
+    // Device pointer for read-modify-write.
+    float* dev_rw();
+    // Pointer for a gradient contribution: *accumulate = 0 when the buffer is
+    // known to be zero (the kernel then overwrites it), 1 otherwise.
+    float* dev_accum(int* accumulate);
+    // Mark the contents as all zeros without touching memory.
+    void set_zero();
+    bool known_zero() const { return zero_; }
+    // Fill with a constant on the device.
+    void fill(float value);
+
+private:
+    void ensure_dev_alloc() const;
+    void sync_host() const;   // make the host mirror current
+    void release();
+
+    size_type n_ = 0;
+    mutable float* d_ = nullptr;           // device buffer (capacity n_), lazily allocated
+    mutable std::vector<float> h_;         // host mirror
+    mutable bool host_valid_ = true;       // h_ holds the current values
+    mutable bool dev_valid_ = true;        // d_ holds the current values
+    bool zero_ = false;                    // logically all zeros (neither copy needs to be valid)
+};
+
+}  // namespace wm

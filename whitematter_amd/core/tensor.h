@@ -1,0 +1,165 @@
+// tensor.h -- whitematter's Tensor with device-resident storage on MI355X.
+//
+// The class API is the reference's (core/tensor.h:12-137): the same public
+// members, factories, op signatures, operators and autograd entry points, so
+// code written against the reference compiles against this header.  The one
+// change is the type of `data` and `grad`: wm::DeviceVector, a
+// std::vector<float>-compatible container whose authoritative copy lives in
+// HBM (see device_vector.h).  The elementwise / broadcast / reduction /
+// softmax ops and their backward closures run as HIP kernels through the
+// C ABI in include/wm_hip.h; they never touch host memory.
+//
+// Ops outside that path (matmul, bmm, conv, pools, concat/stack, transpose,
+// slice, permute, augmentation) are declared for source compatibility and
+// throw std::logic_error: this build covers the elementwise / broadcast /
+// reduction path only.
+//
+// The include guard is the reference header's own (TENSOR_H): this header
+// replaces that one, and the two must never both be active in a translation
+// unit.
+#ifndef TENSOR_H
+#define TENSOR_H
+
+#include <cassert>
+#include <cmath>
+#include <cstdio>
+#include <functional>
+#include <memory>
+#include <random>
+#include <vector>
+
+#include "device_vector.h"
+
+// Global gradient computation flag (reference core/tensor.h:13-20).
+class GradMode {
+public:
+    static bool is_enabled();
+    static void set_enabled(bool enabled);
+
+private:
+    static bool enabled_;
+};
+
+// RAII guard disabling gradient tracking (reference core/tensor.h:22-28).
+class NoGradGuard {
+public:
+    NoGradGuard();
+    ~NoGradGuard();
+
+private:
+    bool prev_mode_;
+};
+
+class Tensor;
+using TensorPtr = std::shared_ptr<Tensor>;
+
+class Tensor : public std::enable_shared_from_this<Tensor> {
+public:
+    wm::DeviceVector data;
+    wm::DeviceVector grad;
+    std::vector<size_t> shape;
+    bool requires_grad;
+
+    std::function<void()> grad_fn;
+    std::vector<TensorPtr> parents;
+
+    Tensor();
+    Tensor(const std::vector<size_t>& shape, bool requires_grad = false);
+    Tensor(const std::vector<float>& data, const std::vector<size_t>& shape, bool requires_grad = false);
+
+    static TensorPtr create(const std::vector<size_t>& shape, bool requires_grad = false);
+    static TensorPtr create(const std::vector<float>& data, const std::vector<size_t>& shape,
+                            bool requires_grad = false);
+    static TensorPtr zeros(const std::vector<size_t>& shape, bool requires_grad = false);
+    static TensorPtr ones(const std::vector<size_t>& shape, bool requires_grad = false);
+    static TensorPtr randn(const std::vector<size_t>& shape, bool requires_grad = false);
+    static TensorPtr xavier(size_t fan_in, size_t fan_out, bool requires_grad = true);
+
+    static TensorPtr concat(const std::vector<TensorPtr>& tensors, int dim = 0);
+    static TensorPtr stack(const std::vector<TensorPtr>& tensors, int dim = 0);
+
+    size_t size() const;
+    size_t ndim() const;
+    float item() const;
+    void zero_grad();
+    void backward();
+
+    float& operator[](size_t idx);
+    float operator[](size_t idx) const;
+    float& at(const std::vector<size_t>& indices);
+    float at(const std::vector<size_t>& indices) const;
+
+    TensorPtr matmul(const TensorPtr& other) const;
+    TensorPtr bmm(const TensorPtr& other) const;
+    TensorPtr add(const TensorPtr& other) const;
+    TensorPtr sub(const TensorPtr& other) const;
+    TensorPtr mul(const TensorPtr& other) const;
+    TensorPtr div(const TensorPtr& other) const;
+    TensorPtr mul(float scalar) const;
+    TensorPtr div(float scalar) const;
+    TensorPtr neg() const;
+    TensorPtr relu() const;
+    TensorPtr sigmoid() const;
+    TensorPtr tanh_() const;
+    TensorPtr log_() const;
+    TensorPtr exp_() const;
+    TensorPtr pow(float exponent) const;
+    TensorPtr pow(const TensorPtr& exponent) const;
+    TensorPtr sqrt() const;
+    TensorPtr abs() const;
+    TensorPtr clamp(float min_val, float max_val) const;
+    TensorPtr softmax(int dim = -1) const;
+    TensorPtr log_softmax(int dim = -1) const;
+    TensorPtr sum(int dim = -1, bool keepdim = false) const;
+    TensorPtr mean(int dim = -1, bool keepdim = false) const;
+    TensorPtr max(int dim, bool keepdim = false) const;
+    TensorPtr min(int dim, bool keepdim = false) const;
+    TensorPtr max(const TensorPtr& other) const;
+    TensorPtr min(const TensorPtr& other) const;
+    TensorPtr argmax(int dim = -1, bool keepdim = false) const;
+    TensorPtr argmin(int dim = -1, bool keepdim = false) const;
+    TensorPtr transpose() const;
+    TensorPtr reshape(const std::vector<size_t>& new_shape) const;
+    TensorPtr slice(size_t start, size_t end, int dim = 0) const;
+    TensorPtr conv2d(const TensorPtr& weight, const TensorPtr& bias, size_t stride = 1, size_t padding = 0) const;
+    TensorPtr conv_transpose2d(const TensorPtr& weight, const TensorPtr& bias, size_t stride = 1,
+                               size_t padding = 0, size_t output_padding = 0) const;
+    TensorPtr maxpool2d(size_t kernel_size, size_t stride = 0) const;
+    TensorPtr avgpool2d(size_t kernel_size, size_t stride = 0) const;
+    TensorPtr flatten(size_t start_dim = 1) const;
+    TensorPtr squeeze(int dim = -1) const;
+    TensorPtr unsqueeze(int dim) const;
+    TensorPtr permute(const std::vector<int>& dims) const;
+
+    TensorPtr flip_horizontal() const;
+    TensorPtr random_flip_horizontal(float p = 0.5f) const;
+    TensorPtr pad2d(size_t padding) const;
+    TensorPtr crop(size_t top, size_t left, size_t height, size_t width) const;
+    TensorPtr random_crop(size_t height, size_t width) const;
+
+    TensorPtr operator+(const TensorPtr& other) const { return add(other); }
+    TensorPtr operator-(const TensorPtr& other) const { return sub(other); }
+    TensorPtr operator*(const TensorPtr& other) const { return mul(other); }
+    TensorPtr operator/(const TensorPtr& other) const { return div(other); }
+    TensorPtr operator*(float scalar) const { return mul(scalar); }
+    TensorPtr operator/(float scalar) const { return div(scalar); }
+    TensorPtr operator-() const { return neg(); }
+
+    void print(const char* name = nullptr) const;
+
+private:
+    void build_topo(std::vector<Tensor*>& topo, std::vector<Tensor*>& visited);
+    bool should_track_grad() const;
+
+    // Shared bodies of the device ops.
+    TensorPtr binary_op(int op, const TensorPtr& other) const;
+    TensorPtr unary_op(int op, float p0, float p1) const;
+    TensorPtr reduce_2d(int op, int dim, bool keepdim, bool global_keep_rank) const;
+    TensorPtr arg_reduce(int op, int dim, bool keepdim) const;
+    TensorPtr softmax_op(bool log) const;
+    TensorPtr copy_as(const std::vector<size_t>& new_shape, bool result_requires_grad, bool copy_grad) const;
+};
+
+TensorPtr operator*(float scalar, const TensorPtr& t);
+
+#endif  // TENSOR_H
