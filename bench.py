@@ -200,7 +200,38 @@ def c4_ops(rows=8192, cols=32000):
                                       "elements": N}
 
 
-CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops}
+def c5_ops(b=32, t=1024, c=4096):
+    h, res, g, dm = synth.config5(b, t, c)
+    rows = b * t
+    N = rows * c
+    # fp16 storage made on the device with the reference's truncating conversion
+    h32, r32 = W.DeviceArray.from_host(h), W.DeviceArray.from_host(res)
+    h16, r16 = W.DeviceArray((rows, c), np.uint16), W.DeviceArray((rows, c), np.uint16)
+    W.call("wm_f32_to_f16_rtz", h16.vp, h32.vp, N)
+    W.call("wm_f32_to_f16_rtz", r16.vp, r32.vp, N)
+    h32.free(); r32.free()
+    dg_, ddm = W.DeviceArray.from_host(g), W.DeviceArray.from_host(dm.reshape(-1))
+    out = W.DeviceArray((rows, c), np.uint16)
+    m = W.DeviceArray((rows,))
+    gh = W.DeviceArray((rows, c)); gh.fill(0.0)
+    gr = W.DeviceArray((rows, c)); gr.fill(0.0)
+    gg = W.DeviceArray((c,)); gg.fill(0.0)
+    lo, hi = W.C.c_float(-4.0), W.C.c_float(4.0)
+    ops = [
+        Op("epilogue fwd", lambda: W.call("wm_epilogue_f16_fwd", out.vp, m.vp, h16.vp, r16.vp, dg_.vp, rows, c, lo,
+                                          hi),
+           N * (2 + 2 + 2) + c * F32 + rows * F32, "epilogue_fwd_kernel", N),
+        Op("epilogue bwd", lambda: W.call("wm_epilogue_f16_bwd", ddm.vp, h16.vp, r16.vp, dg_.vp, gh.vp, 1, gr.vp, 1,
+                                          gg.vp, 1, rows, c, lo, hi),
+           N * (2 + 2 + 8 + 8) + c * F32 + rows * F32 + 2 * c * F32, "epilogue_bwd_kernel", N),
+    ]
+    return ops, [h16, r16, dg_, ddm, out, m, gh, gr, gg], {
+        "workload": "c5: h, res[%d,%d,%d] fp16 storage (truncating conversion), g[%d] fp32; "
+                    "out = tanh_(clamp((h+res)*g, -4, 4)) stored fp16, mean over the last dim; fused fwd + bwd "
+                    "(grads fp32, accumulated)" % (b, t, c, c), "elements": N}
+
+
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops}
 
 
 # ---------------------------------------------------------------------------

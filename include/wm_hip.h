@@ -196,6 +196,28 @@ int wm_softmax_bwd(const float* g, const float* out, float* gx, int accumulate,
 int wm_log_softmax_bwd(const float* g, const float* out, float* gx,
                        int accumulate, int64_t rows, int64_t cols);
 
+/* ---- fused fp16-storage epilogue ----------------------------------------- */
+
+/* out = tanh_(clamp((h + res) * g, lo, hi)), mean[r] = sum_c out[r,c] / cols,
+ * over [rows, cols] activations h, res stored as fp16 (bits of the
+ * reference's float_to_half, core/amp.h:15-38) with fp32 compute; g is a
+ * per-column fp32 vector; out is written as fp16 (truncating, may be NULL)
+ * and mean as fp32.  The composition of the reference ops add (:897), mul
+ * with a broadcast [cols] vector (:1063), clamp (:1524), tanh_ (:1302) and
+ * reshape + mean(1, keepdim) (:2250, :1709) on the half_to_float'ed inputs
+ * (core/amp.h:40-72), in one pass. */
+int wm_epilogue_f16_fwd(uint16_t* out, float* mean, const uint16_t* h, const uint16_t* res,
+                        const float* g, int64_t rows, int64_t cols, float lo, float hi);
+
+/* Backward of wm_epilogue_f16_fwd given dm = dL/dmean ([rows]): the chain of
+ * the reference closures (mean reuses sum's closure, so no 1/cols), with the
+ * forward recomputed from h, res and g.  gh, gres ([rows, cols] fp32) and
+ * gg ([cols], the column sum over rows) each take an accumulate flag and may
+ * be NULL. */
+int wm_epilogue_f16_bwd(const float* dm, const uint16_t* h, const uint16_t* res, const float* g,
+                        float* gh, int acc_h, float* gres, int acc_res, float* gg, int acc_g,
+                        int64_t rows, int64_t cols, float lo, float hi);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,6 +86,32 @@ __device__ __forceinline__ void st_stream(float* p, float4 v) {
 __device__ __forceinline__ float ld_stream1(const float* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_stream1(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
+// fp16 storage conversions with the reference's semantics (core/amp.h:15-72).
+// half -> float is exact, subnormals included; the hardware conversion is
+// exact with fp16 denormals enabled (the default mode for HIP kernels).
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+    return (float)v;
+}
+
+// float -> half truncating toward zero, as float_to_half does: convert with
+// the hardware's round-to-nearest-even, then step one ulp back toward zero if
+// that rounded up in magnitude.  float_to_half sends |x| >= 65536 to Inf and
+// keeps the top NaN payload bits, so those two cases take its bit formula.
+// (Checked against float_to_half on every exponent x every 10-bit mantissa x
+// the low-bit patterns at each truncation point, plus 42M random bit
+// patterns.)
+__device__ __forceinline__ uint32_t float_to_half_bits_rtz(float f) {
+    const uint32_t x = __float_as_uint(f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    if (__builtin_isnan(f)) return sign | 0x7C00u | ((x & 0x7FFFFFu) >> 13);
+    if (fabsf(f) >= 65536.0f) return sign | 0x7C00u;
+    const _Float16 h = (_Float16)f;
+    uint32_t b = __builtin_bit_cast(uint16_t, h);
+    if (fabsf((float)h) > fabsf(f)) b -= 1;
+    return b;
+}
+
 // DPP lane moves inside a 16-lane row (deterministic, no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {

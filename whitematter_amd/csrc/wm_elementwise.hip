@@ -150,43 +150,8 @@ __global__ void __launch_bounds__(kBlock) copy_vec_kernel(float* __restrict__ ds
     }
 }
 
-// float_to_half of core/amp.h:15-38: truncating (round-toward-zero) fp32 ->
-// fp16, overflow to Inf, float denormals and tiny values to signed zero.
-__device__ __forceinline__ uint16_t f32_to_f16_rtz(float f) {
-    uint32_t x = __float_as_uint(f);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    int32_t exponent = (int32_t)((x >> 23) & 0xFFu) - 127 + 15;
-    uint32_t mantissa = x & 0x7FFFFFu;
-    if (exponent <= 0) {
-        if (exponent < -10) return (uint16_t)sign;
-        mantissa = (mantissa | 0x800000u) >> (1 - exponent);
-        return (uint16_t)(sign | (mantissa >> 13));
-    } else if (exponent == 0xFF - 127 + 15) {
-        if (mantissa == 0) return (uint16_t)(sign | 0x7C00u);
-        return (uint16_t)(sign | 0x7C00u | (mantissa >> 13));
-    } else if (exponent > 30) {
-        return (uint16_t)(sign | 0x7C00u);
-    }
-    return (uint16_t)(sign | ((uint32_t)exponent << 10) | (mantissa >> 13));
-}
-
-// half_to_float of core/amp.h:40-72 (exact widening).
-__device__ __forceinline__ float f16_to_f32(uint16_t h) {
-    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-    uint32_t exponent = (h >> 10) & 0x1Fu;
-    uint32_t mantissa = h & 0x3FFu;
-    if (exponent == 0) {
-        if (mantissa == 0) return __uint_as_float(sign);
-        // Subnormal half: value = mantissa * 2^-24, exact in fp32.
-        int lz = __clz(mantissa) - 21;          // shifts to bring bit 10 up
-        mantissa = (mantissa << lz) & 0x3FFu;
-        uint32_t e = (uint32_t)(1 - lz + 127 - 15);
-        return __uint_as_float(sign | (e << 23) | (mantissa << 13));
-    } else if (exponent == 31) {
-        return __uint_as_float(sign | 0x7F800000u | (mantissa << 13));
-    }
-    return __uint_as_float(sign | ((exponent + 127 - 15) << 23) | (mantissa << 13));
-}
+__device__ __forceinline__ uint16_t f32_to_f16_rtz(float f) { return (uint16_t)float_to_half_bits_rtz(f); }
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return half_bits_to_float(h); }
 
 __global__ void __launch_bounds__(kBlock) f32_to_f16_kernel(uint16_t* __restrict__ out, const float* __restrict__ x, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * kBlock;

@@ -1,0 +1,290 @@
+// Fused fp16-storage epilogue: out = tanh(clamp((h + res) * g, lo, hi)) and
+// its row mean, forward and backward, for [rows, cols] activations stored as
+// fp16 with fp32 compute (the AMP storage scheme of the reference's
+// HalfTensor, core/amp.h:256-286).
+//
+// In the reference this is a chain of Tensor ops on fp32 tensors converted
+// from fp16 storage (half_to_float, core/amp.h:40-72): add (core/tensor.cpp
+// :897), mul by a broadcast [cols] vector (:1063), clamp (:1524), tanh_
+// (:1302), then reshape + mean(1, keepdim) (:2250, :1709).  Each op makes a
+// full pass over HBM; here the forward reads h and res once (2 bytes each)
+// and writes out (2 bytes) and the row means, and the backward recomputes the
+// chain from h, res and g instead of reading saved intermediates.
+//
+// Backward of the chain, as the reference closures compose it (mean reuses
+// sum's closure, so its gradient is not divided by cols):
+//   dw = dm[row]                      (mean -> sum closure, :1697-1703)
+//   dv = dw * (1 - w*w)               (tanh_, :1316-1317; w recomputed)
+//   du = lo < u < hi ? dv : 0         (clamp, :1538-1540)
+//   dt = du * g[col],  dg[col] += du * t   (mul, broadcast, :1122-1142)
+//   dh += dt,  dres += dt             (add, :911-920)
+#include "wm_common.hpp"
+
+#include <algorithm>
+
+namespace wm {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float h2f(uint32_t h) { return half_bits_to_float(h); }
+__device__ __forceinline__ uint32_t f2h(float f) { return float_to_half_bits_rtz(f); }
+
+struct Chain {
+    float t, u, w;
+};
+
+__device__ __forceinline__ Chain chain(float h, float r, float g, float lo, float hi) {
+    Chain c;
+    c.t = h + r;
+    c.u = c.t * g;
+    float m = (c.u < hi) ? c.u : hi;       // std::min(hi, u)
+    float v = (lo < m) ? m : lo;           // std::max(lo, .)
+    c.w = tanhf(v);
+    return c;
+}
+
+// Forward: one workgroup per row; each thread takes 8 consecutive columns per
+// step (16 bytes of each fp16 input).  VEC: cols % 8 == 0 and 16-byte aligned.
+template <bool VEC>
+__global__ void __launch_bounds__(kBlock) epilogue_fwd_kernel(uint16_t* __restrict__ out, float* __restrict__ mean,
+                                                               const uint16_t* __restrict__ h,
+                                                               const uint16_t* __restrict__ res,
+                                                               const float* __restrict__ g, int64_t rows,
+                                                               int64_t cols, float lo, float hi) {
+    __shared__ float lds[kBlock / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint16_t* hr = h + r * cols;
+        const uint16_t* rr = res + r * cols;
+        uint16_t* orow = out ? out + r * cols : nullptr;
+        float s = 0.f;
+        if constexpr (VEC) {
+#pragma unroll 2
+            for (int64_t c = (int64_t)threadIdx.x * 8; c < cols; c += kBlock * 8) {
+                const float4 hq = ld_stream(reinterpret_cast<const float*>(hr + c));
+                const float4 rq = ld_stream(reinterpret_cast<const float*>(rr + c));
+                const float4 g0 = *reinterpret_cast<const float4*>(g + c);
+                const float4 g1 = *reinterpret_cast<const float4*>(g + c + 4);
+                const uint32_t hw[4] = {__float_as_uint(hq.x), __float_as_uint(hq.y), __float_as_uint(hq.z),
+                                        __float_as_uint(hq.w)};
+                const uint32_t rw[4] = {__float_as_uint(rq.x), __float_as_uint(rq.y), __float_as_uint(rq.z),
+                                        __float_as_uint(rq.w)};
+                const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                uint32_t ow[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    Chain lo_c = chain(h2f(hw[k] & 0xFFFFu), h2f(rw[k] & 0xFFFFu), gv[2 * k], lo, hi);
+                    Chain hi_c = chain(h2f(hw[k] >> 16), h2f(rw[k] >> 16), gv[2 * k + 1], lo, hi);
+                    s += lo_c.w + hi_c.w;
+                    ow[k] = f2h(lo_c.w) | (f2h(hi_c.w) << 16);
+                }
+                if (orow)
+                    st_stream(reinterpret_cast<float*>(orow + c),
+                              make_float4(__uint_as_float(ow[0]), __uint_as_float(ow[1]), __uint_as_float(ow[2]),
+                                          __uint_as_float(ow[3])));
+            }
+        } else {
+            for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
+                Chain ch = chain(h2f(hr[c]), h2f(rr[c]), g[c], lo, hi);
+                s += ch.w;
+                if (orow) orow[c] = (uint16_t)f2h(ch.w);
+            }
+        }
+        s = block_sum<kBlock>(s, lds);
+        if (threadIdx.x == 0) mean[r] = s / (float)cols;
+    }
+}
+
+// Backward: a workgroup owns 8*kBlock adjacent columns and a chunk of rows.
+// With 128-bit accesses lane i of wave w handles the two 4-column groups at
+// tile + 512 w + 4 i and 256 columns further on, so every load and store
+// instruction of a wave covers one contiguous span (512 B of fp16 input, 1 KB
+// of fp32 gradient).  Each thread keeps its 8 column partials of dg in
+// registers over the chunk's rows (fixed order) and writes them to
+// part[chunk, col] for a fixed-order second pass.
+typedef unsigned int wm_v2u __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void load_half4(const uint16_t* p, float* out) {
+    const wm_v2u q = __builtin_nontemporal_load(reinterpret_cast<const wm_v2u*>(p));
+    out[0] = half_bits_to_float(q.x & 0xFFFFu);
+    out[1] = half_bits_to_float(q.x >> 16);
+    out[2] = half_bits_to_float(q.y & 0xFFFFu);
+    out[3] = half_bits_to_float(q.y >> 16);
+}
+
+template <bool VEC>
+__global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __restrict__ dm,
+                                                               const uint16_t* __restrict__ h,
+                                                               const uint16_t* __restrict__ res,
+                                                               const float* __restrict__ g, float* __restrict__ gh,
+                                                               int acc_h, float* __restrict__ gres, int acc_res,
+                                                               float* __restrict__ part, int64_t rows, int64_t cols,
+                                                               int64_t rows_per_chunk, float lo, float hi) {
+    constexpr int W = VEC ? 8 : 1;
+    int64_t cg[2];  // first column of each 4-column group (VEC), or the one column
+    if constexpr (VEC) {
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+        cg[0] = (int64_t)blockIdx.x * (kBlock * 8) + w * 512 + lane * 4;
+        cg[1] = cg[0] + 256;
+        if (cg[0] >= cols) return;  // cols % 512 == 0 on this path: both groups are in range
+    } else {
+        cg[0] = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+        if (cg[0] >= cols) return;
+    }
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
+    const int64_t r1 = min(rows, r0 + rows_per_chunk);
+    float gv[W], acc[W];
+#pragma unroll
+    for (int j = 0; j < W; ++j) {
+        gv[j] = VEC ? g[cg[j / 4] + (j % 4)] : g[cg[0]];
+        acc[j] = 0.f;
+    }
+#pragma unroll 2
+    for (int64_t r = r0; r < r1; ++r) {
+        const float dw = dm[r];
+        const int64_t roff = r * cols;
+        float hv[W], rv[W];
+        if constexpr (VEC) {
+            load_half4(h + roff + cg[0], hv);
+            load_half4(h + roff + cg[1], hv + 4);
+            load_half4(res + roff + cg[0], rv);
+            load_half4(res + roff + cg[1], rv + 4);
+        } else {
+            hv[0] = half_bits_to_float(h[roff + cg[0]]);
+            rv[0] = half_bits_to_float(res[roff + cg[0]]);
+        }
+        float dt[W];
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            Chain ch = chain(hv[j], rv[j], gv[j], lo, hi);
+            const float dv = dw * (1.0f - ch.w * ch.w);
+            const float du = (ch.u > lo && ch.u < hi) ? dv : 0.0f;
+            dt[j] = du * gv[j];
+            acc[j] += du * ch.t;
+        }
+        if constexpr (VEC) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int64_t off = roff + cg[q];
+                const float4 d = make_float4(dt[4 * q], dt[4 * q + 1], dt[4 * q + 2], dt[4 * q + 3]);
+                if (gh) {
+                    float4 o = d;
+                    if (acc_h) {
+                        const float4 p = ld_stream(gh + off);
+                        o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
+                    }
+                    st_stream(gh + off, o);
+                }
+                if (gres) {
+                    float4 o = d;
+                    if (acc_res) {
+                        const float4 p = ld_stream(gres + off);
+                        o.x += p.x; o.y += p.y; o.z += p.z; o.w += p.w;
+                    }
+                    st_stream(gres + off, o);
+                }
+            }
+        } else {
+            const int64_t off = roff + cg[0];
+            if (gh) gh[off] = acc_h ? gh[off] + dt[0] : dt[0];
+            if (gres) gres[off] = acc_res ? gres[off] + dt[0] : dt[0];
+        }
+    }
+    if (part) {
+        float* pr = part + (int64_t)blockIdx.y * cols;
+        if constexpr (VEC) {
+            *reinterpret_cast<float4*>(pr + cg[0]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            *reinterpret_cast<float4*>(pr + cg[1]) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        } else {
+            pr[cg[0]] = acc[0];
+        }
+    }
+}
+
+// gg[c] (+)= sum_k part[k, c]: 64 columns per workgroup, 4 waves over k.
+__global__ void __launch_bounds__(kBlock) epilogue_gsum_kernel(const float* __restrict__ part, float* __restrict__ gg,
+                                                                int acc, int64_t K, int64_t C) {
+    __shared__ float lds[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    for (int64_t c0 = (int64_t)blockIdx.x * 64; c0 < C; c0 += (int64_t)gridDim.x * 64) {
+        const int64_t c = c0 + lane;
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        if (c < C) {
+            int64_t k = w;
+            for (; k + 12 < K; k += 16) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[j] += part[(k + 4 * j) * C + c];
+            }
+            for (int j = 0; k < K; k += 4, ++j) s[j & 3] += part[k * C + c];
+        }
+        lds[w][lane] = (s[0] + s[1]) + (s[2] + s[3]);
+        __syncthreads();
+        if (w == 0 && c < C) {
+            const float t = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+            gg[c] = acc ? gg[c] + t : t;
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+int wm_epilogue_f16_fwd(uint16_t* out, float* mean, const uint16_t* h, const uint16_t* res, const float* g,
+                        int64_t rows, int64_t cols, float lo, float hi) {
+    if (rows < 0 || cols < 0) return set_error(WM_ERR_INVALID, "wm_epilogue_f16_fwd: negative extent");
+    if (rows == 0 || cols == 0) return WM_OK;
+    if (!mean || !h || !res || !g) return set_error(WM_ERR_INVALID, "wm_epilogue_f16_fwd: null pointer");
+    WM_CHECK_INIT();
+    const bool vec = cols % 8 == 0 && aligned16(h) && aligned16(res) && aligned16(g) && (!out || aligned16(out));
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 16));
+    if (vec)
+        hipLaunchKernelGGL(epilogue_fwd_kernel<true>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
+                           cols, lo, hi);
+    else
+        hipLaunchKernelGGL(epilogue_fwd_kernel<false>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
+                           cols, lo, hi);
+    return check_launch("wm_epilogue_f16_fwd");
+}
+
+int wm_epilogue_f16_bwd(const float* dm, const uint16_t* h, const uint16_t* res, const float* g, float* gh,
+                        int acc_h, float* gres, int acc_res, float* gg, int acc_g, int64_t rows, int64_t cols,
+                        float lo, float hi) {
+    if (rows < 0 || cols < 0) return set_error(WM_ERR_INVALID, "wm_epilogue_f16_bwd: negative extent");
+    if (cols == 0) return WM_OK;
+    if (rows == 0) {
+        if (gg && !acc_g) return wm_fill(gg, 0.f, cols);
+        return WM_OK;
+    }
+    if (!dm || !h || !res || !g) return set_error(WM_ERR_INVALID, "wm_epilogue_f16_bwd: null pointer");
+    if (!gh && !gres && !gg) return WM_OK;
+    WM_CHECK_INIT();
+    const bool vec = cols % 512 == 0 && aligned16(h) && aligned16(res) && aligned16(g) && (!gh || aligned16(gh)) &&
+                     (!gres || aligned16(gres));
+    const int64_t W = vec ? 8 : 1;
+    const int64_t col_tiles = (cols + kBlock * W - 1) / (kBlock * W);
+    int64_t K = std::min<int64_t>(((int64_t)num_cus() * 8 + col_tiles - 1) / col_tiles, (rows + 15) / 16);
+    K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
+    const int64_t rpc = (rows + K - 1) / K;
+    K = (rows + rpc - 1) / rpc;
+    Workspace ws(gg ? (size_t)(K * cols) * sizeof(float) : 0);
+    if (gg && !ws.p) return set_error(WM_ERR_NOMEM, "wm_epilogue_f16_bwd: workspace");
+    dim3 grid((unsigned)col_tiles, (unsigned)K);
+    if (vec)
+        hipLaunchKernelGGL(epilogue_bwd_kernel<true>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres,
+                           acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
+    else
+        hipLaunchKernelGGL(epilogue_bwd_kernel<false>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h,
+                           gres, acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
+    WM_TRY(check_launch("wm_epilogue_f16_bwd"));
+    if (gg) {
+        hipLaunchKernelGGL(epilogue_gsum_kernel, dim3(grid_for(cols, 64, 8)), dim3(kBlock), 0, stream(),
+                           ws.as<float>(), gg, acc_g, K, cols);
+        WM_TRY(check_launch("wm_epilogue_f16_bwd(gsum)"));
+    }
+    return WM_OK;
+}
+
+}  // extern "C"
