@@ -88,8 +88,9 @@ def c2_ops(rows=8192, cols=8192):
             bwd_bytes = big + 2 * big + 2 * vb         # G; A.grad RMW; r.grad RMW
         else:
             bwd_bytes = big + big + vb + 2 * big + 2 * vb  # G, A, vector; grads RMW
-        kf = "binary_rows_kernel"
-        kb = "bwd_colsum_kernel" if other is dr else "bwd_rowsum_kernel"
+        # rocprof kernel-name prefixes (template arguments: op code, operand inner strides)
+        kf = "binary_rows_kernel<%d, 1, %d," % (code, 1 if other is dr else 0)
+        kb = ("bwd_colsum_kernel<%d," % code) if other is dr else ("bwd_rowsum_kernel<%d," % code)
         ops.append(Op(name + " fwd", fwd, fwd_bytes, kf, N))
         ops.append(Op(name + " bwd", bwd, bwd_bytes, kb, N))
     keep = [dA, dc, dr, dG, out, gA, gc, gr]
@@ -297,14 +298,16 @@ def cpu_baseline_c2(sample_rows=1024, cols=8192, reps=3):
 
 # ---------------------------------------------------------------------------
 
-def traffic_for(kernel: str, config: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+def traffic_for(op_name: str, config: str):
+    """HBM bytes per launch of an op's main kernel, from the committed
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json,
+    calibrated against the copy kernel)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     try:
         d = json.load(open(path))
-        return d.get(config, {}).get(kernel)
+        return d.get(config, {}).get(op_name, {}).get("hbm_bytes")
     except Exception:
         return None
 
@@ -367,7 +370,7 @@ def main():
     dom_ms = statistics.mean(dom.ms)
     dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.kernel, args.config),
+                "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.name, args.config),
                 "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes,
                 "avg_ms": round(dom_ms, 4)}
 
