@@ -8,6 +8,8 @@
 //
 // Handles are heap-allocated TensorPtr (std::shared_ptr<Tensor>).
 // amp.h uses std::memcpy without including <cstring> itself.
+#include <xmmintrin.h>
+
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -17,6 +19,18 @@
 
 namespace {
 
+// The reference's executables are linked with -ffast-math, whose start-up
+// file turns on flush-to-zero and denormals-are-zero for the process.  The
+// library is linked without that start-up file (it would change the FP mode
+// of every thread that loads it, the oracle's included); instead each entry
+// point that runs reference arithmetic switches FTZ/DAZ on for its own
+// duration and restores the caller's mode on return.
+struct RefFpMode {
+    unsigned saved;
+    RefFpMode() : saved(_mm_getcsr()) { _mm_setcsr(saved | 0x8040u); }
+    ~RefFpMode() { _mm_setcsr(saved); }
+};
+
 TensorPtr& T(void* h) { return *static_cast<TensorPtr*>(h); }
 void* box(TensorPtr t) { return new TensorPtr(std::move(t)); }
 
@@ -25,6 +39,7 @@ void* box(TensorPtr t) { return new TensorPtr(std::move(t)); }
 extern "C" {
 
 void* wmref_new(const float* data, const int64_t* shape, int nd, int requires_grad) {
+    RefFpMode fp_mode_;
     std::vector<size_t> s(shape, shape + nd);
     size_t n = 1;
     for (auto d : s) n *= d;
@@ -57,6 +72,7 @@ int wmref_get_grad(void* h, float* out) {
 
 // Binary: 0 add, 1 sub, 2 mul, 3 div, 4 pow, 5 max, 6 min (core/tensor.h:73-97).
 void* wmref_binary(int op, void* a, void* b) {
+    RefFpMode fp_mode_;
     const TensorPtr& x = T(a);
     const TensorPtr& y = T(b);
     switch (op) {
@@ -73,6 +89,7 @@ void* wmref_binary(int op, void* a, void* b) {
 // Unary: 0 relu, 1 sigmoid, 2 tanh_, 3 log_, 4 exp_, 5 pow(p0), 6 sqrt,
 // 7 abs, 8 clamp(p0, p1), 9 mul(p0), 10 div(p0), 11 neg.
 void* wmref_unary(int op, void* h, float p0, float p1) {
+    RefFpMode fp_mode_;
     const TensorPtr& x = T(h);
     switch (op) {
         case 0: return box(x->relu());
@@ -93,6 +110,7 @@ void* wmref_unary(int op, void* h, float p0, float p1) {
 // Reductions through the reference API: 0 sum, 1 mean, 2 max, 3 min,
 // 4 argmax, 5 argmin (core/tensor.h:92-99).
 void* wmref_reduce(int op, void* h, int dim, int keepdim) {
+    RefFpMode fp_mode_;
     const TensorPtr& x = T(h);
     bool k = keepdim != 0;
     switch (op) {
@@ -106,10 +124,12 @@ void* wmref_reduce(int op, void* h, int dim, int keepdim) {
 }
 
 void* wmref_softmax(int log, void* h, int dim) {
+    RefFpMode fp_mode_;
     return box(log ? T(h)->log_softmax(dim) : T(h)->softmax(dim));
 }
 
 void* wmref_reshape(void* h, const int64_t* shape, int nd) {
+    RefFpMode fp_mode_;
     std::vector<size_t> s(shape, shape + nd);
     return box(T(h)->reshape(s));
 }
@@ -117,6 +137,7 @@ void* wmref_reshape(void* h, const int64_t* shape, int nd) {
 // Inject an upstream gradient and run this node's closure only:
 // y->grad = g; y->grad_fn().  Returns 0 when the node has no closure.
 int wmref_run_grad_fn(void* h, const float* g) {
+    RefFpMode fp_mode_;
     TensorPtr& y = T(h);
     if (!y->grad_fn) return 0;
     y->grad.assign(g, g + y->data.size());
@@ -126,6 +147,7 @@ int wmref_run_grad_fn(void* h, const float* g) {
 
 // The same in two steps, so a timer can bracket the closure alone.
 int wmref_set_grad(void* h, const float* g) {
+    RefFpMode fp_mode_;
     TensorPtr& y = T(h);
     y->grad.assign(g, g + y->data.size());
     return y->grad_fn ? 1 : 0;
@@ -142,10 +164,12 @@ void wmref_set_grad_enabled(int on) { GradMode::set_enabled(on != 0); }
 
 // fp16 storage conversions of core/amp.h:15-72.
 void wmref_f32_to_f16(const float* x, uint16_t* out, int64_t n) {
+    RefFpMode fp_mode_;
     for (int64_t i = 0; i < n; ++i) out[i] = float_to_half(x[i]);
 }
 
 void wmref_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
+    RefFpMode fp_mode_;
     for (int64_t i = 0; i < n; ++i) out[i] = half_to_float(x[i]);
 }
 

@@ -42,6 +42,27 @@
 #define MINUS(x, y) ((x) - (y))
 #endif
 
+/* Floating-point mode.  A library built with -ffast-math elsewhere in the
+ * process (the reference's, for one) may have switched flush-to-zero and
+ * denormals-are-zero on for the calling thread; every entry point below sets
+ * the mode it is defined with for its own duration and restores the caller's
+ * on return: IEEE (both off) for the strict oracles, both on for the port
+ * build, as in the reference's -ffast-math executables. */
+#if defined(__x86_64__) || defined(__i386__)
+#include <xmmintrin.h>
+static void or_fp_restore(unsigned* saved) { _mm_setcsr(*saved); }
+#ifdef OR_REF_FP_MODE
+#define OR_FP_MODE(c) ((c) | 0x8040u)
+#else
+#define OR_FP_MODE(c) ((c) & ~0x8040u)
+#endif
+#define OR_FP_SCOPE                                                                  \
+    unsigned or_fp_saved_ __attribute__((cleanup(or_fp_restore))) = _mm_getcsr(); \
+    _mm_setcsr(OR_FP_MODE(or_fp_saved_))
+#else
+#define OR_FP_SCOPE (void)0
+#endif
+
 #define OR_MAX_DIMS 8
 
 enum { OR_ADD, OR_SUB, OR_MUL, OR_DIV, OR_POW, OR_MAX, OR_MIN };
@@ -118,6 +139,7 @@ static REAL bin_fwd(int op, float a, float b) {
  * Same-shape fast path and broadcast path visit outputs in the same order. */
 int or_binary(int op, REAL* out, const float* a, const int64_t* as, int an, const float* b, const int64_t* bs,
               int bn) {
+    OR_FP_SCOPE;
     int64_t os[OR_MAX_DIMS], ast[OR_MAX_DIMS], bst[OR_MAX_DIMS], idx[OR_MAX_DIMS] = {0};
     int nd;
     if (or_broadcast_shape(as, an, bs, bn, os, &nd)) return -1;
@@ -143,6 +165,7 @@ int or_binary(int op, REAL* out, const float* a, const int64_t* as, int an, cons
  *   min  :2049-2071 a <= b ? ga += g : gb += g                      */
 int or_binary_bwd(int op, const float* g, const float* a, const int64_t* as, int an, const float* b,
                   const int64_t* bs, int bn, const float* out, REAL* ga, REAL* gb) {
+    OR_FP_SCOPE;
     int64_t os[OR_MAX_DIMS], ast[OR_MAX_DIMS], bst[OR_MAX_DIMS], idx[OR_MAX_DIMS] = {0};
     int nd;
     if (or_broadcast_shape(as, an, bs, bn, os, &nd)) return -1;
@@ -170,7 +193,9 @@ int or_binary_bwd(int op, const float* g, const float* a, const int64_t* as, int
                 if (gb) ACC(gb[ib], -(gg * va / (vb * vb)));
                 break;
             case OR_POW:
-                if (ga) ACC(ga[ia], gg * vb * (REAL)pow(va, vb - (REAL)1.0f));
+                /* b - 1.0f is the reference's float subtraction: it rounds
+                 * (-1.0000001f - 1.0f == -2.0f), which decides pow's domain */
+                if (ga) ACC(ga[ia], gg * vb * (REAL)pow(va, (REAL)(b[ib] - 1.0f)));
                 if (gb) ACC(gb[ib], gg * (REAL)out[i] * (REAL)log(va));
                 break;
             case OR_MAX:
@@ -195,6 +220,7 @@ int or_binary_bwd(int op, const float* g, const float* a, const int64_t* as, int
  * :1363-1383, sqrt :1477-1496, abs :1498-1522, clamp :1524-1546
  * (std::max(lo, std::min(hi, x))), mul(float) :1237-1253. */
 int or_unary(int op, REAL* out, const float* x, int64_t n, float p0, float p1) {
+    OR_FP_SCOPE;
     for (int64_t i = 0; i < n; i++) {
         float v = x[i];
         REAL r;
@@ -220,6 +246,7 @@ int or_unary(int op, REAL* out, const float* x, int64_t n, float p0, float p1) {
  * :1374-1380, sqrt :1489-1494 (reads out), abs :1508-1519, clamp
  * :1533-1544, mul(float) :1246-1251.  gx accumulates. */
 int or_unary_bwd(int op, const float* g, const float* x, const float* out, REAL* gx, int64_t n, float p0, float p1) {
+    OR_FP_SCOPE;
     for (int64_t i = 0; i < n; i++) {
         REAL gg = g[i];
         switch (op) {
@@ -228,7 +255,7 @@ int or_unary_bwd(int op, const float* g, const float* x, const float* out, REAL*
             case OR_TANH: { REAL t = out[i]; ACC(gx[i], gg * ((REAL)1 - t * t)); break; }
             case OR_LOG: { float t = x[i] + 1e-8f; ACC(gx[i], gg / (REAL)t); break; }
             case OR_EXP: ACC(gx[i], gg * (REAL)out[i]); break;
-            case OR_POWS: ACC(gx[i], gg * (REAL)p0 * (REAL)pow((REAL)x[i], (REAL)p0 - (REAL)1)); break;
+            case OR_POWS: ACC(gx[i], gg * (REAL)p0 * (REAL)pow((REAL)x[i], (REAL)(p0 - 1.0f))); break;
             case OR_SQRT: ACC(gx[i], gg / ((REAL)2 * (REAL)out[i])); break;
             case OR_ABSOP:
                 if (x[i] > 0) ACC(gx[i], gg);
@@ -255,6 +282,7 @@ int or_unary_bwd(int op, const float* g, const float* x, const float* out, REAL*
  *   argmax/argmin N-d :2096-2142 / :2170-2216 (same scan; index as fp32)
  * val: REAL values (or fp32-representable indices for arg*); idx: positions. */
 int or_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner, REAL* val, int64_t* idx) {
+    OR_FP_SCOPE;
     if (n == 0 && op > OR_R_MEAN) return -1;
     for (int64_t o = 0; o < outer; o++) {
         for (int64_t i = 0; i < inner; i++) {
@@ -285,6 +313,7 @@ int or_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner, R
  * :1697-1703; mean reuses them, so no 1/n); max/min gx[o, idx, i] += g
  * (:1743-1745, :1774-1778, :1802-1806 and the min twins). */
 int or_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int64_t n, int64_t inner, REAL* gx) {
+    OR_FP_SCOPE;
     for (int64_t o = 0; o < outer; o++) {
         for (int64_t i = 0; i < inner; i++) {
             int64_t slot = o * inner + i;
@@ -305,6 +334,7 @@ int or_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int
 /* softmax :1556-1572: row max (std::max scan), out = exp(x - max), sum,
  * multiply by 1/sum. */
 int or_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
+    OR_FP_SCOPE;
     for (int64_t r = 0; r < rows; r++) {
         const float* xr = x + r * cols;
         REAL* orow = out + r * cols;
@@ -323,6 +353,7 @@ int or_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
 
 /* log_softmax :1601-1616: out = x - (max + log(sum exp(x - max))). */
 int or_log_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
+    OR_FP_SCOPE;
     for (int64_t r = 0; r < rows; r++) {
         const float* xr = x + r * cols;
         float m = xr[0];
@@ -339,6 +370,7 @@ int or_log_softmax(REAL* out, const float* x, int64_t rows, int64_t cols) {
  *   gx[j] += sum_k g[k] * (j == k ? s_j (1 - s_j) : -s_j s_k)
  * with s = the stored fp32 output. */
 int or_softmax_bwd(const float* g, const float* out, REAL* gx, int64_t rows, int64_t cols) {
+    OR_FP_SCOPE;
     for (int64_t r = 0; r < rows; r++) {
         const float* yr = out + r * cols;
         const float* gr = g + r * cols;
@@ -356,6 +388,7 @@ int or_softmax_bwd(const float* g, const float* out, REAL* gx, int64_t rows, int
 
 /* log_softmax closure :1621-1632: gx[j] += g[j] - exp(out[j]) * sum_k g[k]. */
 int or_log_softmax_bwd(const float* g, const float* out, REAL* gx, int64_t rows, int64_t cols) {
+    OR_FP_SCOPE;
     for (int64_t r = 0; r < rows; r++) {
         const float* gr = g + r * cols;
         const float* yr = out + r * cols;
@@ -418,11 +451,13 @@ static float h2f(uint16_t h) {
 }
 
 int or_f32_to_f16(uint16_t* out, const float* x, int64_t n) {
+    OR_FP_SCOPE;
     for (int64_t i = 0; i < n; i++) out[i] = f2h(x[i]);
     return 0;
 }
 
 int or_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
+    OR_FP_SCOPE;
     for (int64_t i = 0; i < n; i++) out[i] = h2f(x[i]);
     return 0;
 }

@@ -93,6 +93,31 @@ def test_oracle_matches_reference_binary(op, sa, sb):
     assert oracle.close_scaled(tb.grad(), gb64, sb64, 1e-5)[0], "grad b"
 
 
+@needs_ref
+def test_oracle_pow_grad_exponent_minus_one_is_float():
+    """d/da of pow reads pow(a, b - 1.0f) with b - 1.0f rounded in float
+    (core/tensor.cpp:1405-1406, :1377-1378): for b = -1.0000001f that is
+    exactly -2, so a negative base still has a finite gradient.  Computing
+    b - 1 in double would give a non-integer exponent and NaN."""
+    a = np.array([-2.0, -0.5, -3.0, 2.0], np.float32)
+    b = np.full(4, -1.0000001, np.float32)
+    assert np.float32(b[0] - np.float32(1.0)) == np.float32(-2.0)
+    ta, tb = ref.tensor(a, True), ref.tensor(b, False)
+    ty = ref.binary("pow", ta, tb)
+    g = np.ones(4, np.float32)
+    ty.run_grad_fn(g)
+    ga64, _ = oracle.get("f64").binary_bwd("pow", g, a, b, ty.data())
+    assert np.all(np.isfinite(ga64))
+    assert np.allclose(ga64, ta.grad(), rtol=1e-6)
+    # pow(Tensor, float) likewise
+    tx = ref.tensor(a, True)
+    tyu = ref.unary("pows", tx, float(b[0]), 0.0)
+    tyu.run_grad_fn(g)
+    gx64 = oracle.get("f64").unary_bwd("pows", g, a, tyu.data(), float(b[0]))
+    assert np.all(np.isfinite(gx64))
+    assert np.allclose(gx64, tx.grad(), rtol=1e-6)
+
+
 UNARY = [("relu", 0, 0), ("sigmoid", 0, 0), ("tanh", 0, 0), ("log", 0, 0), ("exp", 0, 0), ("pows", 2.5, 0),
          ("sqrt", 0, 0), ("abs", 0, 0), ("clamp", -0.5, 0.75)]
 

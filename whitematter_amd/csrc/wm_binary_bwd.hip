@@ -39,7 +39,6 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
     const bool need_a = (ga && da_reads_a<OP>()) || (gb && db_reads_a<OP>());
     const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
     const bool need_o = gb && db_reads_out<OP>() && o;
-    const bool recompute_o = gb && db_reads_out<OP>() && !o;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
@@ -50,25 +49,17 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
         float4 vo = need_o ? ld_stream(o + e) : z;
         float4 oa = (ga && acc_a) ? ld_stream(ga + e) : z;
         float4 ob = (gb && acc_b) ? ld_stream(gb + e) : z;
-        if (recompute_o) {
-            vo.x = binary_fwd<OP>(va.x, vb.x); vo.y = binary_fwd<OP>(va.y, vb.y);
-            vo.z = binary_fwd<OP>(va.z, vb.z); vo.w = binary_fwd<OP>(va.w, vb.w);
-        }
+        const float eg[4] = {vg.x, vg.y, vg.z, vg.w}, ea[4] = {va.x, va.y, va.z, va.w},
+                    eb[4] = {vb.x, vb.y, vb.z, vb.w}, eo[4] = {vo.x, vo.y, vo.z, vo.w};
+        float da[4], db[4];
+        binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, ga != nullptr, gb != nullptr, da, db);
         if (ga) {
-            float4 r;
-            r.x = binary_da<OP>(vg.x, va.x, vb.x);
-            r.y = binary_da<OP>(vg.y, va.y, vb.y);
-            r.z = binary_da<OP>(vg.z, va.z, vb.z);
-            r.w = binary_da<OP>(vg.w, va.w, vb.w);
+            float4 r = make_float4(da[0], da[1], da[2], da[3]);
             if (acc_a) { r.x += oa.x; r.y += oa.y; r.z += oa.z; r.w += oa.w; }
             st_stream(ga + e, r);
         }
         if (gb) {
-            float4 r;
-            r.x = binary_db<OP>(vg.x, va.x, vb.x, vo.x);
-            r.y = binary_db<OP>(vg.y, va.y, vb.y, vo.y);
-            r.z = binary_db<OP>(vg.z, va.z, vb.z, vo.z);
-            r.w = binary_db<OP>(vg.w, va.w, vb.w, vo.w);
+            float4 r = make_float4(db[0], db[1], db[2], db[3]);
             if (acc_b) { r.x += ob.x; r.y += ob.y; r.z += ob.z; r.w += ob.w; }
             st_stream(gb + e, r);
         }
@@ -110,32 +101,20 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
         float4 vf = need_F ? ld_stream(F + off) : z;
         float4 vo = need_o ? ld_stream(o + off) : z;
         float4 old = (gF && accF) ? ld_stream(gF + off) : z;
-        float4 av = VB ? vf : vv, bv = VB ? vv : vf;
-        if (want_o && !o) {
-            vo.x = binary_fwd<OP>(av.x, bv.x); vo.y = binary_fwd<OP>(av.y, bv.y);
-            vo.z = binary_fwd<OP>(av.z, bv.z); vo.w = binary_fwd<OP>(av.w, bv.w);
-        }
+        const float4 av = VB ? vf : vv, bv = VB ? vv : vf;
+        const float eg[4] = {vg.x, vg.y, vg.z, vg.w}, ea[4] = {av.x, av.y, av.z, av.w},
+                    eb[4] = {bv.x, bv.y, bv.z, bv.w}, eo[4] = {vo.x, vo.y, vo.z, vo.w};
+        float da[4], db[4];
+        binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, VB ? gF != nullptr : want_v, VB ? want_v : gF != nullptr, da,
+                              db);
+        const float* dF = VB ? da : db;
+        const float* dV = VB ? db : da;
         if (gF) {
-            float4 d;
-            if constexpr (VB) {
-                d.x = binary_da<OP>(vg.x, av.x, bv.x); d.y = binary_da<OP>(vg.y, av.y, bv.y);
-                d.z = binary_da<OP>(vg.z, av.z, bv.z); d.w = binary_da<OP>(vg.w, av.w, bv.w);
-            } else {
-                d.x = binary_db<OP>(vg.x, av.x, bv.x, vo.x); d.y = binary_db<OP>(vg.y, av.y, bv.y, vo.y);
-                d.z = binary_db<OP>(vg.z, av.z, bv.z, vo.z); d.w = binary_db<OP>(vg.w, av.w, bv.w, vo.w);
-            }
+            float4 d = make_float4(dF[0], dF[1], dF[2], dF[3]);
             if (accF) { d.x += old.x; d.y += old.y; d.z += old.z; d.w += old.w; }
             st_stream(gF + off, d);
         }
-        if (want_v) {
-            if constexpr (VB) {
-                s.x += binary_db<OP>(vg.x, av.x, bv.x, vo.x); s.y += binary_db<OP>(vg.y, av.y, bv.y, vo.y);
-                s.z += binary_db<OP>(vg.z, av.z, bv.z, vo.z); s.w += binary_db<OP>(vg.w, av.w, bv.w, vo.w);
-            } else {
-                s.x += binary_da<OP>(vg.x, av.x, bv.x); s.y += binary_da<OP>(vg.y, av.y, bv.y);
-                s.z += binary_da<OP>(vg.z, av.z, bv.z); s.w += binary_da<OP>(vg.w, av.w, bv.w);
-            }
-        }
+        if (want_v) { s.x += dV[0]; s.y += dV[1]; s.z += dV[2]; s.w += dV[3]; }
     }
     if (want_v) *reinterpret_cast<float4*>(part + (int64_t)blockIdx.y * C + c) = s;
 }
@@ -212,15 +191,13 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
                 float4 vf = need_F ? ld_stream(fr + c) : z4;
                 float4 vo = need_o ? ld_stream(orow + c) : z4;
                 float4 old = (gfr && accF) ? ld_stream(gfr + c) : z4;
-                float e[4] = {vf.x, vf.y, vf.z, vf.w}, gg[4] = {vg.x, vg.y, vg.z, vg.w},
-                      oo[4] = {vo.x, vo.y, vo.z, vo.w}, d[4], sv[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    float av = VB ? e[j] : v, bv = VB ? v : e[j];
-                    if (want_o && !o) oo[j] = binary_fwd<OP>(av, bv);
-                    if constexpr (VB) { d[j] = binary_da<OP>(gg[j], av, bv); sv[j] = binary_db<OP>(gg[j], av, bv, oo[j]); }
-                    else { d[j] = binary_db<OP>(gg[j], av, bv, oo[j]); sv[j] = binary_da<OP>(gg[j], av, bv); }
-                }
+                const float e[4] = {vf.x, vf.y, vf.z, vf.w}, gg[4] = {vg.x, vg.y, vg.z, vg.w},
+                            oo[4] = {vo.x, vo.y, vo.z, vo.w}, vv[4] = {v, v, v, v};
+                float da[4], db[4];
+                binary_grads_n<OP, 4>(gg, VB ? e : vv, VB ? vv : e, oo, need_o, VB ? gfr != nullptr : want_v,
+                                      VB ? want_v : gfr != nullptr, da, db);
+                const float* d = VB ? da : db;
+                const float* sv = VB ? db : da;
                 if (gfr) {
                     float4 nd = make_float4(d[0], d[1], d[2], d[3]);
                     if (accF) { nd.x += old.x; nd.y += old.y; nd.z += old.z; nd.w += old.w; }
@@ -233,11 +210,12 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
             for (int64_t c = c0 + lane; c < c1; c += 64) {
                 float vg = gr[c];
                 float vf = need_F ? fr[c] : 0.f;
-                float av = VB ? vf : v, bv = VB ? v : vf;
-                float vo = need_o ? orow[c] : ((want_o && !o) ? binary_fwd<OP>(av, bv) : 0.f);
-                float d, sv;
-                if constexpr (VB) { d = binary_da<OP>(vg, av, bv); sv = binary_db<OP>(vg, av, bv, vo); }
-                else { d = binary_db<OP>(vg, av, bv, vo); sv = binary_da<OP>(vg, av, bv); }
+                const float av = VB ? vf : v, bv = VB ? v : vf;
+                const float vo = need_o ? orow[c] : 0.f;
+                float da, db;
+                binary_grads<OP>(vg, av, bv, vo, need_o, VB ? gfr != nullptr : want_v,
+                                 VB ? want_v : gfr != nullptr, da, db);
+                const float d = VB ? da : db, sv = VB ? db : da;
                 if (gfr) gfr[c] = accF ? gfr[c] + d : d;
                 s += sv;
             }

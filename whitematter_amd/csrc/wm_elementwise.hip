@@ -186,23 +186,18 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
                                                               const float* __restrict__ b, int64_t n4) {
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
-        float4 va[kUnroll], vb[kUnroll];
+        float4 va[kUnroll], vb[kUnroll], vr[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
+            va[u] = vb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < n4) { va[u] = ld_stream(a + 4 * i); vb[u] = ld_stream(b + 4 * i); }
         }
+        binary_fwd_v<OP, kUnroll>(vr, va, vb);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) {
-                float4 r;
-                r.x = binary_fwd<OP>(va[u].x, vb[u].x);
-                r.y = binary_fwd<OP>(va[u].y, vb[u].y);
-                r.z = binary_fwd<OP>(va[u].z, vb[u].z);
-                r.w = binary_fwd<OP>(va[u].w, vb[u].w);
-                st_stream(out + 4 * i, r);
-            }
+            if (i < n4) st_stream(out + 4 * i, vr[u]);
         }
     }
 }
@@ -229,12 +224,13 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
         const float* br = b + ob;
         float* orow = out + row * inner;
         if constexpr (VEC) {
-            float4 va[kUnroll], vb[kUnroll];
+            float4 va[kUnroll], vb[kUnroll], vr[kUnroll];
             float sa0 = AI ? 0.f : ar[0];
             float sb0 = BI ? 0.f : br[0];
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                va[u] = vb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (c < inner) {
                     va[u] = AI ? (stream_a ? ld_stream(ar + c) : *reinterpret_cast<const float4*>(ar + c))
                                : make_float4(sa0, sa0, sa0, sa0);
@@ -242,17 +238,11 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
                                : make_float4(sb0, sb0, sb0, sb0);
                 }
             }
+            binary_fwd_v<OP, kUnroll>(vr, va, vb);
 #pragma unroll
             for (int u = 0; u < kUnroll; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
-                if (c < inner) {
-                    float4 r;
-                    r.x = binary_fwd<OP>(va[u].x, vb[u].x);
-                    r.y = binary_fwd<OP>(va[u].y, vb[u].y);
-                    r.z = binary_fwd<OP>(va[u].z, vb[u].z);
-                    r.w = binary_fwd<OP>(va[u].w, vb[u].w);
-                    st_stream(orow + c, r);
-                }
+                if (c < inner) st_stream(orow + c, vr[u]);
             }
         } else {
 #pragma unroll
@@ -301,23 +291,18 @@ __global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ o
     const int64_t n4 = n / 4;
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
-        float4 v[kUnroll];
+        float4 v[kUnroll], r[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
+            v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < n4) v[u] = ld_stream(x + 4 * i);
         }
+        unary_fwd_v<OP, kUnroll>(r, v, p0, p1);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) {
-                float4 r;
-                r.x = unary_fwd<OP>(v[u].x, p0, p1);
-                r.y = unary_fwd<OP>(v[u].y, p0, p1);
-                r.z = unary_fwd<OP>(v[u].z, p0, p1);
-                r.w = unary_fwd<OP>(v[u].w, p0, p1);
-                st_stream(out + 4 * i, r);
-            }
+            if (i < n4) st_stream(out + 4 * i, r[u]);
         }
     }
     // Scalar tail (n % 4 elements).
@@ -347,10 +332,11 @@ __global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restri
     const int64_t n4 = n / 4;
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
-        float4 vg[kUnroll], vx[kUnroll], vo[kUnroll], vgx[kUnroll];
+        float4 vg[kUnroll], vx[kUnroll], vo[kUnroll], vgx[kUnroll], r[kUnroll];
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
+            vg[u] = vx[u] = vo[u] = vgx[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < n4) {
                 vg[u] = ld_stream(g + 4 * i);
                 vx[u] = RX ? ld_stream(x + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -358,17 +344,11 @@ __global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restri
                 vgx[u] = ACC ? ld_stream(gx + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
+        unary_bwd_v<OP, ACC, kUnroll>(r, vg, vx, vo, vgx, p0, p1);
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) {
-                float4 r;
-                r.x = ubwd1<OP, ACC>(vg[u].x, vx[u].x, vo[u].x, vgx[u].x, p0, p1);
-                r.y = ubwd1<OP, ACC>(vg[u].y, vx[u].y, vo[u].y, vgx[u].y, p0, p1);
-                r.z = ubwd1<OP, ACC>(vg[u].z, vx[u].z, vo[u].z, vgx[u].z, p0, p1);
-                r.w = ubwd1<OP, ACC>(vg[u].w, vx[u].w, vo[u].w, vgx[u].w, p0, p1);
-                st_stream(gx + 4 * i, r);
-            }
+            if (i < n4) st_stream(gx + 4 * i, r[u]);
         }
     }
     for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "wm_common.hpp"
+#include "wm_pow.hpp"
 
 namespace wm {
 
@@ -18,7 +19,7 @@ __device__ __forceinline__ float binary_fwd(float a, float b) {
     else if constexpr (OP == WM_SUB) return a - b;     // :990 / :1022
     else if constexpr (OP == WM_MUL) return a * b;     // :1072 / :1104
     else if constexpr (OP == WM_DIV) return a / b;     // :1155 / :1191 (IEEE)
-    else if constexpr (OP == WM_POW) return powf(a, b);  // :1394 / :1430
+    else if constexpr (OP == WM_POW) return pow_f32(a, b);  // :1394 / :1430
     else if constexpr (OP == WM_MAX) return (a < b) ? b : a;  // :1910
     else return (b < a) ? b : a;                        // :1997
 }
@@ -31,7 +32,7 @@ __device__ __forceinline__ float binary_da(float g, float a, float b) {
     if constexpr (OP == WM_ADD || OP == WM_SUB) return g;             // :913, :997
     else if constexpr (OP == WM_MUL) return g * b;                     // :1080
     else if constexpr (OP == WM_DIV) return g / b;                     // :1167
-    else if constexpr (OP == WM_POW) return g * b * powf(a, b - 1.0f); // :1405-1406
+    else if constexpr (OP == WM_POW) return g * b * pow_f32(a, b - 1.0f); // :1405-1406
     else if constexpr (OP == WM_MAX) return (a >= b) ? g : 0.0f;       // :1920
     else return (a <= b) ? g : 0.0f;                                   // :2007
 }
@@ -55,11 +56,93 @@ template <int OP> constexpr bool db_reads_b() { return OP == WM_DIV || OP == WM_
 template <int OP> constexpr bool db_reads_out() { return OP == WM_POW; }
 
 // pow's d/db reads the forward output; when the caller passes no output
-// buffer it is recomputed bit-identically (same powf on the same operands),
+// buffer it is recomputed bit-identically (same pow on the same operands),
 // which saves one full-size read.
 template <int OP>
 __device__ __forceinline__ float fwd_out_or(const float* o, int64_t i, float a, float b) {
     return o ? o[i] : binary_fwd<OP>(a, b);
+}
+
+// d/da and d/db of one output element together (only the requested ones are
+// meaningful).  `o` is the forward output when `have_o`, else it is
+// recomputed.  For pow the two share one log2|a|: it feeds the recomputed
+// pow(a, b), pow(a, b - 1) and log(a), which costs about as much as one
+// pow instead of three transcendental calls; those three carry a relative
+// error of ~2e-7 (gradient precision), where binary_da / binary_db use the
+// 1-ulp pow.
+template <int OP>
+__device__ __forceinline__ void binary_grads(float g, float a, float b, float o, bool have_o, bool want_da,
+                                             bool want_db, float& da, float& db) {
+    if constexpr (OP == WM_POW) {
+        const PowGrad p = pow_grad_parts(a, b, want_db && !have_o, want_da, want_db);
+        da = g * b * p.pbm1;
+        db = g * (have_o ? o : p.out) * p.lga;
+    } else {
+        da = binary_da<OP>(g, a, b);
+        db = binary_db<OP>(g, a, b, (db_reads_out<OP>() && !have_o) ? binary_fwd<OP>(a, b) : o);
+    }
+}
+
+// binary_grads over N elements.  pow runs the branch-free table path for all
+// N first and fixes up special operands in one branch afterwards, so the N
+// table lookups overlap instead of each waiting behind its own branch.
+template <int OP, int N>
+__device__ __forceinline__ void binary_grads_n(const float (&g)[N], const float (&a)[N], const float (&b)[N],
+                                               const float (&o)[N], bool have_o, bool want_da, bool want_db,
+                                               float (&da)[N], float (&db)[N]) {
+    if constexpr (OP == WM_POW) {
+        const bool want_out = want_db && !have_o;
+        PowGrad p[N];
+        bool fix = false;
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            p[j] = pow_grad_table(a[j], b[j], want_out, want_da, want_db);
+            fix |= pow_grad_needs_fix(a[j], b[j]);
+        }
+        if (fix) {
+#pragma unroll
+            for (int j = 0; j < N; ++j)
+                if (pow_grad_needs_fix(a[j], b[j])) pow_grad_fix(a[j], b[j], want_out, want_da, want_db, p[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < N; ++j) {
+            da[j] = g[j] * b[j] * p[j].pbm1;
+            db[j] = g[j] * (have_o ? o[j] : p[j].out) * p[j].lga;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < N; ++j) binary_grads<OP>(g[j], a[j], b[j], o[j], have_o, want_da, want_db, da[j], db[j]);
+    }
+}
+
+// binary_fwd over U float4s, with pow's table path first and one fix-up
+// branch after (as in binary_grads_n).
+template <int OP, int U>
+__device__ __forceinline__ void binary_fwd_v(float4 (&r)[U], const float4 (&a)[U], const float4 (&b)[U]) {
+    if constexpr (OP == WM_POW) {
+        bool fix = false;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            r[u] = make_float4(pow_table(a[u].x, b[u].x), pow_table(a[u].y, b[u].y), pow_table(a[u].z, b[u].z),
+                               pow_table(a[u].w, b[u].w));
+            fix |= pow_needs_fix(a[u].x, b[u].x) | pow_needs_fix(a[u].y, b[u].y) | pow_needs_fix(a[u].z, b[u].z) |
+                   pow_needs_fix(a[u].w, b[u].w);
+        }
+        if (fix) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (pow_needs_fix(a[u].x, b[u].x)) r[u].x = powf(a[u].x, b[u].x);
+                if (pow_needs_fix(a[u].y, b[u].y)) r[u].y = powf(a[u].y, b[u].y);
+                if (pow_needs_fix(a[u].z, b[u].z)) r[u].z = powf(a[u].z, b[u].z);
+                if (pow_needs_fix(a[u].w, b[u].w)) r[u].w = powf(a[u].w, b[u].w);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            r[u] = make_float4(binary_fwd<OP>(a[u].x, b[u].x), binary_fwd<OP>(a[u].y, b[u].y),
+                               binary_fwd<OP>(a[u].z, b[u].z), binary_fwd<OP>(a[u].w, b[u].w));
+    }
 }
 
 // ---- unary forward --------------------------------------------------------
@@ -74,7 +157,7 @@ __device__ __forceinline__ float unary_fwd(float x, float p0, float p1) {
         // device implementation measured 2.25 ulp at worst).
         return (float)log((double)(x + 1e-8f));
     else if constexpr (OP == WM_EXP) return expf(x);                    // :1348
-    else if constexpr (OP == WM_POWS) return powf(x, p0);               // :1368
+    else if constexpr (OP == WM_POWS) return pow_f32(x, p0);            // :1368
     else if constexpr (OP == WM_SQRT) return sqrtf(x);                  // :1482
     else if constexpr (OP == WM_ABS) return fabsf(x);                   // :1503
     else if constexpr (OP == WM_CLAMP) {                                // :1529
@@ -93,7 +176,7 @@ __device__ __forceinline__ float unary_bwd(float g, float x, float o, float p0, 
     else if constexpr (OP == WM_TANH) return g * (1.0f - o * o);        // :1316-1317
     else if constexpr (OP == WM_LOG) return g / (x + 1e-8f);            // :1336
     else if constexpr (OP == WM_EXP) return g * o;                      // :1356
-    else if constexpr (OP == WM_POWS) return g * p0 * powf(x, p0 - 1.0f);  // :1377-1378
+    else if constexpr (OP == WM_POWS) return g * p0 * pow_f32(x, p0 - 1.0f);  // :1377-1378
     else if constexpr (OP == WM_SQRT) return g / (2.0f * o);            // :1492
     else if constexpr (OP == WM_ABS)                                    // :1512-1517
         return x > 0.0f ? g : (x < 0.0f ? -g : 0.0f);
@@ -111,6 +194,48 @@ template <int OP> constexpr bool unary_bwd_reads_x() {
 }
 template <int OP> constexpr bool unary_bwd_reads_out() {
     return OP == WM_SIGMOID || OP == WM_TANH || OP == WM_EXP || OP == WM_SQRT;
+}
+
+// unary_fwd over U float4s; pow(x, p0) as in binary_fwd_v.
+template <int OP, int U>
+__device__ __forceinline__ void unary_fwd_v(float4 (&r)[U], const float4 (&x)[U], float p0, float p1) {
+    if constexpr (OP == WM_POWS) {
+        float4 pe[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) pe[u] = make_float4(p0, p0, p0, p0);
+        binary_fwd_v<WM_POW, U>(r, x, pe);
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            r[u] = make_float4(unary_fwd<OP>(x[u].x, p0, p1), unary_fwd<OP>(x[u].y, p0, p1),
+                               unary_fwd<OP>(x[u].z, p0, p1), unary_fwd<OP>(x[u].w, p0, p1));
+    }
+}
+
+// unary_bwd over U float4s, plus the existing gradient when ACC; pow's
+// pow(x, p0 - 1) as in binary_fwd_v.
+template <int OP, bool ACC, int U>
+__device__ __forceinline__ void unary_bwd_v(float4 (&r)[U], const float4 (&g)[U], const float4 (&x)[U],
+                                            const float4 (&o)[U], const float4 (&gx)[U], float p0, float p1) {
+    if constexpr (OP == WM_POWS) {
+        const float pm1 = p0 - 1.0f;
+        float4 pe[U], q[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) pe[u] = make_float4(pm1, pm1, pm1, pm1);
+        binary_fwd_v<WM_POW, U>(q, x, pe);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            r[u] = make_float4(g[u].x * p0 * q[u].x, g[u].y * p0 * q[u].y, g[u].z * p0 * q[u].z, g[u].w * p0 * q[u].w);
+            if (ACC) { r[u].x += gx[u].x; r[u].y += gx[u].y; r[u].z += gx[u].z; r[u].w += gx[u].w; }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            r[u] = make_float4(unary_bwd<OP>(g[u].x, x[u].x, o[u].x, p0, p1), unary_bwd<OP>(g[u].y, x[u].y, o[u].y, p0, p1),
+                               unary_bwd<OP>(g[u].z, x[u].z, o[u].z, p0, p1), unary_bwd<OP>(g[u].w, x[u].w, o[u].w, p0, p1));
+            if (ACC) { r[u].x = gx[u].x + r[u].x; r[u].y = gx[u].y + r[u].y; r[u].z = gx[u].z + r[u].z; r[u].w = gx[u].w + r[u].w; }
+        }
+    }
 }
 
 }  // namespace wm

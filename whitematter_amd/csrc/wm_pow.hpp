@@ -1,0 +1,230 @@
+// Table-driven float pow for the pow kernels.
+//
+// The device powf costs ~166 vector instructions per element on gfx950,
+// which makes pow(Tensor) compute-bound (about a third of the HBM rate).
+// This one evaluates y * log2|x| and the power of two in double precision,
+// where small tables make both halves short:
+//   log2|x|: |x| = 2^k * z with z in [0.699, 1.398); 16 sub-intervals of z
+//            with invc ~ 1/c (20 significant bits, so z * invc is exact in
+//            double) and logc = log2(c); r = z * invc - 1 with |r| < 0.0297;
+//            log2(1 + r) by its series to r^6 (truncation < 4.2e-12).
+//   2^t:     t = kd/32 + r with |r| <= 1/64; 2^(kd/32) from a 32-entry
+//            table and an exponent shift; 2^r = e^(r ln 2) by its series to
+//            degree 3 (truncation < 5.7e-10 relative).
+// The double result is within ~6e-10 (relative) of the exact power, so its
+// one rounding to float is within 1 ulp.  A negative base takes C pow's sign
+// rule (NaN for a non-integer exponent, the magnitude's sign flipped for an
+// odd one) without a branch.  The operands the tables do not cover (zero,
+// subnormal, infinite or NaN bases, |x| == 1, and infinite, NaN or zero
+// exponents) go to the device powf in a branch that a wave skips when none
+// of its lanes needs it.
+//
+// The backward needs pow(a, b), pow(a, b - 1) and log(a) only inside
+// gradients, so it shares one log2|a| and takes the powers of two from the
+// hardware exp2 on a reduced argument (relative error ~2e-7).
+//
+// The file is plain C++ with explicit fma(), so the same code compiles for
+// the host and is checked there against long double powl.
+#pragma once
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+
+#ifdef __HIPCC__
+#define WM_HD __host__ __device__
+#else
+#define WM_HD
+#endif
+
+namespace wm {
+namespace powdetail {
+
+struct LogEntry {
+    double invc, logc;
+};
+
+WM_HD inline const LogEntry* log_table() {
+    static constexpr LogEntry t[16] = {
+        {1.3989067077636719, -0.48429975325710395}, {1.3403148651123047, -0.4225719566348825},
+        {1.2864322662353516, -0.3633754976944188},  {1.236715316772461, -0.3065134402105001},
+        {1.1906986236572266, -0.2518083005440589},  {1.1479816436767578, -0.19909957338273085},
+        {1.108224868774414, -0.14825064686535408},  {1.0711288452148438, -0.09913203113589106},
+        {1.03643798828125, -0.051633800310858485},  {0.9980506896972656, 0.002815004858138399},
+        {0.9481477737426758, 0.07681616674347436},  {0.8951053619384766, 0.15987058435448812},
+        {0.847681999206543, 0.23840494355449127},   {0.8050317764282227, 0.31288236409411413},
+        {0.7664670944213867, 0.38370423872947484},  {0.7314281463623047, 0.4512119502479954},
+    };
+    return t;
+}
+
+// 2^(j/32), j = 0..31
+WM_HD inline const double* exp2_table() {
+    static constexpr double t[32] = {
+        1.0,                1.0218971486541166, 1.0442737824274138, 1.0671404006768237, 1.0905077326652577,
+        1.1143867425958924, 1.1387886347566916, 1.1637248587775775, 1.189207115002721,  1.215247359980469,
+        1.241857812073484,  1.2690509571917332, 1.2968395546510096, 1.3252366431597413, 1.3542555469368927,
+        1.383909881963832,  1.4142135623730951, 1.4451808069770467, 1.4768261459394993, 1.5091644275934228,
+        1.5422108254079407, 1.5759808451078865, 1.6104903319492543, 1.645755478153965,  1.681792830507429,
+        1.718619298122478,  1.7562521603732995, 1.7947090750031072, 1.8340080864093424, 1.8741676341103,
+        1.9152065613971474, 1.9571441241754002,
+    };
+    return t;
+}
+
+WM_HD inline uint32_t bits_of(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+WM_HD inline float float_of(uint32_t u) {
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+WM_HD inline uint32_t low_word(double d) {
+    uint64_t u;
+    std::memcpy(&u, &d, 8);
+    return (uint32_t)u;
+}
+
+// log2(ax) for a normal ax > 0.  Branch-free; any other input gives a
+// meaningless value, but the table index always stays in range.
+WM_HD inline double log2_normal(float ax) {
+    const uint32_t ix = bits_of(ax);
+    const uint32_t OFF = 0x3f330000u;
+    const uint32_t tmp = ix - OFF;
+    const int i = (int)((tmp >> 19) & 15u);
+    const int k = (int)((int32_t)tmp >> 23);
+    const double z = (double)float_of(ix - (tmp & 0xff800000u));
+    const LogEntry e = log_table()[i];
+    const double r = std::fma(z, e.invc, -1.0);
+    // log2(1 + r) = r * (C1 + C2 r + ... + C6 r^5), Cn = (-1)^(n+1) / (n ln 2)
+    const double C1 = 1.4426950408889634, C2 = -0.7213475204444817, C3 = 0.48089834696298783,
+                 C4 = -0.36067376022224085, C5 = 0.28853900817779266, C6 = -0.24044917348149392;
+    double q = std::fma(C6, r, C5);
+    q = std::fma(q, r, C4);
+    q = std::fma(q, r, C3);
+    q = std::fma(q, r, C2);
+    q = std::fma(q, r, C1);
+    return std::fma(q, r, (double)k + e.logc);
+}
+
+// 2^t rounded once to float, within 1 ulp: overflow -> inf, underflow -> 0
+// or a rounded subnormal.  t is clamped to [-200, 200] (NaN -> 200), so the
+// integer conversion is exact and the table index in range.
+WM_HD inline float exp2_to_float(double t) {
+    t = std::fmax(std::fmin(t, 200.0), -200.0);
+    // kd = rint(32 t) by adding 1.5 * 2^52: the low word is then rint(32 t)
+    // in two's complement (|32 t| <= 6400).
+    const double SHIFT = 6755399441055744.0;
+    const double kds = std::fma(t, 32.0, SHIFT);
+    const int ki = (int)low_word(kds);
+    const double kd = kds - SHIFT;
+    const double r = std::fma(kd, -1.0 / 32.0, t);  // exact, |r| <= 1/64
+    // 2^r = 1 + E1 r + E2 r^2 + E3 r^3, En = (ln 2)^n / n!
+    const double E1 = 0.6931471805599453, E2 = 0.2402265069591007, E3 = 0.055504108664821576;
+    double p = std::fma(E3, r, E2);
+    p = std::fma(p, r, E1);
+    p = std::fma(p, r, 1.0);
+    return (float)std::ldexp(exp2_table()[ki & 31] * p, ki >> 5);
+}
+
+// 2^t for values used only inside gradients: relative error ~2e-7 (the
+// hardware exp2 of a float argument in [-0.5, 0.5], then an exact shift;
+// results in the subnormal range round once more).
+WM_HD inline float exp2_grad(double t) {
+    t = std::fmax(std::fmin(t, 200.0), -200.0);
+    const double n = std::rint(t);
+    const float f = (float)(t - n);
+#ifdef __HIP_DEVICE_COMPILE__
+    const float p = __builtin_amdgcn_exp2f(f);
+#else
+    const float p = std::exp2(f);
+#endif
+    return std::ldexp(p, (int)n);
+}
+
+// Operands the table path covers: |x| normal and != 1, y finite and
+// non-zero.  |x| == 1 is excluded because pow(+-1, y) must be exactly +-1,
+// and the table's log2(1) is only zero to ~1e-19, which a huge y would
+// amplify.
+WM_HD inline bool table_ok(float x, float y) {
+    const float ax = std::fabs(x), ay = std::fabs(y);
+    return ax >= 1.17549435e-38f && ax <= 3.40282347e+38f && ax != 1.0f && ay > 0.0f && ay <= 3.40282347e+38f;
+}
+
+// C pow's sign rule for a finite non-zero base, given the magnitude
+// |x|^y: a negative base gives NaN for a non-integer exponent and flips
+// the sign for an odd one.  Branch-free.
+WM_HD inline float apply_sign(float x, float y, float mag) {
+    const float yi = std::rint(y);
+    const bool is_int = yi == y;
+    // |y| >= 2^24 is always even; the clamp keeps the conversion in range.
+    const bool odd = ((int)std::fmin(std::fabs(yi), 16777216.0f) & 1) != 0;
+    const float s = odd ? -mag : mag;
+    return x < 0.0f ? (is_int ? s : NAN) : mag;
+}
+
+}  // namespace powdetail
+
+// The table path alone: equal to pow(x, y) within 1 ulp wherever
+// pow_needs_fix(x, y) is false.  Branch-free, so kernels evaluate it for a
+// whole vector of elements (the table lookups overlap) before fixing up the
+// rare specials.
+WM_HD inline float pow_table(float x, float y) {
+    using namespace powdetail;
+    return apply_sign(x, y, exp2_to_float((double)y * log2_normal(std::fabs(x))));
+}
+
+WM_HD inline bool pow_needs_fix(float x, float y) { return !powdetail::table_ok(x, y); }
+
+// pow(x, y) with C semantics, within 1 ulp.
+WM_HD inline float pow_f32(float x, float y) {
+    return pow_needs_fix(x, y) ? powf(x, y) : pow_table(x, y);
+}
+
+// The three values pow's backward needs, sharing one log2|a|:
+//   out  = pow(a, b)            (the forward output, recomputed; d/db)
+//   pbm1 = pow(a, b - 1.0f)     (d/da = g * b * pbm1)
+//   lga  = log(a)               (d/db = g * out * lga)
+// Only the requested ones are computed (the others are 0).  On the table
+// path out and pbm1 carry a relative error of ~2e-7 and lga is log(a)
+// rounded once from double (NaN for a < 0); pow_grad_fix replaces them with
+// powf / logf where pow_grad_needs_fix.
+struct PowGrad {
+    float out, pbm1, lga;
+};
+
+WM_HD inline PowGrad pow_grad_table(float a, float b, bool want_out, bool want_pbm1, bool want_lga) {
+    using namespace powdetail;
+    PowGrad r = {0.0f, 0.0f, 0.0f};
+    const double l2 = log2_normal(std::fabs(a));
+    if (want_out) r.out = apply_sign(a, b, exp2_grad((double)b * l2));
+    if (want_pbm1) {
+        const float bm1 = b - 1.0f;
+        r.pbm1 = apply_sign(a, bm1, exp2_grad((double)bm1 * l2));
+    }
+    if (want_lga) r.lga = a > 0.0f ? (float)(l2 * 0.6931471805599453) : NAN;
+    return r;
+}
+
+WM_HD inline bool pow_grad_needs_fix(float a, float b) {
+    return !powdetail::table_ok(a, b) || !powdetail::table_ok(a, b - 1.0f);
+}
+
+WM_HD inline void pow_grad_fix(float a, float b, bool want_out, bool want_pbm1, bool want_lga, PowGrad& r) {
+    if (want_out) r.out = powf(a, b);
+    if (want_pbm1) r.pbm1 = powf(a, b - 1.0f);
+    if (want_lga) r.lga = logf(a);
+}
+
+WM_HD inline PowGrad pow_grad_parts(float a, float b, bool want_out, bool want_pbm1, bool want_lga) {
+    PowGrad r = pow_grad_table(a, b, want_out, want_pbm1, want_lga);
+    if (pow_grad_needs_fix(a, b)) pow_grad_fix(a, b, want_out, want_pbm1, want_lga, r);
+    return r;
+}
+
+}  // namespace wm
