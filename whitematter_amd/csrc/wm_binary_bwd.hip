@@ -36,6 +36,7 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
                                                            const float* __restrict__ b, const float* __restrict__ o,
                                                            float* __restrict__ ga, int acc_a, float* __restrict__ gb,
                                                            int acc_b, int64_t n4) {
+    binary_prologue<OP>();
     const bool need_a = (ga && da_reads_a<OP>()) || (gb && db_reads_a<OP>());
     const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
     const bool need_o = gb && db_reads_out<OP>() && o;
@@ -77,6 +78,7 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
                                                              const float* __restrict__ V, const float* __restrict__ o,
                                                              float* __restrict__ gF, int accF, float* __restrict__ part,
                                                              int64_t R, int64_t C, int64_t rows_per_chunk) {
+    binary_prologue<OP>();
     const int64_t c = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 4;
     if (c >= C) return;
     const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
@@ -159,6 +161,7 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
                                                              float* __restrict__ gF, int accF, float* __restrict__ gV,
                                                              int accV, float* __restrict__ part, int64_t R, int64_t C,
                                                              int64_t chunk, int64_t K) {
+    binary_prologue<OP>();
     const int lane = threadIdx.x & 63;
     const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
     const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
@@ -262,6 +265,7 @@ template <int OP, bool WB>
 __global__ void __launch_bounds__(kBlock) bwd_generic_kernel(const float* __restrict__ g, const float* __restrict__ a,
                                                               const float* __restrict__ b, const float* __restrict__ o,
                                                               float* __restrict__ gx, int acc, int64_t nx, GenDims d) {
+    binary_prologue<OP>();
     for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < nx; e += (int64_t)gridDim.x * kBlock) {
         // Output base index from the kept dims of this operand.
         int64_t base = 0;

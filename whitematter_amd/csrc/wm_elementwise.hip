@@ -106,6 +106,10 @@ struct RowDims {
 };
 
 __device__ __forceinline__ void row_offsets(const RowDims& d, int64_t row, int64_t& oa, int64_t& ob) {
+    if (d.nd == 1) {  // one outer dim (the common folded case): row < size[0]
+        oa = row * d.sa[0]; ob = row * d.sb[0];
+        return;
+    }
     oa = 0; ob = 0;
     for (int i = d.nd - 1; i >= 0; --i) {
         int64_t s = d.size[i];
@@ -184,6 +188,7 @@ __global__ void __launch_bounds__(kBlock) f16_to_f32_kernel(float* __restrict__ 
 template <int OP>
 __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__ out, const float* __restrict__ a,
                                                               const float* __restrict__ b, int64_t n4) {
+    binary_prologue<OP>();
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
         float4 va[kUnroll], vb[kUnroll], vr[kUnroll];
@@ -212,12 +217,18 @@ template <int OP, int AI, int BI, bool VEC>
 __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a,
                                                               const float* __restrict__ b, int64_t rows, int64_t inner,
                                                               RowDims d, int stream_a, int stream_b) {
+    binary_prologue<OP>();
     constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * kUnroll;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
-    const int64_t tiles = rows * tiles_per_row;
-    for (int64_t t = blockIdx.x; t < tiles; t += gridDim.x) {
-        const int64_t row = t / tiles_per_row;
-        const int64_t c0 = (t - row * tiles_per_row) * kTile;
+    // Grid-stride over (row, tile) pairs, advanced incrementally so the loop
+    // itself divides nothing (a 64-bit division costs ~40 instructions).
+    const int64_t step_rows = (int64_t)gridDim.x / tiles_per_row;
+    const int64_t step_tiles = (int64_t)gridDim.x - step_rows * tiles_per_row;
+    int64_t row = (int64_t)blockIdx.x / tiles_per_row;
+    int64_t tile = (int64_t)blockIdx.x - row * tiles_per_row;
+    for (; row < rows; row += step_rows, tile += step_tiles) {
+        if (tile >= tiles_per_row) { tile -= tiles_per_row; ++row; if (row >= rows) break; }
+        const int64_t c0 = tile * kTile;
         int64_t oa, ob;
         row_offsets(d, row, oa, ob);
         const float* ar = a + oa;
@@ -277,6 +288,7 @@ __device__ __forceinline__ void full_offsets(const FullDims& d, int64_t i, int64
 template <int OP>
 __global__ void __launch_bounds__(kBlock) binary_generic_kernel(float* __restrict__ out, const float* __restrict__ a,
                                                                  const float* __restrict__ b, int64_t n, FullDims d) {
+    binary_prologue<OP>();
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         int64_t oa, ob;
@@ -288,6 +300,7 @@ __global__ void __launch_bounds__(kBlock) binary_generic_kernel(float* __restric
 template <int OP>
 __global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
                                                             int64_t n, float p0, float p1) {
+    unary_prologue<OP>();
     const int64_t n4 = n / 4;
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
     for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
@@ -313,6 +326,7 @@ __global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ o
 template <int OP>
 __global__ void __launch_bounds__(kBlock) unary_fwd_scalar_kernel(float* __restrict__ out, const float* __restrict__ x,
                                                                    int64_t n, float p0, float p1) {
+    unary_prologue<OP>();
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)
         out[i] = unary_fwd<OP>(x[i], p0, p1);
 }
@@ -327,6 +341,7 @@ template <int OP, bool ACC>
 __global__ void __launch_bounds__(kBlock) unary_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                             const float* __restrict__ o, float* __restrict__ gx,
                                                             int64_t n, float p0, float p1) {
+    unary_prologue<OP>();
     constexpr bool RX = unary_bwd_reads_x<OP>();
     constexpr bool RO = unary_bwd_reads_out<OP>();
     const int64_t n4 = n / 4;
@@ -359,6 +374,7 @@ template <int OP, bool ACC>
 __global__ void __launch_bounds__(kBlock) unary_bwd_scalar_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                                    const float* __restrict__ o, float* __restrict__ gx,
                                                                    int64_t n, float p0, float p1) {
+    unary_prologue<OP>();
     constexpr bool RX = unary_bwd_reads_x<OP>();
     constexpr bool RO = unary_bwd_reads_out<OP>();
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock)

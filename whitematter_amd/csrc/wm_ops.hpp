@@ -24,6 +24,19 @@ __device__ __forceinline__ float binary_fwd(float a, float b) {
     else return (b < a) ? b : a;                        // :1997
 }
 
+// Kernel prologues: a kernel templated on a binary (unary) op code calls
+// binary_prologue<OP>() (unary_prologue<OP>()) first, with all its threads;
+// for pow it loads the pow tables into LDS.
+template <int OP>
+__device__ __forceinline__ void binary_prologue() {
+    if constexpr (OP == WM_POW) pow_tables_to_lds();
+}
+
+template <int OP>
+__device__ __forceinline__ void unary_prologue() {
+    if constexpr (OP == WM_POWS) pow_tables_to_lds();
+}
+
 // ---- binary backward ------------------------------------------------------
 // Contribution to dL/da and dL/db from one output element.  `o` is the
 // forward output (only pow's d/db reads it).

@@ -44,32 +44,51 @@ struct LogEntry {
     double invc, logc;
 };
 
-WM_HD inline const LogEntry* log_table() {
-    static constexpr LogEntry t[16] = {
-        {1.3989067077636719, -0.48429975325710395}, {1.3403148651123047, -0.4225719566348825},
-        {1.2864322662353516, -0.3633754976944188},  {1.236715316772461, -0.3065134402105001},
-        {1.1906986236572266, -0.2518083005440589},  {1.1479816436767578, -0.19909957338273085},
-        {1.108224868774414, -0.14825064686535408},  {1.0711288452148438, -0.09913203113589106},
-        {1.03643798828125, -0.051633800310858485},  {0.9980506896972656, 0.002815004858138399},
-        {0.9481477737426758, 0.07681616674347436},  {0.8951053619384766, 0.15987058435448812},
-        {0.847681999206543, 0.23840494355449127},   {0.8050317764282227, 0.31288236409411413},
-        {0.7664670944213867, 0.38370423872947484},  {0.7314281463623047, 0.4512119502479954},
+struct alignas(16) PowTables {
+    LogEntry log[16];  // {1/c, log2(c)} for the 16 sub-intervals of z
+    double exp2[32];   // 2^(j/32), j = 0..31
+};
+
+WM_HD inline const PowTables& pow_table_data() {
+    static constexpr PowTables t = {
+        {
+            {1.3989067077636719, -0.48429975325710395}, {1.3403148651123047, -0.4225719566348825},
+            {1.2864322662353516, -0.3633754976944188},  {1.236715316772461, -0.3065134402105001},
+            {1.1906986236572266, -0.2518083005440589},  {1.1479816436767578, -0.19909957338273085},
+            {1.108224868774414, -0.14825064686535408},  {1.0711288452148438, -0.09913203113589106},
+            {1.03643798828125, -0.051633800310858485},  {0.9980506896972656, 0.002815004858138399},
+            {0.9481477737426758, 0.07681616674347436},  {0.8951053619384766, 0.15987058435448812},
+            {0.847681999206543, 0.23840494355449127},   {0.8050317764282227, 0.31288236409411413},
+            {0.7664670944213867, 0.38370423872947484},  {0.7314281463623047, 0.4512119502479954},
+        },
+        {
+            1.0,                1.0218971486541166, 1.0442737824274138, 1.0671404006768237, 1.0905077326652577,
+            1.1143867425958924, 1.1387886347566916, 1.1637248587775775, 1.189207115002721,  1.215247359980469,
+            1.241857812073484,  1.2690509571917332, 1.2968395546510096, 1.3252366431597413, 1.3542555469368927,
+            1.383909881963832,  1.4142135623730951, 1.4451808069770467, 1.4768261459394993, 1.5091644275934228,
+            1.5422108254079407, 1.5759808451078865, 1.6104903319492543, 1.645755478153965,  1.681792830507429,
+            1.718619298122478,  1.7562521603732995, 1.7947090750031072, 1.8340080864093424, 1.8741676341103,
+            1.9152065613971474, 1.9571441241754002,
+        },
     };
     return t;
 }
 
-// 2^(j/32), j = 0..31
-WM_HD inline const double* exp2_table() {
-    static constexpr double t[32] = {
-        1.0,                1.0218971486541166, 1.0442737824274138, 1.0671404006768237, 1.0905077326652577,
-        1.1143867425958924, 1.1387886347566916, 1.1637248587775775, 1.189207115002721,  1.215247359980469,
-        1.241857812073484,  1.2690509571917332, 1.2968395546510096, 1.3252366431597413, 1.3542555469368927,
-        1.383909881963832,  1.4142135623730951, 1.4451808069770467, 1.4768261459394993, 1.5091644275934228,
-        1.5422108254079407, 1.5759808451078865, 1.6104903319492543, 1.645755478153965,  1.681792830507429,
-        1.718619298122478,  1.7562521603732995, 1.7947090750031072, 1.8340080864093424, 1.8741676341103,
-        1.9152065613971474, 1.9571441241754002,
-    };
-    return t;
+#ifdef __HIP_DEVICE_COMPILE__
+// On the device the lookups read a copy of the tables in LDS, which every
+// kernel that evaluates pow fills first (pow_tables_to_lds).  Each table
+// entry sits in its own LDS banks, so a wave's lookups never conflict, and
+// they stay off the texture path, which per-lane gathers from global memory
+// had saturated.
+static __shared__ PowTables wm_pow_lds;
+#endif
+
+WM_HD inline const PowTables& pow_tables() {
+#ifdef __HIP_DEVICE_COMPILE__
+    return wm_pow_lds;
+#else
+    return pow_table_data();
+#endif
 }
 
 WM_HD inline uint32_t bits_of(float f) {
@@ -99,7 +118,7 @@ WM_HD inline double log2_normal(float ax) {
     const int i = (int)((tmp >> 19) & 15u);
     const int k = (int)((int32_t)tmp >> 23);
     const double z = (double)float_of(ix - (tmp & 0xff800000u));
-    const LogEntry e = log_table()[i];
+    const LogEntry e = pow_tables().log[i];
     const double r = std::fma(z, e.invc, -1.0);
     // log2(1 + r) = r * (C1 + C2 r + ... + C6 r^5), Cn = (-1)^(n+1) / (n ln 2)
     const double C1 = 1.4426950408889634, C2 = -0.7213475204444817, C3 = 0.48089834696298783,
@@ -129,7 +148,7 @@ WM_HD inline float exp2_to_float(double t) {
     double p = std::fma(E3, r, E2);
     p = std::fma(p, r, E1);
     p = std::fma(p, r, 1.0);
-    return (float)std::ldexp(exp2_table()[ki & 31] * p, ki >> 5);
+    return (float)std::ldexp(pow_tables().exp2[ki & 31] * p, ki >> 5);
 }
 
 // 2^t for values used only inside gradients: relative error ~2e-7 (the
@@ -152,8 +171,7 @@ WM_HD inline float exp2_grad(double t) {
 // and the table's log2(1) is only zero to ~1e-19, which a huge y would
 // amplify.
 WM_HD inline bool table_ok(float x, float y) {
-    const float ax = std::fabs(x), ay = std::fabs(y);
-    return ax >= 1.17549435e-38f && ax <= 3.40282347e+38f && ax != 1.0f && ay > 0.0f && ay <= 3.40282347e+38f;
+    return std::isnormal(x) && std::fabs(x) != 1.0f && std::isfinite(y) && y != 0.0f;
 }
 
 // C pow's sign rule for a finite non-zero base, given the magnitude
@@ -169,6 +187,21 @@ WM_HD inline float apply_sign(float x, float y, float mag) {
 }
 
 }  // namespace powdetail
+
+#ifdef __HIPCC__
+// Copies the pow tables into LDS.  Every kernel that evaluates pow_table,
+// pow_f32 or pow_grad_* calls this first, with all its threads (it contains
+// a barrier); blockDim.x >= 32.
+__device__ inline void pow_tables_to_lds() {
+#ifdef __HIP_DEVICE_COMPILE__
+    static_assert(sizeof(powdetail::PowTables) == 32 * 16, "pow tables are 32 x 16 bytes");
+    if (threadIdx.x < 32)
+        reinterpret_cast<uint4*>(&powdetail::wm_pow_lds)[threadIdx.x] =
+            reinterpret_cast<const uint4*>(&powdetail::pow_table_data())[threadIdx.x];
+    __syncthreads();
+#endif
+}
+#endif
 
 // The table path alone: equal to pow(x, y) within 1 ulp wherever
 // pow_needs_fix(x, y) is false.  Branch-free, so kernels evaluate it for a
