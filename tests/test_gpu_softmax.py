@@ -65,3 +65,33 @@ def test_softmax_all_neg_inf_row(wm):
     x[1] = 0.0
     got = softmax_fwd(x)
     assert np.isnan(got[0]).all() and np.allclose(got[1], 1 / 64)
+
+
+@pytest.mark.parametrize("log", [False, True])
+@pytest.mark.parametrize("cols", [64, 100, 4096, 32000])
+def test_softmax_special_rows(wm, log, cols):
+    """NaN / inf / -inf inputs and wide spreads, row by row (both tile sizes).
+
+    Reference semantics (core/tensor.cpp:1553-1575): any NaN or +inf in a row
+    makes the whole row NaN (NaN propagates through the sum; +inf - +inf is
+    NaN); -inf elements give exactly 0 (softmax) / -inf (log_softmax) while
+    the rest of the row is normal.  Spreads of 100 reach subnormal outputs,
+    which fp32 stores with absolute spacing 2^-149 (hence the atol)."""
+    rows = []
+    r = rng_normal((cols,), 31, 3.0); r[0] = np.nan; rows.append(r)               # NaN first
+    r = rng_normal((cols,), 32, 3.0); r[cols // 2] = np.nan; rows.append(r)       # NaN inside
+    r = rng_normal((cols,), 33, 3.0); r[-1] = np.inf; rows.append(r)              # +inf
+    r = rng_normal((cols,), 34, 3.0); r[::3] = -np.inf; rows.append(r)            # many -inf
+    r = np.full((cols,), -np.inf, np.float32); r[-1] = 1.5; rows.append(r)        # one finite, last
+    r = np.full((cols,), -np.inf, np.float32); r[0] = -3.0; rows.append(r)        # one finite, first
+    r = np.linspace(0.0, -110.0, cols).astype(np.float32); rows.append(r)        # subnormal tail
+    r = rng_normal((cols,), 35, 40.0); rows.append(r)                              # huge spread
+    r = np.full((cols,), 88.0, np.float32); rows.append(r)                         # large equal values
+    x = np.ascontiguousarray(np.stack(rows).astype(np.float32))
+    got = softmax_fwd(x, log)
+    ref = oracle.get("f64").softmax(x, log)
+    scale = oracle.get("abs").softmax(x, log)
+    ok, worst = oracle.close_scaled(got, ref, scale, 1e-5, atol=0.0 if log else 3e-45)
+    assert ok, f"{worst:.3g}x tolerance"
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isneginf(got), np.isneginf(ref))

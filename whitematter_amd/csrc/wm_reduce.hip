@@ -213,11 +213,16 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
 // inner > 1: columns
 // ---------------------------------------------------------------------------
 
-// Thread t of a workgroup owns W adjacent inner positions (W = 4 with
-// 128-bit loads) of output row o, so the workgroup reads 256*W contiguous
-// floats per position of n, and walks positions [k0, k1) of n in increasing
-// order with four loads in flight.  Items are (o, chunk, inner tile)
-// triples, tile fastest.
+// Lane l of each wave owns W adjacent inner positions (W = 4 with 128-bit
+// loads) of output row o, so a wave reads 64*W contiguous floats per position
+// of n.  The workgroup's 4 waves take four contiguous quarters of the chunk
+// [k0, k1) of n, each walking its quarter in increasing order with four loads
+// in flight; the four wave results are combined in wave order through LDS.
+// Splitting the chunk inside the workgroup (rather than over more
+// workgroups) keeps the number of partial results, and so the second pass,
+// four times smaller for the same parallelism.  Items are (o, chunk, inner
+// tile) triples, tile fastest; every thread of a workgroup walks the same
+// items, so the barriers are uniform.
 template <int OP, bool VEC>
 __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __restrict__ x, int64_t outer, int64_t n,
                                                               int64_t inner, int64_t chunk, int64_t K,
@@ -225,7 +230,11 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
                                                               float* __restrict__ pv, int64_t* __restrict__ pi) {
     constexpr int KIND = kind_of(OP);
     constexpr int W = VEC ? 4 : 1;
-    const int64_t tile_elems = (int64_t)kBlock * W;
+    constexpr int NW = kBlock / 64;
+    __shared__ float lv[NW][64 * W];
+    __shared__ int64_t li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t tile_elems = (int64_t)64 * W;
     const int64_t tiles = (inner + tile_elems - 1) / tile_elems;
     const int64_t items = outer * K * tiles;
     for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
@@ -233,64 +242,87 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
         const int64_t ok = item / tiles;
         const int64_t k = ok % K;
         const int64_t o = ok / K;
-        const int64_t i0 = t * tile_elems + (int64_t)threadIdx.x * W;
-        if (i0 >= inner) continue;
+        const int64_t i0 = t * tile_elems + (int64_t)lane * W;
         const int64_t k0 = k * chunk, k1 = min(n, k0 + chunk);
+        const int64_t q = (k1 - k0 + NW - 1) / NW;
+        const int64_t r0 = min(k1, k0 + w * q), r1 = min(k1, r0 + q);
         const float* xp = x + o * n * inner + i0;
         float v[W];
         int64_t pos[W];
 #pragma unroll
         for (int j = 0; j < W; ++j) { v[j] = 0.f; pos[j] = kEmpty; }
-        int64_t p = k0;
-        for (; p + 3 < k1; p += 4) {
-            float a[4][W];
+        if (i0 < inner) {
+            int64_t p = r0;
+            for (; p + 3 < r1; p += 4) {
+                float a[4][W];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if constexpr (VEC) {
-                    float4 q = ld_stream(xp + (p + u) * inner);
-                    a[u][0] = q.x; a[u][1] = q.y; a[u][2] = q.z; a[u][3] = q.w;
-                } else {
-                    a[u][0] = ld_stream1(xp + (p + u) * inner);
+                for (int u = 0; u < 4; ++u) {
+                    if constexpr (VEC) {
+                        float4 qv = ld_stream(xp + (p + u) * inner);
+                        a[u][0] = qv.x; a[u][1] = qv.y; a[u][2] = qv.z; a[u][3] = qv.w;
+                    } else {
+                        a[u][0] = ld_stream1(xp + (p + u) * inner);
+                    }
                 }
-            }
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int j = 0; j < W; ++j) {
+                        if constexpr (KIND == 0) v[j] += a[u][j];
+                        else scan_push<KIND == 1>(v[j], pos[j], a[u][j], p + u);
+                    }
+            }
+            for (; p < r1; ++p) {
+                float a[W];
+                if constexpr (VEC) {
+                    float4 qv = ld_stream(xp + p * inner);
+                    a[0] = qv.x; a[1] = qv.y; a[2] = qv.z; a[3] = qv.w;
+                } else {
+                    a[0] = ld_stream1(xp + p * inner);
+                }
 #pragma unroll
                 for (int j = 0; j < W; ++j) {
-                    if constexpr (KIND == 0) v[j] += a[u][j];
-                    else scan_push<KIND == 1>(v[j], pos[j], a[u][j], p + u);
+                    if constexpr (KIND == 0) v[j] += a[j];
+                    else scan_push<KIND == 1>(v[j], pos[j], a[j], p);
                 }
-        }
-        for (; p < k1; ++p) {
-            float a[W];
-            if constexpr (VEC) {
-                float4 q = ld_stream(xp + p * inner);
-                a[0] = q.x; a[1] = q.y; a[2] = q.z; a[3] = q.w;
-            } else {
-                a[0] = ld_stream1(xp + p * inner);
-            }
-#pragma unroll
-            for (int j = 0; j < W; ++j) {
-                if constexpr (KIND == 0) v[j] += a[j];
-                else scan_push<KIND == 1>(v[j], pos[j], a[j], p);
             }
         }
+        __syncthreads();  // the previous item's LDS reads are done
 #pragma unroll
         for (int j = 0; j < W; ++j) {
-            const int64_t i = i0 + j;
-            if (i >= inner) break;
-            if (K == 1) write_result<OP>(val, idx, o * inner + i, v[j], pos[j], n);
-            else {
-                pv[(o * K + k) * inner + i] = v[j];
-                if (KIND != 0) pi[(o * K + k) * inner + i] = pos[j];
+            lv[w][lane * W + j] = v[j];
+            if constexpr (KIND != 0) li[w][lane * W + j] = pos[j];
+        }
+        __syncthreads();
+        if (w == 0) {
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                const int64_t i = i0 + j;
+                if (i >= inner) break;
+                float tv = lv[0][lane * W + j];
+                int64_t ti = kEmpty;
+                if constexpr (KIND == 0) {
+                    tv = (tv + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
+                } else {
+                    ti = li[0][lane * W + j];
+#pragma unroll
+                    for (int ww = 1; ww < NW; ++ww) combine<KIND == 1>(tv, ti, lv[ww][lane * W + j], li[ww][lane * W + j]);
+                }
+                if (K == 1) write_result<OP>(val, idx, o * inner + i, tv, ti, n);
+                else {
+                    pv[(o * K + k) * inner + i] = tv;
+                    if (KIND != 0) pi[(o * K + k) * inner + i] = ti;
+                }
             }
         }
     }
 }
 
-// Second pass for split columns.  A workgroup owns 64 adjacent output slots;
-// its 4 waves take chunks k = w, w+4, ... and the wave results are combined
-// in wave order through LDS.
+// Second pass for split columns.  A workgroup owns 16 adjacent output slots
+// and its 256 threads form 16 groups of 16 lanes: group g combines chunks
+// k = g, g + 16, g + 32, ... of its lane's slot in increasing k, and the 16
+// group results are combined in group order through LDS.  Small slot tiles
+// spread the pass over many workgroups; it is latency-bound otherwise.
 template <int OP>
 __global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const float* __restrict__ pv,
                                                                        const int64_t* __restrict__ pi, int64_t outer,
@@ -298,53 +330,55 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const floa
                                                                        float* __restrict__ val,
                                                                        int64_t* __restrict__ idx) {
     constexpr int KIND = kind_of(OP);
-    __shared__ float lv[4][64];
-    __shared__ int64_t li[4][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    constexpr int S = 16;          // slots per workgroup
+    constexpr int G = kBlock / S;  // groups
+    __shared__ float lv[G][S];
+    __shared__ int64_t li[KIND != 0 ? G : 1][S];
+    const int c = threadIdx.x & (S - 1), g = threadIdx.x / S;
     const int64_t total = outer * inner;
-    for (int64_t s0 = (int64_t)blockIdx.x * 64; s0 < total; s0 += (int64_t)gridDim.x * 64) {
-        const int64_t s = s0 + lane;
+    for (int64_t s0 = (int64_t)blockIdx.x * S; s0 < total; s0 += (int64_t)gridDim.x * S) {
+        const int64_t s = s0 + c;
         float rv = 0.f;
         int64_t ri = kEmpty;
         if (s < total) {
             const int64_t o = s / inner, i = s - o * inner;
             const float* pvs = pv + o * K * inner + i;
             if constexpr (KIND == 0) {
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
-                int64_t k = w;
-                for (; k + 12 < K; k += 16) {
+                int64_t k = g;
+                for (; k + 3 * G < K; k += 4 * G) {
+                    float b[4];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[j] += pvs[(k + 4 * j) * inner];
+                    for (int u = 0; u < 4; ++u) b[u] = pvs[(k + u * G) * inner];
+                    rv = ((rv + b[0]) + b[1]) + (b[2] + b[3]);
                 }
-                for (int j = 0; k < K; k += 4, ++j) acc[j & 3] += pvs[k * inner];
-                rv = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+                for (; k < K; k += G) rv += pvs[k * inner];
             } else {
                 const int64_t* pis = pi + o * K * inner + i;
-                int64_t k = w;
-                for (; k + 28 < K; k += 32) {
-                    float bv[8];
-                    int64_t bi[8];
+                int64_t k = g;
+                for (; k + 3 * G < K; k += 4 * G) {
+                    float bv[4];
+                    int64_t bi[4];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) { bv[j] = pvs[(k + 4 * j) * inner]; bi[j] = pis[(k + 4 * j) * inner]; }
+                    for (int u = 0; u < 4; ++u) { bv[u] = pvs[(k + u * G) * inner]; bi[u] = pis[(k + u * G) * inner]; }
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) combine<KIND == 1>(rv, ri, bv[j], bi[j]);
+                    for (int u = 0; u < 4; ++u) combine<KIND == 1>(rv, ri, bv[u], bi[u]);
                 }
-                for (; k < K; k += 4) combine<KIND == 1>(rv, ri, pvs[k * inner], pis[k * inner]);
+                for (; k < K; k += G) combine<KIND == 1>(rv, ri, pvs[k * inner], pis[k * inner]);
             }
         }
-        lv[w][lane] = rv;
-        li[w][lane] = ri;
+        lv[g][c] = rv;
+        if constexpr (KIND != 0) li[g][c] = ri;
         __syncthreads();
-        if (w == 0 && s < total) {
-            float tv;
+        if (g == 0 && s < total) {
+            float tv = lv[0][c];
             int64_t ti = kEmpty;
             if constexpr (KIND == 0) {
-                tv = (lv[0][lane] + lv[1][lane]) + (lv[2][lane] + lv[3][lane]);
+#pragma unroll
+                for (int gg = 1; gg < G; ++gg) tv += lv[gg][c];
             } else {
-                tv = lv[0][lane]; ti = li[0][lane];
-                combine<KIND == 1>(tv, ti, lv[1][lane], li[1][lane]);
-                combine<KIND == 1>(tv, ti, lv[2][lane], li[2][lane]);
-                combine<KIND == 1>(tv, ti, lv[3][lane], li[3][lane]);
+                ti = li[0][c];
+#pragma unroll
+                for (int gg = 1; gg < G; ++gg) combine<KIND == 1>(tv, ti, lv[gg][c], li[gg][c]);
             }
             write_result<OP>(val, idx, s, tv, ti, n);
         }
@@ -447,13 +481,13 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
         return WM_OK;
     }
     const bool vec = (inner % 4 == 0) && aligned16(x);
-    const int64_t tile = (int64_t)kBlock * (vec ? 4 : 1);
+    const int64_t tile = (int64_t)64 * (vec ? 4 : 1);
     const int64_t tiles = (inner + tile - 1) / tile;
-    // ~4 workgroups per CU, each thread walking at least 32 positions of n.
+    // ~4 workgroups per CU, each wave walking at least 32 positions of n.
     const int64_t target_blocks = (int64_t)num_cus() * 4;
     int64_t K = 1;
     if (outer * tiles < target_blocks)
-        K = std::min<int64_t>((target_blocks + outer * tiles - 1) / (outer * tiles), (n + 31) / 32);
+        K = std::min<int64_t>((target_blocks + outer * tiles - 1) / (outer * tiles), (n + 127) / 128);
     K = std::max<int64_t>(std::min<int64_t>(K, 4096), 1);
     const int64_t chunk = (n + K - 1) / K;
     K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
@@ -469,7 +503,7 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
                            val, idx, wv.as<float>(), wi.as<int64_t>());
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
-        hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 64, 8)), dim3(kBlock), 0,
+        hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0,
                            st, wv.as<float>(), wi.as<int64_t>(), outer, K, inner, n, val, idx);
         WM_TRY(check_launch("wm_reduce(cols finalize)"));
     }

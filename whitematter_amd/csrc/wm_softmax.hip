@@ -80,33 +80,72 @@ struct RowTile {
     }
 };
 
+// One-barrier block reductions for the forward kernel, which gives the max
+// and the sum separate LDS arrays: a thread can only write a row's partial to
+// one array after every thread has passed the barrier of the other array's
+// reduction for that row, i.e. after all reads of the previous row's values.
+template <int NT>
+__device__ __forceinline__ float block_max_1(float v, float* lds) {
+    constexpr int NW = NT / 64;
+    v = wave_max(v);
+    if (NW == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = lds[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) m = fmaxf(m, lds[i]);
+    return m;
+}
+
+template <int NT>
+__device__ __forceinline__ float block_sum_1(float v, float* lds) {
+    constexpr int NW = NT / 64;
+    v = wave_sum(v);
+    if (NW == 1) return v;
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) t += lds[i];
+    return t;
+}
+
 // LOG = false: softmax, true: log_softmax.
+// Each thread first takes the max m_t of its own slots and the sum
+// s_t = sum exp(x - m_t) (keeping exp(x - m_t) for softmax), so the
+// exponentials are computed while the rest of the workgroup's loads are
+// still arriving; the row max M and the sum S = sum_t s_t exp(m_t - M) then
+// take one barrier each.  softmax writes exp(x - m_t) * exp(m_t - M) / S and
+// log_softmax x - (M + log S): the reference's x - max, exp, sum and scale
+// (core/tensor.cpp:1548-1591, :1593-1635) regrouped, within a few ulp.
+// Padding slots hold -inf and contribute exp(-inf) = 0.  A thread whose slots
+// are all -inf uses 0 in place of m_t and contributes nothing.  NaN and
+// infinite inputs turn the whole row to NaN, as in the reference.
 template <int NT, int ITEMS, bool VEC, bool LOG>
 __global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
                                                           int64_t rows, int64_t cols) {
-    __shared__ float lds[NT / 64];
+    __shared__ float lds_m[NT / 64], lds_s[NT / 64];
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         RowTile<NT, ITEMS, VEC> tile;
         tile.load(x + r * cols, cols, -INFINITY);
-        float m = -INFINITY;
+        float mt = -INFINITY;
 #pragma unroll
         for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) m = fmaxf(m, tile.v[t][e]);
-        m = block_max<NT>(m, lds);
-        float s = 0.f;
+            for (int e = 0; e < 4; ++e) mt = fmaxf(mt, tile.v[t][e]);
+        const float base = mt == -INFINITY ? 0.f : mt;
+        float st = 0.f;
 #pragma unroll
         for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                // Padding slots hold -inf: exp(-inf - m) = 0 (NaN if m is -inf,
-                // which only happens when the whole row is -inf; then every
-                // real element is NaN too, as in the reference).
-                float ex = (tile.col(t, e) < cols) ? expf(tile.v[t][e] - m) : 0.f;
-                s += ex;
+                const float ex = exp_rr(tile.v[t][e] - base);
+                st += ex;
                 if (!LOG) tile.v[t][e] = ex;
             }
-        s = block_sum<NT>(s, lds);
+        const float m = block_max_1<NT>(mt, lds_m);
+        const float ct = mt == -INFINITY ? 0.f : exp_rr(mt - m);
+        const float s = block_sum_1<NT>(st * ct, lds_s);
         if (LOG) {
             const float log_sum = m + logf(s);
 #pragma unroll
@@ -114,11 +153,11 @@ __global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out
 #pragma unroll
                 for (int e = 0; e < 4; ++e) tile.v[t][e] = tile.v[t][e] - log_sum;
         } else {
-            const float inv = 1.0f / s;
+            const float k = ct * (1.0f / s);
 #pragma unroll
             for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) tile.v[t][e] *= inv;
+                for (int e = 0; e < 4; ++e) tile.v[t][e] *= k;
         }
         tile.store(out + r * cols, cols);
     }
@@ -162,7 +201,7 @@ __global__ void __launch_bounds__(NT) softmax_bwd_kernel(const float* __restrict
         for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if (LOG) tg.v[t][e] = tg.v[t][e] - expf(ty.v[t][e]) * s;
+                if (LOG) tg.v[t][e] = tg.v[t][e] - exp_rr(ty.v[t][e]) * s;
                 else tg.v[t][e] = softmax_dx(tg.v[t][e], ty.v[t][e], sd, s);
             }
         if (acc) {
@@ -189,14 +228,14 @@ __global__ void __launch_bounds__(1024) softmax_fwd_long_kernel(float* __restric
         for (int64_t c = threadIdx.x; c < cols; c += 1024) m = fmaxf(m, xr[c]);
         m = block_max<1024>(m, lds);
         float s = 0.f;
-        for (int64_t c = threadIdx.x; c < cols; c += 1024) s += expf(xr[c] - m);
+        for (int64_t c = threadIdx.x; c < cols; c += 1024) s += exp_rr(xr[c] - m);
         s = block_sum<1024>(s, lds);
         if (LOG) {
             const float log_sum = m + logf(s);
             for (int64_t c = threadIdx.x; c < cols; c += 1024) orow[c] = xr[c] - log_sum;
         } else {
             const float inv = 1.0f / s;
-            for (int64_t c = threadIdx.x; c < cols; c += 1024) orow[c] = expf(xr[c] - m) * inv;
+            for (int64_t c = threadIdx.x; c < cols; c += 1024) orow[c] = exp_rr(xr[c] - m) * inv;
         }
         __syncthreads();
     }
@@ -220,7 +259,7 @@ __global__ void __launch_bounds__(1024) softmax_bwd_long_kernel(const float* __r
         s = block_sum<1024>(s, lds);
         if (!LOG) sd = block_sum<1024>(sd, lds);
         for (int64_t c = threadIdx.x; c < cols; c += 1024) {
-            float d = LOG ? gr[c] - expf(yr[c]) * s : softmax_dx(gr[c], yr[c], sd, s);
+            float d = LOG ? gr[c] - exp_rr(yr[c]) * s : softmax_dx(gr[c], yr[c], sd, s);
             dr[c] = acc ? dr[c] + d : d;
         }
         __syncthreads();
