@@ -1,0 +1,92 @@
+/*
+ * wm_optim.h -- C ABI of libwm_hip's parameter-update kernels: the optimizer
+ * steps, gradient clipping and gradient unscaling of whitematter's training
+ * loop (reference core/optimizer.cpp, core/amp.h), next to the Tensor path of
+ * wm_hip.h.
+ *
+ * The reference updates parameters with host loops over each parameter's
+ * std::vector<float> data and grad and keeps the optimizer state (velocity,
+ * first/second moments) in host vectors.  Here parameters, gradients and
+ * state stay in HBM and each update is one streaming pass.  The drop-in C++
+ * optimizer classes (whitematter_amd/core/optimizer.{h,cpp}) call these
+ * entry points from step(), clip_grad_norm_() and friends.
+ *
+ * Conventions are those of wm_hip.h (status codes, wm_last_error(), device
+ * pointers, one library stream).  Every update computes exactly the float
+ * expression of the reference loop it names, in the same operation order,
+ * with IEEE division and square root and no contraction into fused
+ * multiply-adds, so results equal a strict IEEE evaluation of the reference
+ * source bit for bit.  Updates are in place (p, state and g may not alias
+ * each other).
+ */
+#ifndef WM_OPTIM_H
+#define WM_OPTIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* SGD::step, core/optimizer.cpp:22-36.  velocity may be NULL when
+ * momentum == 0 (the reference keeps no velocity then):
+ *   momentum > 0:  v = momentum * v + g;  p -= lr * v
+ *   otherwise:     p -= lr * g                                            */
+int wm_sgd_step(float* p, const float* g, float* velocity, int64_t n, float lr, float momentum);
+
+/* Adam::step, core/optimizer.cpp:46-66, one parameter tensor; the caller
+ * increments t and passes bias_correction{1,2} = 1 - beta{1,2}^t computed
+ * as the reference does (float(1.0 - pow(double(beta), t))):
+ *   m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g g
+ *   p -= lr * (m / bc1) / (sqrt(v / bc2) + eps)                            */
+int wm_adam_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                 float eps, float bias_correction1, float bias_correction2);
+
+/* AdamW::step, core/optimizer.cpp:76-100 (decoupled weight decay):
+ *   p -= lr * ((m / bc1) / (sqrt(v / bc2) + eps) + weight_decay * p)       */
+int wm_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                  float eps, float bias_correction1, float bias_correction2, float weight_decay);
+
+/* RMSprop::step, core/optimizer.cpp:112-138.  buffer may be NULL when
+ * momentum == 0.  g is not modified (the weight-decayed gradient is local):
+ *   g' = g + weight_decay * p   (only when weight_decay != 0)
+ *   v = alpha v + (1 - alpha) g' g';  avg = sqrt(v) + eps
+ *   momentum > 0:  buf = momentum * buf + g' / avg;  p -= lr * buf
+ *   otherwise:     p -= lr * g' / avg                                      */
+int wm_rmsprop_step(float* p, const float* g, float* v, float* buffer, int64_t n, float lr, float alpha, float eps,
+                    float momentum, float weight_decay);
+
+/* get_grad_norm's accumulation, core/optimizer.cpp:145-153: *total (one
+ * device float) += sum of g[i]^2 over this tensor.  The tensor's sum is a
+ * fixed-order tree and is added to *total on the device in call order, so a
+ * sequence of calls is deterministic; the reference's sequential float sum is
+ * matched to the sum tolerance, not bit for bit. */
+int wm_grad_sumsq_accumulate(const float* g, int64_t n, float* total);
+
+/* clip_grad_norm_'s scaling, core/optimizer.cpp:155-164, with the norm read
+ * on the device (no host round trip):
+ *   clip_coef = max_norm / (sqrt(*total_sumsq) + 1e-6f);
+ *   if (clip_coef < 1) g[i] *= clip_coef                                   */
+int wm_clip_grad_norm_scale(float* g, int64_t n, const float* total_sumsq, float max_norm);
+
+/* clip_grad_value_, core/optimizer.cpp:166-177:
+ *   g > c -> c;  g < -c -> -c;  otherwise (NaN included) unchanged         */
+int wm_clip_grad_value(float* g, int64_t n, float clip_value);
+
+/* GradScaler::unscale, core/amp.h:125-147, over a list of gradient tensors
+ * (host arrays of `count` device pointers and sizes, in the optimizer's
+ * parameter order; NULL or size-0 entries are skipped like an empty grad).
+ * Walks the tensors in order multiplying each element by inv_scale and stops
+ * at the first element whose product is not finite: tensors before it are
+ * fully unscaled, its own tensor up to (not including) that element, the
+ * rest untouched -- the reference's early break.  *found_inf (host) is set to
+ * 1 if such an element exists, else 0.  Synchronises with the library stream
+ * (the stopping position decides what is written). */
+int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float inv_scale, int* found_inf);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WM_OPTIM_H */

@@ -18,6 +18,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 KINDS = {"f32": ("liboracle_f32.so", np.float32), "f64": ("liboracle_f64.so", np.float64),
          "abs": ("liboracle_abs.so", np.float64), "port": ("liboracle_port.so", np.float32)}
 REF_PATH = os.path.join(HERE, "_ref", "libwmref.so")
+# the same reference sources built without fast-math (IEEE, no contraction)
+REF_IEEE_PATH = os.path.join(HERE, "_ref", "libwmref_ieee.so")
 
 BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3, "pow": 4, "max": 5, "min": 6}
 UNARY = {"relu": 0, "sigmoid": 1, "tanh": 2, "log": 3, "exp": 4, "pows": 5, "sqrt": 6,
@@ -144,6 +146,61 @@ class Oracle:
         self.L.or_f16_to_f32(_fp(out), _fp(h), C.c_int64(h.size))
         return out
 
+    # ---- parameter updates (float in every build); arrays are updated in
+    # place, as the reference's step() does ----------------------------------
+
+    def _optim_sigs(self):
+        if getattr(self, "_optim_ready", False):
+            return
+        L = self.L
+        L.or_bias_correction.argtypes = [C.c_float, C.c_int]
+        L.or_bias_correction.restype = C.c_float
+        L.or_sgd_step.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_float, C.c_float]
+        L.or_adam_step.argtypes = [C.c_void_p] * 4 + [C.c_int64] + [C.c_float] * 7 + [C.c_int]
+        L.or_rmsprop_step.argtypes = [C.c_void_p] * 4 + [C.c_int64] + [C.c_float] * 5
+        L.or_grad_sumsq.argtypes = [C.c_void_p, C.c_int64]
+        L.or_grad_sumsq.restype = C.c_double
+        L.or_clip_grad_value.argtypes = [C.c_void_p, C.c_int64, C.c_float]
+        L.or_unscale_tensor.argtypes = [C.c_void_p, C.c_int64, C.c_float]
+        L.or_unscale_tensor.restype = C.c_int64
+        self._optim_ready = True
+
+    @staticmethod
+    def _f32(a):
+        assert a is None or (a.dtype == np.float32 and a.flags.c_contiguous), "float32 C-contiguous arrays"
+        return a
+
+    def bias_correction(self, beta, t):
+        self._optim_sigs()
+        return np.float32(self.L.or_bias_correction(beta, t))
+
+    def sgd_step(self, p, g, vel, lr, momentum):
+        self._optim_sigs()
+        self.L.or_sgd_step(_fp(self._f32(p)), _fp(self._f32(g)), _fp(self._f32(vel)), p.size, lr, momentum)
+
+    def adam_step(self, p, g, m, v, lr, beta1, beta2, eps, bc1, bc2, weight_decay=0.0, decoupled=False):
+        self._optim_sigs()
+        self.L.or_adam_step(_fp(self._f32(p)), _fp(self._f32(g)), _fp(self._f32(m)), _fp(self._f32(v)), p.size, lr,
+                            beta1, beta2, eps, bc1, bc2, weight_decay, int(decoupled))
+
+    def rmsprop_step(self, p, g, v, buf, lr, alpha, eps, momentum, weight_decay):
+        self._optim_sigs()
+        self.L.or_rmsprop_step(_fp(self._f32(p)), _fp(self._f32(g)), _fp(self._f32(v)), _fp(self._f32(buf)), p.size,
+                               lr, alpha, eps, momentum, weight_decay)
+
+    def grad_sumsq(self, g):
+        self._optim_sigs()
+        g = np.ascontiguousarray(g, np.float32)
+        return self.L.or_grad_sumsq(_fp(g), g.size)
+
+    def clip_grad_value(self, g, c):
+        self._optim_sigs()
+        self.L.or_clip_grad_value(_fp(self._f32(g)), g.size, c)
+
+    def unscale_tensor(self, g, inv_scale):
+        self._optim_sigs()
+        return self.L.or_unscale_tensor(_fp(self._f32(g)), g.size, inv_scale)
+
 
 def get(kind: str) -> Oracle:
     if kind not in _libs:
@@ -198,6 +255,22 @@ class RefTensor:
             pass
 
 
+class RefOptimizer:
+    """A reference optimizer (core/optimizer.h) over RefTensor parameters."""
+
+    def __init__(self, L, h, params):
+        self.L, self.h, self.params = L, h, params
+
+    def step(self):
+        self.L.wmref_optim_step(self.h)
+
+    def __del__(self):
+        try:
+            self.L.wmref_optim_free(self.h)
+        except Exception:
+            pass
+
+
 class Reference:
     def __init__(self, path: str = REF_PATH):
         if not os.path.exists(path):
@@ -236,7 +309,49 @@ class Reference:
         L.wmref_f32_to_f16.restype = None
         L.wmref_f16_to_f32.argtypes = [C.c_void_p, C.c_void_p, C.c_int64]
         L.wmref_f16_to_f32.restype = None
+        L.wmref_optim_new.argtypes = [C.c_int, C.c_void_p, C.c_int] + [C.c_float] * 5
+        L.wmref_optim_new.restype = C.c_void_p
+        for fn in ("wmref_optim_step", "wmref_optim_free"):
+            getattr(L, fn).argtypes = [C.c_void_p]
+            getattr(L, fn).restype = None
+        L.wmref_grad_norm.argtypes = [C.c_void_p, C.c_int]
+        L.wmref_grad_norm.restype = C.c_float
+        L.wmref_clip_grad_norm.argtypes = [C.c_void_p, C.c_int, C.c_float]
+        L.wmref_clip_grad_norm.restype = None
+        L.wmref_clip_grad_value.argtypes = [C.c_void_p, C.c_int, C.c_float]
+        L.wmref_clip_grad_value.restype = None
+        L.wmref_unscale.argtypes = [C.c_void_p, C.c_int, C.c_float]
+        L.wmref_unscale.restype = C.c_int
         self.L = L
+
+    @staticmethod
+    def _handles(params):
+        return (C.c_void_p * max(1, len(params)))(*[p.h for p in params]), len(params)
+
+    def optimizer(self, kind, params, lr, a=0.0, b=0.0, c=0.0, d=0.0):
+        """kind: "sgd" (a = momentum), "adam" (a, b, c = beta1, beta2, eps),
+        "adamw" (+ d = weight_decay), "rmsprop" (a = alpha, b = eps,
+        c = momentum, d = weight_decay).  Returns a RefOptimizer."""
+        code = {"sgd": 0, "adam": 1, "adamw": 2, "rmsprop": 3}[kind]
+        hs, n = self._handles(params)
+        return RefOptimizer(self.L, self.L.wmref_optim_new(code, hs, n, lr, a, b, c, d), params)
+
+    def grad_norm(self, params):
+        hs, n = self._handles(params)
+        return np.float32(self.L.wmref_grad_norm(hs, n))
+
+    def clip_grad_norm(self, params, max_norm):
+        hs, n = self._handles(params)
+        self.L.wmref_clip_grad_norm(hs, n, max_norm)
+
+    def clip_grad_value(self, params, c):
+        hs, n = self._handles(params)
+        self.L.wmref_clip_grad_value(hs, n, c)
+
+    def unscale(self, params, scale):
+        """GradScaler(scale).unscale(...); returns True when it found inf/NaN."""
+        hs, n = self._handles(params)
+        return bool(self.L.wmref_unscale(hs, n, scale))
 
     def tensor(self, data, requires_grad=False, shape: Optional[Sequence[int]] = None) -> RefTensor:
         data = np.ascontiguousarray(data, np.float32)

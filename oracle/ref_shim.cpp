@@ -16,6 +16,7 @@
 
 #include "tensor.h"
 #include "amp.h"
+#include "optimizer.h"
 
 namespace {
 
@@ -25,9 +26,14 @@ namespace {
 // of every thread that loads it, the oracle's included); instead each entry
 // point that runs reference arithmetic switches FTZ/DAZ on for its own
 // duration and restores the caller's mode on return.
+// The IEEE build (WMREF_IEEE, no fast-math) runs with both modes off.
 struct RefFpMode {
     unsigned saved;
+#ifdef WMREF_IEEE
+    RefFpMode() : saved(_mm_getcsr()) { _mm_setcsr(saved & ~0x8040u); }
+#else
     RefFpMode() : saved(_mm_getcsr()) { _mm_setcsr(saved | 0x8040u); }
+#endif
     ~RefFpMode() { _mm_setcsr(saved); }
 };
 
@@ -153,10 +159,16 @@ int wmref_set_grad(void* h, const float* g) {
     return y->grad_fn ? 1 : 0;
 }
 
-void wmref_call_grad_fn(void* h) { T(h)->grad_fn(); }
+void wmref_call_grad_fn(void* h) {
+    RefFpMode fp_mode_;
+    T(h)->grad_fn();
+}
 
 // Full reverse pass from a scalar root (core/tensor.cpp:763-781).
-void wmref_backward(void* h) { T(h)->backward(); }
+void wmref_backward(void* h) {
+    RefFpMode fp_mode_;
+    T(h)->backward();
+}
 
 void wmref_zero_grad(void* h) { T(h)->zero_grad(); }
 
@@ -171,6 +183,62 @@ void wmref_f32_to_f16(const float* x, uint16_t* out, int64_t n) {
 void wmref_f16_to_f32(const uint16_t* x, float* out, int64_t n) {
     RefFpMode fp_mode_;
     for (int64_t i = 0; i < n; ++i) out[i] = half_to_float(x[i]);
+}
+
+// ---- parameter updates (core/optimizer.cpp, core/amp.h:125-147) -----------
+
+static std::vector<TensorPtr> param_list(void** params, int np) {
+    std::vector<TensorPtr> ps;
+    for (int i = 0; i < np; ++i) ps.push_back(T(params[i]));
+    return ps;
+}
+
+// kind 0: SGD(lr, momentum = a); 1: Adam(lr, beta1 = a, beta2 = b, eps = c);
+// 2: AdamW(lr, a, b, c, weight_decay = d); 3: RMSprop(lr, alpha = a, eps = b,
+// momentum = c, weight_decay = d).
+void* wmref_optim_new(int kind, void** params, int np, float lr, float a, float b, float c, float d) {
+    RefFpMode fp_mode_;
+    std::vector<TensorPtr> ps = param_list(params, np);
+    switch (kind) {
+        case 0: return new SGD(ps, lr, a);
+        case 1: return new Adam(ps, lr, a, b, c);
+        case 2: return new AdamW(ps, lr, a, b, c, d);
+        case 3: return new RMSprop(ps, lr, a, b, c, d);
+        default: return nullptr;
+    }
+}
+
+void wmref_optim_step(void* o) {
+    RefFpMode fp_mode_;
+    static_cast<Optimizer*>(o)->step();
+}
+
+void wmref_optim_free(void* o) { delete static_cast<Optimizer*>(o); }
+
+float wmref_grad_norm(void** params, int np) {
+    RefFpMode fp_mode_;
+    return get_grad_norm(param_list(params, np));
+}
+
+void wmref_clip_grad_norm(void** params, int np, float max_norm) {
+    RefFpMode fp_mode_;
+    std::vector<TensorPtr> ps = param_list(params, np);
+    clip_grad_norm_(ps, max_norm);
+}
+
+void wmref_clip_grad_value(void** params, int np, float c) {
+    RefFpMode fp_mode_;
+    std::vector<TensorPtr> ps = param_list(params, np);
+    clip_grad_value_(ps, c);
+}
+
+// GradScaler(scale).unscale over the params (through an SGD holding them);
+// returns 1 when a non-finite gradient stopped it.
+int wmref_unscale(void** params, int np, float scale) {
+    RefFpMode fp_mode_;
+    SGD opt(param_list(params, np), 0.1f);
+    GradScaler scaler(scale);
+    return scaler.unscale(&opt) ? 0 : 1;
 }
 
 }  // extern "C"

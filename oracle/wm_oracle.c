@@ -461,3 +461,99 @@ int or_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
     for (int64_t i = 0; i < n; i++) out[i] = h2f(x[i]);
     return 0;
 }
+
+/* ---- parameter updates: core/optimizer.cpp, core/amp.h ---------------------
+ * The steps are float arithmetic in every build (the reference's types); the
+ * strict builds evaluate the reference's expressions in source order with
+ * IEEE operations and no contraction, which is the bit-exact target of the
+ * device kernels.  The sum of squares accumulates in REAL. */
+
+/* Adam/AdamW's `1.0f - std::pow(beta, t)`: std::pow(float, int) is the
+ * double pow, the subtraction is double and the assignment rounds to float
+ * (core/optimizer.cpp:48-49, :78-79). */
+float or_bias_correction(float beta, int t) {
+    OR_FP_SCOPE;
+    return (float)(1.0 - pow((double)beta, (double)t));
+}
+
+/* SGD::step, core/optimizer.cpp:22-36 */
+int or_sgd_step(float* p, const float* g, float* vel, int64_t n, float lr, float momentum) {
+    OR_FP_SCOPE;
+    for (int64_t j = 0; j < n; j++) {
+        if (momentum > 0.0f) {
+            vel[j] = momentum * vel[j] + g[j];
+            p[j] -= lr * vel[j];
+        } else {
+            p[j] -= lr * g[j];
+        }
+    }
+    return 0;
+}
+
+/* Adam::step :46-66 (decoupled = 0) and AdamW::step :76-100 (decoupled = 1),
+ * for one parameter tensor with the bias corrections of the current t. */
+int or_adam_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                 float eps, float bc1, float bc2, float weight_decay, int decoupled) {
+    OR_FP_SCOPE;
+    for (int64_t j = 0; j < n; j++) {
+        float gj = g[j];
+        m[j] = beta1 * m[j] + (1.0f - beta1) * gj;
+        v[j] = beta2 * v[j] + (1.0f - beta2) * gj * gj;
+        float m_hat = m[j] / bc1;
+        float v_hat = v[j] / bc2;
+        if (decoupled) p[j] -= lr * (m_hat / (sqrtf(v_hat) + eps) + weight_decay * p[j]);
+        else p[j] -= lr * m_hat / (sqrtf(v_hat) + eps);
+    }
+    return 0;
+}
+
+/* RMSprop::step, core/optimizer.cpp:112-138 */
+int or_rmsprop_step(float* p, const float* g, float* v, float* buf, int64_t n, float lr, float alpha, float eps,
+                    float momentum, float weight_decay) {
+    OR_FP_SCOPE;
+    for (int64_t j = 0; j < n; j++) {
+        float gj = g[j];
+        if (weight_decay != 0.0f) gj += weight_decay * p[j];
+        v[j] = alpha * v[j] + (1.0f - alpha) * gj * gj;
+        float avg = sqrtf(v[j]) + eps;
+        if (momentum > 0.0f) {
+            buf[j] = momentum * buf[j] + gj / avg;
+            p[j] -= lr * buf[j];
+        } else {
+            p[j] -= lr * gj / avg;
+        }
+    }
+    return 0;
+}
+
+/* get_grad_norm's accumulation for one tensor, core/optimizer.cpp:145-153,
+ * in REAL (the fp64 build is the sum contract's reference). */
+double or_grad_sumsq(const float* g, int64_t n) {
+    OR_FP_SCOPE;
+    REAL t = 0;
+    for (int64_t i = 0; i < n; i++) t += (REAL)g[i] * (REAL)g[i];
+    return (double)t;
+}
+
+/* clip_grad_value_, core/optimizer.cpp:166-177 */
+int or_clip_grad_value(float* g, int64_t n, float c) {
+    OR_FP_SCOPE;
+    for (int64_t i = 0; i < n; i++) {
+        if (g[i] > c) g[i] = c;
+        else if (g[i] < -c) g[i] = -c;
+    }
+    return 0;
+}
+
+/* GradScaler::unscale's inner loop for one tensor, core/amp.h:134-142:
+ * scales g in place up to the first element whose product is not finite
+ * and returns that position (n when there is none). */
+int64_t or_unscale_tensor(float* g, int64_t n, float inv_scale) {
+    OR_FP_SCOPE;
+    for (int64_t i = 0; i < n; i++) {
+        float v = g[i] * inv_scale;
+        if (!isfinite(v)) return i;
+        g[i] = v;
+    }
+    return n;
+}

@@ -1,4 +1,5 @@
-"""ctypes binding of libwm_hip.so (the C ABI declared in include/wm_hip.h).
+"""ctypes binding of libwm_hip.so (the C ABI declared in include/wm_hip.h and
+include/wm_optim.h).
 
 The library is the product: every call here launches hand-written HIP
 kernels on the GPU.  There is deliberately no CPU fallback -- if the shared
@@ -67,6 +68,15 @@ _SIGS = {
     "wm_epilogue_f16_fwd": [_vp, _vp, _vp, _vp, _vp, C.c_int64, C.c_int64, C.c_float, C.c_float],
     "wm_epilogue_f16_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int,
                             C.c_int64, C.c_int64, C.c_float, C.c_float],
+    # include/wm_optim.h
+    "wm_sgd_step": [_vp, _vp, _vp, C.c_int64, C.c_float, C.c_float],
+    "wm_adam_step": [_vp, _vp, _vp, _vp, C.c_int64] + [C.c_float] * 6,
+    "wm_adamw_step": [_vp, _vp, _vp, _vp, C.c_int64] + [C.c_float] * 7,
+    "wm_rmsprop_step": [_vp, _vp, _vp, _vp, C.c_int64] + [C.c_float] * 5,
+    "wm_grad_sumsq_accumulate": [_vp, C.c_int64, _vp],
+    "wm_clip_grad_norm_scale": [_vp, C.c_int64, _vp, C.c_float],
+    "wm_clip_grad_value": [_vp, C.c_int64, C.c_float],
+    "wm_grad_unscale": [C.c_int, _vp, _vp, C.c_float, C.POINTER(C.c_int)],
 }
 
 

@@ -127,6 +127,20 @@ __device__ __forceinline__ float exp_rr(float d) {
     return ldexpf(__builtin_amdgcn_exp2f(r), (int)n);
 }
 
+// Two floats -> two truncated halves packed low/high, as two
+// float_to_half_bits_rtz calls.  The hardware's packed round-toward-zero
+// conversion is exactly the truncation for every finite |x| < 65536 (normal
+// and subnormal halves alike); NaN, infinities and |x| >= 65536 take the
+// reference's bit formula in a branch a wave skips when none of its lanes
+// holds one.
+__device__ __forceinline__ uint32_t float2_to_half2_bits_rtz(float a, float b) {
+    typedef __fp16 wm_h2 __attribute__((ext_vector_type(2)));
+    uint32_t bits = __builtin_bit_cast(uint32_t, (wm_h2)__builtin_amdgcn_cvt_pkrtz(a, b));
+    if (!(fabsf(a) < 65536.0f) || !(fabsf(b) < 65536.0f))
+        bits = float_to_half_bits_rtz(a) | (float_to_half_bits_rtz(b) << 16);
+    return bits;
+}
+
 // DPP lane moves inside a 16-lane row (deterministic, no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {

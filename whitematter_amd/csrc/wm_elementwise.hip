@@ -163,8 +163,8 @@ __global__ void __launch_bounds__(kBlock) f32_to_f16_kernel(uint16_t* __restrict
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
         float4 v = reinterpret_cast<const float4*>(x)[i];
         uint2 o;
-        o.x = (uint32_t)f32_to_f16_rtz(v.x) | ((uint32_t)f32_to_f16_rtz(v.y) << 16);
-        o.y = (uint32_t)f32_to_f16_rtz(v.z) | ((uint32_t)f32_to_f16_rtz(v.w) << 16);
+        o.x = float2_to_half2_bits_rtz(v.x, v.y);
+        o.y = float2_to_half2_bits_rtz(v.z, v.w);
         reinterpret_cast<uint2*>(out)[i] = o;
     }
     for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)

@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(kBlock) epilogue_fwd_kernel(uint16_t* __restri
                     Chain lo_c = chain(h2f(hw[k] & 0xFFFFu), h2f(rw[k] & 0xFFFFu), gv[2 * k], lo, hi);
                     Chain hi_c = chain(h2f(hw[k] >> 16), h2f(rw[k] >> 16), gv[2 * k + 1], lo, hi);
                     s += lo_c.w + hi_c.w;
-                    ow[k] = f2h(lo_c.w) | (f2h(hi_c.w) << 16);
+                    ow[k] = float2_to_half2_bits_rtz(lo_c.w, hi_c.w);
                 }
                 if (orow)
                     st_stream(reinterpret_cast<float*>(orow + c),

@@ -138,7 +138,7 @@ __device__ __forceinline__ void binary_fwd_v(float4 (&r)[U], const float4 (&a)[U
         for (int u = 0; u < U; ++u) {
             r[u] = make_float4(pow_table(a[u].x, b[u].x), pow_table(a[u].y, b[u].y), pow_table(a[u].z, b[u].z),
                                pow_table(a[u].w, b[u].w));
-            fix |= pow_needs_fix(a[u].x, b[u].x) | pow_needs_fix(a[u].y, b[u].y) | pow_needs_fix(a[u].z, b[u].z) |
+            fix |= pow_needs_fix(a[u].x, b[u].x) || pow_needs_fix(a[u].y, b[u].y) || pow_needs_fix(a[u].z, b[u].z) ||
                    pow_needs_fix(a[u].w, b[u].w);
         }
         if (fix) {

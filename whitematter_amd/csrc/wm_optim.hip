@@ -1,0 +1,399 @@
+// Parameter-update kernels: optimizer steps (SGD, Adam, AdamW, RMSprop),
+// gradient clipping and gradient unscaling (reference core/optimizer.cpp,
+// core/amp.h:125-147).
+//
+// Every update is one streaming pass over the parameter's arrays: each
+// element's state is read once and written once, 128-bit non-temporal
+// accesses when every array is 16-byte aligned and n % 4 == 0.  The
+// arithmetic is the reference loop body's float expression in its source
+// order, with contraction into fused multiply-adds switched off and IEEE
+// division and square root (hipcc's defaults for float), so the results
+// equal a strict IEEE evaluation of the reference source bit for bit.
+//
+// The two reductions (sum of squares for the gradient norm, first non-finite
+// position for unscaling) are fixed-partition two-pass reductions: per-block
+// partials, then one block combining them in order, so they are
+// deterministic.
+#include "wm_common.hpp"
+#include "../../include/wm_optim.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace wm {
+
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------------------
+// Per-element updates (the reference loop bodies)
+// ---------------------------------------------------------------------------
+
+struct SgdArgs {
+    float lr, momentum;
+};
+
+// core/optimizer.cpp:26-33
+template <bool MOM>
+__device__ __forceinline__ void sgd_elem(float& p, float g, float& vel, const SgdArgs& a) {
+#pragma clang fp contract(off)
+    if constexpr (MOM) {
+        vel = a.momentum * vel + g;
+        p = p - a.lr * vel;
+    } else {
+        p = p - a.lr * g;
+    }
+}
+
+struct AdamArgs {
+    float lr, beta1, beta2, omb1, omb2, eps, bc1, bc2, wd;
+};
+
+// core/optimizer.cpp:55-64 (Adam), :85-98 (AdamW, DECOUPLED)
+template <bool DECOUPLED>
+__device__ __forceinline__ void adam_elem(float& p, float g, float& m, float& v, const AdamArgs& a) {
+#pragma clang fp contract(off)
+    m = a.beta1 * m + a.omb1 * g;
+    v = a.beta2 * v + a.omb2 * g * g;
+    const float m_hat = m / a.bc1;
+    const float v_hat = v / a.bc2;
+    if constexpr (DECOUPLED) p = p - a.lr * (m_hat / (sqrtf(v_hat) + a.eps) + a.wd * p);
+    else p = p - a.lr * m_hat / (sqrtf(v_hat) + a.eps);
+}
+
+struct RmsArgs {
+    float lr, alpha, oma, eps, momentum, wd;
+};
+
+// core/optimizer.cpp:116-136
+template <bool WD, bool MOM>
+__device__ __forceinline__ void rms_elem(float& p, float g, float& v, float& buf, const RmsArgs& a) {
+#pragma clang fp contract(off)
+    if constexpr (WD) g = g + a.wd * p;
+    v = a.alpha * v + a.oma * g * g;
+    const float avg = sqrtf(v) + a.eps;
+    if constexpr (MOM) {
+        buf = a.momentum * buf + g / avg;
+        p = p - a.lr * buf;
+    } else {
+        p = p - a.lr * g / avg;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One streaming kernel for all updates: p and g, plus up to two state arrays
+// (s1, s2), updated by UPD::apply(p, g, s1, s2).
+// ---------------------------------------------------------------------------
+
+template <int KIND, bool A, bool B>
+struct Upd;  // KIND 0: SGD (A = momentum); 1: Adam (A = decoupled); 2: RMSprop (A = wd, B = momentum)
+
+template <bool A, bool B>
+struct Upd<0, A, B> {
+    SgdArgs a;
+    static constexpr int NS = A ? 1 : 0;
+    __device__ __forceinline__ void operator()(float& p, float g, float& s1, float&) const { sgd_elem<A>(p, g, s1, a); }
+};
+template <bool A, bool B>
+struct Upd<1, A, B> {
+    AdamArgs a;
+    static constexpr int NS = 2;
+    __device__ __forceinline__ void operator()(float& p, float g, float& s1, float& s2) const {
+        adam_elem<A>(p, g, s1, s2, a);
+    }
+};
+template <bool A, bool B>
+struct Upd<2, A, B> {
+    RmsArgs a;
+    static constexpr int NS = B ? 2 : 1;
+    __device__ __forceinline__ void operator()(float& p, float g, float& s1, float& s2) const {
+        rms_elem<A, B>(p, g, s1, s2, a);
+    }
+};
+
+template <class U>
+__global__ void __launch_bounds__(kBlock) update_vec_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                             float* __restrict__ s1, float* __restrict__ s2,
+                                                             int64_t n4, U upd) {
+    constexpr int NS = U::NS;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        const int64_t e = 4 * i;
+        float4 vp = ld_stream(p + e);
+        const float4 vg = ld_stream(g + e);
+        float4 v1 = NS > 0 ? ld_stream(s1 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 v2 = NS > 1 ? ld_stream(s2 + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        upd(vp.x, vg.x, v1.x, v2.x);
+        upd(vp.y, vg.y, v1.y, v2.y);
+        upd(vp.z, vg.z, v1.z, v2.z);
+        upd(vp.w, vg.w, v1.w, v2.w);
+        st_stream(p + e, vp);
+        if (NS > 0) st_stream(s1 + e, v1);
+        if (NS > 1) st_stream(s2 + e, v2);
+    }
+}
+
+template <class U>
+__global__ void __launch_bounds__(kBlock) update_scalar_kernel(float* __restrict__ p, const float* __restrict__ g,
+                                                                float* __restrict__ s1, float* __restrict__ s2,
+                                                                int64_t n, U upd) {
+    constexpr int NS = U::NS;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float vp = p[i];
+        float v1 = NS > 0 ? s1[i] : 0.f;
+        float v2 = NS > 1 ? s2[i] : 0.f;
+        upd(vp, g[i], v1, v2);
+        p[i] = vp;
+        if (NS > 0) s1[i] = v1;
+        if (NS > 1) s2[i] = v2;
+    }
+}
+
+template <class U>
+int launch_update(float* p, const float* g, float* s1, float* s2, int64_t n, const U& upd, const char* what) {
+    if (n == 0) return WM_OK;
+    constexpr int NS = U::NS;
+    const bool vec = n % 4 == 0 && aligned16(p) && aligned16(g) && (NS < 1 || aligned16(s1)) &&
+                     (NS < 2 || aligned16(s2));
+    if (vec)
+        hipLaunchKernelGGL(update_vec_kernel<U>, dim3(grid_for(n / 4, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
+                           s1, s2, n / 4, upd);
+    else
+        hipLaunchKernelGGL(update_scalar_kernel<U>, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
+                           s1, s2, n, upd);
+    return check_launch(what);
+}
+
+// ---------------------------------------------------------------------------
+// Sum of squares (gradient norm) and clipping
+// ---------------------------------------------------------------------------
+
+constexpr int kMaxPart = 1024;
+
+__global__ void __launch_bounds__(kBlock) sumsq_partial_kernel(const float* __restrict__ g, int64_t n,
+                                                                float* __restrict__ part) {
+    __shared__ float lds[kBlock / 64];
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    float s = 0.f;
+    const bool vec = ((uintptr_t)g & 15u) == 0;
+    const int64_t n4 = vec ? n / 4 : 0;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        const float4 v = ld_stream(g + 4 * i);
+        s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) s += g[i] * g[i];
+    s = block_sum<kBlock>(s, lds);
+    if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+// *total += sum(part[0..nb)), one block, fixed order.
+__global__ void __launch_bounds__(kBlock) sumsq_finalize_kernel(const float* __restrict__ part, int nb,
+                                                                 float* __restrict__ total) {
+    __shared__ float lds[kBlock / 64];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < nb; i += kBlock) s += part[i];
+    s = block_sum<kBlock>(s, lds);
+    if (threadIdx.x == 0) *total = *total + s;
+}
+
+__global__ void __launch_bounds__(kBlock) clip_norm_kernel(float* __restrict__ g, int64_t n,
+                                                            const float* __restrict__ total, float max_norm) {
+    const float clip_coef = max_norm / (sqrtf(*total) + 1e-6f);
+    if (!(clip_coef < 1.0f)) return;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) g[i] = g[i] * clip_coef;
+}
+
+__global__ void __launch_bounds__(kBlock) clip_value_kernel(float* __restrict__ g, int64_t n, float c) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        const float v = g[i];
+        g[i] = v > c ? c : (v < -c ? -c : v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Unscaling: first position whose scaled value is not finite, then a prefix
+// scale.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int64_t min_i64(int64_t a, int64_t b) { return a < b ? a : b; }
+
+// part[block] = smallest i of the block's stride set with !isfinite(g[i] * s),
+// or n.
+__global__ void __launch_bounds__(kBlock) first_bad_partial_kernel(const float* __restrict__ g, int64_t n, float s,
+                                                                    int64_t* __restrict__ part) {
+    __shared__ int64_t lds[kBlock];
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    int64_t first = n;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        if (!__builtin_isfinite(g[i] * s)) { first = i; break; }  // later i of this thread are larger
+    }
+    lds[threadIdx.x] = first;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = lds[0];
+}
+
+__global__ void __launch_bounds__(kBlock) first_bad_finalize_kernel(const int64_t* __restrict__ part, int nb,
+                                                                     int64_t n, int64_t* __restrict__ out) {
+    __shared__ int64_t lds[kBlock];
+    int64_t first = n;
+    for (int i = threadIdx.x; i < nb; i += kBlock) first = min_i64(first, part[i]);
+    lds[threadIdx.x] = first;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) *out = lds[0];
+}
+
+__global__ void __launch_bounds__(kBlock) scale_prefix_kernel(float* __restrict__ g, int64_t count, float s) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < count; i += stride) g[i] = g[i] * s;
+}
+
+static int check_n(int64_t n, const char* what) {
+    if (n < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
+    return WM_OK;
+}
+
+}  // namespace wm
+
+using namespace wm;
+
+extern "C" {
+
+int wm_sgd_step(float* p, const float* g, float* velocity, int64_t n, float lr, float momentum) {
+    WM_TRY(check_n(n, "wm_sgd_step"));
+    if (n == 0) return WM_OK;
+    if (!p || !g) return set_error(WM_ERR_INVALID, "wm_sgd_step: null pointer");
+    WM_CHECK_INIT();
+    const SgdArgs a{lr, momentum};
+    if (momentum > 0.0f) {
+        if (!velocity) return set_error(WM_ERR_INVALID, "wm_sgd_step: momentum > 0 needs a velocity buffer");
+        return launch_update(p, g, velocity, nullptr, n, Upd<0, true, false>{a}, "wm_sgd_step");
+    }
+    return launch_update(p, g, nullptr, nullptr, n, Upd<0, false, false>{a}, "wm_sgd_step");
+}
+
+static int adam_common(bool decoupled, float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1,
+                       float beta2, float eps, float bc1, float bc2, float wd, const char* what) {
+    WM_TRY(check_n(n, what));
+    if (n == 0) return WM_OK;
+    if (!p || !g || !m || !v) return set_error(WM_ERR_INVALID, std::string(what) + ": null pointer");
+    WM_CHECK_INIT();
+    const AdamArgs a{lr, beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bc1, bc2, wd};
+    if (decoupled) return launch_update(p, g, m, v, n, Upd<1, true, false>{a}, what);
+    return launch_update(p, g, m, v, n, Upd<1, false, false>{a}, what);
+}
+
+int wm_adam_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                 float eps, float bias_correction1, float bias_correction2) {
+    return adam_common(false, p, g, m, v, n, lr, beta1, beta2, eps, bias_correction1, bias_correction2, 0.0f,
+                       "wm_adam_step");
+}
+
+int wm_adamw_step(float* p, const float* g, float* m, float* v, int64_t n, float lr, float beta1, float beta2,
+                  float eps, float bias_correction1, float bias_correction2, float weight_decay) {
+    return adam_common(true, p, g, m, v, n, lr, beta1, beta2, eps, bias_correction1, bias_correction2, weight_decay,
+                       "wm_adamw_step");
+}
+
+int wm_rmsprop_step(float* p, const float* g, float* v, float* buffer, int64_t n, float lr, float alpha, float eps,
+                    float momentum, float weight_decay) {
+    WM_TRY(check_n(n, "wm_rmsprop_step"));
+    if (n == 0) return WM_OK;
+    if (!p || !g || !v) return set_error(WM_ERR_INVALID, "wm_rmsprop_step: null pointer");
+    const bool mom = momentum > 0.0f, wd = weight_decay != 0.0f;
+    if (mom && !buffer) return set_error(WM_ERR_INVALID, "wm_rmsprop_step: momentum > 0 needs a momentum buffer");
+    WM_CHECK_INIT();
+    const RmsArgs a{lr, alpha, 1.0f - alpha, eps, momentum, weight_decay};
+    if (wd && mom) return launch_update(p, g, v, buffer, n, Upd<2, true, true>{a}, "wm_rmsprop_step");
+    if (wd) return launch_update(p, g, v, nullptr, n, Upd<2, true, false>{a}, "wm_rmsprop_step");
+    if (mom) return launch_update(p, g, v, buffer, n, Upd<2, false, true>{a}, "wm_rmsprop_step");
+    return launch_update(p, g, v, nullptr, n, Upd<2, false, false>{a}, "wm_rmsprop_step");
+}
+
+int wm_grad_sumsq_accumulate(const float* g, int64_t n, float* total) {
+    WM_TRY(check_n(n, "wm_grad_sumsq_accumulate"));
+    if (!total) return set_error(WM_ERR_INVALID, "wm_grad_sumsq_accumulate: null total");
+    if (n == 0) return WM_OK;
+    if (!g) return set_error(WM_ERR_INVALID, "wm_grad_sumsq_accumulate: null pointer");
+    WM_CHECK_INIT();
+    const int nb = (int)std::min<int64_t>(grid_for(n / 4 + 1, kBlock, 4), kMaxPart);
+    Workspace ws((size_t)nb * sizeof(float));
+    if (!ws.p) return set_error(WM_ERR_NOMEM, "wm_grad_sumsq_accumulate: workspace");
+    hipLaunchKernelGGL(sumsq_partial_kernel, dim3(nb), dim3(kBlock), 0, stream(), g, n, ws.as<float>());
+    WM_TRY(check_launch("wm_grad_sumsq_accumulate"));
+    hipLaunchKernelGGL(sumsq_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), ws.as<float>(), nb, total);
+    return check_launch("wm_grad_sumsq_accumulate(finalize)");
+}
+
+int wm_clip_grad_norm_scale(float* g, int64_t n, const float* total_sumsq, float max_norm) {
+    WM_TRY(check_n(n, "wm_clip_grad_norm_scale"));
+    if (n == 0) return WM_OK;
+    if (!g || !total_sumsq) return set_error(WM_ERR_INVALID, "wm_clip_grad_norm_scale: null pointer");
+    WM_CHECK_INIT();
+    hipLaunchKernelGGL(clip_norm_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n, total_sumsq,
+                       max_norm);
+    return check_launch("wm_clip_grad_norm_scale");
+}
+
+int wm_clip_grad_value(float* g, int64_t n, float clip_value) {
+    WM_TRY(check_n(n, "wm_clip_grad_value"));
+    if (n == 0) return WM_OK;
+    if (!g) return set_error(WM_ERR_INVALID, "wm_clip_grad_value: null pointer");
+    WM_CHECK_INIT();
+    hipLaunchKernelGGL(clip_value_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n,
+                       clip_value);
+    return check_launch("wm_clip_grad_value");
+}
+
+int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float inv_scale, int* found_inf) {
+    if (count < 0) return set_error(WM_ERR_INVALID, "wm_grad_unscale: negative count");
+    if (!found_inf) return set_error(WM_ERR_INVALID, "wm_grad_unscale: null found_inf");
+    *found_inf = 0;
+    if (count == 0) return WM_OK;
+    if (!grads || !sizes) return set_error(WM_ERR_INVALID, "wm_grad_unscale: null pointer");
+    for (int k = 0; k < count; ++k)
+        if (sizes[k] < 0) return set_error(WM_ERR_INVALID, "wm_grad_unscale: negative size");
+    WM_CHECK_INIT();
+    // 1. first non-finite scaled position of every tensor (n when none)
+    Workspace firsts((size_t)count * sizeof(int64_t));
+    Workspace part((size_t)kMaxPart * sizeof(int64_t));
+    if (!firsts.p || !part.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
+    std::vector<int64_t> host(count, 0);
+    for (int k = 0; k < count; ++k) {
+        if (!grads[k] || sizes[k] == 0) continue;
+        const int nb = (int)std::min<int64_t>(grid_for(sizes[k], kBlock, 4), kMaxPart);
+        hipLaunchKernelGGL(first_bad_partial_kernel, dim3(nb), dim3(kBlock), 0, stream(), grads[k], sizes[k],
+                           inv_scale, part.as<int64_t>());
+        WM_TRY(check_launch("wm_grad_unscale(find)"));
+        hipLaunchKernelGGL(first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<int64_t>(), nb,
+                           sizes[k], firsts.as<int64_t>() + k);
+        WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
+    }
+    WM_TRY(wm_d2h(host.data(), firsts.p, (size_t)count * sizeof(int64_t)));
+    // 2. scale every element before the first non-finite one, in order
+    for (int k = 0; k < count; ++k) {
+        if (!grads[k] || sizes[k] == 0) continue;
+        const int64_t upto = host[k];
+        if (upto > 0) {
+            hipLaunchKernelGGL(scale_prefix_kernel, dim3(grid_for(upto, kBlock, 16)), dim3(kBlock), 0, stream(),
+                               grads[k], upto, inv_scale);
+            WM_TRY(check_launch("wm_grad_unscale(scale)"));
+        }
+        if (upto < sizes[k]) {
+            *found_inf = 1;
+            break;
+        }
+    }
+    return WM_OK;
+}
+
+}  // extern "C"
