@@ -11,6 +11,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include "optimizer.h"
 #include "tensor.h"
 #include "wm_hip.h"
 
@@ -133,4 +134,40 @@ PYBIND11_MODULE(_tensor, m) {
         .def("__neg__", [](const TensorPtr& a) { return -(*a); });
 
     m.def("set_grad_enabled", &GradMode::set_enabled);
+
+    // Drop-in optimizers (optimizer.h): steps and clipping run on the device;
+    // state(i) copies one parameter's state buffers to numpy.
+    py::class_<Optimizer>(m, "Optimizer")
+        .def("step", &Optimizer::step)
+        .def("zero_grad", &Optimizer::zero_grad)
+        .def_readwrite("lr", &Optimizer::lr);
+    auto states = [](const std::vector<wm::DeviceVector>& a, const std::vector<wm::DeviceVector>& b, size_t i) {
+        py::list out;
+        if (i < a.size()) out.append(to_numpy(a[i], {a[i].size()}));
+        if (i < b.size()) out.append(to_numpy(b[i], {b[i].size()}));
+        return out;
+    };
+    py::class_<SGD, Optimizer>(m, "SGD")
+        .def(py::init<const std::vector<TensorPtr>&, float, float>(), py::arg("params"), py::arg("lr"),
+             py::arg("momentum") = 0.0f)
+        .def("state", [states](const SGD& o, size_t i) { return states(o.velocity, {}, i); });
+    py::class_<Adam, Optimizer>(m, "Adam")
+        .def(py::init<const std::vector<TensorPtr>&, float, float, float, float>(), py::arg("params"),
+             py::arg("lr") = 0.001f, py::arg("beta1") = 0.9f, py::arg("beta2") = 0.999f, py::arg("eps") = 1e-8f)
+        .def_readonly("t", &Adam::t)
+        .def("state", [states](const Adam& o, size_t i) { return states(o.m, o.v, i); });
+    py::class_<AdamW, Optimizer>(m, "AdamW")
+        .def(py::init<const std::vector<TensorPtr>&, float, float, float, float, float>(), py::arg("params"),
+             py::arg("lr") = 0.001f, py::arg("beta1") = 0.9f, py::arg("beta2") = 0.999f, py::arg("eps") = 1e-8f,
+             py::arg("weight_decay") = 0.01f)
+        .def_readonly("t", &AdamW::t)
+        .def("state", [states](const AdamW& o, size_t i) { return states(o.m, o.v, i); });
+    py::class_<RMSprop, Optimizer>(m, "RMSprop")
+        .def(py::init<const std::vector<TensorPtr>&, float, float, float, float, float>(), py::arg("params"),
+             py::arg("lr") = 0.01f, py::arg("alpha") = 0.99f, py::arg("eps") = 1e-8f, py::arg("momentum") = 0.0f,
+             py::arg("weight_decay") = 0.0f)
+        .def("state", [states](const RMSprop& o, size_t i) { return states(o.v, o.buffer, i); });
+    m.def("clip_grad_norm_", [](std::vector<TensorPtr> ps, float max_norm) { clip_grad_norm_(ps, max_norm); });
+    m.def("clip_grad_value_", [](std::vector<TensorPtr> ps, float c) { clip_grad_value_(ps, c); });
+    m.def("get_grad_norm", &get_grad_norm);
 }

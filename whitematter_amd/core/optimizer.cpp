@@ -1,0 +1,199 @@
+// optimizer.cpp -- the drop-in optimizers: step() and the clipping helpers
+// run the update kernels of include/wm_optim.h on each parameter's device
+// buffers (core/optimizer.cpp:1-177); the schedulers keep the reference's
+// host arithmetic (:179-259).
+#include "optimizer.h"
+
+#include <stdexcept>
+#include <string>
+
+#include "wm_hip.h"
+#include "wm_optim.h"
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != WM_OK) throw std::runtime_error(std::string(what) + ": " + wm_last_error());
+}
+
+int64_t numel(const TensorPtr& p) { return (int64_t)p->data.size(); }
+
+// One zero-initialised state buffer per parameter.  A fresh DeviceVector of
+// zeros is only a flag; the first kernel that writes it materialises it.
+std::vector<wm::DeviceVector> zero_state(const std::vector<TensorPtr>& params) {
+    std::vector<wm::DeviceVector> s;
+    s.reserve(params.size());
+    for (const auto& p : params) s.emplace_back(p->data.size(), 0.0f);
+    return s;
+}
+
+// 1 - beta^t as the reference computes it: std::pow(float, int) is the
+// double pow, and the float assignment rounds once (core/optimizer.cpp:48).
+float bias_correction(float beta, int t) { return (float)(1.0 - std::pow((double)beta, (double)t)); }
+
+}  // namespace
+
+Optimizer::Optimizer(const std::vector<TensorPtr>& params, float lr) : params(params), lr(lr) {}
+
+void Optimizer::zero_grad() {
+    for (auto& p : params) p->zero_grad();
+}
+
+SGD::SGD(const std::vector<TensorPtr>& params, float lr, float momentum) : Optimizer(params, lr), momentum(momentum) {
+    if (momentum > 0.0f) velocity = zero_state(params);
+}
+
+void SGD::step() {
+    for (size_t i = 0; i < params.size(); ++i) {
+        auto& p = params[i];
+        check(wm_sgd_step(p->data.dev_rw(), p->grad.dev(), momentum > 0.0f ? velocity[i].dev_rw() : nullptr,
+                          numel(p), lr, momentum),
+              "SGD::step");
+    }
+}
+
+Adam::Adam(const std::vector<TensorPtr>& params, float lr, float beta1, float beta2, float eps)
+    : Optimizer(params, lr), beta1(beta1), beta2(beta2), eps(eps), t(0), m(zero_state(params)),
+      v(zero_state(params)) {}
+
+void Adam::step() {
+    ++t;
+    const float bc1 = bias_correction(beta1, t), bc2 = bias_correction(beta2, t);
+    for (size_t i = 0; i < params.size(); ++i) {
+        auto& p = params[i];
+        check(wm_adam_step(p->data.dev_rw(), p->grad.dev(), m[i].dev_rw(), v[i].dev_rw(), numel(p), lr, beta1, beta2,
+                           eps, bc1, bc2),
+              "Adam::step");
+    }
+}
+
+AdamW::AdamW(const std::vector<TensorPtr>& params, float lr, float beta1, float beta2, float eps, float weight_decay)
+    : Optimizer(params, lr), beta1(beta1), beta2(beta2), eps(eps), weight_decay(weight_decay), t(0),
+      m(zero_state(params)), v(zero_state(params)) {}
+
+void AdamW::step() {
+    ++t;
+    const float bc1 = bias_correction(beta1, t), bc2 = bias_correction(beta2, t);
+    for (size_t i = 0; i < params.size(); ++i) {
+        auto& p = params[i];
+        check(wm_adamw_step(p->data.dev_rw(), p->grad.dev(), m[i].dev_rw(), v[i].dev_rw(), numel(p), lr, beta1,
+                            beta2, eps, bc1, bc2, weight_decay),
+              "AdamW::step");
+    }
+}
+
+RMSprop::RMSprop(const std::vector<TensorPtr>& params, float lr, float alpha, float eps, float momentum,
+                 float weight_decay)
+    : Optimizer(params, lr), alpha(alpha), eps(eps), momentum(momentum), weight_decay(weight_decay),
+      v(zero_state(params)) {
+    if (momentum > 0.0f) buffer = zero_state(params);
+}
+
+void RMSprop::step() {
+    for (size_t i = 0; i < params.size(); ++i) {
+        auto& p = params[i];
+        check(wm_rmsprop_step(p->data.dev_rw(), p->grad.dev(), v[i].dev_rw(),
+                              momentum > 0.0f ? buffer[i].dev_rw() : nullptr, numel(p), lr, alpha, eps, momentum,
+                              weight_decay),
+              "RMSprop::step");
+    }
+}
+
+// ---- clipping ---------------------------------------------------------------
+
+namespace {
+
+// Sum of squares of every gradient into a one-element device buffer, in
+// parameter order (get_grad_norm's loop, core/optimizer.cpp:145-153).
+wm::DeviceVector grad_sumsq(const std::vector<TensorPtr>& params) {
+    wm::DeviceVector total(1, 0.0f);
+    float* t = total.dev_rw();
+    for (const auto& p : params)
+        if (!p->grad.empty()) check(wm_grad_sumsq_accumulate(p->grad.dev(), (int64_t)p->grad.size(), t), "get_grad_norm");
+    return total;
+}
+
+}  // namespace
+
+float get_grad_norm(const std::vector<TensorPtr>& params) {
+    const wm::DeviceVector total = grad_sumsq(params);
+    return std::sqrt(total[0]);
+}
+
+// The clip coefficient is computed on the device from the device-side norm,
+// so clipping never waits for the host.
+void clip_grad_norm_(std::vector<TensorPtr>& params, float max_norm) {
+    const wm::DeviceVector total = grad_sumsq(params);
+    for (auto& p : params)
+        if (!p->grad.empty())
+            check(wm_clip_grad_norm_scale(p->grad.dev_rw(), (int64_t)p->grad.size(), total.dev(), max_norm),
+                  "clip_grad_norm_");
+}
+
+void clip_grad_value_(std::vector<TensorPtr>& params, float clip_value) {
+    for (auto& p : params)
+        if (!p->grad.empty())
+            check(wm_clip_grad_value(p->grad.dev_rw(), (int64_t)p->grad.size(), clip_value), "clip_grad_value_");
+}
+
+// ---- schedulers (host arithmetic, core/optimizer.cpp:179-259) ----------------
+
+LRScheduler::LRScheduler(Optimizer* optimizer) : optimizer(optimizer), base_lr(optimizer->lr), last_epoch(-1) {}
+
+void LRScheduler::step() {
+    ++last_epoch;
+    optimizer->lr = get_lr();
+}
+
+StepLR::StepLR(Optimizer* optimizer, int step_size, float gamma)
+    : LRScheduler(optimizer), step_size(step_size), gamma(gamma) {}
+
+float StepLR::get_lr() {
+    return last_epoch == -1 ? base_lr : base_lr * std::pow(gamma, last_epoch / step_size);
+}
+
+ExponentialLR::ExponentialLR(Optimizer* optimizer, float gamma) : LRScheduler(optimizer), gamma(gamma) {}
+
+float ExponentialLR::get_lr() { return last_epoch == -1 ? base_lr : base_lr * std::pow(gamma, last_epoch); }
+
+CosineAnnealingLR::CosineAnnealingLR(Optimizer* optimizer, int T_max, float eta_min)
+    : LRScheduler(optimizer), T_max(T_max), eta_min(eta_min) {}
+
+float CosineAnnealingLR::get_lr() {
+    if (last_epoch == -1) return base_lr;
+    return eta_min + (base_lr - eta_min) * (1.0f + std::cos(M_PI * last_epoch / T_max)) / 2.0f;
+}
+
+CosineAnnealingWarmRestarts::CosineAnnealingWarmRestarts(Optimizer* optimizer, int T_0, int T_mult, float eta_min)
+    : LRScheduler(optimizer), T_0(T_0), T_mult(T_mult), eta_min(eta_min), T_cur(0), T_i(T_0) {}
+
+float CosineAnnealingWarmRestarts::get_lr() {
+    return eta_min + (base_lr - eta_min) * (1.0f + std::cos(M_PI * T_cur / T_i)) / 2.0f;
+}
+
+void CosineAnnealingWarmRestarts::step() {
+    ++last_epoch;
+    if (++T_cur >= T_i) {
+        T_cur = 0;
+        T_i *= T_mult;
+    }
+    optimizer->lr = get_lr();
+}
+
+ReduceLROnPlateau::ReduceLROnPlateau(Optimizer* optimizer, float factor, int patience, float min_lr, bool mode_min)
+    : optimizer(optimizer), factor(factor), patience(patience), min_lr(min_lr), num_bad_epochs(0),
+      best(mode_min ? 1e10f : -1e10f), mode_min(mode_min) {}
+
+void ReduceLROnPlateau::step(float metric) {
+    if (mode_min ? metric < best : metric > best) {
+        best = metric;
+        num_bad_epochs = 0;
+    } else {
+        ++num_bad_epochs;
+    }
+    if (num_bad_epochs > patience) {
+        const float reduced = optimizer->lr * factor;
+        if (reduced >= min_lr) optimizer->lr = reduced;
+        num_bad_epochs = 0;
+    }
+}
