@@ -232,7 +232,83 @@ def c5_ops(b=32, t=1024, c=4096):
                     "(grads fp32, accumulated)" % (b, t, c, c), "elements": N}
 
 
-CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops}
+def gpt2_small_shapes():
+    """Parameter shapes of a GPT-2-small-sized model (124M parameters): the
+    tensor list an optimizer step walks (many small bias / norm vectors next
+    to a few large matrices)."""
+    d, v, ctx, layers = 768, 50257, 1024, 12
+    shapes = [(v, d), (ctx, d)]
+    for _ in range(layers):
+        shapes += [(d,), (d,), (d, 3 * d), (3 * d,), (d, d), (d,), (d,), (d,), (d, 4 * d), (4 * d,), (4 * d, d), (d,)]
+    shapes += [(d,), (d,)]
+    return shapes
+
+
+def opt_ops():
+    """Parameter updates: one optimizer step / clipping / unscaling pass over a
+    GPT-2-small-sized parameter list, one multi-tensor launch per pass as the
+    drop-in optimizers issue them."""
+    shapes = gpt2_small_shapes()
+    rng = np.random.default_rng(0)
+    P, G, S1, S2 = [], [], [], []
+    for i, s in enumerate(shapes):
+        n = int(np.prod(s))
+        P.append(W.DeviceArray.from_host((rng.standard_normal(n) * 0.02).astype(np.float32)))
+        G.append(W.DeviceArray.from_host((rng.standard_normal(n) * 1e-3).astype(np.float32)))
+        S1.append(W.DeviceArray((n,))); S1[-1].fill(0.0)
+        S2.append(W.DeviceArray((n,))); S2[-1].fill(0.0)
+    N = sum(int(np.prod(s)) for s in shapes)
+    sizes = [int(np.prod(s)) for s in shapes]
+    total = W.DeviceArray((1,))
+    gptrs = (W.C.c_void_p * len(G))(*[g.ptr for g in G])
+    gsizes = (W.C.c_int64 * len(G))(*sizes)
+    found = W.C.c_int()
+    L = W.lib()
+    t = [0]
+
+    pP, _a = W.ptr_array([p.ptr for p in P])
+    pG, _b = W.ptr_array([g.ptr for g in G])
+    pS1, _c = W.ptr_array([x.ptr for x in S1])
+    pS2, _d = W.ptr_array([x.ptr for x in S2])
+    pN, _e = W.i64_array(sizes)
+    cnt = len(sizes)
+
+    # the drop-in optimizers' step(): one multi-tensor launch over the list
+    def adam():
+        t[0] += 1
+        bc1 = np.float32(1.0 - 0.9 ** t[0]); bc2 = np.float32(1.0 - 0.999 ** t[0])
+        W.check(L.wm_adamw_step_multi(cnt, pP, pG, pS1, pS2, pN, 1e-4, 0.9, 0.999, 1e-8, bc1, bc2, 0.01))
+
+    def sgd():
+        W.check(L.wm_sgd_step_multi(cnt, pP, pG, pS1, pN, 1e-4, 0.9))
+
+    def rms():
+        W.check(L.wm_rmsprop_step_multi(cnt, pP, pG, pS2, None, pN, 1e-4, 0.99, 1e-8, 0.0, 0.0))
+
+    def clip():
+        W.check(L.wm_grad_sumsq_multi(cnt, pG, pN, total.vp))
+        # max_norm 0 clips on every call (coefficient 0 < 1), so the timed pass
+        # always reads and writes every gradient
+        W.check(L.wm_clip_grad_norm_scale_multi(cnt, pG, pN, total.vp, 0.0))
+
+    def unscale():
+        W.check(L.wm_grad_unscale(len(G), W.C.cast(gptrs, W.C.c_void_p), W.C.cast(gsizes, W.C.c_void_p), 1.0,
+                                  W.C.byref(found)))
+
+    ops = [
+        Op("AdamW step", adam, N * 28, "multi_update_kernel<wm::Upd<1, true", N),
+        Op("SGD momentum step", sgd, N * 20, "multi_update_kernel<wm::Upd<0, true", N),
+        Op("RMSprop step", rms, N * 20, "multi_update_kernel<wm::Upd<2, false, false", N),
+        Op("clip_grad_norm_", clip, N * 12, "multi_sumsq_kernel", N),
+        Op("GradScaler unscale", unscale, N * 12, "multi_first_bad_kernel", N),
+    ]
+    return ops, P + G + S1 + S2 + [total], {
+        "workload": "opt: %d parameter tensors, %d parameters (GPT-2-small shapes), fp32 params / grads / "
+                    "state; one AdamW, SGD-momentum and RMSprop step, clip_grad_norm_ and GradScaler unscale, "
+                    "each one multi-tensor launch (pair) over the list" % (len(shapes), N), "elements": N}
+
+
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops}
 
 
 # ---------------------------------------------------------------------------

@@ -81,9 +81,39 @@ int wm_clip_grad_value(float* g, int64_t n, float clip_value);
  * at the first element whose product is not finite: tensors before it are
  * fully unscaled, its own tensor up to (not including) that element, the
  * rest untouched -- the reference's early break.  *found_inf (host) is set to
- * 1 if such an element exists, else 0.  Synchronises with the library stream
+ * 1 if such an element exists, else 0.  One search launch over the whole list
+ * and one scaling launch; synchronises with the library stream in between
  * (the stopping position decides what is written). */
 int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float inv_scale, int* found_inf);
+
+/* ---- multi-tensor variants ----------------------------------------------
+ * The same updates over a whole parameter list in one launch: host arrays of
+ * `count` device pointers (one per parameter tensor) and sizes; zero-size
+ * entries are skipped.  Each element gets exactly the single-tensor update,
+ * so results equal calling the single-tensor entry point per tensor in list
+ * order.  The list's descriptor table is uploaded on the library stream
+ * through pinned staging; the call does not wait for the GPU.  This is what
+ * the drop-in optimizers' step() uses: a model's many small parameter tensors
+ * would otherwise cost one kernel launch each.                             */
+int wm_sgd_step_multi(int count, float* const* p, const float* const* g, float* const* velocity, const int64_t* n,
+                      float lr, float momentum);
+int wm_adam_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
+                       const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
+                       float bias_correction2);
+int wm_adamw_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
+                        const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
+                        float bias_correction2, float weight_decay);
+int wm_rmsprop_step_multi(int count, float* const* p, const float* const* g, float* const* v, float* const* buffer,
+                          const int64_t* n, float lr, float alpha, float eps, float momentum, float weight_decay);
+
+/* get_grad_norm's sum of squares over a gradient list: *total (device) =
+ * sum over every element of every tensor, a fixed-order two-pass sum.      */
+int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, float* total);
+
+/* clip_grad_norm_'s scaling and clip_grad_value_ over a gradient list.      */
+int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, const float* total_sumsq,
+                                  float max_norm);
+int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float clip_value);
 
 #ifdef __cplusplus
 }

@@ -162,3 +162,72 @@ def test_unscale(wm, bad):
     assert found.value == found_or == (0 if bad is None else 1)
     for d, gm in zip(ds, mine):
         assert oracle.bit_equal(d.get(), gm)
+
+
+# ---- multi-tensor entry points --------------------------------------------
+
+MULTI_SIZES = [(4096, False), (0, False), (7, False), (200003, False), (1000, True), (65536, False), (131077, True)]
+
+
+def _ptrs(slots):
+    return W.ptr_array([s.vp if s is not None else None for s in slots])
+
+
+@pytest.mark.parametrize("kind,hp", CONFIGS, ids=lambda v: v if isinstance(v, str) else "-".join(map(str, v.values())))
+def test_multi_steps_bitexact(wm, kind, hp):
+    """One launch over a list of tensors (empty, tiny, multi-chunk, misaligned)
+    equals the single-tensor update of each: bit-exact against the oracle."""
+    lr, a, b, c, d = hp["lr"], hp.get("a", 0.0), hp.get("b", 0.0), hp.get("c", 0.0), hp.get("d", 0.0)
+    mine, dev = [], []
+    for i, (n, mis) in enumerate(MULTI_SIZES):
+        arrs = [rng(7 * i).standard_normal(n).astype(np.float32), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+        mine.append(arrs)
+        dev.append([Slot(x, mis) for x in arrs])
+    ns, _ns = W.i64_array([n for n, _ in MULTI_SIZES])
+    for t in range(1, 4):
+        gs = [(rng(100 * t + i).standard_normal(n) * 10.0 ** rng(t + i).uniform(-3, 1, n)).astype(np.float32)
+              for i, (n, _) in enumerate(MULTI_SIZES)]
+        dgs = [Slot(g, mis) for g, (_, mis) in zip(gs, MULTI_SIZES)]
+        P, _p = _ptrs([x[0] for x in dev])
+        G, _g = _ptrs(dgs)
+        S1, _s1 = _ptrs([x[1] for x in dev])
+        S2, _s2 = _ptrs([x[2] for x in dev])
+        cnt = len(MULTI_SIZES)
+        if kind == "sgd":
+            W.call("wm_sgd_step_multi", cnt, P, G, S1 if a > 0 else None, ns, lr, a)
+        elif kind == "adam":
+            W.call("wm_adam_step_multi", cnt, P, G, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t))
+        elif kind == "adamw":
+            W.call("wm_adamw_step_multi", cnt, P, G, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t), d)
+        else:
+            W.call("wm_rmsprop_step_multi", cnt, P, G, S1, S2 if c > 0 else None, ns, lr, a, b, c, d)
+        for arrs, g in zip(mine, gs):
+            oracle_step(kind, hp, arrs[0], g, arrs[1], arrs[2], t)
+        for i, (arrs, slots) in enumerate(zip(mine, dev)):
+            for j in range(3):
+                assert oracle.bit_equal(slots[j].get(), arrs[j]), (kind, t, i, j)
+
+
+def test_multi_norm_clip_value(wm):
+    gs = [(rng(80 + i).standard_normal(n) * 3).astype(np.float32) for i, (n, _) in enumerate(MULTI_SIZES)]
+    ds = [Slot(g, mis) for g, (_, mis) in zip(gs, MULTI_SIZES)]
+    G, _g = _ptrs(ds)
+    ns, _ns = W.i64_array([n for n, _ in MULTI_SIZES])
+    total = W.DeviceArray((1,))
+    total.fill(123.0)                                   # overwritten, not accumulated
+    W.call("wm_grad_sumsq_multi", len(gs), G, ns, total.vp)
+    t_gpu = np.float32(total.to_host()[0])
+    t64 = sum(oracle.get("f64").grad_sumsq(g) for g in gs)
+    assert abs(float(t_gpu) - t64) <= 1e-5 * t64
+    W.call("wm_clip_grad_norm_scale_multi", len(gs), G, ns, total.vp, 10.0)
+    coef = np.float32(10.0) / (np.sqrt(t_gpu, dtype=np.float32) + np.float32(1e-6))
+    assert coef < 1
+    for d_, g in zip(ds, gs):
+        assert oracle.bit_equal(d_.get(), g * coef)
+    W.call("wm_clip_grad_value_multi", len(gs), G, ns, 0.5)
+    for d_, g in zip(ds, gs):
+        mine = g * coef
+        o32.clip_grad_value(mine, 0.5)
+        assert oracle.bit_equal(d_.get(), mine)

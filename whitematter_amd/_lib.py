@@ -77,7 +77,26 @@ _SIGS = {
     "wm_clip_grad_norm_scale": [_vp, C.c_int64, _vp, C.c_float],
     "wm_clip_grad_value": [_vp, C.c_int64, C.c_float],
     "wm_grad_unscale": [C.c_int, _vp, _vp, C.c_float, C.POINTER(C.c_int)],
+    "wm_sgd_step_multi": [C.c_int, _vp, _vp, _vp, _vp, C.c_float, C.c_float],
+    "wm_adam_step_multi": [C.c_int, _vp, _vp, _vp, _vp, _vp] + [C.c_float] * 6,
+    "wm_adamw_step_multi": [C.c_int, _vp, _vp, _vp, _vp, _vp] + [C.c_float] * 7,
+    "wm_rmsprop_step_multi": [C.c_int, _vp, _vp, _vp, _vp, _vp] + [C.c_float] * 5,
+    "wm_grad_sumsq_multi": [C.c_int, _vp, _vp, _vp],
+    "wm_clip_grad_norm_scale_multi": [C.c_int, _vp, _vp, _vp, C.c_float],
+    "wm_clip_grad_value_multi": [C.c_int, _vp, _vp, C.c_float],
 }
+
+
+def ptr_array(ptrs):
+    """A host array of device pointers (None -> NULL) for the multi-tensor
+    entry points, as a void*."""
+    arr = (C.c_void_p * max(1, len(ptrs)))(*[(p.value if isinstance(p, C.c_void_p) else p) for p in ptrs])
+    return C.cast(arr, C.c_void_p), arr
+
+
+def i64_array(vals):
+    arr = (C.c_int64 * max(1, len(vals)))(*[int(v) for v in vals])
+    return C.cast(arr, C.c_void_p), arr
 
 
 class WMError(RuntimeError):

@@ -39,17 +39,43 @@ void Optimizer::zero_grad() {
     for (auto& p : params) p->zero_grad();
 }
 
+namespace {
+
+// The parameter list as the multi-tensor entry points take it: device
+// pointers of every parameter's data / grad / state, in parameter order.
+struct Lists {
+    std::vector<float*> p, s1, s2;
+    std::vector<const float*> g;
+    std::vector<int64_t> n;
+};
+
+Lists param_lists(std::vector<TensorPtr>& params, std::vector<wm::DeviceVector>* s1,
+                  std::vector<wm::DeviceVector>* s2) {
+    Lists l;
+    for (size_t i = 0; i < params.size(); ++i) {
+        auto& p = params[i];
+        l.n.push_back(numel(p));
+        l.p.push_back(p->data.dev_rw());
+        l.g.push_back(p->grad.dev());
+        l.s1.push_back(s1 ? (*s1)[i].dev_rw() : nullptr);
+        l.s2.push_back(s2 ? (*s2)[i].dev_rw() : nullptr);
+    }
+    return l;
+}
+
+}  // namespace
+
 SGD::SGD(const std::vector<TensorPtr>& params, float lr, float momentum) : Optimizer(params, lr), momentum(momentum) {
     if (momentum > 0.0f) velocity = zero_state(params);
 }
 
+// One launch per step over every parameter (core/optimizer.cpp:22-36 per element).
 void SGD::step() {
-    for (size_t i = 0; i < params.size(); ++i) {
-        auto& p = params[i];
-        check(wm_sgd_step(p->data.dev_rw(), p->grad.dev(), momentum > 0.0f ? velocity[i].dev_rw() : nullptr,
-                          numel(p), lr, momentum),
-              "SGD::step");
-    }
+    if (params.empty()) return;
+    Lists l = param_lists(params, momentum > 0.0f ? &velocity : nullptr, nullptr);
+    check(wm_sgd_step_multi((int)params.size(), l.p.data(), l.g.data(), momentum > 0.0f ? l.s1.data() : nullptr,
+                            l.n.data(), lr, momentum),
+          "SGD::step");
 }
 
 Adam::Adam(const std::vector<TensorPtr>& params, float lr, float beta1, float beta2, float eps)
@@ -58,13 +84,11 @@ Adam::Adam(const std::vector<TensorPtr>& params, float lr, float beta1, float be
 
 void Adam::step() {
     ++t;
-    const float bc1 = bias_correction(beta1, t), bc2 = bias_correction(beta2, t);
-    for (size_t i = 0; i < params.size(); ++i) {
-        auto& p = params[i];
-        check(wm_adam_step(p->data.dev_rw(), p->grad.dev(), m[i].dev_rw(), v[i].dev_rw(), numel(p), lr, beta1, beta2,
-                           eps, bc1, bc2),
-              "Adam::step");
-    }
+    if (params.empty()) return;
+    Lists l = param_lists(params, &m, &v);
+    check(wm_adam_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(), l.s2.data(), l.n.data(), lr,
+                             beta1, beta2, eps, bias_correction(beta1, t), bias_correction(beta2, t)),
+          "Adam::step");
 }
 
 AdamW::AdamW(const std::vector<TensorPtr>& params, float lr, float beta1, float beta2, float eps, float weight_decay)
@@ -73,13 +97,11 @@ AdamW::AdamW(const std::vector<TensorPtr>& params, float lr, float beta1, float 
 
 void AdamW::step() {
     ++t;
-    const float bc1 = bias_correction(beta1, t), bc2 = bias_correction(beta2, t);
-    for (size_t i = 0; i < params.size(); ++i) {
-        auto& p = params[i];
-        check(wm_adamw_step(p->data.dev_rw(), p->grad.dev(), m[i].dev_rw(), v[i].dev_rw(), numel(p), lr, beta1,
-                            beta2, eps, bc1, bc2, weight_decay),
-              "AdamW::step");
-    }
+    if (params.empty()) return;
+    Lists l = param_lists(params, &m, &v);
+    check(wm_adamw_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(), l.s2.data(), l.n.data(), lr,
+                              beta1, beta2, eps, bias_correction(beta1, t), bias_correction(beta2, t), weight_decay),
+          "AdamW::step");
 }
 
 RMSprop::RMSprop(const std::vector<TensorPtr>& params, float lr, float alpha, float eps, float momentum,
@@ -90,26 +112,44 @@ RMSprop::RMSprop(const std::vector<TensorPtr>& params, float lr, float alpha, fl
 }
 
 void RMSprop::step() {
-    for (size_t i = 0; i < params.size(); ++i) {
-        auto& p = params[i];
-        check(wm_rmsprop_step(p->data.dev_rw(), p->grad.dev(), v[i].dev_rw(),
-                              momentum > 0.0f ? buffer[i].dev_rw() : nullptr, numel(p), lr, alpha, eps, momentum,
-                              weight_decay),
-              "RMSprop::step");
-    }
+    if (params.empty()) return;
+    Lists l = param_lists(params, &v, momentum > 0.0f ? &buffer : nullptr);
+    check(wm_rmsprop_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(),
+                                momentum > 0.0f ? l.s2.data() : nullptr, l.n.data(), lr, alpha, eps, momentum,
+                                weight_decay),
+          "RMSprop::step");
 }
 
 // ---- clipping ---------------------------------------------------------------
 
 namespace {
 
-// Sum of squares of every gradient into a one-element device buffer, in
-// parameter order (get_grad_norm's loop, core/optimizer.cpp:145-153).
+// Every non-empty gradient of the list, for the multi-tensor calls (a
+// parameter whose grad is empty contributes nothing, as in the reference's
+// loops over grad.size()).
+struct GradList {
+    std::vector<float*> g;
+    std::vector<int64_t> n;
+};
+
+GradList grad_list(const std::vector<TensorPtr>& params, bool write) {
+    GradList l;
+    for (const auto& p : params) {
+        if (p->grad.empty()) continue;
+        l.g.push_back(write ? p->grad.dev_rw() : const_cast<float*>(p->grad.dev()));
+        l.n.push_back((int64_t)p->grad.size());
+    }
+    return l;
+}
+
+// get_grad_norm's sum of squares (core/optimizer.cpp:145-153) into a
+// one-element device buffer.
 wm::DeviceVector grad_sumsq(const std::vector<TensorPtr>& params) {
     wm::DeviceVector total(1, 0.0f);
+    GradList l = grad_list(params, false);
     float* t = total.dev_rw();
-    for (const auto& p : params)
-        if (!p->grad.empty()) check(wm_grad_sumsq_accumulate(p->grad.dev(), (int64_t)p->grad.size(), t), "get_grad_norm");
+    if (!l.g.empty())
+        check(wm_grad_sumsq_multi((int)l.g.size(), l.g.data(), l.n.data(), t), "get_grad_norm");
     return total;
 }
 
@@ -124,16 +164,16 @@ float get_grad_norm(const std::vector<TensorPtr>& params) {
 // so clipping never waits for the host.
 void clip_grad_norm_(std::vector<TensorPtr>& params, float max_norm) {
     const wm::DeviceVector total = grad_sumsq(params);
-    for (auto& p : params)
-        if (!p->grad.empty())
-            check(wm_clip_grad_norm_scale(p->grad.dev_rw(), (int64_t)p->grad.size(), total.dev(), max_norm),
-                  "clip_grad_norm_");
+    GradList l = grad_list(params, true);
+    if (!l.g.empty())
+        check(wm_clip_grad_norm_scale_multi((int)l.g.size(), l.g.data(), l.n.data(), total.dev(), max_norm),
+              "clip_grad_norm_");
 }
 
 void clip_grad_value_(std::vector<TensorPtr>& params, float clip_value) {
-    for (auto& p : params)
-        if (!p->grad.empty())
-            check(wm_clip_grad_value(p->grad.dev_rw(), (int64_t)p->grad.size(), clip_value), "clip_grad_value_");
+    GradList l = grad_list(params, true);
+    if (!l.g.empty())
+        check(wm_clip_grad_value_multi((int)l.g.size(), l.g.data(), l.n.data(), clip_value), "clip_grad_value_");
 }
 
 // ---- schedulers (host arithmetic, core/optimizer.cpp:179-259) ----------------

@@ -37,6 +37,10 @@ struct Workspace {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
+// Enqueue a copy of a small host table to device memory on the library
+// stream without synchronising (pinned staging; see wm_runtime.hip).
+int upload_async(void* dev_dst, const void* host_src, size_t bytes);
+
 // Check the launch that was just enqueued.
 int check_launch(const char* what);
 

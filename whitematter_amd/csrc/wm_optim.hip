@@ -257,6 +257,275 @@ __global__ void __launch_bounds__(kBlock) scale_prefix_kernel(float* __restrict_
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < count; i += stride) g[i] = g[i] * s;
 }
 
+// ---------------------------------------------------------------------------
+// Multi-tensor launches: one kernel over every tensor of a parameter list.
+// The list is cut into chunks of kChunk elements (a tensor's last chunk may
+// be shorter); a descriptor table in device memory gives each tensor's
+// arrays, size and first chunk, and each workgroup finds its chunk's tensor
+// by binary search.  One launch per optimizer step instead of one per
+// parameter tensor: a model's many small bias and norm vectors otherwise
+// cost a kernel launch each, longer than their memory traffic.
+// ---------------------------------------------------------------------------
+
+constexpr int64_t kChunk = 65536;  // elements per work item (a multiple of 4)
+
+struct MultiEntry {
+    float* p;          // updated array (params; gradients for clipping / unscaling)
+    const float* g;    // gradient (updates only)
+    float* s1;         // state arrays (may be null)
+    float* s2;
+    int64_t n;
+    int64_t chunk0;    // global index of the tensor's first chunk
+    int vec;           // every array of the tensor is 16-byte aligned
+    int pad;
+};
+
+__device__ __forceinline__ int find_entry(const MultiEntry* tab, int count, int64_t c) {
+    int lo = 0, hi = count - 1;  // largest k with tab[k].chunk0 <= c
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tab[mid].chunk0 <= c) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+template <class U>
+__global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* __restrict__ tab, int count,
+                                                               int64_t chunks, U upd) {
+    constexpr int NS = U::NS;
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const MultiEntry e = tab[find_entry(tab, count, c)];
+        const int64_t start = (c - e.chunk0) * kChunk;
+        const int64_t end = min(e.n, start + kChunk);
+        int64_t tail = start;
+        if (e.vec) {
+            const int64_t end4 = start + ((end - start) & ~int64_t(3));
+            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
+                float4 vp = ld_stream(e.p + i);
+                const float4 vg = ld_stream(e.g + i);
+                float4 v1 = NS > 0 ? ld_stream(e.s1 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                float4 v2 = NS > 1 ? ld_stream(e.s2 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                upd(vp.x, vg.x, v1.x, v2.x);
+                upd(vp.y, vg.y, v1.y, v2.y);
+                upd(vp.z, vg.z, v1.z, v2.z);
+                upd(vp.w, vg.w, v1.w, v2.w);
+                st_stream(e.p + i, vp);
+                if (NS > 0) st_stream(e.s1 + i, v1);
+                if (NS > 1) st_stream(e.s2 + i, v2);
+            }
+            tail = end4;
+        }
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) {
+            float vp = e.p[i];
+            float v1 = NS > 0 ? e.s1[i] : 0.f;
+            float v2 = NS > 1 ? e.s2[i] : 0.f;
+            upd(vp, e.g[i], v1, v2);
+            e.p[i] = vp;
+            if (NS > 0) e.s1[i] = v1;
+            if (NS > 1) e.s2[i] = v2;
+        }
+    }
+}
+
+// In-place per-element maps on the p arrays: kind 0 scales by clip_grad_norm_'s
+// coefficient when it is < 1 (read from *total on the device), kind 1 clips to
+// [-a, a], kind 2 multiplies by a every element before the cutoff (table row
+// cut_tensor, element cut_index) in parameter order.
+__global__ void __launch_bounds__(kBlock) multi_map_kernel(const MultiEntry* __restrict__ tab, int count,
+                                                            int64_t chunks, int kind, const float* __restrict__ total,
+                                                            float a, int cut_tensor, int64_t cut_index) {
+    float coef = 1.0f;
+    if (kind == 0) {
+        coef = a / (sqrtf(*total) + 1e-6f);
+        if (!(coef < 1.0f)) return;
+    }
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const int k = find_entry(tab, count, c);
+        const MultiEntry e = tab[k];
+        const int64_t start = (c - e.chunk0) * kChunk;
+        int64_t end = min(e.n, start + kChunk);
+        if (kind == 2) {
+            if (k > cut_tensor) continue;
+            if (k == cut_tensor) end = min(end, cut_index);
+        }
+        auto map1 = [&](float v) {
+            if (kind == 0) return v * coef;
+            if (kind == 1) return v > a ? a : (v < -a ? -a : v);
+            return v * a;
+        };
+        int64_t tail = start;
+        if (e.vec && end > start) {
+            const int64_t end4 = start + ((end - start) & ~int64_t(3));
+            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
+                float4 v = ld_stream(e.p + i);
+                v.x = map1(v.x); v.y = map1(v.y); v.z = map1(v.z); v.w = map1(v.w);
+                st_stream(e.p + i, v);
+            }
+            tail = end4;
+        }
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) e.p[i] = map1(e.p[i]);
+    }
+}
+
+// part[c] = sum of squares of chunk c.
+__global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* __restrict__ tab, int count,
+                                                              int64_t chunks, float* __restrict__ part) {
+    __shared__ float lds[kBlock / 64];
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const MultiEntry e = tab[find_entry(tab, count, c)];
+        const int64_t start = (c - e.chunk0) * kChunk;
+        const int64_t end = min(e.n, start + kChunk);
+        float s = 0.f;
+        int64_t tail = start;
+        if (e.vec) {
+            const int64_t end4 = start + ((end - start) & ~int64_t(3));
+            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
+                const float4 v = ld_stream(e.p + i);
+                s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            tail = end4;
+        }
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) s += e.p[i] * e.p[i];
+        s = block_sum<kBlock>(s, lds);
+        if (threadIdx.x == 0) part[c] = s;
+        __syncthreads();
+    }
+}
+
+// *total = (accumulate ? *total : 0) + sum(part[0..chunks)), one block, fixed order.
+__global__ void __launch_bounds__(kBlock) multi_sum_finalize_kernel(const float* __restrict__ part, int64_t chunks,
+                                                                     float* __restrict__ total, int accumulate) {
+    __shared__ float lds[kBlock / 64];
+    float s = 0.f;
+    for (int64_t i = threadIdx.x; i < chunks; i += kBlock) s += part[i];
+    s = block_sum<kBlock>(s, lds);
+    if (threadIdx.x == 0) *total = accumulate ? *total + s : s;
+}
+
+// first[c] = smallest in-tensor index of chunk c whose scaled value is not
+// finite, or the tensor's n.
+__global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntry* __restrict__ tab, int count,
+                                                                  int64_t chunks, float scale,
+                                                                  int64_t* __restrict__ first) {
+    __shared__ int64_t lds[kBlock];
+    for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+        const MultiEntry e = tab[find_entry(tab, count, c)];
+        const int64_t start = (c - e.chunk0) * kChunk;
+        const int64_t end = min(e.n, start + kChunk);
+        int64_t f = e.n;
+        int64_t tail = start;
+        if (e.vec) {
+            const int64_t end4 = start + ((end - start) & ~int64_t(3));
+            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
+                const float4 v = ld_stream(e.p + i);
+                const bool b0 = !__builtin_isfinite(v.x * scale), b1 = !__builtin_isfinite(v.y * scale),
+                           b2 = !__builtin_isfinite(v.z * scale), b3 = !__builtin_isfinite(v.w * scale);
+                if (b0 || b1 || b2 || b3) {
+                    f = i + (b0 ? 0 : b1 ? 1 : b2 ? 2 : 3);
+                    break;
+                }
+            }
+            tail = end4;
+        }
+        if (f == e.n)
+            for (int64_t i = tail + threadIdx.x; i < end; i += kBlock)
+                if (!__builtin_isfinite(e.p[i] * scale)) { f = i; break; }
+        lds[threadIdx.x] = f;
+        __syncthreads();
+        for (int w = kBlock / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) first[c] = lds[0];
+        __syncthreads();
+    }
+}
+
+// out[0], out[1] = (entry, index) of the first non-finite position in chunk
+// order (= parameter order), or (count, 0).  One block.
+__global__ void __launch_bounds__(kBlock) multi_first_bad_finalize_kernel(const MultiEntry* __restrict__ tab,
+                                                                           int count, int64_t chunks,
+                                                                           const int64_t* __restrict__ first,
+                                                                           int64_t* __restrict__ out) {
+    __shared__ int64_t lds[kBlock];
+    int64_t best = chunks;  // first chunk holding a non-finite value
+    for (int64_t c = threadIdx.x; c < chunks; c += kBlock) {
+        if (first[c] < tab[find_entry(tab, count, c)].n) { best = c; break; }
+    }
+    lds[threadIdx.x] = best;
+    __syncthreads();
+    for (int w = kBlock / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int64_t c = lds[0];
+        if (c < chunks) {
+            out[0] = find_entry(tab, count, c);
+            out[1] = first[c];
+        } else {
+            out[0] = count;
+            out[1] = 0;
+        }
+    }
+}
+
+// Descriptor table of a parameter list on the device (entries with n == 0 or
+// a null array are dropped; `index` maps table rows back to list positions).
+struct MultiTable {
+    std::vector<MultiEntry> host;
+    std::vector<int> index;
+    int64_t chunks = 0;
+    Workspace* dev = nullptr;
+    ~MultiTable() { delete dev; }
+
+    int build(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
+              const int64_t* n, int ns, const char* what) {
+        for (int k = 0; k < count; ++k) {
+            if (n[k] < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
+            if (n[k] == 0) continue;
+            MultiEntry e{};
+            e.p = p[k];
+            e.g = g ? g[k] : nullptr;
+            e.s1 = ns > 0 && s1 ? s1[k] : nullptr;
+            e.s2 = ns > 1 && s2 ? s2[k] : nullptr;
+            if (!e.p || (g && !e.g) || (ns > 0 && !e.s1) || (ns > 1 && !e.s2))
+                return set_error(WM_ERR_INVALID, std::string(what) + ": null pointer");
+            e.n = n[k];
+            e.chunk0 = chunks;
+            e.vec = aligned16(e.p) && (!e.g || aligned16(e.g)) && (!e.s1 || aligned16(e.s1)) &&
+                    (!e.s2 || aligned16(e.s2));
+            chunks += (n[k] + kChunk - 1) / kChunk;
+            host.push_back(e);
+            index.push_back(k);
+        }
+        if (host.empty()) return WM_OK;
+        dev = new Workspace(host.size() * sizeof(MultiEntry));
+        if (!dev->p) return set_error(WM_ERR_NOMEM, std::string(what) + ": descriptor table");
+        return upload_async(dev->p, host.data(), host.size() * sizeof(MultiEntry));
+    }
+    const MultiEntry* table() const { return dev->as<MultiEntry>(); }
+    int count() const { return (int)host.size(); }
+    unsigned grid() const { return grid_for(chunks, 1, 8); }
+};
+
+template <class U>
+int launch_multi(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
+                 const int64_t* n, const U& upd, const char* what) {
+    if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
+    if (count == 0) return WM_OK;
+    if (!p || !g || !n || (U::NS > 0 && !s1) || (U::NS > 1 && !s2))
+        return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
+    WM_CHECK_INIT();
+    MultiTable t;
+    WM_TRY(t.build(count, p, g, s1, s2, n, U::NS, what));
+    if (t.chunks == 0) return WM_OK;
+    hipLaunchKernelGGL(multi_update_kernel<U>, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                       t.chunks, upd);
+    return check_launch(what);
+}
+
 static int check_n(int64_t n, const char* what) {
     if (n < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
     return WM_OK;
@@ -360,40 +629,109 @@ int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float 
     *found_inf = 0;
     if (count == 0) return WM_OK;
     if (!grads || !sizes) return set_error(WM_ERR_INVALID, "wm_grad_unscale: null pointer");
+    std::vector<float*> gl(grads, grads + count);
+    std::vector<int64_t> nl(sizes, sizes + count);
     for (int k = 0; k < count; ++k)
-        if (sizes[k] < 0) return set_error(WM_ERR_INVALID, "wm_grad_unscale: negative size");
+        if (!gl[k]) nl[k] = 0;  // a missing gradient is skipped like an empty one
     WM_CHECK_INIT();
-    // 1. first non-finite scaled position of every tensor (n when none)
-    Workspace firsts((size_t)count * sizeof(int64_t));
-    Workspace part((size_t)kMaxPart * sizeof(int64_t));
-    if (!firsts.p || !part.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
-    std::vector<int64_t> host(count, 0);
-    for (int k = 0; k < count; ++k) {
-        if (!grads[k] || sizes[k] == 0) continue;
-        const int nb = (int)std::min<int64_t>(grid_for(sizes[k], kBlock, 4), kMaxPart);
-        hipLaunchKernelGGL(first_bad_partial_kernel, dim3(nb), dim3(kBlock), 0, stream(), grads[k], sizes[k],
-                           inv_scale, part.as<int64_t>());
-        WM_TRY(check_launch("wm_grad_unscale(find)"));
-        hipLaunchKernelGGL(first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<int64_t>(), nb,
-                           sizes[k], firsts.as<int64_t>() + k);
-        WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
-    }
-    WM_TRY(wm_d2h(host.data(), firsts.p, (size_t)count * sizeof(int64_t)));
-    // 2. scale every element before the first non-finite one, in order
-    for (int k = 0; k < count; ++k) {
-        if (!grads[k] || sizes[k] == 0) continue;
-        const int64_t upto = host[k];
-        if (upto > 0) {
-            hipLaunchKernelGGL(scale_prefix_kernel, dim3(grid_for(upto, kBlock, 16)), dim3(kBlock), 0, stream(),
-                               grads[k], upto, inv_scale);
-            WM_TRY(check_launch("wm_grad_unscale(scale)"));
-        }
-        if (upto < sizes[k]) {
-            *found_inf = 1;
-            break;
-        }
-    }
+    MultiTable t;
+    WM_TRY(t.build(count, gl.data(), nullptr, nullptr, nullptr, nl.data(), 0, "wm_grad_unscale"));
+    if (t.chunks == 0) return WM_OK;
+    // 1. the first non-finite scaled position in parameter order
+    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
+    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
+    hipLaunchKernelGGL(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                       t.chunks, inv_scale, first.as<int64_t>());
+    WM_TRY(check_launch("wm_grad_unscale(find)"));
+    hipLaunchKernelGGL(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                       t.chunks, first.as<int64_t>(), where.as<int64_t>());
+    WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
+    int64_t cut[2] = {0, 0};
+    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
+    // 2. scale everything before it (everything when there is none)
+    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                       2, nullptr, inv_scale, (int)cut[0], cut[1]);
+    WM_TRY(check_launch("wm_grad_unscale(scale)"));
+    *found_inf = cut[0] < t.count() ? 1 : 0;
     return WM_OK;
+}
+
+// ---- multi-tensor variants ---------------------------------------------------
+
+int wm_sgd_step_multi(int count, float* const* p, const float* const* g, float* const* velocity, const int64_t* n,
+                      float lr, float momentum) {
+    const SgdArgs a{lr, momentum};
+    if (momentum > 0.0f)
+        return launch_multi(count, p, g, velocity, nullptr, n, Upd<0, true, false>{a}, "wm_sgd_step_multi");
+    return launch_multi(count, p, g, nullptr, nullptr, n, Upd<0, false, false>{a}, "wm_sgd_step_multi");
+}
+
+int wm_adam_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
+                       const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
+                       float bias_correction2) {
+    const AdamArgs a{lr, beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bias_correction1, bias_correction2, 0.0f};
+    return launch_multi(count, p, g, m, v, n, Upd<1, false, false>{a}, "wm_adam_step_multi");
+}
+
+int wm_adamw_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
+                        const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
+                        float bias_correction2, float weight_decay) {
+    const AdamArgs a{lr,  beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bias_correction1, bias_correction2,
+                     weight_decay};
+    return launch_multi(count, p, g, m, v, n, Upd<1, true, false>{a}, "wm_adamw_step_multi");
+}
+
+int wm_rmsprop_step_multi(int count, float* const* p, const float* const* g, float* const* v, float* const* buffer,
+                          const int64_t* n, float lr, float alpha, float eps, float momentum, float weight_decay) {
+    const RmsArgs a{lr, alpha, 1.0f - alpha, eps, momentum, weight_decay};
+    const bool mom = momentum > 0.0f, wd = weight_decay != 0.0f;
+    const char* what = "wm_rmsprop_step_multi";
+    if (wd && mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, true, true>{a}, what);
+    if (wd) return launch_multi(count, p, g, v, nullptr, n, Upd<2, true, false>{a}, what);
+    if (mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, false, true>{a}, what);
+    return launch_multi(count, p, g, v, nullptr, n, Upd<2, false, false>{a}, what);
+}
+
+static int multi_grads(int count, const float* const* g, const int64_t* n, MultiTable& t, const char* what) {
+    if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
+    if (count > 0 && (!g || !n)) return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
+    WM_CHECK_INIT();
+    return t.build(count, const_cast<float* const*>(g), nullptr, nullptr, nullptr, n, 0, what);
+}
+
+int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, float* total) {
+    if (!total) return set_error(WM_ERR_INVALID, "wm_grad_sumsq_multi: null total");
+    MultiTable t;
+    WM_TRY(multi_grads(count, g, n, t, "wm_grad_sumsq_multi"));
+    if (t.chunks == 0) return wm_fill(total, 0.0f, 1);
+    Workspace part((size_t)t.chunks * sizeof(float));
+    if (!part.p) return set_error(WM_ERR_NOMEM, "wm_grad_sumsq_multi: workspace");
+    hipLaunchKernelGGL(multi_sumsq_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                       t.chunks, part.as<float>());
+    WM_TRY(check_launch("wm_grad_sumsq_multi"));
+    hipLaunchKernelGGL(multi_sum_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<float>(), t.chunks,
+                       total, 0);
+    return check_launch("wm_grad_sumsq_multi(finalize)");
+}
+
+int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, const float* total_sumsq,
+                                  float max_norm) {
+    if (!total_sumsq) return set_error(WM_ERR_INVALID, "wm_clip_grad_norm_scale_multi: null total");
+    MultiTable t;
+    WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_norm_scale_multi"));
+    if (t.chunks == 0) return WM_OK;
+    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                       0, total_sumsq, max_norm, 0, (int64_t)0);
+    return check_launch("wm_clip_grad_norm_scale_multi");
+}
+
+int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float clip_value) {
+    MultiTable t;
+    WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_value_multi"));
+    if (t.chunks == 0) return WM_OK;
+    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                       1, nullptr, clip_value, 0, (int64_t)0);
+    return check_launch("wm_clip_grad_value_multi");
 }
 
 }  // extern "C"

@@ -8,6 +8,8 @@
 // them back stream-ordered instead.
 #include "wm_common.hpp"
 
+#include <algorithm>
+#include <cstring>
 #include <mutex>
 #include <map>
 #include <unordered_map>
@@ -141,6 +143,46 @@ int check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return set_error(WM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return WM_OK;
+}
+
+// Stream-ordered upload of a small host table (kernel launch descriptors)
+// without waiting for the stream: the bytes go through a pinned staging
+// buffer; before the buffer is rewritten the host waits for the event of the
+// previous upload's copy, which has normally long completed.
+namespace {
+void* g_stage = nullptr;
+size_t g_stage_bytes = 0;
+hipEvent_t g_stage_ev = nullptr;
+bool g_stage_pending = false;
+}  // namespace
+
+int upload_async(void* dev_dst, const void* host_src, size_t bytes) {
+    if (bytes == 0) return WM_OK;
+    WM_CHECK_INIT();
+    std::lock_guard<std::mutex> lk(g_mu);
+    hipError_t e = hipSuccess;
+    if (g_stage_pending) {
+        if ((e = hipEventSynchronize(g_stage_ev)) != hipSuccess)
+            return set_error(WM_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
+        g_stage_pending = false;
+    }
+    if (bytes > g_stage_bytes) {
+        if (g_stage) (void)hipHostFree(g_stage);
+        g_stage = nullptr;
+        g_stage_bytes = 0;
+        const size_t want = std::max<size_t>(bytes, size_t(64) << 10);
+        if ((e = hipHostMalloc(&g_stage, want, hipHostMallocDefault)) != hipSuccess)
+            return set_error(WM_ERR_NOMEM, std::string("upload: pinned staging: ") + hipGetErrorString(e));
+        g_stage_bytes = want;
+    }
+    if (!g_stage_ev && (e = hipEventCreateWithFlags(&g_stage_ev, hipEventDisableTiming)) != hipSuccess)
+        return set_error(WM_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
+    std::memcpy(g_stage, host_src, bytes);
+    if ((e = hipMemcpyAsync(dev_dst, g_stage, bytes, hipMemcpyHostToDevice, g_dev.stream)) != hipSuccess ||
+        (e = hipEventRecord(g_stage_ev, g_dev.stream)) != hipSuccess)
+        return set_error(WM_ERR_HIP, std::string("upload: ") + hipGetErrorString(e));
+    g_stage_pending = true;
     return WM_OK;
 }
 
