@@ -308,7 +308,6 @@ def opt_ops():
                     "each one multi-tensor launch (pair) over the list" % (len(shapes), N), "elements": N}
 
 
-CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops}
 
 
 # ---------------------------------------------------------------------------
@@ -374,6 +373,49 @@ def cpu_baseline_c2(sample_rows=1024, cols=8192, reps=3):
 
 # ---------------------------------------------------------------------------
 
+def loss_ops(rows=8192, cols=32000):
+    """Loss heads on the softmax config's logits: the fused CrossEntropy and
+    Focal heads and NLL, forward and backward (prediction gradient known-zero,
+    as in a training step), and BCEWithLogits over the same elements."""
+    L, _ = synth.config4(rows, cols)
+    lab = np.floor(synth.uniform((rows,), synth.seed_for(6, 0), 0, cols)).clip(0, cols - 1).astype(np.float32)
+    tgt = synth.uniform((rows, cols), synth.seed_for(6, 1), 0, 1)
+    dL, dlab, dt = W.DeviceArray.from_host(L), W.DeviceArray.from_host(lab), W.DeviceArray.from_host(tgt)
+    del L, tgt
+    ce_st, fo_st = W.DeviceArray((rows, W.CE_STATS)), W.DeviceArray((rows, W.FOCAL_STATS))
+    loss = W.DeviceArray((1,))
+    one = W.DeviceArray.from_host(np.float32([1.0]))
+    gx = W.DeviceArray((rows, cols))
+    N = rows * cols
+    big = N * F32
+    g2, am1 = W.C.c_float(2.0), W.C.c_float(-1.0)
+    zero = W.C.c_float(0.0)
+    nf = W.C.c_float(float(N))
+    ops = [
+        Op("CrossEntropy fwd", lambda: W.call("wm_cross_entropy_fwd", dL.vp, dlab.vp, rows, cols, ce_st.vp, loss.vp),
+           big + rows * (F32 + 2 * F32), "head_fwd_kernel", N),
+        Op("CrossEntropy bwd", lambda: W.call("wm_cross_entropy_bwd", dL.vp, dlab.vp, ce_st.vp, one.vp, gx.vp, 0,
+                                              rows, cols),
+           2 * big + rows * (F32 + 2 * F32), "head_bwd_kernel<0", N),
+        Op("Focal fwd", lambda: W.call("wm_focal_fwd", dL.vp, dlab.vp, rows, cols, g2, am1, fo_st.vp, loss.vp),
+           big + rows * (F32 + 8 * F32), "head_fwd_kernel", N),
+        Op("Focal bwd", lambda: W.call("wm_focal_bwd", dL.vp, dlab.vp, fo_st.vp, one.vp, gx.vp, 0, rows, cols, g2,
+                                       am1),
+           2 * big + rows * (F32 + 8 * F32), "head_bwd_kernel<1", N),
+        Op("NLL bwd", lambda: W.call("wm_nll_bwd", dlab.vp, one.vp, gx.vp, 0, rows, cols), big + rows * F32,
+           "head_bwd_kernel<2", N),
+        Op("BCEWithLogits fwd", lambda: W.call("wm_pointwise_loss_fwd", 2, dL.vp, dt.vp, N, zero, zero, nf, loss.vp),
+           2 * big, "pw_fwd_kernel", N),
+        Op("BCEWithLogits bwd", lambda: W.call("wm_pointwise_loss_bwd", 2, dL.vp, dt.vp, N, zero, zero, nf, one.vp,
+                                               gx.vp, 0),
+           3 * big, "pw_bwd_kernel", N),
+    ]
+    return ops, [dL, dlab, dt, ce_st, fo_st, loss, one, gx], {
+        "workload": "loss: logits[%d,%d] fp32 (the c4 recipe) with uniform class labels; fused CrossEntropy and "
+                    "Focal(gamma 2) heads and NLL fwd+bwd (gradient buffer known-zero), BCEWithLogits over the "
+                    "same elements with U[0,1] targets" % (rows, cols), "elements": N}
+
+
 def traffic_for(op_name: str, config: str):
     """HBM bytes per launch of an op's main kernel, from the committed
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json,
@@ -386,6 +428,9 @@ def traffic_for(op_name: str, config: str):
         return d.get(config, {}).get(op_name, {}).get("hbm_bytes")
     except Exception:
         return None
+
+
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops}
 
 
 def main():

@@ -202,6 +202,100 @@ class Oracle:
         return self.L.or_unscale_tensor(_fp(self._f32(g)), g.size, inv_scale)
 
 
+# ---- losses (core/loss.cpp) --------------------------------------------------
+
+LOSS_KINDS = {"smooth_l1": 0, "bce": 1, "bce_logits": 2, "kldiv": 3, "kldiv_log": 4, "binary_focal": 5}
+
+
+def _loss_sigs(o):
+    if getattr(o, "_loss_ready", False):
+        return
+    L, vp, i64, f = o.L, C.c_void_p, C.c_int64, C.c_float
+    L.or_cross_entropy.argtypes = [vp, vp, i64, i64, vp]
+    L.or_cross_entropy_bwd.argtypes = [vp, vp, i64, i64, f, vp]
+    L.or_nll.argtypes = [vp, vp, i64, i64, vp]
+    L.or_nll_bwd.argtypes = [vp, i64, i64, f, vp]
+    L.or_focal.argtypes = [vp, vp, i64, i64, f, f, vp]
+    L.or_focal_bwd.argtypes = [vp, vp, i64, i64, f, f, f, vp]
+    L.or_pointwise_loss.argtypes = [C.c_int, vp, vp, i64, f, f, f, vp]
+    L.or_pointwise_loss_bwd.argtypes = [C.c_int, vp, vp, i64, f, f, f, f, vp]
+    o._loss_ready = True
+
+
+def _f32c(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def _loss_methods():
+    """Loss entry points of an Oracle build: each forward returns the loss as
+    a REAL scalar, each backward a fresh gradient array (the closure's
+    contribution to a zero gradient)."""
+
+    def cross_entropy(self, x, labels):
+        _loss_sigs(self)
+        x, labels = _f32c(x), _f32c(labels)
+        out = np.zeros(1, self.dtype)
+        self.L.or_cross_entropy(_fp(x), _fp(labels), x.shape[0], x.shape[1], _fp(out))
+        return out[0]
+
+    def cross_entropy_bwd(self, x, labels, loss_grad=1.0):
+        _loss_sigs(self)
+        x, labels = _f32c(x), _f32c(labels)
+        gx = np.zeros(x.shape, self.dtype)
+        self.L.or_cross_entropy_bwd(_fp(x), _fp(labels), x.shape[0], x.shape[1], loss_grad, _fp(gx))
+        return gx
+
+    def nll(self, x, labels):
+        _loss_sigs(self)
+        x, labels = _f32c(x), _f32c(labels)
+        out = np.zeros(1, self.dtype)
+        self.L.or_nll(_fp(x), _fp(labels), x.shape[0], x.shape[1], _fp(out))
+        return out[0]
+
+    def nll_bwd(self, shape, labels, loss_grad=1.0):
+        _loss_sigs(self)
+        labels = _f32c(labels)
+        gx = np.zeros(shape, self.dtype)
+        self.L.or_nll_bwd(_fp(labels), shape[0], shape[1], loss_grad, _fp(gx))
+        return gx
+
+    def focal(self, x, labels, gamma=2.0, alpha=-1.0):
+        _loss_sigs(self)
+        x, labels = _f32c(x), _f32c(labels)
+        out = np.zeros(1, self.dtype)
+        self.L.or_focal(_fp(x), _fp(labels), x.shape[0], x.shape[1], gamma, alpha, _fp(out))
+        return out[0]
+
+    def focal_bwd(self, x, labels, gamma=2.0, alpha=-1.0, loss_grad=1.0):
+        _loss_sigs(self)
+        x, labels = _f32c(x), _f32c(labels)
+        gx = np.zeros(x.shape, self.dtype)
+        self.L.or_focal_bwd(_fp(x), _fp(labels), x.shape[0], x.shape[1], gamma, alpha, loss_grad, _fp(gx))
+        return gx
+
+    def pointwise_loss(self, kind, x, y, p0=0.0, p1=0.0, denom=None):
+        _loss_sigs(self)
+        x, y = _f32c(x), _f32c(y)
+        out = np.zeros(1, self.dtype)
+        d = float(x.size) if denom is None else float(denom)
+        self.L.or_pointwise_loss(LOSS_KINDS[kind], _fp(x), _fp(y), x.size, p0, p1, d, _fp(out))
+        return out[0]
+
+    def pointwise_loss_bwd(self, kind, x, y, p0=0.0, p1=0.0, denom=None, loss_grad=1.0):
+        _loss_sigs(self)
+        x, y = _f32c(x), _f32c(y)
+        gx = np.zeros(x.shape, self.dtype)
+        d = float(x.size) if denom is None else float(denom)
+        self.L.or_pointwise_loss_bwd(LOSS_KINDS[kind], _fp(x), _fp(y), x.size, p0, p1, d, loss_grad, _fp(gx))
+        return gx
+
+    return {k: v for k, v in locals().items() if callable(v)}
+
+
+for _name, _fn in _loss_methods().items():
+    setattr(Oracle, _name, _fn)
+
+
 def get(kind: str) -> Oracle:
     if kind not in _libs:
         _libs[kind] = Oracle(kind)
@@ -322,6 +416,8 @@ class Reference:
         L.wmref_clip_grad_value.restype = None
         L.wmref_unscale.argtypes = [C.c_void_p, C.c_int, C.c_float]
         L.wmref_unscale.restype = C.c_int
+        L.wmref_loss.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_float, C.c_float]
+        L.wmref_loss.restype = C.c_void_p
         self.L = L
 
     @staticmethod
@@ -352,6 +448,21 @@ class Reference:
         """GradScaler(scale).unscale(...); returns True when it found inf/NaN."""
         hs, n = self._handles(params)
         return bool(self.L.wmref_unscale(hs, n, scale))
+
+    LOSSES = {"mse": 0, "l1": 1, "smooth_l1": 2, "cross_entropy": 3, "nll": 4, "bce": 5, "bce_logits": 6,
+              "kldiv": 7, "focal": 8, "binary_focal": 9}
+
+    def loss(self, kind, pred, target, p0=0.0, p1=0.0, pred_shape=None, target_shape=None):
+        """Forward and backward of the reference loss class `kind` on fresh
+        tensors: returns (loss value, prediction gradient).  For "kldiv",
+        p0 != 0 selects log_target; for the focal losses p0 = gamma and
+        p1 = alpha; for "smooth_l1" p0 = beta."""
+        tp = self.tensor(pred, True, pred_shape)
+        tt = self.tensor(target, False, target_shape)
+        tl = RefTensor(self.L, self.L.wmref_loss(self.LOSSES[kind], tp.h, tt.h, p0, p1))
+        value = np.float32(tl.data()[0])
+        tl.backward()
+        return value, tp.grad()
 
     def tensor(self, data, requires_grad=False, shape: Optional[Sequence[int]] = None) -> RefTensor:
         data = np.ascontiguousarray(data, np.float32)

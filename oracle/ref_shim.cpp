@@ -17,6 +17,9 @@
 #include "tensor.h"
 #include "amp.h"
 #include "optimizer.h"
+#include "loss.h"
+
+#include <memory>
 
 namespace {
 
@@ -239,6 +242,29 @@ int wmref_unscale(void** params, int np, float scale) {
     SGD opt(param_list(params, np), 0.1f);
     GradScaler scaler(scale);
     return scaler.unscale(&opt) ? 0 : 1;
+}
+
+// Loss forward through the reference's loss classes (core/loss.h:6-74):
+// 0 MSE, 1 L1, 2 SmoothL1(beta = p0), 3 CrossEntropy, 4 NLL, 5 BCE,
+// 6 BCEWithLogits, 7 KLDiv(log_target = p0 != 0), 8 Focal(gamma = p0,
+// alpha = p1), 9 BinaryFocal(gamma = p0, alpha = p1).  Returns the loss
+// tensor; wmref_backward on it runs the closures.
+void* wmref_loss(int kind, void* pred, void* target, float p0, float p1) {
+    RefFpMode fp_mode_;
+    std::unique_ptr<LossFunction> l;
+    switch (kind) {
+        case 0: l.reset(new MSELoss()); break;
+        case 1: l.reset(new L1Loss()); break;
+        case 2: l.reset(new SmoothL1Loss(p0)); break;
+        case 3: l.reset(new CrossEntropyLoss()); break;
+        case 4: l.reset(new NLLLoss()); break;
+        case 5: l.reset(new BCELoss()); break;
+        case 6: l.reset(new BCEWithLogitsLoss()); break;
+        case 7: l.reset(new KLDivLoss(p0 != 0.0f)); break;
+        case 8: l.reset(new FocalLoss(p0, p1)); break;
+        default: l.reset(new BinaryFocalLoss(p0, p1)); break;
+    }
+    return box(l->forward(T(pred), T(target)));
 }
 
 }  // extern "C"

@@ -557,3 +557,260 @@ int64_t or_unscale_tensor(float* g, int64_t n, float inv_scale) {
     }
     return n;
 }
+
+/* ---- losses: core/loss.cpp ------------------------------------------------
+ * Every function returns the loss through *loss (REAL) and accumulates the
+ * prediction's gradient into gx (+=, caller-initialised), given the value of
+ * the loss tensor's grad[0] (loss_grad) that the closure reads.
+ *
+ * Labels: the reference reads static_cast<size_t>(target->data[i])
+ * (loss.cpp:80); a value that does not truncate to a class in [0, classes)
+ * is an out-of-bounds access there.  Here such a row's loss term is NaN and
+ * its gradient row NaN (cross entropy, focal) or untouched (NLL): the
+ * behaviour the device heads define for it. */
+
+static int64_t or_label(float t, int64_t classes) {
+    if (!(t > -1.0f) || !(t < 9.0e18f)) return -1;
+    int64_t c = (int64_t)t;
+    return c < classes ? c : -1;
+}
+
+/* std::max / std::min on floats: (a < b) ? b : a and (b < a) ? b : a. */
+static REAL or_std_max(REAL a, REAL b) { return a < b ? b : a; }
+static REAL or_std_min(REAL a, REAL b) { return b < a ? b : a; }
+
+#ifdef OR_ABS
+#define PLUS(x, y) (MAG(x) + MAG(y))
+#else
+#define PLUS(x, y) ((x) + (y))
+#endif
+
+/* Row max and log(sum exp(x - max)) of log_softmax, core/tensor.cpp:1601-1612. */
+static REAL or_row_log_sum(const float* xr, int64_t cols) {
+    float m = xr[0];
+    for (int64_t j = 1; j < cols; j++) m = (m < xr[j]) ? xr[j] : m;
+    REAL s = 0;
+    for (int64_t j = 0; j < cols; j++) s += (REAL)exp((REAL)xr[j] - (REAL)m);
+    return (REAL)m + (REAL)log(s);
+}
+
+/* CrossEntropyLoss::forward, loss.cpp:67-84: log_probs = log_softmax(x)
+ * (:74), result -= log_probs[i, label] over the batch, result /= batch. */
+int or_cross_entropy(const float* x, const float* labels, int64_t rows, int64_t cols, REAL* loss) {
+    OR_FP_SCOPE;
+    REAL res = 0;
+    for (int64_t r = 0; r < rows; r++) {
+        int64_t lab = or_label(labels[r], cols);
+        REAL lp = lab >= 0 ? MINUS((REAL)x[r * cols + lab], or_row_log_sum(x + r * cols, cols)) : (REAL)NAN;
+        ACC(res, -lp);
+    }
+    *loss = res / (REAL)(float)rows;
+    return 0;
+}
+
+/* Its backward: the closure at loss.cpp:87-93 (log_probs->grad[label] -=
+ * scale, scale = grad / batch) followed by log_softmax's closure
+ * (core/tensor.cpp:1621-1632) on that gradient. */
+int or_cross_entropy_bwd(const float* x, const float* labels, int64_t rows, int64_t cols, float loss_grad, REAL* gx) {
+    OR_FP_SCOPE;
+    REAL scale = (REAL)loss_grad / (REAL)(float)rows;
+    for (int64_t r = 0; r < rows; r++) {
+        const float* xr = x + r * cols;
+        int64_t lab = or_label(labels[r], cols);
+        REAL log_sum = or_row_log_sum(xr, cols);
+        REAL gl = (REAL)0 - scale;            /* log_probs->grad[label], from 0 */
+        REAL gs = lab >= 0 ? gl : (REAL)NAN;  /* the row's gradient sum */
+        for (int64_t j = 0; j < cols; j++) {
+            REAL lp = (REAL)xr[j] - log_sum;  /* log_probs[j] */
+            REAL sm = (REAL)exp(lp);
+            REAL g = (j == lab) ? gl : (REAL)0;
+            ACC(gx[r * cols + j], MINUS(g, sm * gs));
+        }
+    }
+    return 0;
+}
+
+/* NLLLoss::forward, loss.cpp:99-115. */
+int or_nll(const float* pred, const float* labels, int64_t rows, int64_t cols, REAL* loss) {
+    OR_FP_SCOPE;
+    REAL res = 0;
+    for (int64_t r = 0; r < rows; r++) {
+        int64_t lab = or_label(labels[r], cols);
+        ACC(res, -(lab >= 0 ? (REAL)pred[r * cols + lab] : (REAL)NAN));
+    }
+    *loss = res / (REAL)(float)rows;
+    return 0;
+}
+
+/* NLLLoss's closure, loss.cpp:118-124: grad[i, label] -= grad / batch. */
+int or_nll_bwd(const float* labels, int64_t rows, int64_t cols, float loss_grad, REAL* gx) {
+    OR_FP_SCOPE;
+    REAL scale = (REAL)loss_grad / (REAL)(float)rows;
+    for (int64_t r = 0; r < rows; r++) {
+        int64_t lab = or_label(labels[r], cols);
+        if (lab >= 0) ACC(gx[r * cols + lab], -scale);
+    }
+    return 0;
+}
+
+/* softmax of one row as core/tensor.cpp:1556-1572 computes it. */
+static void or_row_softmax(const float* xr, int64_t cols, REAL* p) {
+    float m = xr[0];
+    for (int64_t j = 1; j < cols; j++) m = (m < xr[j]) ? xr[j] : m;
+    REAL s = 0;
+    for (int64_t j = 0; j < cols; j++) {
+        p[j] = (REAL)exp((REAL)xr[j] - (REAL)m);
+        s += p[j];
+    }
+    REAL inv = (REAL)1 / s;
+    for (int64_t j = 0; j < cols; j++) p[j] *= inv;
+}
+
+/* FocalLoss::forward, loss.cpp:260-294. */
+int or_focal(const float* x, const float* labels, int64_t rows, int64_t cols, float gamma, float alpha, REAL* loss) {
+    OR_FP_SCOPE;
+    REAL* p = (REAL*)malloc(sizeof(REAL) * (size_t)(cols > 0 ? cols : 1));
+    if (!p) return 1;
+    const REAL eps = (REAL)1e-7f;
+    REAL res = 0;
+    for (int64_t r = 0; r < rows; r++) {
+        int64_t lab = or_label(labels[r], cols);
+        or_row_softmax(x + r * cols, cols, p);
+        REAL pt = or_std_max(lab >= 0 ? p[lab] : (REAL)NAN, eps);
+        REAL fw = (REAL)pow((REAL)1 - pt, (REAL)gamma);
+        REAL li = -fw * (REAL)log(pt);
+        if (alpha >= 0) li *= (REAL)alpha;
+        ACC(res, li);
+    }
+    free(p);
+    *loss = res / (REAL)(float)rows;
+    return 0;
+}
+
+/* FocalLoss's closure, loss.cpp:296-328, over every class of every row. */
+int or_focal_bwd(const float* x, const float* labels, int64_t rows, int64_t cols, float gamma, float alpha,
+                 float loss_grad, REAL* gx) {
+    OR_FP_SCOPE;
+    REAL* p = (REAL*)malloc(sizeof(REAL) * (size_t)(cols > 0 ? cols : 1));
+    if (!p) return 1;
+    const REAL eps = (REAL)1e-7f, gm = (REAL)gamma;
+    REAL scale = (REAL)loss_grad / (REAL)(float)rows;
+    for (int64_t r = 0; r < rows; r++) {
+        int64_t lab = or_label(labels[r], cols);
+        or_row_softmax(x + r * cols, cols, p);
+        REAL pt = or_std_max(lab >= 0 ? p[lab] : (REAL)NAN, eps);
+        REAL q = (REAL)1 - pt;
+        for (int64_t c = 0; c < cols; c++) {
+            REAL pc = lab >= 0 ? p[c] : (REAL)NAN;
+            REAL gv;
+            if (c == lab) {
+                REAL term1 = gm * (REAL)log(pt) * (REAL)pow(q, gm);
+                REAL term2 = -(REAL)pow(q, gm);
+                gv = PLUS(pc * PLUS(term1, term2), (REAL)pow(q, gm));
+            } else {
+                REAL ft = (REAL)pow(q, gm - (REAL)1);
+                gv = -pc * (ft * PLUS(gm * pt * (REAL)log(pt), q));
+            }
+            if (alpha >= 0) gv *= (REAL)alpha;
+            ACC(gx[r * cols + c], scale * gv);
+        }
+    }
+    free(p);
+    return 0;
+}
+
+/* The element-wise losses: one term per element (the quantity the loop adds
+ * to the result; a subtracted one negated) and one gradient increment.
+ * kind: 0 SmoothL1 (p0 = beta), 1 BCE, 2 BCEWithLogits, 3 KLDiv,
+ * 4 KLDiv with log_target, 5 BinaryFocal (p0 = gamma, p1 = alpha). */
+static REAL or_pw_term(int kind, float xf, float yf, float p0, float p1) {
+    const REAL x = xf, y = yf, one = 1;
+    const REAL eps = (REAL)1e-7f, hi = (REAL)(1.0f - 1e-7f);
+    switch (kind) {
+        case 0: { /* loss.cpp:29-38 */
+            REAL ad = x - y, b = p0;
+            if (ad < 0) ad = -ad;
+            REAL d = MINUS(x, y); /* |x| + |y| in the magnitude build */
+            return ad < b ? (REAL)0.5f * d * d / b : MINUS(ad, (REAL)0.5f * b);
+        }
+        case 1: { /* :140-144 */
+            REAL p = or_std_max(or_std_min(x, hi), eps);
+            return -PLUS(y * (REAL)log(p), (one - y) * (REAL)log(one - p));
+        }
+        case 2: /* :175-181 */
+            return PLUS(MINUS(or_std_max(x, 0), x * y), (REAL)log(one + (REAL)exp(-fabs((double)x))));
+        case 3: /* :228-233 */
+            return y > 0 ? y * MINUS((REAL)log(y), x) : (REAL)0;
+        case 4: { /* :218-226 */
+            REAL t = (REAL)exp(y);
+            return t > 0 ? t * MINUS(y, x) : (REAL)0;
+        }
+        default: { /* :344-364 */
+            REAL p = one / (one + (REAL)exp(-x));
+            p = or_std_max(or_std_min(p, hi), eps);
+            REAL pt = y * p + (one - y) * (one - p);
+            REAL fw = (REAL)pow(one - pt, (REAL)p0);
+            REAL at = p1 >= 0 ? y * (REAL)p1 + (one - y) * (one - (REAL)p1) : one;
+            return -(at * fw * (REAL)log(pt));
+        }
+    }
+}
+
+static REAL or_pw_grad(int kind, float xf, float yf, float p0, float p1, REAL scale) {
+    const REAL x = xf, y = yf, one = 1;
+    const REAL eps = (REAL)1e-7f, hi = (REAL)(1.0f - 1e-7f);
+    switch (kind) {
+        case 0: { /* :49-61 */
+            REAL d = x - y, b = p0;
+            REAL ad = d < 0 ? -d : d;
+            return ad < b ? scale * d / b : scale * (d > 0 ? one : -one);
+        }
+        case 1: { /* :153-159 */
+            REAL p = or_std_max(or_std_min(x, hi), eps);
+            return scale * PLUS(-y / p, (one - y) / (one - p));
+        }
+        case 2: { /* :190-197 */
+            REAL s = one / (one + (REAL)exp(-x));
+            return scale * MINUS(s, y);
+        }
+        case 3: /* :244-253 */
+            return scale * (-y);
+        case 4:
+            return scale * (-(REAL)exp(y));
+        default: { /* :375-414 */
+            REAL p = one / (one + (REAL)exp(-x));
+            p = or_std_max(or_std_min(p, hi), eps);
+            REAL pt = y * p + (one - y) * (one - p);
+            REAL q = one - pt;
+            REAL at = p1 >= 0 ? y * (REAL)p1 + (one - y) * (one - (REAL)p1) : one;
+            REAL dpt = ((REAL)2 * y - one) * (p * (one - p));
+            REAL fg;
+            if (p0 == 0) {
+                fg = -at / pt * dpt;
+            } else {
+                REAL br = PLUS(q / pt, -(REAL)p0 * (REAL)log(pt));
+                fg = -at * dpt * (REAL)pow(q, (REAL)p0 - one) * br;
+            }
+            return scale * fg;
+        }
+    }
+}
+
+/* The loop over the elements and the final division (by n, or by the batch
+ * size for the KL divergence): loss.cpp:29-39 and the matching lines of each
+ * loss. */
+int or_pointwise_loss(int kind, const float* x, const float* y, int64_t n, float p0, float p1, float denom, REAL* loss) {
+    OR_FP_SCOPE;
+    REAL res = 0;
+    for (int64_t i = 0; i < n; i++) ACC(res, or_pw_term(kind, x[i], y[i], p0, p1));
+    *loss = res / (REAL)denom;
+    return 0;
+}
+
+int or_pointwise_loss_bwd(int kind, const float* x, const float* y, int64_t n, float p0, float p1, float denom,
+                          float loss_grad, REAL* gx) {
+    OR_FP_SCOPE;
+    REAL scale = (REAL)loss_grad / (REAL)denom;
+    for (int64_t i = 0; i < n; i++) ACC(gx[i], or_pw_grad(kind, x[i], y[i], p0, p1, scale));
+    return 0;
+}

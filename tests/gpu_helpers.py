@@ -1,5 +1,7 @@
 """Helpers shared by the GPU parity tests: run one op through the C ABI and
 return host arrays."""
+import ctypes as C
+
 import numpy as np
 
 from whitematter_amd import _lib as W
@@ -82,3 +84,112 @@ def softmax_bwd(g, out, gx0=None, log=False):
     W.call("wm_log_softmax_bwd" if log else "wm_softmax_bwd", dg.vp, dout.vp, dgx.vp,
            int(gx0 is not None), g.shape[0], g.shape[1])
     return dgx.to_host()
+
+
+# ---- loss heads (include/wm_loss.h) -------------------------------------------
+
+def _scalar_dev(v):
+    return dev(np.float32([v]))
+
+
+def _grad_buffer(shape, g0):
+    """Gradient buffer: g0 for the accumulate mode, else NaN-filled (a
+    known-zero buffer that the kernel must overwrite without reading)."""
+    if g0 is not None:
+        return dev(g0), 1
+    d = W.DeviceArray(shape)
+    d.fill(np.nan)
+    return d, 0
+
+
+def ce_fwd(x, lab):
+    """-> (loss, stats [rows, 2]) through wm_cross_entropy_fwd."""
+    rows, cols = x.shape
+    dx, dl = dev(x), dev(lab)
+    stats, loss = W.DeviceArray((max(rows, 1), W.CE_STATS)), W.DeviceArray((1,))
+    W.call("wm_cross_entropy_fwd", dx.vp, dl.vp, rows, cols, stats.vp, loss.vp)
+    return loss.to_host()[0], stats.to_host()[:rows]
+
+
+def ce_bwd(x, lab, loss_grad=1.0, g0=None):
+    rows, cols = x.shape
+    dx, dl = dev(x), dev(lab)
+    stats, loss = W.DeviceArray((max(rows, 1), W.CE_STATS)), W.DeviceArray((1,))
+    W.call("wm_cross_entropy_fwd", dx.vp, dl.vp, rows, cols, stats.vp, loss.vp)
+    gx, acc = _grad_buffer(x.shape, g0)
+    lg = _scalar_dev(loss_grad)  # referenced until the call returns
+    W.call("wm_cross_entropy_bwd", dx.vp, dl.vp, stats.vp, lg.vp, gx.vp, acc, rows, cols)
+    return gx.to_host()
+
+
+def nll_fwd(x, lab):
+    rows, cols = x.shape
+    dx, dl, loss = dev(x), dev(lab), W.DeviceArray((1,))
+    W.call("wm_nll_fwd", dx.vp, dl.vp, rows, cols, loss.vp)
+    return loss.to_host()[0]
+
+
+def nll_bwd(shape, lab, loss_grad=1.0, g0=None):
+    dl = dev(lab)
+    gx, acc = _grad_buffer(shape, g0)
+    lg = _scalar_dev(loss_grad)
+    W.call("wm_nll_bwd", dl.vp, lg.vp, gx.vp, acc, shape[0], shape[1])
+    return gx.to_host()
+
+
+def focal_fwd(x, lab, gamma, alpha):
+    rows, cols = x.shape
+    dx, dl = dev(x), dev(lab)
+    stats, loss = W.DeviceArray((max(rows, 1), W.FOCAL_STATS)), W.DeviceArray((1,))
+    W.call("wm_focal_fwd", dx.vp, dl.vp, rows, cols, C.c_float(gamma), C.c_float(alpha), stats.vp, loss.vp)
+    return loss.to_host()[0], stats.to_host()[:rows]
+
+
+def focal_bwd(x, lab, gamma, alpha, loss_grad=1.0, g0=None):
+    rows, cols = x.shape
+    dx, dl = dev(x), dev(lab)
+    stats, loss = W.DeviceArray((max(rows, 1), W.FOCAL_STATS)), W.DeviceArray((1,))
+    W.call("wm_focal_fwd", dx.vp, dl.vp, rows, cols, C.c_float(gamma), C.c_float(alpha), stats.vp, loss.vp)
+    gx, acc = _grad_buffer(x.shape, g0)
+    lg = _scalar_dev(loss_grad)
+    W.call("wm_focal_bwd", dx.vp, dl.vp, stats.vp, lg.vp, gx.vp, acc, rows, cols,
+           C.c_float(gamma), C.c_float(alpha))
+    return gx.to_host()
+
+
+POINTWISE_KIND = {"smooth_l1": 0, "bce": 1, "bce_logits": 2, "kldiv": 3, "kldiv_log": 4, "binary_focal": 5}
+
+
+def _offset_dev(a, offset):
+    """a on the device starting `offset` floats into its allocation (offset 1
+    gives a pointer that is not 16-byte aligned, the kernels' scalar path)."""
+    buf = np.zeros(a.size + offset, np.float32)
+    buf[offset:] = a.ravel()
+    d = dev(buf)
+    return d, C.c_void_p(d.ptr + 4 * offset)
+
+
+def pw_fwd(kind, x, y, p0=0.0, p1=0.0, denom=None, offset=0):
+    dxa, dx = _offset_dev(x, offset)
+    dya, dy = _offset_dev(y, offset)
+    loss = W.DeviceArray((1,))
+    d = float(x.size if denom is None else denom)
+    W.call("wm_pointwise_loss_fwd", POINTWISE_KIND[kind], dx, dy, x.size, C.c_float(p0), C.c_float(p1),
+           C.c_float(d), loss.vp)
+    return loss.to_host()[0]
+
+
+def pw_bwd(kind, x, y, p0=0.0, p1=0.0, denom=None, loss_grad=1.0, g0=None, offset=0):
+    dxa, dx = _offset_dev(x, offset)
+    dya, dy = _offset_dev(y, offset)
+    if g0 is not None:
+        dga, dg = _offset_dev(g0, offset)
+        acc = 1
+    else:
+        dga, dg = _offset_dev(np.full(x.size, np.nan, np.float32), offset)
+        acc = 0
+    d = float(x.size if denom is None else denom)
+    lg = _scalar_dev(loss_grad)
+    W.call("wm_pointwise_loss_bwd", POINTWISE_KIND[kind], dx, dy, x.size, C.c_float(p0), C.c_float(p1),
+           C.c_float(d), lg.vp, dg, acc)
+    return dga.to_host()[offset:].reshape(x.shape)

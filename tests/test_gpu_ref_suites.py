@@ -60,3 +60,18 @@ def test_reference_optimizer_suite_against_drop_in_optimizers():
         assert name in passed, (name, out[-2000:])
     for name, msg in failed.items():
         assert "not part of the MI355X" in msg, (name, msg)
+
+
+LOSS_BIN = os.path.join(ROOT, "oracle", "_ref", "run_ref_loss")
+
+
+@pytest.mark.skipif(not os.path.exists(LOSS_BIN), reason="oracle/_ref/run_ref_loss not built")
+def test_reference_loss_suite_against_drop_in_losses():
+    """tests/test_loss.cpp against the drop-in losses: every test passes."""
+    r = subprocess.run([LOSS_BIN], capture_output=True, text=True, timeout=300)
+    out = r.stdout + r.stderr
+    passed = set(re.findall(r"\[PASS\] (\S+)", out))
+    failed = dict(re.findall(r"\[FAIL\] (\S+)[^\n]*\n\s*(.*)", out))
+    print(out[-3000:])
+    assert not failed, failed
+    assert len(passed) >= 22, out[-2000:]

@@ -84,7 +84,20 @@ _SIGS = {
     "wm_grad_sumsq_multi": [C.c_int, _vp, _vp, _vp],
     "wm_clip_grad_norm_scale_multi": [C.c_int, _vp, _vp, _vp, C.c_float],
     "wm_clip_grad_value_multi": [C.c_int, _vp, _vp, C.c_float],
+    # include/wm_loss.h
+    "wm_cross_entropy_fwd": [_vp, _vp, C.c_int64, C.c_int64, _vp, _vp],
+    "wm_cross_entropy_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int64],
+    "wm_nll_fwd": [_vp, _vp, C.c_int64, C.c_int64, _vp],
+    "wm_nll_bwd": [_vp, _vp, _vp, C.c_int, C.c_int64, C.c_int64],
+    "wm_focal_fwd": [_vp, _vp, C.c_int64, C.c_int64, C.c_float, C.c_float, _vp, _vp],
+    "wm_focal_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int64, C.c_float, C.c_float],
+    "wm_pointwise_loss_fwd": [C.c_int, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, _vp],
+    "wm_pointwise_loss_bwd": [C.c_int, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, _vp, _vp, C.c_int],
 }
+
+# enum wm_pointwise_loss
+L_SMOOTH_L1, L_BCE, L_BCE_LOGITS, L_KLDIV, L_KLDIV_LOG, L_BINARY_FOCAL = range(6)
+CE_STATS, FOCAL_STATS = 2, 8
 
 
 def ptr_array(ptrs):

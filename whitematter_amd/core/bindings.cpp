@@ -11,6 +11,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include "loss.h"
 #include "optimizer.h"
 #include "tensor.h"
 #include "wm_hip.h"
@@ -170,4 +171,28 @@ PYBIND11_MODULE(_tensor, m) {
     m.def("clip_grad_norm_", [](std::vector<TensorPtr> ps, float max_norm) { clip_grad_norm_(ps, max_norm); });
     m.def("clip_grad_value_", [](std::vector<TensorPtr> ps, float c) { clip_grad_value_(ps, c); });
     m.def("get_grad_norm", &get_grad_norm);
+
+    py::class_<LossFunction>(m, "LossFunction")
+        .def("forward", &LossFunction::forward)
+        .def("__call__", [](LossFunction& l, const TensorPtr& p, const TensorPtr& t) { return l(p, t); });
+    py::class_<MSELoss, LossFunction>(m, "MSELoss").def(py::init<>());
+    py::class_<L1Loss, LossFunction>(m, "L1Loss").def(py::init<>());
+    py::class_<SmoothL1Loss, LossFunction>(m, "SmoothL1Loss")
+        .def(py::init<float>(), py::arg("beta") = 1.0f)
+        .def_readwrite("beta", &SmoothL1Loss::beta);
+    py::class_<CrossEntropyLoss, LossFunction>(m, "CrossEntropyLoss").def(py::init<>());
+    py::class_<NLLLoss, LossFunction>(m, "NLLLoss").def(py::init<>());
+    py::class_<BCELoss, LossFunction>(m, "BCELoss").def(py::init<>());
+    py::class_<BCEWithLogitsLoss, LossFunction>(m, "BCEWithLogitsLoss").def(py::init<>());
+    py::class_<KLDivLoss, LossFunction>(m, "KLDivLoss")
+        .def(py::init<bool>(), py::arg("log_target") = false)
+        .def_readwrite("log_target", &KLDivLoss::log_target);
+    py::class_<FocalLoss, LossFunction>(m, "FocalLoss")
+        .def(py::init<float, float>(), py::arg("gamma") = 2.0f, py::arg("alpha") = -1.0f)
+        .def_readwrite("gamma", &FocalLoss::gamma)
+        .def_readwrite("alpha", &FocalLoss::alpha);
+    py::class_<BinaryFocalLoss, LossFunction>(m, "BinaryFocalLoss")
+        .def(py::init<float, float>(), py::arg("gamma") = 2.0f, py::arg("alpha") = 0.25f)
+        .def_readwrite("gamma", &BinaryFocalLoss::gamma)
+        .def_readwrite("alpha", &BinaryFocalLoss::alpha);
 }

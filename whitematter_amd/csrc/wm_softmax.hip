@@ -11,116 +11,19 @@
 //   dx_j += y_j * (g_j - sum_k g_k y_k)
 // which is that Jacobian contracted with g.  Rows longer than the register
 // tile stream through three passes instead.
-#include "wm_common.hpp"
+#include "wm_rows.hpp"
 
 #include <algorithm>
 
 namespace wm {
 
-template <int NT>
-__device__ __forceinline__ float block_max(float v, float* lds) {
-    constexpr int NW = NT / 64;
-    v = wave_max(v);
-    if (NW == 1) return v;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = lds[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) m = fmaxf(m, lds[i]);
-    return m;
-}
-
-// Registers of one thread: ITEMS float4 slots.  Element e of slot t lives at
-// column (t * NT + tid) * 4 + e (VEC) or t * NT * 4 + e * NT + tid (scalar),
-// so each load instruction of a wave is contiguous either way.
-template <int NT, int ITEMS, bool VEC>
-struct RowTile {
-    float v[ITEMS][4];
-
-    __device__ __forceinline__ static int64_t col(int t, int e) {
-        return VEC ? ((int64_t)(t * NT + (int)threadIdx.x) * 4 + e) : ((int64_t)t * NT * 4 + (int64_t)e * NT + threadIdx.x);
-    }
-
-    __device__ __forceinline__ void load(const float* row, int64_t cols, float fill) {
-#pragma unroll
-        for (int t = 0; t < ITEMS; ++t) {
-            if constexpr (VEC) {
-                int64_t c = col(t, 0);
-                if (c < cols) {
-                    float4 q = ld_stream(row + c);
-                    v[t][0] = q.x; v[t][1] = q.y; v[t][2] = q.z; v[t][3] = q.w;
-                } else {
-                    v[t][0] = v[t][1] = v[t][2] = v[t][3] = fill;
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    int64_t c = col(t, e);
-                    v[t][e] = c < cols ? ld_stream1(row + c) : fill;
-                }
-            }
-        }
-    }
-
-    __device__ __forceinline__ void store(float* row, int64_t cols) const {
-#pragma unroll
-        for (int t = 0; t < ITEMS; ++t) {
-            if constexpr (VEC) {
-                int64_t c = col(t, 0);
-                if (c < cols) st_stream(row + c, make_float4(v[t][0], v[t][1], v[t][2], v[t][3]));
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    int64_t c = col(t, e);
-                    if (c < cols) st_stream1(row + c, v[t][e]);
-                }
-            }
-        }
-    }
-};
-
-// One-barrier block reductions for the forward kernel, which gives the max
-// and the sum separate LDS arrays: a thread can only write a row's partial to
-// one array after every thread has passed the barrier of the other array's
-// reduction for that row, i.e. after all reads of the previous row's values.
-template <int NT>
-__device__ __forceinline__ float block_max_1(float v, float* lds) {
-    constexpr int NW = NT / 64;
-    v = wave_max(v);
-    if (NW == 1) return v;
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = lds[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) m = fmaxf(m, lds[i]);
-    return m;
-}
-
-template <int NT>
-__device__ __forceinline__ float block_sum_1(float v, float* lds) {
-    constexpr int NW = NT / 64;
-    v = wave_sum(v);
-    if (NW == 1) return v;
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) t += lds[i];
-    return t;
-}
-
-// LOG = false: softmax, true: log_softmax.
-// Each thread first takes the max m_t of its own slots and the sum
-// s_t = sum exp(x - m_t) (keeping exp(x - m_t) for softmax), so the
-// exponentials are computed while the rest of the workgroup's loads are
-// still arriving; the row max M and the sum S = sum_t s_t exp(m_t - M) then
-// take one barrier each.  softmax writes exp(x - m_t) * exp(m_t - M) / S and
-// log_softmax x - (M + log S): the reference's x - max, exp, sum and scale
-// (core/tensor.cpp:1548-1591, :1593-1635) regrouped, within a few ulp.
-// Padding slots hold -inf and contribute exp(-inf) = 0.  A thread whose slots
-// are all -inf uses 0 in place of m_t and contributes nothing.  NaN and
-// infinite inputs turn the whole row to NaN, as in the reference.
+// LOG = false: softmax, true: log_softmax.  row_max_sum (wm_rows.hpp) gives
+// the row max M, the sum S = sum exp(x - M) (regrouped per thread) and each
+// thread's exp(x - m_t) for softmax; softmax writes exp(x - m_t) *
+// exp(m_t - M) / S and log_softmax x - (M + log S): the reference's x - max,
+// exp, sum and scale (core/tensor.cpp:1548-1591, :1593-1635) regrouped,
+// within a few ulp.  NaN and infinite inputs turn the whole row to NaN, as in
+// the reference.
 template <int NT, int ITEMS, bool VEC, bool LOG>
 __global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
                                                           int64_t rows, int64_t cols) {
@@ -128,32 +31,15 @@ __global__ void __launch_bounds__(NT) softmax_fwd_kernel(float* __restrict__ out
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         RowTile<NT, ITEMS, VEC> tile;
         tile.load(x + r * cols, cols, -INFINITY);
-        float mt = -INFINITY;
-#pragma unroll
-        for (int t = 0; t < ITEMS; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) mt = fmaxf(mt, tile.v[t][e]);
-        const float base = mt == -INFINITY ? 0.f : mt;
-        float st = 0.f;
-#pragma unroll
-        for (int t = 0; t < ITEMS; ++t)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float ex = exp_rr(tile.v[t][e] - base);
-                st += ex;
-                if (!LOG) tile.v[t][e] = ex;
-            }
-        const float m = block_max_1<NT>(mt, lds_m);
-        const float ct = mt == -INFINITY ? 0.f : exp_rr(mt - m);
-        const float s = block_sum_1<NT>(st * ct, lds_s);
+        const RowMaxSum ms = row_max_sum<NT, ITEMS, VEC, !LOG>(tile, lds_m, lds_s);
         if (LOG) {
-            const float log_sum = m + logf(s);
+            const float log_sum = ms.m + logf(ms.s);
 #pragma unroll
             for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) tile.v[t][e] = tile.v[t][e] - log_sum;
         } else {
-            const float k = ct * (1.0f / s);
+            const float k = ms.ct * (1.0f / ms.s);
 #pragma unroll
             for (int t = 0; t < ITEMS; ++t)
 #pragma unroll
@@ -269,23 +155,6 @@ __global__ void __launch_bounds__(1024) softmax_bwd_long_kernel(const float* __r
 // ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
-
-// Pick the register tile: NT = 64 for rows up to 2048 columns, else 1024;
-// ITEMS the smallest power of two (<= 8) covering the row.
-struct TileChoice {
-    int nt = 0, items = 0;  // nt == 0: long-row path
-};
-
-static TileChoice choose_tile(int64_t cols) {
-    TileChoice t;
-    const int nts[2] = {64, 1024};
-    for (int nt : nts) {
-        for (int items = 1; items <= 8; items *= 2) {
-            if (cols <= (int64_t)nt * 4 * items) { t.nt = nt; t.items = items; return t; }
-        }
-    }
-    return t;
-}
 
 template <bool LOG>
 int launch_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
