@@ -1,0 +1,87 @@
+/*
+ * wm_layers.h -- C ABI of libwm_hip's normalisation and attention-softmax
+ * kernels: the reduction / softmax work inside whitematter's LayerNorm,
+ * BatchNorm2d and MultiHeadAttention modules (reference core/layer.cpp),
+ * which the reference writes as raw host loops that bypass its Tensor ops.
+ *
+ * Conventions are those of wm_hip.h: status codes, wm_last_error(), device
+ * pointers to contiguous row-major fp32, one library stream, and for every
+ * gradient output an `accumulate` flag (1 = "+=", 0 = the buffer is known to
+ * be zero and is overwritten).  A NULL gradient pointer means that input does
+ * not require grad (the reference's `if (x->requires_grad)` branches).
+ *
+ * Statistics the backward needs (per-row / per-channel mean and 1/std) are
+ * written by the forward into caller-provided device arrays, as the
+ * reference's closures capture them; the backward reads the input again
+ * (the reference recomputes x_norm from input->data in its closure).
+ */
+#ifndef WM_LAYERS_H
+#define WM_LAYERS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* LayerNorm::forward, core/layer.cpp:395-446, over the trailing n elements
+ * of each of `rows` instances:
+ *   mean_r = sum(x_r) / n;  var_r = sum((x_r - mean_r)^2) / n
+ *   inv_std_r = 1 / sqrt(var_r + eps)
+ *   y = gamma * ((x - mean_r) * inv_std_r) + beta
+ * gamma, beta [n]; mean, inv_std [rows] (written).                         */
+int wm_layernorm_fwd(const float* x, const float* gamma, const float* beta, int64_t rows, int64_t n, float eps,
+                     float* y, float* mean, float* inv_std);
+
+/* LayerNorm's closure, core/layer.cpp:447-504:
+ *   x_norm = (x - mean_r) * inv_std_r
+ *   dgamma (+)= sum_r g * x_norm;  dbeta (+)= sum_r g
+ *   gx (+)= inv_std_r * (g*gamma - mean_i(g*gamma) - x_norm * mean_i(g*gamma*x_norm))   */
+int wm_layernorm_bwd(const float* g, const float* x, const float* gamma, const float* mean, const float* inv_std,
+                     int64_t rows, int64_t n, float* gx, int acc_x, float* dgamma, int acc_gamma, float* dbeta,
+                     int acc_beta);
+
+/* BatchNorm2d::forward, core/layer.cpp:202-280, x [batch, channels, spatial]
+ * (spatial = H * W), per channel over batch * spatial elements.
+ * training != 0: batch statistics (biased variance), and the running
+ * statistics are updated in place:
+ *   running_mean = (1 - momentum) * running_mean + momentum * mean
+ *   running_var  = (1 - momentum) * running_var  + momentum * var
+ * training == 0: mean / var are running_mean / running_var (not updated).
+ *   inv_std = 1 / sqrt(var + eps);  y = gamma * ((x - mean) * inv_std) + beta
+ * mean, inv_std [channels] (written: what the closure captures).            */
+int wm_batchnorm2d_fwd(const float* x, const float* gamma, const float* beta, float* running_mean,
+                       float* running_var, int64_t batch, int64_t channels, int64_t spatial, float eps,
+                       float momentum, int training, float* y, float* mean, float* inv_std);
+
+/* BatchNorm2d's closure, core/layer.cpp:281-374 (the same formula in both
+ * modes, with the captured mean / inv_std), n = batch * spatial:
+ *   dgamma (+)= sum g * x_norm;  dbeta (+)= sum g
+ *   dvar  = sum (g*gamma) * (x - mean) * -0.5 * inv_std^3
+ *   dmean = sum (g*gamma) * (-inv_std) + dvar * sum(-2 (x - mean)) / n
+ *   gx (+)= (g*gamma) * inv_std + dvar * 2 (x - mean) / n + dmean / n       */
+int wm_batchnorm2d_bwd(const float* g, const float* x, const float* gamma, const float* mean, const float* inv_std,
+                       int64_t batch, int64_t channels, int64_t spatial, float* gx, int acc_x, float* dgamma,
+                       int acc_gamma, float* dbeta, int acc_beta);
+
+/* MultiHeadAttention's softmax over the keys, core/layer.cpp:1210-1237, with
+ * the mask add of :1198-1204 fused in front of it.  scores [batch, heads,
+ * tq, tk] are the scaled dot products (Q K^T / sqrt(head_dim)); mask is NULL
+ * or [mask_batches, 1, tq, tk] with mask_batches 1 (broadcast over the
+ * batch) or batch; it is added to the scores before the softmax:
+ *   s = scores + mask;  m = max(-FLT_MAX, max_j s_j)
+ *   attn_j = exp(s_j - m) / sum_k exp(s_k - m)                              */
+int wm_attention_softmax_fwd(const float* scores, const float* mask, int64_t mask_batches, int64_t batch,
+                             int64_t heads, int64_t tq, int64_t tk, float* attn);
+
+/* Its backward, core/layer.cpp:1343-1360, over rows = batch*heads*tq rows:
+ *   d_scores_j = attn_j * (d_attn_j - sum_k attn_k d_attn_k)
+ * d_scores is written (the reference assigns a fresh tensor).              */
+int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t rows, int64_t tk, float* d_scores);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WM_LAYERS_H */

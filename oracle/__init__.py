@@ -296,6 +296,98 @@ for _name, _fn in _loss_methods().items():
     setattr(Oracle, _name, _fn)
 
 
+# ---- normalisation layers and the attention softmax (core/layer.cpp) -----------
+
+def _layer_sigs(o):
+    if getattr(o, "_layer_ready", False):
+        return
+    L, vp, i64, f = o.L, C.c_void_p, C.c_int64, C.c_float
+    L.or_layernorm.argtypes = [vp, vp, vp, i64, i64, f, vp, vp, vp]
+    L.or_layernorm_bwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, vp, vp, vp]
+    L.or_batchnorm2d.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, f, f, C.c_int, vp, vp, vp]
+    L.or_batchnorm2d_bwd.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, vp, vp, vp]
+    L.or_attention_softmax.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp]
+    L.or_attention_softmax_bwd.argtypes = [vp, vp, i64, i64, vp]
+    o._layer_ready = True
+
+
+def _layer_methods():
+    """LayerNorm / BatchNorm2d / attention-softmax entry points of an Oracle
+    build.  Saved statistics come back as REAL arrays; the backward takes
+    them as fp32 (the values a closure captures).  Gradients are fresh
+    arrays (the closure's contribution to zero gradients)."""
+
+    def layernorm(self, x, gamma, beta, eps=1e-5):
+        _layer_sigs(self)
+        x, gamma, beta = _f32c(x), _f32c(gamma), _f32c(beta)
+        n = gamma.size
+        rows = x.size // n
+        y = np.zeros(x.shape, self.dtype)
+        mean, inv = np.zeros(rows, self.dtype), np.zeros(rows, self.dtype)
+        self.L.or_layernorm(_fp(x), _fp(gamma), _fp(beta), rows, n, eps, _fp(y), _fp(mean), _fp(inv))
+        return y, mean, inv
+
+    def layernorm_bwd(self, g, x, gamma, mean, inv):
+        _layer_sigs(self)
+        g, x, gamma, mean, inv = _f32c(g), _f32c(x), _f32c(gamma), _f32c(mean), _f32c(inv)
+        n = gamma.size
+        rows = x.size // n
+        gx = np.zeros(x.shape, self.dtype)
+        dg, db = np.zeros(n, self.dtype), np.zeros(n, self.dtype)
+        self.L.or_layernorm_bwd(_fp(g), _fp(x), _fp(gamma), _fp(mean), _fp(inv), rows, n, _fp(gx), _fp(dg), _fp(db))
+        return gx, dg, db
+
+    def batchnorm2d(self, x, gamma, beta, running_mean, running_var, eps=1e-5, momentum=0.1, training=True):
+        """x [B, C, H, W] (or [B, C, S]); returns (y, mean, inv_std,
+        running_mean', running_var')."""
+        _layer_sigs(self)
+        x, gamma, beta = _f32c(x), _f32c(gamma), _f32c(beta)
+        B, Cc = x.shape[0], x.shape[1]
+        S = x.size // (B * Cc) if B * Cc else 0
+        rm, rv = _f32c(running_mean).copy(), _f32c(running_var).copy()
+        y = np.zeros(x.shape, self.dtype)
+        mean, inv = np.zeros(Cc, self.dtype), np.zeros(Cc, self.dtype)
+        self.L.or_batchnorm2d(_fp(x), _fp(gamma), _fp(beta), _fp(rm), _fp(rv), B, Cc, S, eps, momentum,
+                              int(training), _fp(y), _fp(mean), _fp(inv))
+        return y, mean, inv, rm, rv
+
+    def batchnorm2d_bwd(self, g, x, gamma, mean, inv):
+        _layer_sigs(self)
+        g, x, gamma, mean, inv = _f32c(g), _f32c(x), _f32c(gamma), _f32c(mean), _f32c(inv)
+        B, Cc = x.shape[0], x.shape[1]
+        S = x.size // (B * Cc) if B * Cc else 0
+        gx = np.zeros(x.shape, self.dtype)
+        dg, db = np.zeros(Cc, self.dtype), np.zeros(Cc, self.dtype)
+        self.L.or_batchnorm2d_bwd(_fp(g), _fp(x), _fp(gamma), _fp(mean), _fp(inv), B, Cc, S, _fp(gx), _fp(dg),
+                                  _fp(db))
+        return gx, dg, db
+
+    def attention_softmax(self, scores, mask=None):
+        """scores [B, H, tq, tk]; mask None or [Bm, 1, tq, tk]."""
+        _layer_sigs(self)
+        scores = _f32c(scores)
+        B, H, tq, tk = scores.shape
+        m = _f32c(mask) if mask is not None else None
+        attn = np.zeros(scores.shape, self.dtype)
+        self.L.or_attention_softmax(_fp(scores), _fp(m), m.shape[0] if m is not None else 0, B, H, tq, tk,
+                                    _fp(attn))
+        return attn
+
+    def attention_softmax_bwd(self, attn, d_attn):
+        _layer_sigs(self)
+        attn, d_attn = _f32c(attn), _f32c(d_attn)
+        tk = attn.shape[-1]
+        ds = np.zeros(attn.shape, self.dtype)
+        self.L.or_attention_softmax_bwd(_fp(attn), _fp(d_attn), attn.size // tk, tk, _fp(ds))
+        return ds
+
+    return {k: v for k, v in locals().items() if callable(v)}
+
+
+for _name, _fn in _layer_methods().items():
+    setattr(Oracle, _name, _fn)
+
+
 def get(kind: str) -> Oracle:
     if kind not in _libs:
         _libs[kind] = Oracle(kind)
@@ -336,6 +428,11 @@ class RefTensor:
         g = np.ascontiguousarray(g, np.float32)
         return self.L.wmref_set_grad(self.h, _fp(g))
 
+    def set_data(self, v):
+        v = np.ascontiguousarray(v, np.float32)
+        assert v.size == self.L.wmref_numel(self.h)
+        self.L.wmref_set_data(self.h, _fp(v))
+
     def call_grad_fn(self):
         self.L.wmref_call_grad_fn(self.h)
 
@@ -361,6 +458,35 @@ class RefOptimizer:
     def __del__(self):
         try:
             self.L.wmref_optim_free(self.h)
+        except Exception:
+            pass
+
+
+class RefModule:
+    """A reference Module (core/layer.h) behind oracle/_ref/libwmref.so."""
+
+    def __init__(self, L, h):
+        self.L, self.h = L, h
+
+    def forward(self, x: RefTensor) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_module_forward(self.h, x.h))
+
+    def mha(self, q: RefTensor, k: RefTensor, v: RefTensor, mask: Optional[RefTensor] = None) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_mha_forward(self.h, q.h, k.h, v.h, mask.h if mask else None))
+
+    def params(self):
+        return [RefTensor(self.L, self.L.wmref_module_param(self.h, i))
+                for i in range(self.L.wmref_module_nparams(self.h))]
+
+    def buffer(self, which=0) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_module_buffer(self.h, which))
+
+    def train(self, on=True):
+        self.L.wmref_module_train(self.h, int(on))
+
+    def __del__(self):
+        try:
+            self.L.wmref_module_free(self.h)
         except Exception:
             pass
 
@@ -418,6 +544,26 @@ class Reference:
         L.wmref_unscale.restype = C.c_int
         L.wmref_loss.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_float, C.c_float]
         L.wmref_loss.restype = C.c_void_p
+        L.wmref_module_new.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_float, C.c_float]
+        L.wmref_module_new.restype = C.c_void_p
+        L.wmref_module_free.argtypes = [C.c_void_p]
+        L.wmref_module_free.restype = None
+        L.wmref_module_train.argtypes = [C.c_void_p, C.c_int]
+        L.wmref_module_train.restype = None
+        L.wmref_module_forward.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_module_forward.restype = C.c_void_p
+        L.wmref_mha_forward.argtypes = [C.c_void_p] * 5
+        L.wmref_mha_forward.restype = C.c_void_p
+        L.wmref_module_nparams.argtypes = [C.c_void_p]
+        L.wmref_module_nparams.restype = C.c_int
+        L.wmref_module_param.argtypes = [C.c_void_p, C.c_int]
+        L.wmref_module_param.restype = C.c_void_p
+        L.wmref_module_buffer.argtypes = [C.c_void_p, C.c_int]
+        L.wmref_module_buffer.restype = C.c_void_p
+        L.wmref_set_data.argtypes = [C.c_void_p, C.c_void_p]
+        L.wmref_set_data.restype = None
+        L.wmref_causal_mask.argtypes = [C.c_int64]
+        L.wmref_causal_mask.restype = C.c_void_p
         self.L = L
 
     @staticmethod
@@ -463,6 +609,17 @@ class Reference:
         value = np.float32(tl.data()[0])
         tl.backward()
         return value, tp.grad()
+
+    MODULES = {"layernorm": 0, "batchnorm2d": 1, "mha": 2}
+
+    def module(self, kind, shape, p0=1e-5, p1=0.1) -> RefModule:
+        """LayerNorm(shape, eps=p0), BatchNorm2d(shape[0], eps=p0,
+        momentum=p1) or MultiHeadAttention(shape[0], shape[1])."""
+        sa, nd = _shape(shape)
+        return RefModule(self.L, self.L.wmref_module_new(self.MODULES[kind], sa, nd, p0, p1))
+
+    def causal_mask(self, seq_len) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_causal_mask(seq_len))
 
     def tensor(self, data, requires_grad=False, shape: Optional[Sequence[int]] = None) -> RefTensor:
         data = np.ascontiguousarray(data, np.float32)

@@ -18,6 +18,7 @@
 #include "amp.h"
 #include "optimizer.h"
 #include "loss.h"
+#include "layer.h"
 
 #include <memory>
 
@@ -70,6 +71,11 @@ int wmref_requires_grad(void* h) { return T(h)->requires_grad ? 1 : 0; }
 
 void wmref_get_data(void* h, float* out) {
     std::memcpy(out, T(h)->data.data(), T(h)->data.size() * sizeof(float));
+}
+
+// Overwrite a tensor's values (its size is unchanged).
+void wmref_set_data(void* h, const float* v) {
+    std::memcpy(T(h)->data.data(), v, T(h)->data.size() * sizeof(float));
 }
 
 // Returns 0 (and writes nothing) when the tensor has no grad buffer.
@@ -266,5 +272,54 @@ void* wmref_loss(int kind, void* pred, void* target, float p0, float p1) {
     }
     return box(l->forward(T(pred), T(target)));
 }
+
+// Modules of the reference (core/layer.h): 0 LayerNorm(normalized shape,
+// eps = p0), 1 BatchNorm2d(num_features = shape[0], eps = p0, momentum =
+// p1), 2 MultiHeadAttention(embed_dim = shape[0], num_heads = shape[1]).
+void* wmref_module_new(int kind, const int64_t* shape, int nd, float p0, float p1) {
+    RefFpMode fp_mode_;
+    std::vector<size_t> s(shape, shape + nd);
+    switch (kind) {
+        case 0: return new LayerNorm(s, p0);
+        case 1: return new BatchNorm2d(s[0], p0, p1);
+        default: return new MultiHeadAttention(s[0], s[1]);
+    }
+}
+
+void wmref_module_free(void* m) { delete static_cast<Module*>(m); }
+
+// BatchNorm2d's training flag.
+void wmref_module_train(void* m, int on) {
+    if (auto* bn = dynamic_cast<BatchNorm2d*>(static_cast<Module*>(m))) bn->training = on != 0;
+}
+
+void* wmref_module_forward(void* m, void* input) {
+    RefFpMode fp_mode_;
+    return box(static_cast<Module*>(m)->forward(T(input)));
+}
+
+// MultiHeadAttention::forward(query, key, value, mask); mask may be NULL.
+void* wmref_mha_forward(void* m, void* q, void* k, void* v, void* mask) {
+    RefFpMode fp_mode_;
+    auto* a = static_cast<MultiHeadAttention*>(static_cast<Module*>(m));
+    return box(a->forward(T(q), T(k), T(v), mask ? T(mask) : TensorPtr()));
+}
+
+int wmref_module_nparams(void* m) { return (int)static_cast<Module*>(m)->parameters().size(); }
+
+// The i-th parameter tensor (shared with the module).
+void* wmref_module_param(void* m, int i) { return box(static_cast<Module*>(m)->parameters()[(size_t)i]); }
+
+// Buffers: BatchNorm2d running_mean (0) / running_var (1); MHA
+// attn_weights (0).
+void* wmref_module_buffer(void* m, int which) {
+    Module* mod = static_cast<Module*>(m);
+    if (auto* bn = dynamic_cast<BatchNorm2d*>(mod)) return box(which == 0 ? bn->running_mean : bn->running_var);
+    if (auto* a = dynamic_cast<MultiHeadAttention*>(mod)) return box(a->attn_weights);
+    return nullptr;
+}
+
+// Causal mask, MultiHeadAttention::causal_mask.
+void* wmref_causal_mask(int64_t seq_len) { return box(MultiHeadAttention::causal_mask((size_t)seq_len)); }
 
 }  // extern "C"

@@ -814,3 +814,196 @@ int or_pointwise_loss_bwd(int kind, const float* x, const float* y, int64_t n, f
     for (int64_t i = 0; i < n; i++) ACC(gx[i], or_pw_grad(kind, x[i], y[i], p0, p1, scale));
     return 0;
 }
+
+/* ---- normalisation layers and the attention softmax: core/layer.cpp -------
+ * Statistics the backward captures (mean, inv_std) are outputs of the
+ * forward (REAL) and inputs of the backward (float: the values the closure
+ * captured).  Gradients accumulate (+=) into caller-initialised arrays; a
+ * NULL gradient array is skipped. */
+
+/* LayerNorm::forward, layer.cpp:395-446.  The statistics are computed
+ * with plain arithmetic in every build (the magnitude build's scales use the
+ * true mean and 1/std); only the output takes magnitudes. */
+int or_layernorm(const float* x, const float* gamma, const float* beta, int64_t rows, int64_t n, float eps, REAL* y,
+                 REAL* mean, REAL* inv_std) {
+    OR_FP_SCOPE;
+    const REAL nf = (REAL)(float)n;
+    for (int64_t r = 0; r < rows; r++) {
+        const float* xr = x + r * n;
+        REAL s = 0;
+        for (int64_t i = 0; i < n; i++) s += (REAL)xr[i];
+        REAL m = s / nf;
+        REAL q = 0;
+        for (int64_t i = 0; i < n; i++) {
+            REAL d = (REAL)xr[i] - m;
+            q += d * d;
+        }
+        REAL var = q / nf;
+        REAL iv = (REAL)1 / (REAL)sqrt(var + (REAL)eps);
+        for (int64_t i = 0; i < n; i++) {
+            REAL xn = MINUS((REAL)xr[i], m) * iv;
+            y[r * n + i] = PLUS((REAL)gamma[i] * xn, (REAL)beta[i]);
+        }
+        mean[r] = m;
+        inv_std[r] = iv;
+    }
+    return 0;
+}
+
+/* LayerNorm's closure, layer.cpp:453-504. */
+int or_layernorm_bwd(const float* g, const float* x, const float* gamma, const float* mean, const float* inv_std,
+                     int64_t rows, int64_t n, REAL* gx, REAL* dgamma, REAL* dbeta) {
+    OR_FP_SCOPE;
+    const REAL nf = (REAL)(float)n;
+    for (int64_t r = 0; r < rows; r++) {
+        const float* gr = g + r * n;
+        const float* xr = x + r * n;
+        const REAL m = mean[r], iv = inv_std[r];
+        for (int64_t i = 0; i < n; i++) {
+            REAL xn = MINUS((REAL)xr[i], m) * iv;
+            if (dgamma) ACC(dgamma[i], (REAL)gr[i] * xn);
+            if (dbeta) ACC(dbeta[i], (REAL)gr[i]);
+        }
+        REAL s1 = 0, s2 = 0;
+        for (int64_t i = 0; i < n; i++) {
+            REAL dy = gr[i];
+            REAL xn = MINUS((REAL)xr[i], m) * iv;
+            ACC(s1, dy * (REAL)gamma[i]);
+            ACC(s2, dy * (REAL)gamma[i] * xn);
+        }
+        REAL mdg = s1 / nf, mdgx = s2 / nf;
+        if (gx)
+            for (int64_t i = 0; i < n; i++) {
+                REAL dy = gr[i];
+                REAL xn = MINUS((REAL)xr[i], m) * iv;
+                ACC(gx[r * n + i], iv * MINUS(MINUS(dy * (REAL)gamma[i], mdg), xn * mdgx));
+            }
+    }
+    return 0;
+}
+
+/* BatchNorm2d::forward, layer.cpp:202-280, x [B, C, S].  running_mean /
+ * running_var are updated in place when training (rounded to float, what the
+ * reference stores).  Statistics in plain arithmetic in every build, as for
+ * LayerNorm. */
+int or_batchnorm2d(const float* x, const float* gamma, const float* beta, float* running_mean, float* running_var,
+                   int64_t B, int64_t C, int64_t S, float eps, float momentum, int training, REAL* y, REAL* mean,
+                   REAL* inv_std) {
+    OR_FP_SCOPE;
+    const REAL nf = (REAL)(float)(B * S);
+    for (int64_t c = 0; c < C; c++) {
+        REAL m, var;
+        if (training) {
+            REAL s = 0;
+            for (int64_t b = 0; b < B; b++)
+                for (int64_t i = 0; i < S; i++) s += (REAL)x[(b * C + c) * S + i];
+            m = s / nf;
+            REAL q = 0;
+            for (int64_t b = 0; b < B; b++)
+                for (int64_t i = 0; i < S; i++) {
+                    REAL d = (REAL)x[(b * C + c) * S + i] - m;
+                    q += d * d;
+                }
+            var = q / nf;
+            const REAL mo = (REAL)momentum;
+            running_mean[c] = (float)(((REAL)1 - mo) * (REAL)running_mean[c] + mo * m);
+            running_var[c] = (float)(((REAL)1 - mo) * (REAL)running_var[c] + mo * var);
+        } else {
+            m = running_mean[c];
+            var = running_var[c];
+        }
+        mean[c] = m;
+        inv_std[c] = (REAL)1 / (REAL)sqrt(var + (REAL)eps);
+    }
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t c = 0; c < C; c++)
+            for (int64_t i = 0; i < S; i++) {
+                int64_t idx = (b * C + c) * S + i;
+                REAL xn = MINUS((REAL)x[idx], mean[c]) * inv_std[c];
+                y[idx] = PLUS((REAL)gamma[c] * xn, (REAL)beta[c]);
+            }
+    return 0;
+}
+
+/* BatchNorm2d's closure, layer.cpp:287-374, with the captured mean / inv_std. */
+int or_batchnorm2d_bwd(const float* g, const float* x, const float* gamma, const float* mean, const float* inv_std,
+                       int64_t B, int64_t C, int64_t S, REAL* gx, REAL* dgamma, REAL* dbeta) {
+    OR_FP_SCOPE;
+    const REAL nf = (REAL)(float)(B * S);
+    for (int64_t c = 0; c < C; c++) {
+        const REAL m = mean[c], iv = inv_std[c], gm = gamma[c];
+        REAL dg = 0, db = 0, dvar = 0, sdx = 0, sxd = 0;
+        for (int64_t b = 0; b < B; b++)
+            for (int64_t i = 0; i < S; i++) {
+                int64_t idx = (b * C + c) * S + i;
+                REAL xn = MINUS((REAL)x[idx], m) * iv;
+                ACC(dg, (REAL)g[idx] * xn);
+                ACC(db, (REAL)g[idx]);
+            }
+        for (int64_t b = 0; b < B; b++)
+            for (int64_t i = 0; i < S; i++) {
+                int64_t idx = (b * C + c) * S + i;
+                REAL dxn = (REAL)g[idx] * gm;
+                ACC(dvar, dxn * MINUS((REAL)x[idx], m) * (REAL)-0.5f * iv * iv * iv);
+            }
+        for (int64_t b = 0; b < B; b++)
+            for (int64_t i = 0; i < S; i++) {
+                int64_t idx = (b * C + c) * S + i;
+                ACC(sdx, (REAL)g[idx] * gm * (-iv));
+                ACC(sxd, (REAL)-2.0f * MINUS((REAL)x[idx], m));
+            }
+        REAL dmean = PLUS(sdx, dvar * sxd / nf);
+        if (gx)
+            for (int64_t b = 0; b < B; b++)
+                for (int64_t i = 0; i < S; i++) {
+                    int64_t idx = (b * C + c) * S + i;
+                    REAL dxn = (REAL)g[idx] * gm;
+                    REAL t = PLUS(PLUS(dxn * iv, dvar * (REAL)2.0f * MINUS((REAL)x[idx], m) / nf), dmean / nf);
+                    ACC(gx[idx], t);
+                }
+        if (dgamma) ACC(dgamma[c], dg);
+        if (dbeta) ACC(dbeta[c], db);
+    }
+    return 0;
+}
+
+/* MultiHeadAttention's mask add (layer.cpp:1198-1204) and softmax
+ * (:1210-1237): max from -FLT_MAX, exp, sum, division.  mask NULL or
+ * [mask_batches, 1, tq, tk]. */
+int or_attention_softmax(const float* scores, const float* mask, int64_t mask_batches, int64_t B, int64_t H,
+                         int64_t tq, int64_t tk, REAL* attn) {
+    OR_FP_SCOPE;
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t h = 0; h < H; h++)
+            for (int64_t i = 0; i < tq; i++) {
+                const int64_t r = (b * H + h) * tq + i;
+                const float* mr = mask ? mask + ((mask_batches == 1 ? 0 : b) * tq + i) * tk : NULL;
+                REAL* ar = attn + r * tk;
+                REAL mx = (REAL)-3.40282347e+38f;
+                for (int64_t j = 0; j < tk; j++) {
+                    REAL s = mr ? (REAL)scores[r * tk + j] + (REAL)mr[j] : (REAL)scores[r * tk + j];
+                    ar[j] = s;
+                    mx = (mx < s) ? s : mx;
+                }
+                REAL sum = 0;
+                for (int64_t j = 0; j < tk; j++) {
+                    ar[j] = (REAL)exp(ar[j] - mx);
+                    sum += ar[j];
+                }
+                for (int64_t j = 0; j < tk; j++) ar[j] /= sum;
+            }
+    return 0;
+}
+
+/* Its backward, layer.cpp:1343-1360: d = attn * (d_attn - sum(attn * d_attn)). */
+int or_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t rows, int64_t tk, REAL* ds) {
+    OR_FP_SCOPE;
+    for (int64_t r = 0; r < rows; r++) {
+        const float* ar = attn + r * tk;
+        const float* dr = d_attn + r * tk;
+        REAL dot = 0;
+        for (int64_t j = 0; j < tk; j++) ACC(dot, (REAL)ar[j] * (REAL)dr[j]);
+        for (int64_t j = 0; j < tk; j++) ds[r * tk + j] = (REAL)ar[j] * MINUS((REAL)dr[j], dot);
+    }
+    return 0;
+}

@@ -193,3 +193,74 @@ def pw_bwd(kind, x, y, p0=0.0, p1=0.0, denom=None, loss_grad=1.0, g0=None, offse
     W.call("wm_pointwise_loss_bwd", POINTWISE_KIND[kind], dx, dy, x.size, C.c_float(p0), C.c_float(p1),
            C.c_float(d), lg.vp, dg, acc)
     return dga.to_host()[offset:].reshape(x.shape)
+
+
+# ---- LayerNorm / BatchNorm2d / attention softmax (include/wm_layers.h) ---------
+
+def _opt_grad(shape, g0, want):
+    """(device buffer or None, accumulate flag) for an optional gradient."""
+    if not want:
+        return None, 0
+    return _grad_buffer(shape, g0)
+
+
+def layernorm_fwd(x, gamma, beta, eps=1e-5):
+    n = gamma.size
+    rows = x.size // n
+    dx, dgm, dbt = dev(x), dev(gamma), dev(beta)
+    y, mean, inv = W.DeviceArray(x.shape), W.DeviceArray((max(rows, 1),)), W.DeviceArray((max(rows, 1),))
+    W.call("wm_layernorm_fwd", dx.vp, dgm.vp, dbt.vp, rows, n, C.c_float(eps), y.vp, mean.vp, inv.vp)
+    return y.to_host(), mean.to_host()[:rows], inv.to_host()[:rows]
+
+
+def layernorm_bwd(g, x, gamma, mean, inv, gx0=None, dg0=None, db0=None, want=(True, True, True)):
+    n = gamma.size
+    rows = x.size // n
+    dg_, dx, dgm, dm, di = dev(g), dev(x), dev(gamma), dev(mean), dev(inv)
+    gx, ax = _opt_grad(x.shape, gx0, want[0])
+    gg, ag = _opt_grad((n,), dg0, want[1])
+    gb, ab = _opt_grad((n,), db0, want[2])
+    W.call("wm_layernorm_bwd", dg_.vp, dx.vp, dgm.vp, dm.vp, di.vp, rows, n, gx.vp if gx else None, ax,
+           gg.vp if gg else None, ag, gb.vp if gb else None, ab)
+    return tuple(b.to_host() if b is not None else None for b in (gx, gg, gb))
+
+
+def batchnorm_fwd(x, gamma, beta, rm, rv, training=True, eps=1e-5, momentum=0.1):
+    B, Cc = x.shape[0], x.shape[1]
+    S = x.size // (B * Cc) if B * Cc else 0
+    dx, dgm, dbt, drm, drv = dev(x), dev(gamma), dev(beta), dev(rm), dev(rv)
+    y, mean, inv = W.DeviceArray(x.shape), W.DeviceArray((max(Cc, 1),)), W.DeviceArray((max(Cc, 1),))
+    W.call("wm_batchnorm2d_fwd", dx.vp, dgm.vp, dbt.vp, drm.vp, drv.vp, B, Cc, S, C.c_float(eps),
+           C.c_float(momentum), int(training), y.vp, mean.vp, inv.vp)
+    return y.to_host(), mean.to_host()[:Cc], inv.to_host()[:Cc], drm.to_host(), drv.to_host()
+
+
+def batchnorm_bwd(g, x, gamma, mean, inv, gx0=None, dg0=None, db0=None, want=(True, True, True)):
+    B, Cc = x.shape[0], x.shape[1]
+    S = x.size // (B * Cc) if B * Cc else 0
+    dg_, dx, dgm, dm, di = dev(g), dev(x), dev(gamma), dev(mean), dev(inv)
+    gx, ax = _opt_grad(x.shape, gx0, want[0])
+    gg, ag = _opt_grad((Cc,), dg0, want[1])
+    gb, ab = _opt_grad((Cc,), db0, want[2])
+    W.call("wm_batchnorm2d_bwd", dg_.vp, dx.vp, dgm.vp, dm.vp, di.vp, B, Cc, S, gx.vp if gx else None, ax,
+           gg.vp if gg else None, ag, gb.vp if gb else None, ab)
+    return tuple(b.to_host() if b is not None else None for b in (gx, gg, gb))
+
+
+def attn_softmax_fwd(scores, mask=None):
+    B, H, tq, tk = scores.shape
+    ds_ = dev(scores)
+    dm = dev(mask) if mask is not None else None
+    out = W.DeviceArray(scores.shape)
+    W.call("wm_attention_softmax_fwd", ds_.vp, dm.vp if dm else None, mask.shape[0] if mask is not None else 0,
+           B, H, tq, tk, out.vp)
+    return out.to_host()
+
+
+def attn_softmax_bwd(attn, d_attn):
+    tk = attn.shape[-1]
+    da, dd = dev(attn), dev(d_attn)
+    out = W.DeviceArray(attn.shape)
+    out.fill(np.nan)
+    W.call("wm_attention_softmax_bwd", da.vp, dd.vp, attn.size // tk, tk, out.vp)
+    return out.to_host()

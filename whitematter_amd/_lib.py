@@ -93,6 +93,15 @@ _SIGS = {
     "wm_focal_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int64, C.c_float, C.c_float],
     "wm_pointwise_loss_fwd": [C.c_int, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, _vp],
     "wm_pointwise_loss_bwd": [C.c_int, _vp, _vp, C.c_int64, C.c_float, C.c_float, C.c_float, _vp, _vp, C.c_int],
+    # include/wm_layers.h
+    "wm_layernorm_fwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_float, _vp, _vp, _vp],
+    "wm_layernorm_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int, _vp, C.c_int],
+    "wm_batchnorm2d_fwd": [_vp, _vp, _vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_float, C.c_int,
+                           _vp, _vp, _vp],
+    "wm_batchnorm2d_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int,
+                           _vp, C.c_int],
+    "wm_attention_softmax_fwd": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
+    "wm_attention_softmax_bwd": [_vp, _vp, C.c_int64, C.c_int64, _vp],
 }
 
 # enum wm_pointwise_loss
