@@ -416,6 +416,76 @@ def loss_ops(rows=8192, cols=32000):
                     "same elements with U[0,1] targets" % (rows, cols), "elements": N}
 
 
+def norm_ops():
+    """Row-3 kernels at transformer / CNN sizes: LayerNorm over [32768, 4096]
+    (the c5 block's activations), BatchNorm2d over [64, 256, 56, 56] in
+    training mode, and the attention softmax over [8, 16, 1024, 1024] scores
+    with a causal mask; each forward and backward (gradients known-zero)."""
+    rows, n = 32768, 4096
+    x = synth.normal((rows, n), synth.seed_for(7, 0), 1.0, 2.0)
+    g = synth.normal((rows, n), synth.seed_for(7, 1))
+    dx, dg = W.DeviceArray.from_host(x), W.DeviceArray.from_host(g)
+    del x, g
+    gam = W.DeviceArray.from_host(synth.uniform((n,), synth.seed_for(7, 2), 0.5, 1.5))
+    bet = W.DeviceArray.from_host(synth.normal((n,), synth.seed_for(7, 3)))
+    y, gx = W.DeviceArray((rows, n)), W.DeviceArray((rows, n))
+    mean, inv = W.DeviceArray((rows,)), W.DeviceArray((rows,))
+    dgam, dbet = W.DeviceArray((n,)), W.DeviceArray((n,))
+    eps = W.C.c_float(1e-5)
+
+    B, C, H = 64, 256, 56
+    S = H * H
+    bx = synth.normal((B, C, S), synth.seed_for(8, 0), 0.5, 2.0)
+    bg = synth.normal((B, C, S), synth.seed_for(8, 1))
+    dbx, dbg = W.DeviceArray.from_host(bx), W.DeviceArray.from_host(bg)
+    del bx, bg
+    bgam = W.DeviceArray.from_host(synth.uniform((C,), synth.seed_for(8, 2), 0.5, 1.5))
+    bbet = W.DeviceArray.from_host(synth.normal((C,), synth.seed_for(8, 3)))
+    rm, rv = W.DeviceArray((C,)), W.DeviceArray((C,))
+    rm.fill(0.0)
+    rv.fill(1.0)
+    by, bgx = W.DeviceArray((B, C, S)), W.DeviceArray((B, C, S))
+    bmean, binv, bdg, bdb = (W.DeviceArray((C,)) for _ in range(4))
+    mom = W.C.c_float(0.1)
+
+    AB, AH, T = 8, 16, 1024
+    sc = synth.normal((AB, AH, T, T), synth.seed_for(9, 0), 0.0, 3.0)
+    da = synth.normal((AB, AH, T, T), synth.seed_for(9, 1))
+    dsc, dda = W.DeviceArray.from_host(sc), W.DeviceArray.from_host(da)
+    del sc, da
+    mask = W.DeviceArray.from_host(np.where(np.triu(np.ones((T, T)), 1) > 0, -1e9, 0).astype(np.float32))
+    att, dsc_out = W.DeviceArray((AB, AH, T, T)), W.DeviceArray((AB, AH, T, T))
+
+    NL, NB, NA = rows * n, B * C * S, AB * AH * T * T
+    ops = [
+        Op("LayerNorm fwd", lambda: W.call("wm_layernorm_fwd", dx.vp, gam.vp, bet.vp, rows, n, eps, y.vp, mean.vp,
+                                           inv.vp),
+           2 * NL * F32 + 2 * n * F32 + 2 * rows * F32, "ln_fwd_kernel", NL),
+        Op("LayerNorm bwd", lambda: W.call("wm_layernorm_bwd", dg.vp, dx.vp, gam.vp, mean.vp, inv.vp, rows, n, gx.vp,
+                                           0, dgam.vp, 0, dbet.vp, 0),
+           3 * NL * F32 + 3 * n * F32 + 2 * rows * F32, "ln_bwd_kernel", NL),
+        Op("BatchNorm2d fwd (train)", lambda: W.call("wm_batchnorm2d_fwd", dbx.vp, bgam.vp, bbet.vp, rm.vp, rv.vp, B,
+                                                     C, S, eps, mom, 1, by.vp, bmean.vp, binv.vp),
+           2 * NB * F32, "bn_apply_kernel", NB),
+        Op("BatchNorm2d bwd", lambda: W.call("wm_batchnorm2d_bwd", dbg.vp, dbx.vp, bgam.vp, bmean.vp, binv.vp, B, C, S,
+                                             bgx.vp, 0, bdg.vp, 0, bdb.vp, 0),
+           3 * NB * F32, "bn_bwd_apply_kernel", NB),
+        Op("attention softmax fwd", lambda: W.call("wm_attention_softmax_fwd", dsc.vp, mask.vp, 1, AB, AH, T, T,
+                                                   att.vp),
+           2 * NA * F32 + T * T * F32, "attn_softmax_fwd_kernel", NA),
+        Op("attention softmax bwd", lambda: W.call("wm_attention_softmax_bwd", att.vp, dda.vp, AB * AH * T, T,
+                                                   dsc_out.vp),
+           3 * NA * F32, "attn_softmax_bwd_kernel", NA),
+    ]
+    keep = [dx, dg, gam, bet, y, gx, mean, inv, dgam, dbet, dbx, dbg, bgam, bbet, rm, rv, by, bgx, bmean, binv, bdg,
+            bdb, dsc, dda, mask, att, dsc_out]
+    return ops, keep, {
+        "workload": "norm: LayerNorm x[%d,%d] fp32 (eps 1e-5); BatchNorm2d x[%d,%d,%d,%d] training mode; "
+                    "attention softmax scores[%d,%d,%d,%d] + causal mask [1,1,%d,%d]; fwd+bwd each, gradients "
+                    "known-zero; algorithmic bytes = one read of each input and one write of each output"
+                    % (rows, n, B, C, H, H, AB, AH, T, T, T, T), "elements": NL + NB + NA}
+
+
 def traffic_for(op_name: str, config: str):
     """HBM bytes per launch of an op's main kernel, from the committed
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json,
@@ -430,7 +500,8 @@ def traffic_for(op_name: str, config: str):
         return None
 
 
-CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops}
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
+           "norm": norm_ops}
 
 
 def main():

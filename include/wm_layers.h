@@ -71,7 +71,8 @@ int wm_batchnorm2d_bwd(const float* g, const float* x, const float* gamma, const
  * or [mask_batches, 1, tq, tk] with mask_batches 1 (broadcast over the
  * batch) or batch; it is added to the scores before the softmax:
  *   s = scores + mask;  m = max(-FLT_MAX, max_j s_j)
- *   attn_j = exp(s_j - m) / sum_k exp(s_k - m)                              */
+ *   attn_j = exp(s_j - m) / sum_k exp(s_k - m)
+ * (the quotient taken as a product with the row sum's reciprocal).         */
 int wm_attention_softmax_fwd(const float* scores, const float* mask, int64_t mask_batches, int64_t batch,
                              int64_t heads, int64_t tq, int64_t tk, float* attn);
 
@@ -79,6 +80,14 @@ int wm_attention_softmax_fwd(const float* scores, const float* mask, int64_t mas
  *   d_scores_j = attn_j * (d_attn_j - sum_k attn_k d_attn_k)
  * d_scores is written (the reference assigns a fresh tensor).              */
 int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t rows, int64_t tk, float* d_scores);
+
+/* Dropout's mask, core/layer.cpp:47-73: mask_i = u_i > p ? 1 / (1 - p) : 0,
+ * with u_i in [0, 1) the top 24 bits of splitmix64(seed + i) (a counter-
+ * based generator, so any element can be drawn independently; the
+ * reference draws from a sequential std::mt19937, whose stream a device
+ * cannot reproduce -- the distribution is the same, the bits are not).
+ * The drop-in multiplies the input by this mask.                           */
+int wm_dropout_mask(float* mask, int64_t n, float p, uint64_t seed);
 
 #ifdef __cplusplus
 }

@@ -381,6 +381,12 @@ def _layer_methods():
         self.L.or_attention_softmax_bwd(_fp(attn), _fp(d_attn), attn.size // tk, tk, _fp(ds))
         return ds
 
+    def dropout_mask(self, n, p, seed):
+        self.L.or_dropout_mask.argtypes = [C.c_void_p, C.c_int64, C.c_float, C.c_uint64]
+        mask = np.zeros(n, np.float32)
+        self.L.or_dropout_mask(_fp(mask), n, p, seed)
+        return mask
+
     return {k: v for k, v in locals().items() if callable(v)}
 
 

@@ -2,12 +2,10 @@
 //
 // Runner for the reference's own optimizer suite (tests/test_optimizer.cpp in
 // the reference), compiled where it lies against this build's drop-in
-// Tensor and optimizers (whitematter_amd/core/tensor.h and optimizer.h,
-// force-included so that they stand in for the reference's headers), with
-// the reference's core/layer.cpp and core/loss.cpp (the Linear layer and the
-// losses the suite trains with) compiled against the same headers.  Built by
-// oracle/Makefile into oracle/_ref/run_ref_optim; run on the GPU by
-// tests/test_gpu_ref_suites.py.
+// Tensor, optimizers, losses and modules (whitematter_amd/core/tensor.h,
+// optimizer.h, loss.h, layer.h, force-included so that they stand in for the
+// reference's headers).  Built by oracle/Makefile into
+// oracle/_ref/run_ref_optim; run on the GPU by tests/test_gpu_ref_suites.py.
 #include "test_framework.h"
 
 TestSuite* create_optimizer_tests();

@@ -1007,3 +1007,20 @@ int or_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t row
     }
     return 0;
 }
+
+/* Dropout's mask as the device draws it (the generator is this build's own:
+ * splitmix64 of seed + i, top 24 bits as u in [0, 1)); keep when u > p
+ * (core/layer.cpp:59), scale 1 / (1 - p) in float (:55). */
+int or_dropout_mask(float* mask, int64_t n, float p, uint64_t seed) {
+    OR_FP_SCOPE;
+    const float scale = 1.0f / (1.0f - p);
+    for (int64_t i = 0; i < n; i++) {
+        uint64_t z = seed + (uint64_t)i + 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        float u = (float)(uint32_t)(z >> 40) * 0x1p-24f;
+        mask[i] = u > p ? scale : 0.0f;
+    }
+    return 0;
+}

@@ -29,7 +29,7 @@ def close(got, ref, scale, rtol=1e-5, atol=1e-30):
 # ---- LayerNorm -------------------------------------------------------------------
 
 LN_SHAPES = [(1, 1), (4, 3), (33, 100), (7, 256), (5, 257), (3, 512), (9, 768), (4, 1000), (6, 2048), (3, 4096),
-             (2, 5000), (2, 8192), (2, 8193), (3, 20000), (1000, 64)]
+             (2, 5000), (2, 8192), (2, 8193), (3, 20000), (1000, 64), (4096, 256), (3000, 1000)]
 
 
 def ln_inputs(rows, n, seed):

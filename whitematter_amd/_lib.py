@@ -102,6 +102,7 @@ _SIGS = {
                            _vp, C.c_int],
     "wm_attention_softmax_fwd": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
     "wm_attention_softmax_bwd": [_vp, _vp, C.c_int64, C.c_int64, _vp],
+    "wm_dropout_mask": [_vp, C.c_int64, C.c_float, C.c_uint64],
 }
 
 # enum wm_pointwise_loss

@@ -11,6 +11,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include "layer.h"
 #include "loss.h"
 #include "optimizer.h"
 #include "tensor.h"
@@ -171,6 +172,32 @@ PYBIND11_MODULE(_tensor, m) {
     m.def("clip_grad_norm_", [](std::vector<TensorPtr> ps, float max_norm) { clip_grad_norm_(ps, max_norm); });
     m.def("clip_grad_value_", [](std::vector<TensorPtr> ps, float c) { clip_grad_value_(ps, c); });
     m.def("get_grad_norm", &get_grad_norm);
+
+    // Modules whose bodies run on the device (core/layer.h).
+    py::class_<Module>(m, "Module")
+        .def("forward", &Module::forward)
+        .def("__call__", [](Module& mod, const TensorPtr& x) { return mod(x); })
+        .def("parameters", &Module::parameters)
+        .def("num_parameters", &Module::num_parameters);
+    py::class_<LayerNorm, Module>(m, "LayerNorm")
+        .def(py::init<size_t, float>(), py::arg("normalized_shape"), py::arg("eps") = 1e-5f)
+        .def(py::init<std::vector<size_t>, float>(), py::arg("normalized_shape"), py::arg("eps") = 1e-5f)
+        .def_readwrite("gamma", &LayerNorm::gamma)
+        .def_readwrite("beta", &LayerNorm::beta);
+    py::class_<BatchNorm2d, Module>(m, "BatchNorm2d")
+        .def(py::init<size_t, float, float>(), py::arg("num_features"), py::arg("eps") = 1e-5f,
+             py::arg("momentum") = 0.1f)
+        .def("train", &BatchNorm2d::train)
+        .def("eval", &BatchNorm2d::eval)
+        .def_readwrite("training", &BatchNorm2d::training)
+        .def_readwrite("gamma", &BatchNorm2d::gamma)
+        .def_readwrite("beta", &BatchNorm2d::beta)
+        .def_readwrite("running_mean", &BatchNorm2d::running_mean)
+        .def_readwrite("running_var", &BatchNorm2d::running_var);
+    py::class_<Dropout, Module>(m, "Dropout")
+        .def(py::init<float>(), py::arg("p") = 0.5f)
+        .def("train", &Dropout::train)
+        .def("eval", &Dropout::eval);
 
     py::class_<LossFunction>(m, "LossFunction")
         .def("forward", &LossFunction::forward)

@@ -25,8 +25,11 @@
 //
 // MultiHeadAttention's softmax (core/layer.cpp:1198-1237, backward
 // :1343-1360): one row of scores per workgroup with the mask row added in
-// registers, the reference's max-from--FLT_MAX and division, and its plain
-// backward attn * (d_attn - sum(attn * d_attn)).
+// registers, the reference's max-from--FLT_MAX, and its plain backward
+// attn * (d_attn - sum(attn * d_attn)).  The reference divides each
+// exponential by the row sum; here they are multiplied by one reciprocal per
+// row (within an ulp of the quotient, inside the softmax tolerance, and an
+// IEEE division per element would cost more than the row's memory traffic).
 #include "wm_rows.hpp"
 
 #include <algorithm>
@@ -81,8 +84,8 @@ __global__ void __launch_bounds__(NT) ln_fwd_kernel(const float* __restrict__ x,
     using Tile = RowTile<NT, ITEMS, VEC>;
     __shared__ float lds_a[NT / 64], lds_b[NT / 64];
     Tile gt, bt;  // this thread's columns of gamma / beta, the same in every row
-    gt.load(gamma, n, 0.f);
-    bt.load(beta, n, 0.f);
+    gt.template load<true>(gamma, n, 0.f);
+    bt.template load<true>(beta, n, 0.f);
     const float nf = (float)n;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         Tile t;
@@ -127,7 +130,7 @@ __global__ void __launch_bounds__(NT) ln_bwd_kernel(const float* __restrict__ g,
     using Tile = RowTile<NT, ITEMS, VEC>;
     __shared__ float2 lds2[2][NT / 64];
     Tile gt;
-    gt.load(gamma, n, 0.f);
+    gt.template load<true>(gamma, n, 0.f);
     float pg[ITEMS][4], pb[ITEMS][4];
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
@@ -203,6 +206,53 @@ __global__ void __launch_bounds__(256) colsum_parts_kernel(const float* __restri
         const float t = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
         out[c] = acc ? out[c] + t : t;
     }
+}
+
+// First stage for many partial rows: workgroup (x, y) sums partial rows
+// [y * chunk, (y + 1) * chunk) of 64 columns into out2[y][c]; each wave takes
+// every 4th row with four independent accumulators (loads in flight), the
+// waves combine in LDS in a fixed order.  colsum_parts_kernel then sums the
+// out2 rows.
+__global__ void __launch_bounds__(256) colsum_stage_kernel(const float* __restrict__ part, int64_t parts, int64_t n,
+                                                            int64_t chunk, float* __restrict__ out2) {
+    __shared__ float lds[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+    const int64_t p0 = (int64_t)blockIdx.y * chunk;
+    const int64_t p1 = p0 + chunk < parts ? p0 + chunk : parts;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (c < n) {
+        int64_t p = p0 + w;
+        for (; p + 12 < p1; p += 16) {
+            a0 += part[p * n + c];
+            a1 += part[(p + 4) * n + c];
+            a2 += part[(p + 8) * n + c];
+            a3 += part[(p + 12) * n + c];
+        }
+        for (; p < p1; p += 4) a0 += part[p * n + c];
+    }
+    lds[w][lane] = (a0 + a1) + (a2 + a3);
+    __syncthreads();
+    if (w == 0 && c < n) out2[(int64_t)blockIdx.y * n + c] = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+}
+
+// Column sums of [parts, n] partial rows into out (+= when acc): one pass
+// for up to 64 rows, else colsum_stage_kernel first.
+int colsum_parts(const float* part, int64_t parts, int64_t n, float* out, int acc, const char* what) {
+    hipStream_t st = stream();
+    const dim3 cg((unsigned)((n + 63) / 64));
+    if (parts <= 64) {
+        hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, part, parts, n, out, acc);
+        return check_launch(what);
+    }
+    const int64_t chunk = 64, parts2 = (parts + chunk - 1) / chunk;
+    Workspace w2((size_t)(parts2 * n) * sizeof(float));
+    if (!w2.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
+    hipLaunchKernelGGL(colsum_stage_kernel, dim3(cg.x, (unsigned)parts2), dim3(256), 0, st, part, parts, n, chunk,
+                       w2.as<float>());
+    WM_TRY(check_launch(what));
+    hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, w2.as<float>(), parts2, n, out, acc);
+    return check_launch(what);
 }
 
 // Rows longer than the register tile: three streaming passes per row.
@@ -294,18 +344,13 @@ struct BnGeom {
     int64_t chunks;        // chunks per channel (gridDim.x)
 };
 
-__device__ __forceinline__ void seg_range(const BnGeom& gm, int64_t& s0, int64_t& s1) {
-    s0 = gm.nseg * (int64_t)blockIdx.x / gm.chunks;
-    s1 = gm.nseg * ((int64_t)blockIdx.x + 1) / gm.chunks;
-}
-
-// Visit every unit of this workgroup's chunk: f(plane_offset_in_floats,
-// unit_index_in_plane), four units per thread per step, loads first.
+// Visit every unit of this workgroup's chunk (blockIdx.x) of its channel
+// (blockIdx.y): f(plane_offset_in_floats, unit_index_in_plane), four units
+// per thread per step, loads first.
 template <bool VEC, class F>
 __device__ __forceinline__ void bn_for_chunk(const BnGeom& gm, F&& f) {
-    int64_t s0, s1;
-    seg_range(gm, s0, s1);
-    const int64_t c = blockIdx.y;
+    const int64_t k = blockIdx.x, c = blockIdx.y;
+    const int64_t s0 = gm.nseg * k / gm.chunks, s1 = gm.nseg * (k + 1) / gm.chunks;
     for (int64_t sg = s0; sg < s1; ++sg) {
         const int64_t b = sg / gm.spp, u0 = (sg - b * gm.spp) * kSeg;
         const int64_t base = (b * gm.C + c) * gm.S;
@@ -313,6 +358,8 @@ __device__ __forceinline__ void bn_for_chunk(const BnGeom& gm, F&& f) {
     }
 }
 
+// Cached loads: the apply pass reads x again right after, and a tensor that
+// fits the last-level cache is then served from it.
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_stats_kernel(const float* __restrict__ x, BnGeom gm,
                                                         double* __restrict__ part) {
@@ -325,7 +372,8 @@ __global__ void __launch_bounds__(256) bn_stats_kernel(const float* __restrict__
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int64_t u = u0 + threadIdx.x + k * 256;
-                v[k] = u < gm.units && u < u0 + kSeg ? ld_stream(p + u * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[k] = u < gm.units && u < u0 + kSeg ? *reinterpret_cast<const float4*>(p + u * 4)
+                                                     : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -338,7 +386,7 @@ __global__ void __launch_bounds__(256) bn_stats_kernel(const float* __restrict__
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int64_t u = u0 + threadIdx.x + k * 256;
-                v[k] = u < gm.units && u < u0 + kSeg ? ld_stream1(p + u) : 0.f;
+                v[k] = u < gm.units && u < u0 + kSeg ? p[u] : 0.f;
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -422,7 +470,8 @@ __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__
 }
 
 // Backward sums per chunk: sum(g), sum(g (x - mean)), sum(x - mean), with
-// x - mean in float as the closure computes it.
+// x - mean in float as the closure computes it (cached loads, as in
+// bn_stats_kernel: the dx pass re-reads g and x).
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_bwd_sums_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                            const float* __restrict__ mean, BnGeom gm,
@@ -437,8 +486,8 @@ __global__ void __launch_bounds__(256) bn_bwd_sums_kernel(const float* __restric
             for (int k = 0; k < 4; ++k) {
                 const int64_t u = u0 + threadIdx.x + k * 256;
                 const bool in = u < gm.units && u < u0 + kSeg;
-                gv[k] = in ? ld_stream(g + base + u * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                xv[k] = in ? ld_stream(x + base + u * 4) : make_float4(mc, mc, mc, mc);
+                gv[k] = in ? *reinterpret_cast<const float4*>(g + base + u * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[k] = in ? *reinterpret_cast<const float4*>(x + base + u * 4) : make_float4(mc, mc, mc, mc);
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -452,7 +501,7 @@ __global__ void __launch_bounds__(256) bn_bwd_sums_kernel(const float* __restric
             for (int k = 0; k < 4; ++k) {
                 const int64_t u = u0 + threadIdx.x + k * 256;
                 if (u < gm.units && u < u0 + kSeg) {
-                    const float gv = ld_stream1(g + base + u), d = ld_stream1(x + base + u) - mc;
+                    const float gv = g[base + u], d = x[base + u] - mc;
                     s1 += gv;
                     s2 += (double)gv * d;
                     s3 += d;
@@ -568,7 +617,7 @@ __global__ void __launch_bounds__(NT) attn_softmax_fwd_kernel(const float* __res
         if (mask) {
             const int64_t b = r / heads_tq, i = r % tq;
             Tile mt;
-            mt.load(mask + b * mask_bstride + i * tk, tk, 0.f);
+            mt.template load<true>(mask + b * mask_bstride + i * tk, tk, 0.f);
 #pragma unroll
             for (int k = 0; k < ITEMS; ++k)
 #pragma unroll
@@ -589,11 +638,11 @@ __global__ void __launch_bounds__(NT) attn_softmax_fwd_kernel(const float* __res
                 t.v[k][e] = exp_rr(t.v[k][e] - m);  // padding: exp(-inf) = 0
                 s += t.v[k][e];
             }
-        s = block_sum_1<NT>(s, lds_s);
+        const float rs = 1.0f / block_sum_1<NT>(s, lds_s);
 #pragma unroll
         for (int k = 0; k < ITEMS; ++k)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) t.v[k][e] = t.v[k][e] / s;
+            for (int e = 0; e < 4; ++e) t.v[k][e] = t.v[k][e] * rs;
         t.store(attn + r * tk, tk);
     }
 }
@@ -643,8 +692,8 @@ __global__ void __launch_bounds__(1024) attn_softmax_fwd_long_kernel(const float
             ar[c] = e;
             s += e;
         }
-        s = block_sum_1<1024>(s, lds_s);
-        for (int64_t c = threadIdx.x; c < tk; c += 1024) ar[c] = ar[c] / s;
+        const float rs = 1.0f / block_sum_1<1024>(s, lds_s);
+        for (int64_t c = threadIdx.x; c < tk; c += 1024) ar[c] = ar[c] * rs;
         __syncthreads();
     }
 }
@@ -661,6 +710,26 @@ __global__ void __launch_bounds__(1024) attn_softmax_bwd_long_kernel(const float
         for (int64_t c = threadIdx.x; c < tk; c += 1024) dot += ar[c] * dr[c];
         dot = block_sum_1<1024>(dot, lds[k2 & 1]);
         for (int64_t c = threadIdx.x; c < tk; c += 1024) ds[r * tk + c] = ar[c] * (dr[c] - dot);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dropout mask
+// ---------------------------------------------------------------------------
+
+// splitmix64 (Vigna): one 64-bit state step, a bijective mix of the counter.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(256) dropout_mask_kernel(float* __restrict__ mask, int64_t n, float p, float scale,
+                                                            uint64_t seed) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        const float u = (float)(uint32_t)(splitmix64(seed + (uint64_t)i) >> 40) * 0x1p-24f;
+        mask[i] = u > p ? scale : 0.0f;
     }
 }
 
@@ -732,10 +801,9 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
         hipLaunchKernelGGL(ln_param_parts_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)chunks), dim3(256), 0,
                            st, g, x, mean, inv, rows, n, rpc, wg.as<float>(), wb.as<float>());
         WM_TRY(check_launch("wm_layernorm_bwd(params)"));
-        const dim3 cg((unsigned)((n + 63) / 64));
-        if (dgamma) hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, wg.as<float>(), chunks, n, dgamma, acc_g);
-        if (dbeta) hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, wb.as<float>(), chunks, n, dbeta, acc_b);
-        return check_launch("wm_layernorm_bwd(colsum)");
+        if (dgamma) WM_TRY(colsum_parts(wg.as<float>(), chunks, n, dgamma, acc_g, "wm_layernorm_bwd(colsum)"));
+        if (dbeta) WM_TRY(colsum_parts(wb.as<float>(), chunks, n, dbeta, acc_b, "wm_layernorm_bwd(colsum)"));
+        return WM_OK;
     }
     // Fused path: G workgroups, each leaving one [n] partial per parameter
     // gradient.  G also bounds the partial traffic: at least 32 rows each.
@@ -761,10 +829,9 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
 #undef WM_LNB
     if (!launched) return set_error(WM_ERR_INVALID, "wm_layernorm_bwd: no tile");
     WM_TRY(check_launch("wm_layernorm_bwd"));
-    const dim3 cg((unsigned)((n + 63) / 64));
-    if (dgamma) hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, wg.as<float>(), G, n, dgamma, acc_g);
-    if (dbeta) hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, wb.as<float>(), G, n, dbeta, acc_b);
-    return want_p ? check_launch("wm_layernorm_bwd(colsum)") : WM_OK;
+    if (dgamma) WM_TRY(colsum_parts(wg.as<float>(), G, n, dgamma, acc_g, "wm_layernorm_bwd(colsum)"));
+    if (dbeta) WM_TRY(colsum_parts(wb.as<float>(), G, n, dbeta, acc_b, "wm_layernorm_bwd(colsum)"));
+    return WM_OK;
 }
 
 BnGeom bn_geom(int64_t B, int64_t C, int64_t S, bool vec) {
@@ -947,6 +1014,16 @@ int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t row
     WM_ASB(1024, 1) WM_ASB(1024, 2) WM_ASB(1024, 4) WM_ASB(1024, 8)
 #undef WM_ASB
     return set_error(WM_ERR_INVALID, "wm_attention_softmax_bwd: no tile");
+}
+
+int wm_dropout_mask(float* mask, int64_t n, float p, uint64_t seed) {
+    if (n < 0) return set_error(WM_ERR_INVALID, "wm_dropout_mask: negative size");
+    if (n == 0) return WM_OK;
+    if (!mask) return set_error(WM_ERR_INVALID, "wm_dropout_mask: null pointer");
+    WM_CHECK_INIT();
+    const float scale = 1.0f / (1.0f - p);  // core/layer.cpp:55
+    hipLaunchKernelGGL(dropout_mask_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream(), mask, n, p, scale, seed);
+    return check_launch("wm_dropout_mask");
 }
 
 }  // extern "C"

@@ -32,13 +32,17 @@ struct RowTile {
         return VEC ? ((int64_t)(t * NT + (int)threadIdx.x) * 4 + e) : ((int64_t)t * NT * 4 + (int64_t)e * NT + threadIdx.x);
     }
 
+    // CACHED = false: non-temporal loads (data read once); true: ordinary
+    // cached loads for rows that other workgroups read again (a broadcast
+    // mask row, per-column parameters).
+    template <bool CACHED = false>
     __device__ __forceinline__ void load(const float* row, int64_t cols, float fill) {
 #pragma unroll
         for (int t = 0; t < ITEMS; ++t) {
             if constexpr (VEC) {
                 int64_t c = col(t, 0);
                 if (c < cols) {
-                    float4 q = ld_stream(row + c);
+                    float4 q = CACHED ? *reinterpret_cast<const float4*>(row + c) : ld_stream(row + c);
                     v[t][0] = q.x; v[t][1] = q.y; v[t][2] = q.z; v[t][3] = q.w;
                 } else {
                     v[t][0] = v[t][1] = v[t][2] = v[t][3] = fill;
@@ -47,7 +51,7 @@ struct RowTile {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     int64_t c = col(t, e);
-                    v[t][e] = c < cols ? ld_stream1(row + c) : fill;
+                    v[t][e] = c < cols ? (CACHED ? row[c] : ld_stream1(row + c)) : fill;
                 }
             }
         }
