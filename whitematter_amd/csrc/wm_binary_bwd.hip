@@ -41,28 +41,42 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
     const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
     const bool need_o = gb && db_reads_out<OP>() && o;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
-        const int64_t e = 4 * i;
-        float4 vg = ld_stream(g + e);
-        float4 va = need_a ? ld_stream(a + e) : z;
-        float4 vb = need_b ? ld_stream(b + e) : z;
-        float4 vo = need_o ? ld_stream(o + e) : z;
-        float4 oa = (ga && acc_a) ? ld_stream(ga + e) : z;
-        float4 ob = (gb && acc_b) ? ld_stream(gb + e) : z;
-        const float eg[4] = {vg.x, vg.y, vg.z, vg.w}, ea[4] = {va.x, va.y, va.z, va.w},
-                    eb[4] = {vb.x, vb.y, vb.z, vb.w}, eo[4] = {vo.x, vo.y, vo.z, vo.w};
-        float da[4], db[4];
-        binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, ga != nullptr, gb != nullptr, da, db);
-        if (ga) {
-            float4 r = make_float4(da[0], da[1], da[2], da[3]);
-            if (acc_a) { r.x += oa.x; r.y += oa.y; r.z += oa.z; r.w += oa.w; }
-            st_stream(ga + e, r);
+    // kSlots float4 per thread per step (kBlock apart), loads first.
+    constexpr int kSlots = 4;
+    const int64_t stride = (int64_t)gridDim.x * kBlock * kSlots;
+    for (int64_t i0 = (int64_t)blockIdx.x * kBlock * kSlots + threadIdx.x; i0 < n4; i0 += stride) {
+        float4 vg[kSlots], va[kSlots], vb[kSlots], vo[kSlots], oa[kSlots], ob[kSlots];
+#pragma unroll
+        for (int u = 0; u < kSlots; ++u) {
+            const int64_t i = i0 + (int64_t)u * kBlock;
+            const bool in = i < n4;
+            const int64_t e = 4 * i;
+            vg[u] = in ? ld_stream(g + e) : z;
+            va[u] = in && need_a ? ld_stream(a + e) : z;
+            vb[u] = in && need_b ? ld_stream(b + e) : z;
+            vo[u] = in && need_o ? ld_stream(o + e) : z;
+            oa[u] = in && ga && acc_a ? ld_stream(ga + e) : z;
+            ob[u] = in && gb && acc_b ? ld_stream(gb + e) : z;
         }
-        if (gb) {
-            float4 r = make_float4(db[0], db[1], db[2], db[3]);
-            if (acc_b) { r.x += ob.x; r.y += ob.y; r.z += ob.z; r.w += ob.w; }
-            st_stream(gb + e, r);
+#pragma unroll
+        for (int u = 0; u < kSlots; ++u) {
+            const int64_t i = i0 + (int64_t)u * kBlock;
+            if (i >= n4) continue;
+            const int64_t e = 4 * i;
+            const float eg[4] = {vg[u].x, vg[u].y, vg[u].z, vg[u].w}, ea[4] = {va[u].x, va[u].y, va[u].z, va[u].w},
+                        eb[4] = {vb[u].x, vb[u].y, vb[u].z, vb[u].w}, eo[4] = {vo[u].x, vo[u].y, vo[u].z, vo[u].w};
+            float da[4], db[4];
+            binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, ga != nullptr, gb != nullptr, da, db);
+            if (ga) {
+                float4 r = make_float4(da[0], da[1], da[2], da[3]);
+                if (acc_a) { r.x += oa[u].x; r.y += oa[u].y; r.z += oa[u].z; r.w += oa[u].w; }
+                st_stream(ga + e, r);
+            }
+            if (gb) {
+                float4 r = make_float4(db[0], db[1], db[2], db[3]);
+                if (acc_b) { r.x += ob[u].x; r.y += ob[u].y; r.z += ob[u].z; r.w += ob[u].w; }
+                st_stream(gb + e, r);
+            }
         }
     }
 }
@@ -96,7 +110,10 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 vv = need_V ? *reinterpret_cast<const float4*>(V + c) : z;
     float4 s = z;
-#pragma unroll 4
+    // One row per iteration: walking rows 32 KiB apart, several rows' loads in
+    // flight per thread measured slower than one (more workgroups carry the
+    // memory-level parallelism instead).
+#pragma unroll 1
     for (int64_t r = r0; r < r1; ++r) {
         const int64_t off = r * C + c;
         float4 vg = ld_stream(g + off);
@@ -186,27 +203,42 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
         float* gfr = gF ? gF + r * C : nullptr;
         float s = 0.f;
         if constexpr (VEC) {
-            float4 s4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-            for (int64_t c = c0 + lane * 4; c < c1; c += 256) {
-                const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                float4 vg = ld_stream(gr + c);
-                float4 vf = need_F ? ld_stream(fr + c) : z4;
-                float4 vo = need_o ? ld_stream(orow + c) : z4;
-                float4 old = (gfr && accF) ? ld_stream(gfr + c) : z4;
-                const float e[4] = {vf.x, vf.y, vf.z, vf.w}, gg[4] = {vg.x, vg.y, vg.z, vg.w},
-                            oo[4] = {vo.x, vo.y, vo.z, vo.w}, vv[4] = {v, v, v, v};
-                float da[4], db[4];
-                binary_grads_n<OP, 4>(gg, VB ? e : vv, VB ? vv : e, oo, need_o, VB ? gfr != nullptr : want_v,
-                                      VB ? want_v : gfr != nullptr, da, db);
-                const float* d = VB ? da : db;
-                const float* sv = VB ? db : da;
-                if (gfr) {
-                    float4 nd = make_float4(d[0], d[1], d[2], d[3]);
-                    if (accF) { nd.x += old.x; nd.y += old.y; nd.z += old.z; nd.w += old.w; }
-                    st_stream(gfr + c, nd);
+            // kSlots float4 per lane per step (256 columns apart), every load
+            // of the step issued before any store.  pow's gradient math is
+            // register-heavy: two slots keep it at 4+ waves per SIMD.
+            constexpr int kSlots = OP == WM_POW ? 2 : 4;
+            const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            float4 s4 = z4;
+            for (int64_t cb = c0 + lane * 4; cb < c1; cb += 256 * kSlots) {
+                float4 vg[kSlots], vf[kSlots], vo[kSlots], old[kSlots];
+#pragma unroll
+                for (int u = 0; u < kSlots; ++u) {
+                    const int64_t c = cb + u * 256;
+                    const bool in = c < c1;
+                    vg[u] = in ? ld_stream(gr + c) : z4;
+                    vf[u] = in && need_F ? ld_stream(fr + c) : z4;
+                    vo[u] = in && need_o ? ld_stream(orow + c) : z4;
+                    old[u] = in && gfr && accF ? ld_stream(gfr + c) : z4;
                 }
-                s4.x += sv[0]; s4.y += sv[1]; s4.z += sv[2]; s4.w += sv[3];
+#pragma unroll
+                for (int u = 0; u < kSlots; ++u) {
+                    const int64_t c = cb + u * 256;
+                    if (c >= c1) continue;
+                    const float e[4] = {vf[u].x, vf[u].y, vf[u].z, vf[u].w},
+                                gg[4] = {vg[u].x, vg[u].y, vg[u].z, vg[u].w},
+                                oo[4] = {vo[u].x, vo[u].y, vo[u].z, vo[u].w}, vv[4] = {v, v, v, v};
+                    float da[4], db[4];
+                    binary_grads_n<OP, 4>(gg, VB ? e : vv, VB ? vv : e, oo, need_o, VB ? gfr != nullptr : want_v,
+                                          VB ? want_v : gfr != nullptr, da, db);
+                    const float* d = VB ? da : db;
+                    const float* sv = VB ? db : da;
+                    if (gfr) {
+                        float4 nd = make_float4(d[0], d[1], d[2], d[3]);
+                        if (accF) { nd.x += old[u].x; nd.y += old[u].y; nd.z += old[u].z; nd.w += old[u].w; }
+                        st_stream(gfr + c, nd);
+                    }
+                    s4.x += sv[0]; s4.y += sv[1]; s4.z += sv[2]; s4.w += sv[3];
+                }
             }
             s = (s4.x + s4.y) + (s4.z + s4.w);
         } else {
@@ -329,7 +361,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
     if (a_full && b_full) {
         if (numel % 4 == 0 && aligned) {
             int64_t n4 = numel / 4;
-            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock, 32)), dim3(kBlock), 0, st, g, a, b, o,
+            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock * 4, 32)), dim3(kBlock), 0, st, g, a, b, o,
                                ga, acc_a, gb, acc_b, n4);
             return check_launch("wm_binary_bwd(flat)");
         }
@@ -350,7 +382,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
         const bool colvec = (nd == 2 && sv[0] == 1 && sv[1] == 0) || (nd == 1 && sv[0] == 0);
         if (rowvec && C % 4 == 0 && aligned) {
             const int64_t col_tiles = (C + kBlock * 4 - 1) / (kBlock * 4);
-            int64_t K = std::min<int64_t>((2048 + col_tiles - 1) / col_tiles, (R + 15) / 16);
+            int64_t K = std::min<int64_t>((1024 + col_tiles - 1) / col_tiles, (R + 15) / 16);
             K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
             const int64_t rpc = (R + K - 1) / K;
             K = (R + rpc - 1) / rpc;

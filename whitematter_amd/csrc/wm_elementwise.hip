@@ -17,6 +17,22 @@ namespace wm {
 constexpr int kBlock = 256;   // 4 waves
 constexpr int kUnroll = 4;    // float4 loads in flight per thread per step
 
+// pow's forward evaluates ~40 vector instructions per element with 16
+// doubles live per float4, so it keeps half as many float4s per thread: at
+// kUnroll it needs ~150 VGPRs (3 waves per SIMD), which leaves too few
+// waves to cover the loads.
+// With that, asking for 6 workgroups of kBlock threads per CU (6 waves per
+// SIMD) caps it at 80 VGPRs, which pow(x, scalar) and pow with one exponent
+// per row meet without spills (two tensor operands would spill).
+template <int OP>
+constexpr int fwd_unroll() {
+    return OP == WM_POW || OP == WM_POWS ? 2 : kUnroll;
+}
+template <int OP>
+constexpr int fwd_min_blocks() {
+    return OP == WM_POW || OP == WM_POWS ? 6 : 1;
+}
+
 // ---------------------------------------------------------------------------
 // Broadcast layout (host)
 // ---------------------------------------------------------------------------
@@ -189,18 +205,19 @@ template <int OP>
 __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__ out, const float* __restrict__ a,
                                                               const float* __restrict__ b, int64_t n4) {
     binary_prologue<OP>();
-    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
-    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
-        float4 va[kUnroll], vb[kUnroll], vr[kUnroll];
+    constexpr int U = fwd_unroll<OP>();
+    const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < n4; base += stride) {
+        float4 va[U], vb[U], vr[U];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
             va[u] = vb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < n4) { va[u] = ld_stream(a + 4 * i); vb[u] = ld_stream(b + 4 * i); }
         }
-        binary_fwd_v<OP, kUnroll>(vr, va, vb);
+        binary_fwd_v<OP, U>(vr, va, vb);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
             if (i < n4) st_stream(out + 4 * i, vr[u]);
         }
@@ -214,11 +231,12 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
 // SA/SB: the operand is streamed (read once: it has a row stride), else it
 // is a row vector reused by every row and stays on cached loads.
 template <int OP, int AI, int BI, bool VEC>
-__global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a,
-                                                              const float* __restrict__ b, int64_t rows, int64_t inner,
-                                                              RowDims d, int stream_a, int stream_b) {
+__global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
+    binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b, int64_t rows,
+                       int64_t inner, RowDims d, int stream_a, int stream_b) {
     binary_prologue<OP>();
-    constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * kUnroll;
+    constexpr int U = fwd_unroll<OP>();
+    constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * U;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
     // Grid-stride over (row, tile) pairs, advanced incrementally so the loop
     // itself divides nothing (a 64-bit division costs ~40 instructions).
@@ -235,11 +253,11 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
         const float* br = b + ob;
         float* orow = out + row * inner;
         if constexpr (VEC) {
-            float4 va[kUnroll], vb[kUnroll], vr[kUnroll];
+            float4 va[U], vb[U], vr[U];
             float sa0 = AI ? 0.f : ar[0];
             float sb0 = BI ? 0.f : br[0];
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
                 va[u] = vb[u] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (c < inner) {
@@ -249,15 +267,15 @@ __global__ void __launch_bounds__(kBlock) binary_rows_kernel(float* __restrict__
                                : make_float4(sb0, sb0, sb0, sb0);
                 }
             }
-            binary_fwd_v<OP, kUnroll>(vr, va, vb);
+            binary_fwd_v<OP, U>(vr, va, vb);
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
                 if (c < inner) st_stream(orow + c, vr[u]);
             }
         } else {
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 int64_t c = c0 + (int64_t)u * kBlock + threadIdx.x;
                 if (c < inner) orow[c] = binary_fwd<OP>(ar[AI ? c : 0], br[BI ? c : 0]);
             }
@@ -298,22 +316,23 @@ __global__ void __launch_bounds__(kBlock) binary_generic_kernel(float* __restric
 }
 
 template <int OP>
-__global__ void __launch_bounds__(kBlock) unary_fwd_kernel(float* __restrict__ out, const float* __restrict__ x,
-                                                            int64_t n, float p0, float p1) {
+__global__ void __launch_bounds__(kBlock, fwd_min_blocks<OP>())
+    unary_fwd_kernel(float* __restrict__ out, const float* __restrict__ x, int64_t n, float p0, float p1) {
     unary_prologue<OP>();
+    constexpr int U = fwd_unroll<OP>();
     const int64_t n4 = n / 4;
-    const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
-    for (int64_t base = (int64_t)blockIdx.x * kBlock * kUnroll + threadIdx.x; base < n4; base += stride) {
-        float4 v[kUnroll], r[kUnroll];
+    const int64_t stride = (int64_t)gridDim.x * kBlock * U;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < n4; base += stride) {
+        float4 v[U], r[U];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
             v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (i < n4) v[u] = ld_stream(x + 4 * i);
         }
-        unary_fwd_v<OP, kUnroll>(r, v, p0, p1);
+        unary_fwd_v<OP, U>(r, v, p0, p1);
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
             if (i < n4) st_stream(out + 4 * i, r[u]);
         }
@@ -394,7 +413,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     // Same shape (or both fully contiguous after folding): flat float4 walk.
     if (nd == 1 && ia == 1 && ib == 1 && (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         int64_t n4 = inner / 4;
-        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * kUnroll, 32)), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
                            out, a, b, n4);
         return check_launch("wm_binary(flat)");
     }
@@ -408,7 +427,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         }
         // float4 path: every row start is a multiple of 4 floats when inner is.
         bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
-        int64_t tile = (vec ? 4 : 1) * kBlock * kUnroll;
+        int64_t tile = (vec ? 4 : 1) * kBlock * fwd_unroll<OP>();
         int64_t tiles = rows * ((inner + tile - 1) / tile);
         dim3 grid(grid_for(tiles, 1, 32));
         // An operand with a row stride is read once; a row vector is re-read by every row.
@@ -447,7 +466,7 @@ template <int OP>
 int launch_unary(float* out, const float* x, int64_t n, float p0, float p1) {
     hipStream_t s = stream();
     if (aligned16(out) && aligned16(x)) {
-        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * kUnroll, 32)), dim3(kBlock), 0, s,
+        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
                            out, x, n, p0, p1);
     } else {
         hipLaunchKernelGGL(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
