@@ -42,13 +42,16 @@ from whitematter_amd import _lib as W  # noqa: E402
 from whitematter_amd import synth  # noqa: E402
 
 PEAK_GBPS = 8000.0  # MI355X HBM3E
+PEAK_F32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
 METRIC = "achieved HBM GB/s (% of MI355X peak) per op; speedup vs host-CPU ref"
+METRIC_MFMA = "achieved fp32 matrix-core TFLOP/s (% of MI355X dense fp32 peak) per op"
 F32 = 4
 
 
 class Op:
-    def __init__(self, name, launch, nbytes, kernel, elems):
+    def __init__(self, name, launch, nbytes, kernel, elems, flops=None):
         self.name, self.launch, self.bytes, self.kernel, self.elems = name, launch, nbytes, kernel, elems
+        self.flops = flops  # set for matrix-core ops: their roofline is TFLOP/s, not HBM
         self.ms = []
 
 
@@ -486,6 +489,38 @@ def norm_ops():
                     % (rows, n, B, C, H, H, AB, AH, T, T, T, T), "elements": NL + NB + NA}
 
 
+def gemm_ops(n=8192, batch=64, t=1024, hd=128):
+    """Matrix-product kernels (include/wm_gemm.h) on the matrix cores, fp32:
+    Tensor::matmul [n, n] @ [n, n] forward and backward (two products), and
+    Tensor::bmm at attention shape [batch, t, hd] @ [batch, hd, t] forward and
+    backward.  flops = 2 m n k per product."""
+    a = W.DeviceArray.from_host(synth.normal((n, n), synth.seed_for(10, 0)))
+    b = W.DeviceArray.from_host(synth.normal((n, n), synth.seed_for(10, 1)))
+    g = W.DeviceArray.from_host(synth.normal((n, n), synth.seed_for(10, 2)))
+    c, ga, gb = W.DeviceArray((n, n)), W.DeviceArray((n, n)), W.DeviceArray((n, n))
+    qa = W.DeviceArray.from_host(synth.normal((batch, t, hd), synth.seed_for(11, 0)))
+    kb = W.DeviceArray.from_host(synth.normal((batch, hd, t), synth.seed_for(11, 1)))
+    sg = W.DeviceArray.from_host(synth.normal((batch, t, t), synth.seed_for(11, 2)))
+    sc, gq, gk = W.DeviceArray((batch, t, t)), W.DeviceArray((batch, t, hd)), W.DeviceArray((batch, hd, t))
+    mm = 2 * n * n * n
+    bm = 2 * batch * t * t * hd
+    ops = [
+        Op("matmul fwd", lambda: W.call("wm_matmul", a.vp, b.vp, n, n, n, c.vp), 3 * n * n * F32, "gemm_kernel", n * n,
+           mm),
+        Op("matmul bwd", lambda: W.call("wm_matmul_bwd", g.vp, a.vp, b.vp, n, n, n, ga.vp, 0, gb.vp, 0),
+           6 * n * n * F32, "gemm_kernel", 2 * n * n, 2 * mm),
+        Op("bmm fwd", lambda: W.call("wm_bmm", qa.vp, kb.vp, batch, t, hd, t, sc.vp),
+           (2 * batch * t * hd + batch * t * t) * F32, "gemm_kernel", batch * t * t, bm),
+        Op("bmm bwd", lambda: W.call("wm_bmm_bwd", sg.vp, qa.vp, kb.vp, batch, t, hd, t, gq.vp, 0, gk.vp, 0),
+           (batch * t * t * 2 + 4 * batch * t * hd) * F32, "gemm_kernel", 2 * batch * t * hd, 2 * bm),
+    ]
+    keep = [a, b, g, c, ga, gb, qa, kb, sg, sc, gq, gk]
+    return ops, keep, {"workload": "gemm: Tensor::matmul [%d,%d]@[%d,%d] and Tensor::bmm [%d,%d,%d]@[%d,%d,%d], fp32 "
+                                   "on v_mfma_f32_32x32x2_f32, forward and backward (gradients overwritten)"
+                                   % (n, n, n, n, batch, t, hd, batch, hd, t),
+                       "elements": n * n + batch * t * t}
+
+
 def traffic_for(op_name: str, config: str):
     """HBM bytes per launch of an op's main kernel, from the committed
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json,
@@ -500,7 +535,7 @@ def traffic_for(op_name: str, config: str):
         return None
 
 
-CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
+CONFIGS = {"gemm": gemm_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
            "norm": norm_ops}
 
 
@@ -557,14 +592,27 @@ def main():
         per_op[op.name] = {"ms": round(ms, 4), "ms_median": round(statistics.median(op.ms), 4),
                            "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
                            "Gelem_per_s": round(op.elems / (ms * 1e-3) / 1e9, 2), "bytes": op.bytes}
-    value = step_bytes / (step_ms * 1e-3) / 1e9
+        if op.flops:
+            tf = op.flops / (ms * 1e-3) / 1e12
+            per_op[op.name].update({"TFLOPs": round(tf, 1), "pct_mfma_peak": round(100 * tf / PEAK_F32_MFMA_TFLOPS, 1),
+                                    "flops": op.flops})
+    mfma = all(op.flops for op in ops)
     dom = max(ops, key=lambda o: statistics.mean(o.ms))
     dom_ms = statistics.mean(dom.ms)
-    dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.name, args.config),
-                "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes,
-                "avg_ms": round(dom_ms, 4)}
+    if mfma:
+        value = sum(op.flops for op in ops) / (step_ms * 1e-3) / 1e12
+        dom_tf = dom.flops / (dom_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(dom_tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(dom_tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": traffic_for(dom.name, args.config),
+                    "kernel": dom.kernel, "op": dom.name, "algorithmic_flops": dom.flops,
+                    "avg_ms": round(dom_ms, 4)}
+    else:
+        value = step_bytes / (step_ms * 1e-3) / 1e9
+        dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.name, args.config),
+                    "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes,
+                    "avg_ms": round(dom_ms, 4)}
 
     # calibration copy kernel (its own launches, after the timed region)
     n_copy = 1 << 28  # 1 GiB
@@ -596,9 +644,9 @@ def main():
                 d["speedup_vs_cpu"] = round(t * scale / d["ms"], 1)
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC_MFMA if mfma else METRIC,
         "value": round(value, 1),
-        "unit": "GB/s",
+        "unit": "TFLOP/s" if mfma else "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -608,7 +656,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded splitmix64 -> Box-Muller fp64 -> fp32, BASELINE config recipe)",
-        "config": dict(workload, pct_of_peak=round(100 * value / PEAK_GBPS, 1), cus=cus,
+        "config": dict(workload, pct_of_peak=round(100 * value / (PEAK_F32_MFMA_TFLOPS if mfma else PEAK_GBPS), 1),
+                       cus=cus,
                        timing="HIP events on the library stream per op; 512 MiB flush between ops "
                               "(untimed); ms_per_step = sum of op kernel times",
                        wall_s_timed_loop=round(wall, 3)),

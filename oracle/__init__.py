@@ -394,6 +394,105 @@ for _name, _fn in _layer_methods().items():
     setattr(Oracle, _name, _fn)
 
 
+def _gemm_sigs(o):
+    if getattr(o, "_gemm_ready", False):
+        return
+    L, vp, i64 = o.L, C.c_void_p, C.c_int64
+    L.or_bmm.argtypes = [vp, vp, i64, i64, i64, i64, vp]
+    L.or_bmm_bwd.argtypes = [vp, vp, vp, i64, i64, i64, i64, vp, vp]
+    L.or_mha_forward.argtypes = [vp] * 4 + [i64] + [vp] * 8 + [i64] * 5 + [vp] * 6
+    L.or_mha_backward.argtypes = [vp] * 13 + [i64] * 5 + [vp] * 11
+    L.or_mha_backward.restype = C.c_int
+    o._gemm_ready = True
+
+
+def _gemm_methods():
+    """Matrix products (Tensor::matmul / bmm) and MultiHeadAttention of an
+    Oracle build.  Inputs are fp32; results are REAL arrays."""
+
+    def bmm(self, a, b):
+        """a [batch, m, k] @ b [batch, k, n] (2-D operands: one product)."""
+        _gemm_sigs(self)
+        a, b = _f32c(a), _f32c(b)
+        two_d = a.ndim == 2
+        a3, b3 = (a[None], b[None]) if two_d else (a, b)
+        P, m, k = a3.shape
+        n = b3.shape[2]
+        c = np.zeros((P, m, n), self.dtype)
+        self.L.or_bmm(_fp(a3), _fp(b3), P, m, k, n, _fp(c))
+        return c[0] if two_d else c
+
+    matmul = bmm
+
+    def bmm_bwd(self, g, a, b, ga0=None, gb0=None, need_a=True, need_b=True):
+        """(ga0 + g @ b^T, gb0 + a^T @ g) per problem; ga0 / gb0 default to 0."""
+        _gemm_sigs(self)
+        g, a, b = _f32c(g), _f32c(a), _f32c(b)
+        two_d = a.ndim == 2
+        g3, a3, b3 = (g[None], a[None], b[None]) if two_d else (g, a, b)
+        P, m, k = a3.shape
+        n = b3.shape[2]
+        ga = (np.array(ga0, self.dtype).reshape(a3.shape) if ga0 is not None else np.zeros(a3.shape, self.dtype))
+        gb = (np.array(gb0, self.dtype).reshape(b3.shape) if gb0 is not None else np.zeros(b3.shape, self.dtype))
+        self.L.or_bmm_bwd(_fp(g3), _fp(a3), _fp(b3), P, m, k, n, _fp(ga) if need_a else None,
+                          _fp(gb) if need_b else None)
+        ga, gb = (ga[0], gb[0]) if two_d else (ga, gb)
+        return (ga if need_a else None), (gb if need_b else None)
+
+    matmul_bwd = bmm_bwd
+
+    def mha_forward(self, q, k, v, params, heads, mask=None):
+        """MultiHeadAttention::forward.  params = (Wq, Wk, Wv, Wo, bq, bk, bv,
+        bo).  Returns dict(out, attn, Q, K, V, ctx).  (The abs build's values
+        are not error scales here: its softmax is not a sum of terms.)"""
+        _gemm_sigs(self)
+        q, k, v = _f32c(q), _f32c(k), _f32c(v)
+        ps = [_f32c(x) for x in params]
+        B, Sq, E = q.shape
+        Sk = k.shape[1]
+        m = _f32c(mask) if mask is not None else None
+        r = {"out": np.zeros((B, Sq, E), self.dtype), "attn": np.zeros((B, heads, Sq, Sk), self.dtype),
+             "Q": np.zeros((B, Sq, E), self.dtype), "K": np.zeros((B, Sk, E), self.dtype),
+             "V": np.zeros((B, Sk, E), self.dtype), "ctx": np.zeros((B, Sq, E), self.dtype)}
+        self.L.or_mha_forward(_fp(q), _fp(k), _fp(v), _fp(m), m.shape[0] if m is not None else 0,
+                              *[_fp(x) for x in ps], B, Sq, Sk, E, heads,
+                              *[_fp(r[x]) for x in ("out", "attn", "Q", "K", "V", "ctx")])
+        return r
+
+    def mha_backward(self, dout, q, k, v, params, heads, saved, need=(True, True, True), alias=False):
+        """The closure: dict of gradients (gWq, gWk, gWv, gWo, gbq, gbk, gbv,
+        gbo, gq, gk, gv) added to zeros.  saved = the forward's Q, K, V, attn,
+        ctx (fp32).  alias: q, k, v are one tensor (self attention), whose
+        gradient collects all three contributions in 'gq'."""
+        _gemm_sigs(self)
+        dout, q, k, v = _f32c(dout), _f32c(q), _f32c(k), _f32c(v)
+        Wq, Wk, Wv, Wo = [_f32c(x) for x in params[:4]]
+        sv = [_f32c(saved[x]) for x in ("Q", "K", "V", "attn", "ctx")]
+        B, Sq, E = q.shape
+        Sk = k.shape[1]
+        z = {n: np.zeros((E, E), self.dtype) for n in ("gWq", "gWk", "gWv", "gWo")}
+        z.update({n: np.zeros(E, self.dtype) for n in ("gbq", "gbk", "gbv", "gbo")})
+        z["gq"] = np.zeros(q.shape, self.dtype) if need[0] else None
+        if alias:
+            z["gk"] = z["gq"] if need[1] else None
+            z["gv"] = z["gq"] if need[2] else None
+        else:
+            z["gk"] = np.zeros(k.shape, self.dtype) if need[1] else None
+            z["gv"] = np.zeros(v.shape, self.dtype) if need[2] else None
+        rc = self.L.or_mha_backward(_fp(dout), _fp(q), _fp(k), _fp(v), _fp(Wq), _fp(Wk), _fp(Wv), _fp(Wo),
+                                    *[_fp(x) for x in sv], B, Sq, Sk, E, heads,
+                                    *[_fp(z[n]) for n in ("gWq", "gWk", "gWv", "gWo", "gbq", "gbk", "gbv", "gbo",
+                                                          "gq", "gk", "gv")])
+        assert rc == 0
+        return z
+
+    return {k: v for k, v in locals().items() if callable(v)}
+
+
+for _name, _fn in _gemm_methods().items():
+    setattr(Oracle, _name, _fn)
+
+
 def get(kind: str) -> Oracle:
     if kind not in _libs:
         _libs[kind] = Oracle(kind)
@@ -506,6 +605,8 @@ class Reference:
             getattr(L, fn).restype = C.c_void_p
         L.wmref_new.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         L.wmref_binary.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
+        L.wmref_matmul.restype = C.c_void_p
+        L.wmref_matmul.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
         L.wmref_unary.argtypes = [C.c_int, C.c_void_p, C.c_float, C.c_float]
         L.wmref_reduce.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int]
         L.wmref_softmax.argtypes = [C.c_int, C.c_void_p, C.c_int]
@@ -616,7 +717,7 @@ class Reference:
         tl.backward()
         return value, tp.grad()
 
-    MODULES = {"layernorm": 0, "batchnorm2d": 1, "mha": 2}
+    MODULES = {"layernorm": 0, "batchnorm2d": 1, "mha": 2, "linear": 3}
 
     def module(self, kind, shape, p0=1e-5, p1=0.1) -> RefModule:
         """LayerNorm(shape, eps=p0), BatchNorm2d(shape[0], eps=p0,
@@ -635,6 +736,12 @@ class Reference:
 
     def binary(self, op, a: RefTensor, b: RefTensor) -> RefTensor:
         return RefTensor(self.L, self.L.wmref_binary(BINARY[op], a.h, b.h))
+
+    def matmul(self, a: RefTensor, b: RefTensor) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_matmul(0, a.h, b.h))
+
+    def bmm(self, a: RefTensor, b: RefTensor) -> RefTensor:
+        return RefTensor(self.L, self.L.wmref_matmul(1, a.h, b.h))
 
     # 0 relu .. 8 clamp as in UNARY; 9 mul(s), 10 div(s), 11 neg
     def unary(self, op, x: RefTensor, p0=0.0, p1=0.0) -> RefTensor:

@@ -101,6 +101,13 @@ void* wmref_binary(int op, void* a, void* b) {
     }
 }
 
+// Tensor::matmul (batched = 0, core/tensor.cpp:783) or Tensor::bmm
+// (batched = 1, :827).
+void* wmref_matmul(int batched, void* a, void* b) {
+    RefFpMode fp_mode_;
+    return box(batched ? T(a)->bmm(T(b)) : T(a)->matmul(T(b)));
+}
+
 // Unary: 0 relu, 1 sigmoid, 2 tanh_, 3 log_, 4 exp_, 5 pow(p0), 6 sqrt,
 // 7 abs, 8 clamp(p0, p1), 9 mul(p0), 10 div(p0), 11 neg.
 void* wmref_unary(int op, void* h, float p0, float p1) {
@@ -275,14 +282,16 @@ void* wmref_loss(int kind, void* pred, void* target, float p0, float p1) {
 
 // Modules of the reference (core/layer.h): 0 LayerNorm(normalized shape,
 // eps = p0), 1 BatchNorm2d(num_features = shape[0], eps = p0, momentum =
-// p1), 2 MultiHeadAttention(embed_dim = shape[0], num_heads = shape[1]).
+// p1), 2 MultiHeadAttention(embed_dim = shape[0], num_heads = shape[1]),
+// 3 Linear(in_features = shape[0], out_features = shape[1]).
 void* wmref_module_new(int kind, const int64_t* shape, int nd, float p0, float p1) {
     RefFpMode fp_mode_;
     std::vector<size_t> s(shape, shape + nd);
     switch (kind) {
         case 0: return new LayerNorm(s, p0);
         case 1: return new BatchNorm2d(s[0], p0, p1);
-        default: return new MultiHeadAttention(s[0], s[1]);
+        case 2: return new MultiHeadAttention(s[0], s[1]);
+        default: return new Linear(s[0], s[1]);
     }
 }
 

@@ -1024,3 +1024,220 @@ int or_dropout_mask(float* mask, int64_t n, float p, uint64_t seed) {
     }
     return 0;
 }
+
+/* ---- matrix products: core/tensor.cpp:281-331, :783-895 ----------------- */
+
+/* Tensor::matmul / bmm forward (:783-795, :827-852) through matmul_blocked
+ * (:281-331): C starts at zero and, for a fixed (i, j), the blocked loop adds
+ * a_ik * b_kj for k ascending (k blocks in order, k in order inside a
+ * block), one product and one addition each.  a [batch, m, k], b [batch, k,
+ * n], c [batch, m, n]. */
+int or_bmm(const float* a, const float* b, int64_t batch, int64_t m, int64_t k, int64_t n, REAL* c) {
+    OR_FP_SCOPE;
+    for (int64_t p = 0; p < batch; p++) {
+        const float* A = a + p * m * k;
+        const float* B = b + p * k * n;
+        REAL* Cp = c + p * m * n;
+        for (int64_t i = 0; i < m; i++)
+            for (int64_t j = 0; j < n; j++) {
+                REAL s = 0;
+                for (int64_t l = 0; l < k; l++) ACC(s, (REAL)A[i * k + l] * (REAL)B[l * n + j]);
+                Cp[i * n + j] = s;
+            }
+    }
+    return 0;
+}
+
+/* Their closures (:797-815, :857-893), adding into ga / gb (NULL = no grad):
+ *   ga[i][l] += sum_j g[i][j] * b[l][j]   (j ascending; simd_dot's scalar
+ *                                           form in a build without AVX)
+ *   gb[l][j] += sum_i a[i][l] * g[i][j]   (i ascending)
+ * Each sum is formed first and then added to the gradient. */
+int or_bmm_bwd(const float* g, const float* a, const float* b, int64_t batch, int64_t m, int64_t k, int64_t n,
+               REAL* ga, REAL* gb) {
+    OR_FP_SCOPE;
+    for (int64_t p = 0; p < batch; p++) {
+        const float* G = g + p * m * n;
+        const float* A = a + p * m * k;
+        const float* B = b + p * k * n;
+        if (ga)
+            for (int64_t i = 0; i < m; i++)
+                for (int64_t l = 0; l < k; l++) {
+                    REAL s = 0;
+                    for (int64_t j = 0; j < n; j++) ACC(s, (REAL)G[i * n + j] * (REAL)B[l * n + j]);
+                    REAL* d = ga + p * m * k + i * k + l;
+                    *d = PLUS(*d, s);
+                }
+        if (gb)
+            for (int64_t l = 0; l < k; l++)
+                for (int64_t j = 0; j < n; j++) {
+                    REAL s = 0;
+                    for (int64_t i = 0; i < m; i++) ACC(s, (REAL)A[i * k + l] * (REAL)G[i * n + j]);
+                    REAL* d = gb + p * k * n + l * n + j;
+                    *d = PLUS(*d, s);
+                }
+    }
+    return 0;
+}
+
+/* ---- MultiHeadAttention: core/layer.cpp:1103-1437 ------------------------- */
+
+/* y[r][d] = bias[d] + sum_k x[r][k] * W[d][k], k ascending, the sum starting
+ * from the bias (:1133-1175, :1262-1276). */
+static void or_proj(const float* x, const float* W, const float* bias, int64_t rows, int64_t E, REAL* y) {
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t d = 0; d < E; d++) {
+            REAL s = (REAL)bias[d];
+            for (int64_t k = 0; k < E; k++) ACC(s, (REAL)x[r * E + k] * (REAL)W[d * E + k]);
+            y[r * E + d] = s;
+        }
+}
+
+/* MultiHeadAttention::forward(query, key, value, mask), :1103-1280.
+ * q [B, Sq, E]; k, v [B, Sk, E]; mask NULL or [Bm, 1, Sq, Sk]; W [E, E]
+ * (row d = output feature d), b [E].  Writes out [B, Sq, E], attn
+ * [B, H, Sq, Sk] and the intermediates the closure captures: Q [B, Sq, E],
+ * K, V [B, Sk, E], ctx [B, Sq, E].  The f32 build rounds every product and
+ * sum as the reference's loops do. */
+int or_mha_forward(const float* q, const float* k, const float* v, const float* mask, int64_t mask_batches,
+                   const float* Wq, const float* Wk, const float* Wv, const float* Wo, const float* bq,
+                   const float* bk, const float* bv, const float* bo, int64_t B, int64_t Sq, int64_t Sk, int64_t E,
+                   int64_t H, REAL* out, REAL* attn, REAL* Q, REAL* K, REAL* V, REAL* ctx) {
+    OR_FP_SCOPE;
+    const int64_t hd = E / H;
+    const float scale = 1.0f / sqrtf((float)hd);
+    or_proj(q, Wq, bq, B * Sq, E, Q);
+    or_proj(k, Wk, bk, B * Sk, E, K);
+    or_proj(v, Wv, bv, B * Sk, E, V);
+    /* scores: dot over the head's slice, times scale, plus the mask (:1180-1208);
+     * softmax over Sk (:1210-1237), as or_attention_softmax. */
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t h = 0; h < H; h++)
+            for (int64_t i = 0; i < Sq; i++) {
+                REAL* ar = attn + ((b * H + h) * Sq + i) * Sk;
+                const float* mr = mask ? mask + ((mask_batches == 1 ? 0 : b) * Sq + i) * Sk : NULL;
+                for (int64_t j = 0; j < Sk; j++) {
+                    REAL dot = 0;
+                    for (int64_t d = 0; d < hd; d++)
+                        ACC(dot, Q[(b * Sq + i) * E + h * hd + d] * K[(b * Sk + j) * E + h * hd + d]);
+                    REAL s = dot * (REAL)scale;
+                    if (mr) s = PLUS(s, (REAL)mr[j]);
+                    ar[j] = s;
+                }
+                REAL mx = (REAL)-3.40282347e+38f;
+                for (int64_t j = 0; j < Sk; j++) mx = (mx < ar[j]) ? ar[j] : mx;
+                REAL sum = 0;
+                for (int64_t j = 0; j < Sk; j++) {
+                    ar[j] = (REAL)exp(ar[j] - mx);
+                    sum += ar[j];
+                }
+                for (int64_t j = 0; j < Sk; j++) ar[j] /= sum;
+            }
+    /* context[b, i, h*hd + d] = sum_j attn * V (:1242-1259) */
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t h = 0; h < H; h++)
+            for (int64_t i = 0; i < Sq; i++)
+                for (int64_t d = 0; d < hd; d++) {
+                    REAL s = 0;
+                    for (int64_t j = 0; j < Sk; j++)
+                        ACC(s, attn[((b * H + h) * Sq + i) * Sk + j] * V[(b * Sk + j) * E + h * hd + d]);
+                    ctx[(b * Sq + i) * E + h * hd + d] = s;
+                }
+    /* output projection (:1262-1276), from the context as stored (fp32 in the
+     * reference; REAL here) */
+    for (int64_t r = 0; r < B * Sq; r++)
+        for (int64_t d = 0; d < E; d++) {
+            REAL s = (REAL)bo[d];
+            for (int64_t kk = 0; kk < E; kk++) ACC(s, ctx[r * E + kk] * (REAL)Wo[d * E + kk]);
+            out[r * E + d] = s;
+        }
+    return 0;
+}
+
+/* Its closure, :1299-1433, given dout [B, Sq, E] and the captured
+ * intermediates (fp32, as the reference stores them).  Parameter gradients
+ * are always added (the reference does not test their requires_grad); gq,
+ * gk, gv may be NULL (input does not require grad) and may alias (self
+ * attention adds all three into one gradient).  Accumulation order follows
+ * the reference's loops: every += goes straight into its target. */
+int or_mha_backward(const float* dout, const float* q, const float* k, const float* v, const float* Wq,
+                    const float* Wk, const float* Wv, const float* Wo, const float* Q, const float* K,
+                    const float* V, const float* attn, const float* ctx, int64_t B, int64_t Sq, int64_t Sk,
+                    int64_t E, int64_t H, REAL* gWq, REAL* gWk, REAL* gWv, REAL* gWo, REAL* gbq, REAL* gbk,
+                    REAL* gbv, REAL* gbo, REAL* gq, REAL* gk, REAL* gv) {
+    OR_FP_SCOPE;
+    const int64_t hd = E / H;
+    const float scale = 1.0f / sqrtf((float)hd);
+    REAL* dctx = (REAL*)calloc((size_t)(B * Sq * E), sizeof(REAL));
+    REAL* dattn = (REAL*)calloc((size_t)(B * H * Sq * Sk), sizeof(REAL));
+    REAL* dV = (REAL*)calloc((size_t)(B * Sk * E), sizeof(REAL));
+    REAL* ds = (REAL*)calloc((size_t)(B * H * Sq * Sk), sizeof(REAL));
+    REAL* dQ = (REAL*)calloc((size_t)(B * Sq * E), sizeof(REAL));
+    REAL* dK = (REAL*)calloc((size_t)(B * Sk * E), sizeof(REAL));
+    if (!dctx || !dattn || !dV || !ds || !dQ || !dK) {
+        free(dctx), free(dattn), free(dV), free(ds), free(dQ), free(dK);
+        return 1;
+    }
+    /* output projection (:1305-1318) */
+    for (int64_t r = 0; r < B * Sq; r++)
+        for (int64_t d = 0; d < E; d++) {
+            const REAL g = (REAL)dout[r * E + d];
+            gbo[d] = PLUS(gbo[d], g);
+            for (int64_t kk = 0; kk < E; kk++) {
+                ACC(gWo[d * E + kk], g * (REAL)ctx[r * E + kk]);
+                ACC(dctx[r * E + kk], g * (REAL)Wo[d * E + kk]);
+            }
+        }
+    /* attn @ V (:1320-1339) */
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t h = 0; h < H; h++)
+            for (int64_t i = 0; i < Sq; i++)
+                for (int64_t d = 0; d < hd; d++) {
+                    const REAL dc = dctx[(b * Sq + i) * E + h * hd + d];
+                    for (int64_t j = 0; j < Sk; j++) {
+                        const int64_t ai = ((b * H + h) * Sq + i) * Sk + j;
+                        const int64_t vi = (b * Sk + j) * E + h * hd + d;
+                        ACC(dattn[ai], dc * (REAL)V[vi]);
+                        ACC(dV[vi], dc * (REAL)attn[ai]);
+                    }
+                }
+    /* softmax (:1341-1360): ds = attn * (dattn - sum(attn * dattn)) */
+    for (int64_t r = 0; r < B * H * Sq; r++) {
+        REAL dot = 0;
+        for (int64_t j = 0; j < Sk; j++) ACC(dot, (REAL)attn[r * Sk + j] * dattn[r * Sk + j]);
+        for (int64_t j = 0; j < Sk; j++) ds[r * Sk + j] = (REAL)attn[r * Sk + j] * MINUS(dattn[r * Sk + j], dot);
+    }
+    /* Q @ K^T (:1362-1383): d_s = ds * scale, then into dQ and dK */
+    for (int64_t b = 0; b < B; b++)
+        for (int64_t h = 0; h < H; h++)
+            for (int64_t i = 0; i < Sq; i++)
+                for (int64_t j = 0; j < Sk; j++) {
+                    const REAL d_s = ds[((b * H + h) * Sq + i) * Sk + j] * (REAL)scale;
+                    for (int64_t d = 0; d < hd; d++) {
+                        const int64_t qi = (b * Sq + i) * E + h * hd + d;
+                        const int64_t ki = (b * Sk + j) * E + h * hd + d;
+                        ACC(dQ[qi], d_s * (REAL)K[ki]);
+                        ACC(dK[ki], d_s * (REAL)Q[qi]);
+                    }
+                }
+    /* V, K, Q projections (:1385-1433) */
+    const struct {
+        const REAL* dY;
+        const float* x;
+        const float* W;
+        REAL *gW, *gb, *gx;
+        int64_t S;
+    } proj[3] = {{dV, v, Wv, gWv, gbv, gv, Sk}, {dK, k, Wk, gWk, gbk, gk, Sk}, {dQ, q, Wq, gWq, gbq, gq, Sq}};
+    for (int t = 0; t < 3; t++)
+        for (int64_t r = 0; r < B * proj[t].S; r++)
+            for (int64_t d = 0; d < E; d++) {
+                const REAL dy = proj[t].dY[r * E + d];
+                proj[t].gb[d] = PLUS(proj[t].gb[d], dy);
+                for (int64_t kk = 0; kk < E; kk++) {
+                    ACC(proj[t].gW[d * E + kk], dy * (REAL)proj[t].x[r * E + kk]);
+                    if (proj[t].gx) ACC(proj[t].gx[r * E + kk], dy * (REAL)proj[t].W[d * E + kk]);
+                }
+            }
+    free(dctx), free(dattn), free(dV), free(ds), free(dQ), free(dK);
+    return 0;
+}

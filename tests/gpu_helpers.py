@@ -264,3 +264,67 @@ def attn_softmax_bwd(attn, d_attn):
     out.fill(np.nan)
     W.call("wm_attention_softmax_bwd", da.vp, dd.vp, attn.size // tk, tk, out.vp)
     return out.to_host()
+
+
+# ---- matrix products (include/wm_gemm.h) ------------------------------------------
+
+def matmul(a, b):
+    """a [m, k] @ b [k, n] (2-D) or bmm for 3-D operands."""
+    da, db = dev(a), dev(b)
+    if a.ndim == 2:
+        m, k = a.shape
+        n = b.shape[1]
+        out = W.DeviceArray((m, n))
+        out.fill(np.nan)
+        W.call("wm_matmul", da.vp, db.vp, m, k, n, out.vp)
+    else:
+        P, m, k = a.shape
+        n = b.shape[2]
+        out = W.DeviceArray((P, m, n))
+        out.fill(np.nan)
+        W.call("wm_bmm", da.vp, db.vp, P, m, k, n, out.vp)
+    return out.to_host()
+
+
+def matmul_bwd(g, a, b, ga0=None, gb0=None, need_a=True, need_b=True):
+    """(ga0 + g @ b^T, gb0 + a^T @ g) per problem through wm_matmul_bwd /
+    wm_bmm_bwd; a gradient without a start value is written (accumulate 0)
+    into a NaN-filled buffer."""
+    dg, da, db = dev(g), dev(a), dev(b)
+    keep = []
+
+    def grad_buf(shape, start, need):
+        if not need:
+            return None, 0
+        if start is not None:
+            d = dev(np.asarray(start, np.float32))
+            keep.append(d)
+            return d, 1
+        d = W.DeviceArray(shape)
+        d.fill(np.nan)
+        keep.append(d)
+        return d, 0
+
+    ga, acc_a = grad_buf(a.shape, ga0, need_a)
+    gb, acc_b = grad_buf(b.shape, gb0, need_b)
+    if a.ndim == 2:
+        m, k = a.shape
+        n = b.shape[1]
+        W.call("wm_matmul_bwd", dg.vp, da.vp, db.vp, m, k, n, W.ptr(ga), acc_a, W.ptr(gb), acc_b)
+    else:
+        P, m, k = a.shape
+        n = b.shape[2]
+        W.call("wm_bmm_bwd", dg.vp, da.vp, db.vp, P, m, k, n, W.ptr(ga), acc_a, W.ptr(gb), acc_b)
+    return (ga.to_host() if ga else None), (gb.to_host() if gb else None)
+
+
+def gemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, c0, ldc, accumulate, bias=None, batch=1, batch_inner=1,
+         strides=None):
+    """wm_gemm on host arrays holding the operands' storage (flat); returns
+    the C storage after the call (c0 is its initial content)."""
+    da, db, dc = dev(np.asarray(a, np.float32)), dev(np.asarray(b, np.float32)), dev(np.asarray(c0, np.float32))
+    dbias = dev(np.asarray(bias, np.float32)) if bias is not None else None
+    st = (C.c_int64 * 6)(*strides) if strides is not None else None
+    W.call("wm_gemm", int(ta), int(tb), m, n, k, C.c_float(alpha), da.vp, lda, db.vp, ldb, dc.vp, ldc,
+           int(accumulate), W.ptr(dbias), batch, batch_inner, st)
+    return dc.to_host()

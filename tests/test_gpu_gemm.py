@@ -1,0 +1,159 @@
+"""GPU parity of the fp32 matrix products (include/wm_gemm.h) through the C
+ABI: Tensor::matmul / Tensor::bmm and their closures (core/tensor.cpp:
+783-895) and the general strided product.
+
+Contract: within 1e-5 of the fp64 oracle (or_bmm / or_bmm_bwd, pinned in
+test_oracle_gemm.py) relative to the abs oracle's sum_k |a_ik * b_kj| (plus
+|C| and |bias| where they are added); bit-exact where every partial sum is
+exact in fp32 (small integers).  Sizes past the oracle's seconds are checked
+against numpy's float64 product, which test_oracle_gemm.py pins to the fp64
+oracle.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from gpu_helpers import gemm, matmul, matmul_bwd, rng_normal, rng_uniform
+
+pytestmark = pytest.mark.gpu
+
+o64, oab = oracle.get("f64"), oracle.get("abs")
+
+
+def close(got, ref, scale, rtol=1e-5):
+    ok, worst = oracle.close_scaled(got, ref, scale, rtol, 1e-30)
+    assert ok, f"{worst:.3g}x tolerance"
+
+
+SHAPES = [(1, 1, 1), (2, 3, 2), (3, 5, 7), (33, 65, 17), (64, 31, 129), (5, 1, 4), (7, 40, 1), (128, 32, 128),
+          (128, 64, 256), (129, 33, 127), (256, 100, 200), (300, 513, 257)]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+def test_matmul_forward(wm, shape):
+    m, k, n = shape
+    a, b = rng_normal((m, k), 1), rng_normal((k, n), 2)
+    close(matmul(a, b), o64.matmul(a, b), oab.matmul(a, b))
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_matmul_backward(wm, shape, accumulate):
+    m, k, n = shape
+    a, b, g = rng_normal((m, k), 3), rng_normal((k, n), 4), rng_normal((m, n), 5)
+    ga0 = rng_normal((m, k), 6) if accumulate else None
+    gb0 = rng_normal((k, n), 7) if accumulate else None
+    ga, gb = matmul_bwd(g, a, b, ga0, gb0)
+    ra, rb = o64.matmul_bwd(g, a, b, ga0, gb0)
+    sa, sb = oab.matmul_bwd(g, a, b, None if ga0 is None else np.abs(ga0), None if gb0 is None else np.abs(gb0))
+    close(ga, ra, sa)
+    close(gb, rb, sb)
+
+
+@pytest.mark.parametrize("need", [(True, False), (False, True)])
+def test_matmul_backward_one_side(wm, need):
+    a, b, g = rng_normal((40, 24), 8), rng_normal((24, 56), 9), rng_normal((40, 56), 10)
+    ga, gb = matmul_bwd(g, a, b, need_a=need[0], need_b=need[1])
+    ra, rb = o64.matmul_bwd(g, a, b)
+    sa, sb = oab.matmul_bwd(g, a, b)
+    assert (ga is None) != need[0] and (gb is None) != need[1]
+    if need[0]:
+        close(ga, ra, sa)
+    else:
+        close(gb, rb, sb)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 3, 2), (2, 2, 3, 2), (4, 33, 17, 65), (3, 128, 64, 128), (6, 70, 129, 40)],
+                         ids=str)
+def test_bmm_forward_backward(wm, shape):
+    P, m, k, n = shape
+    a, b, g = rng_normal((P, m, k), 11), rng_normal((P, k, n), 12), rng_normal((P, m, n), 13)
+    close(matmul(a, b), o64.bmm(a, b), oab.bmm(a, b))
+    ga0, gb0 = rng_normal((P, m, k), 14), rng_normal((P, k, n), 15)
+    ga, gb = matmul_bwd(g, a, b, ga0, gb0)
+    ra, rb = o64.bmm_bwd(g, a, b, ga0, gb0)
+    sa, sb = oab.bmm_bwd(g, a, b, np.abs(ga0), np.abs(gb0))
+    close(ga, ra, sa)
+    close(gb, rb, sb)
+
+
+def test_known_answer_and_small_integers_exact(wm):
+    a = np.float32([1, 2, 3, 4, 5, 6]).reshape(2, 3)
+    assert np.array_equal(matmul(a, a.reshape(3, 2)), [[22, 28], [49, 64]])  # test_tensor.cpp matmul_2d
+    for m, k, n, seed in ((17, 23, 11, 20), (130, 70, 129, 21), (256, 256, 256, 22)):
+        r = np.random.default_rng(seed)
+        ai = r.integers(-8, 9, (m, k)).astype(np.float32)
+        bi = r.integers(-8, 9, (k, n)).astype(np.float32)
+        gi = r.integers(-4, 5, (m, n)).astype(np.float32)
+        exact = ai.astype(np.int64) @ bi.astype(np.int64)
+        assert np.array_equal(matmul(ai, bi), exact)
+        ga, gb = matmul_bwd(gi, ai, bi)
+        assert np.array_equal(ga, gi.astype(np.int64) @ bi.astype(np.int64).T)
+        assert np.array_equal(gb, ai.astype(np.int64).T @ gi.astype(np.int64))
+
+
+def op_store(x, trans, ld):
+    """Row-major storage of op(X) = x (trans: store x^T) with row stride ld."""
+    s = x.T if trans else x
+    buf = np.full((s.shape[0], ld), np.nan, np.float32)
+    buf[:, :s.shape[1]] = s
+    return buf
+
+
+@pytest.mark.parametrize("trans", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=lambda t: "NT"[t[0]] + "NT"[t[1]])
+@pytest.mark.parametrize("mnk", [(1, 1, 1), (5, 3, 7), (128, 128, 32), (130, 129, 33), (257, 64, 100),
+                                 (64, 300, 513)], ids=str)
+@pytest.mark.parametrize("pad", [0, 3, 4])
+def test_gemm_transposes_strides_alpha_accumulate_bias(wm, trans, mnk, pad):
+    ta, tb = trans
+    m, n, k = mnk
+    A, B = rng_normal((m, k), 30), rng_normal((k, n), 31)
+    C0, bias = rng_normal((m, n), 32), rng_normal((n,), 33)
+    sa, sb = op_store(A, ta, (m if ta else k) + pad), op_store(B, tb, (k if tb else n) + pad)
+    ldc = n + pad
+    c0 = np.full((m, ldc), 7.0, np.float32)
+    c0[:, :n] = C0
+    alpha = 0.375
+    got = gemm(ta, tb, m, n, k, alpha, sa, sa.shape[1], sb, sb.shape[1], c0, ldc, True, bias)
+    ref = alpha * o64.matmul(A, B) + C0 + bias
+    scale = alpha * oab.matmul(A, B) + np.abs(C0) + np.abs(bias)
+    close(got[:, :n], ref, scale)
+    assert np.all(got[:, n:] == 7.0)  # the row padding of C is untouched
+    # overwrite, no bias
+    got = gemm(ta, tb, m, n, k, 1.0, sa, sa.shape[1], sb, sb.shape[1], c0, ldc, False)
+    close(got[:, :n], o64.matmul(A, B), oab.matmul(A, B))
+
+
+def test_gemm_k_zero_and_empty(wm):
+    c0 = rng_normal((3, 4), 40)
+    bias = rng_normal((4,), 41)
+    got = gemm(0, 0, 3, 4, 0, 1.0, np.zeros(1, np.float32), 1, np.zeros(1, np.float32), 4, c0, 4, True, bias)
+    assert np.array_equal(got, c0 + bias)
+    got = gemm(0, 0, 3, 4, 0, 1.0, np.zeros(1, np.float32), 1, np.zeros(1, np.float32), 4, c0, 4, False)
+    assert np.array_equal(got, np.zeros((3, 4), np.float32))
+    assert matmul(np.zeros((0, 5), np.float32), rng_normal((5, 3), 42)).shape == (0, 3)
+
+
+def test_gemm_two_level_batch_per_head_slices(wm):
+    """scores[b, h] = Q[b, :, h] @ K[b, :, h]^T * alpha on [B, S, H * hd]
+    activations, as MultiHeadAttention slices its heads."""
+    B, Sq, Sk, H, hd = 3, 37, 45, 4, 16
+    E = H * hd
+    Q, K = rng_normal((B, Sq, E), 43), rng_normal((B, Sk, E), 44)
+    out = np.full((B, H, Sq, Sk), np.nan, np.float32)
+    alpha = 0.25
+    got = gemm(0, 1, Sq, Sk, hd, alpha, Q, E, K, E, out, Sk, False, None, B * H, H,
+               (Sq * E, hd, Sk * E, hd, H * Sq * Sk, Sq * Sk))
+    Qh = Q.reshape(B, Sq, H, hd).transpose(0, 2, 1, 3).reshape(B * H, Sq, hd)
+    Kh = K.reshape(B, Sk, H, hd).transpose(0, 2, 3, 1).reshape(B * H, hd, Sk)
+    ref = alpha * o64.bmm(np.ascontiguousarray(Qh), np.ascontiguousarray(Kh))
+    scale = alpha * oab.bmm(np.ascontiguousarray(Qh), np.ascontiguousarray(Kh))
+    close(got.reshape(B * H, Sq, Sk), ref, scale)
+
+
+@pytest.mark.parametrize("shape", [(2048, 2048, 2048), (1500, 900, 1700), (4096, 1024, 4096)], ids=str)
+def test_matmul_large_vs_float64(wm, shape):
+    m, k, n = shape
+    a, b = rng_normal((m, k), 50), rng_uniform((k, n), 51, -1.0, 1.0)
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    close(matmul(a, b), a64 @ b64, np.abs(a64) @ np.abs(b64))

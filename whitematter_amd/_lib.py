@@ -1,5 +1,4 @@
-"""ctypes binding of libwm_hip.so (the C ABI declared in include/wm_hip.h and
-include/wm_optim.h).
+"""ctypes binding of libwm_hip.so (the C ABI declared in include/*.h).
 
 The library is the product: every call here launches hand-written HIP
 kernels on the GPU.  There is deliberately no CPU fallback -- if the shared
@@ -103,6 +102,13 @@ _SIGS = {
     "wm_attention_softmax_fwd": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
     "wm_attention_softmax_bwd": [_vp, _vp, C.c_int64, C.c_int64, _vp],
     "wm_dropout_mask": [_vp, C.c_int64, C.c_float, C.c_uint64],
+    # include/wm_gemm.h
+    "wm_gemm": [C.c_int, C.c_int, C.c_int64, C.c_int64, C.c_int64, C.c_float, _vp, C.c_int64, _vp, C.c_int64,
+                _vp, C.c_int64, C.c_int, _vp, C.c_int64, C.c_int64, _i64p],
+    "wm_matmul": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, _vp],
+    "wm_matmul_bwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int],
+    "wm_bmm": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
+    "wm_bmm_bwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int],
 }
 
 # enum wm_pointwise_loss

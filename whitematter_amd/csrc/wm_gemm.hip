@@ -1,0 +1,373 @@
+// wm_gemm.hip -- fp32 matrix products on the gfx950 matrix cores
+// (include/wm_gemm.h): Tensor::matmul / bmm and their backward
+// (core/tensor.cpp:783-895), and the strided product the drop-in Linear and
+// MultiHeadAttention modules use.
+//
+// One kernel covers every case.  A workgroup of 4 waves computes a 128 x 128
+// tile of C; each wave a 64 x 64 quarter as 2 x 2 blocks of
+// v_mfma_f32_32x32x2_f32.  k advances in stages of 32: the next stage's tiles
+// of op(A) and op(B) are loaded from HBM into registers while the matrix
+// cores work on the current ones from LDS (two LDS buffers, one barrier per
+// stage).
+//
+// Each operand tile keeps its HBM orientation in LDS, so every global load
+// is a float4 along the contiguous dimension and every LDS write is a plain
+// vector store:
+//   k-contiguous operands (A untransposed, B transposed): LDS [row][k] with a
+//     36-float pitch; an MFMA fragment is four 16-byte LDS reads;
+//   row-contiguous operands (A transposed, B untransposed): LDS [k][row]
+//     with a 130-float pitch; a fragment is one 4-byte read per k.
+// An MFMA step takes two k values per lane (one per half-wave).  Which k
+// goes to which step is free as long as A and B agree: half h takes
+// k = 16h .. 16h+15 of the stage.  The pitches keep a quarter-wave's reads
+// on distinct banks, and the two half-waves' rows 16 k apart on opposite
+// halves of the banks (16 * 130 = 32 mod 64).
+//
+// Interior tiles load and store without bounds checks; tiles on the edge of
+// C or the last k stage take an element-wise path that reads only inside
+// the operands and zero-fills the rest.
+//
+// Sums are fp32 in the matrix cores' order (see include/wm_gemm.h).
+#include "wm_common.hpp"
+
+#include "../../include/wm_gemm.h"
+
+#include <algorithm>
+
+namespace wm {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kTile = 128;      // C tile rows and columns per workgroup
+constexpr int kBK = 32;         // k per stage
+constexpr int kPitchK = kBK + 4;      // LDS [row][k] pitch (floats)
+constexpr int kPitchR = kTile + 2;    // LDS [k][row] pitch (floats)
+constexpr int kThreads = 256;   // 4 waves as 2 x 2, each 64 x 64 of C
+constexpr int kOperandFloats = kTile * kPitchK > kBK * kPitchR ? kTile * kPitchK : kBK * kPitchR;
+
+struct GemmParams {
+    const float* a;
+    const float* b;
+    float* c;
+    const float* bias;
+    int64_t m, n, k, lda, ldb, ldc;
+    int64_t batch, batch_inner;
+    int64_t sa0, sa1, sb0, sb1, sc0, sc1;
+    float alpha;
+    int accumulate;
+    int tiles_m, tiles_n;
+};
+
+// One operand's 128 x 32 tile per stage (rows of op(A), or columns of
+// op(B), by k).  KC: element (r, kk) at base[r * ld + kk], else at
+// base[kk * ld + r].  Each thread moves four float4s:
+//   KC:  slot i = row t/8 + 32 i, k 4 (t % 8) .. + 3      -> LDS [row][k]
+//   !KC: slot i = k t/32 + 8 i, rows 4 (t % 32) .. + 3     -> LDS [k][row]
+template <bool KC>
+struct Operand {
+    const float* base;
+    int64_t ld, rows, r0;
+    int64_t lane_off;  // this thread's first element relative to (r0, k0 = 0)
+    float4 v[4];
+
+    __device__ __forceinline__ void init(const float* b, int64_t ld_, int64_t rows_, int64_t r0_) {
+        const int t = (int)threadIdx.x;
+        base = b;
+        ld = ld_;
+        rows = rows_;
+        r0 = r0_;
+        lane_off = KC ? (r0 + t / 8) * ld + 4 * (t % 8) : (int64_t)(t / 32) * ld + r0 + 4 * (t % 32);
+    }
+
+    // Interior tile, whole stage inside k, 16-byte aligned rows.
+    __device__ __forceinline__ void load_fast(int64_t k0) {
+        const float* p = base + lane_off + (KC ? k0 : k0 * ld);
+        const int64_t step = KC ? 32 * ld : 8 * ld;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const float4*>(p + i * step);
+    }
+
+    // Any tile: element by element, reading only inside rows x kdim.
+    __device__ __forceinline__ void load_edge(int64_t kdim, int64_t k0) {
+        const int t = (int)threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t r = KC ? r0 + t / 8 + 32 * i : r0 + 4 * (t % 32) + j;
+                const int64_t kk = KC ? k0 + 4 * (t % 8) + j : k0 + t / 32 + 8 * i;
+                e[j] = (r < rows && kk < kdim) ? (KC ? base[r * ld + kk] : base[kk * ld + r]) : 0.0f;
+            }
+            v[i] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    }
+
+    __device__ __forceinline__ void store(float* lds) const {
+        const int t = (int)threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (KC) {
+                *reinterpret_cast<float4*>(lds + (t / 8 + 32 * i) * kPitchK + 4 * (t % 8)) = v[i];
+            } else {
+                float* q = lds + (t / 32 + 8 * i) * kPitchR + 4 * (t % 32);
+                *reinterpret_cast<float2*>(q) = make_float2(v[i].x, v[i].y);
+                *reinterpret_cast<float2*>(q + 2) = make_float2(v[i].z, v[i].w);
+            }
+        }
+    }
+
+    // Fragment values of tile row `row`, k = kk .. kk + 3 of the stage.
+    __device__ __forceinline__ static float4 frag(const float* lds, int row, int kk) {
+        if constexpr (KC) {
+            return *reinterpret_cast<const float4*>(lds + row * kPitchK + kk);
+        } else {
+            return make_float4(lds[kk * kPitchR + row], lds[(kk + 1) * kPitchR + row], lds[(kk + 2) * kPitchR + row],
+                               lds[(kk + 3) * kPitchR + row]);
+        }
+    }
+};
+
+// Tile order inside one problem: groups of 8 tile-rows walked column by
+// column, so the workgroups resident at one time share panels of A and B.
+__device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int kGroup = 8;
+    const int per_group = kGroup * tiles_n;
+    const int g = t / per_group;
+    const int first = g * kGroup;
+    const int rows = min(tiles_m - first, kGroup);
+    const int in = t - g * per_group;
+    tm = first + in % rows;
+    tn = in / rows;
+}
+
+template <bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
+    __shared__ __attribute__((aligned(16))) float lds[2][2][kOperandFloats];  // [stage][A, B]
+
+    const int ntiles = P.tiles_m * P.tiles_n;
+    // Workgroups are dealt to the 8 XCDs in turn; renumber them so each XCD
+    // (own L2) takes a contiguous run of tiles.
+    int t = (int)blockIdx.x;
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    int tm, tn;
+    tile_of(t, P.tiles_m, P.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+    const bool interior = VEC && m0 + kTile <= P.m && n0 + kTile <= P.n;
+
+    const int lane = (int)threadIdx.x & 63;
+    const int wave = (int)threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, r = lane & 31;
+    const int nk = (int)((P.k + kBK - 1) / kBK);
+    const int nk_fast = interior ? (int)(P.k / kBK) : 0;  // stages that take the unchecked loads
+
+    // op(A) row r, k kk: A[r * lda + kk] (TA = 0) or A[kk * lda + r].
+    // op(B) column r, k kk: B[kk * ldb + r] (TB = 0) or B[r * ldb + kk].
+    using OpA = Operand<!TA>;
+    using OpB = Operand<TB>;
+
+    for (int64_t p = blockIdx.y; p < P.batch; p += gridDim.y) {
+        const int64_t po = p / P.batch_inner, pi = p - po * P.batch_inner;
+        OpA a;
+        OpB b;
+        a.init(P.a + po * P.sa0 + pi * P.sa1, P.lda, P.m, m0);
+        b.init(P.b + po * P.sb0 + pi * P.sb1, P.ldb, P.n, n0);
+        float* C = P.c + po * P.sc0 + pi * P.sc1;
+
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+        if (nk > 0) {
+            if (nk_fast > 0) {
+                a.load_fast(0);
+                b.load_fast(0);
+            } else {
+                a.load_edge(P.k, 0);
+                b.load_edge(P.k, 0);
+            }
+            a.store(lds[0][0]);
+            b.store(lds[0][1]);
+        }
+        __syncthreads();
+
+        for (int s = 0; s < nk; ++s) {
+            const int cur = s & 1;
+            const bool more = s + 1 < nk;
+            if (more) {
+                const int64_t k0 = (int64_t)(s + 1) * kBK;
+                if (s + 1 < nk_fast) {
+                    a.load_fast(k0);
+                    b.load_fast(k0);
+                } else {
+                    a.load_edge(P.k, k0);
+                    b.load_edge(P.k, k0);
+                }
+            }
+            const float* As = lds[cur][0];
+            const float* Bs = lds[cur][1];
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) {
+                const int kk = 16 * half + 4 * kq;
+                float4 av[2], bv[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) av[i] = OpA::frag(As, wm * 64 + i * 32 + r, kk);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) bv[j] = OpB::frag(Bs, wn * 64 + j * 32 + r, kk);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+                    }
+            }
+            if (more) {
+                a.store(lds[cur ^ 1][0]);
+                b.store(lds[cur ^ 1][1]);
+            }
+            __syncthreads();
+        }
+
+        // Accumulator element q of a 32 x 32 block sits at row
+        // 8 * (q / 4) + 4 * half + q % 4, column r.
+        const float alpha = P.alpha;
+        const bool accum = P.accumulate != 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t row0 = m0 + wm * 64 + i * 32 + 4 * half;
+                const int64_t col = n0 + wn * 64 + j * 32 + r;
+                if (!interior && col >= P.n) continue;
+                const float bcol = P.bias ? P.bias[col] : 0.0f;
+                float* c0 = C + row0 * P.ldc + col;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int dr = 8 * (q >> 2) + (q & 3);
+                    if (!interior && row0 + dr >= P.m) continue;
+                    float* dst = c0 + dr * P.ldc;
+                    float v = alpha * acc[i][j][q];
+                    if (accum) v = *dst + v;
+                    if (P.bias) v = v + bcol;
+                    *dst = v;
+                }
+            }
+        __syncthreads();  // the next problem's first stage reuses LDS buffer 0
+    }
+}
+
+int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
+    GemmParams P = P0;
+    const int64_t tm = (P.m + kTile - 1) / kTile, tn = (P.n + kTile - 1) / kTile;
+    if (tm * tn > (int64_t)0x7fffffff) return set_error(WM_ERR_INVALID, "wm_gemm: too many tiles");
+    P.tiles_m = (int)tm;
+    P.tiles_n = (int)tn;
+    // The unchecked float4 loads need 16-byte aligned rows in both operands.
+    const bool vec = P.lda % 4 == 0 && P.ldb % 4 == 0 && aligned16(P.a) && aligned16(P.b) &&
+                     (P.batch == 1 || (P.sa0 % 4 == 0 && P.sa1 % 4 == 0 && P.sb0 % 4 == 0 && P.sb1 % 4 == 0));
+    dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch, 65535));
+    hipStream_t s = stream();
+#define WM_GEMM(TA, TB, V) hipLaunchKernelGGL((gemm_kernel<TA, TB, V>), grid, dim3(kThreads), 0, s, P)
+    if (vec) {
+        if (!ta && !tb) WM_GEMM(false, false, true);
+        else if (!ta && tb) WM_GEMM(false, true, true);
+        else if (ta && !tb) WM_GEMM(true, false, true);
+        else WM_GEMM(true, true, true);
+    } else {
+        if (!ta && !tb) WM_GEMM(false, false, false);
+        else if (!ta && tb) WM_GEMM(false, true, false);
+        else if (ta && !tb) WM_GEMM(true, false, false);
+        else WM_GEMM(true, true, false);
+    }
+#undef WM_GEMM
+    return check_launch("wm_gemm");
+}
+
+}  // namespace
+}  // namespace wm
+
+using namespace wm;
+
+int wm_gemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, const float* a, int64_t lda,
+            const float* b, int64_t ldb, float* c, int64_t ldc, int accumulate, const float* bias, int64_t batch,
+            int64_t batch_inner, const int64_t* strides) {
+    if (m < 0 || n < 0 || k < 0 || batch < 0) return set_error(WM_ERR_INVALID, "wm_gemm: negative extent");
+    if (batch_inner < 1 || (batch > 0 && batch % batch_inner != 0))
+        return set_error(WM_ERR_INVALID, "wm_gemm: batch_inner must divide batch");
+    if (m == 0 || n == 0 || batch == 0) return WM_OK;
+    if (batch > 1 && !strides) return set_error(WM_ERR_INVALID, "wm_gemm: batch > 1 needs strides");
+    if (!c || (k > 0 && (!a || !b))) return set_error(WM_ERR_INVALID, "wm_gemm: null pointer");
+    const int64_t a_cols = trans_a ? m : k, b_cols = trans_b ? k : n;
+    if (lda < std::max<int64_t>(1, a_cols) || ldb < std::max<int64_t>(1, b_cols) || ldc < n)
+        return set_error(WM_ERR_INVALID, "wm_gemm: leading dimension smaller than a row");
+    WM_CHECK_INIT();
+    GemmParams P{};
+    P.a = a;
+    P.b = b;
+    P.c = c;
+    P.bias = bias;
+    P.m = m;
+    P.n = n;
+    P.k = k;
+    P.lda = lda;
+    P.ldb = ldb;
+    P.ldc = ldc;
+    P.batch = batch;
+    P.batch_inner = batch_inner;
+    if (strides) {
+        P.sa0 = strides[0];
+        P.sa1 = strides[1];
+        P.sb0 = strides[2];
+        P.sb1 = strides[3];
+        P.sc0 = strides[4];
+        P.sc1 = strides[5];
+    }
+    P.alpha = alpha;
+    P.accumulate = accumulate ? 1 : 0;
+    return launch_gemm(trans_a != 0, trans_b != 0, P);
+}
+
+int wm_matmul(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c) {
+    return wm_gemm(0, 0, m, n, k, 1.0f, a, std::max<int64_t>(k, 1), b, std::max<int64_t>(n, 1), c, n, 0, nullptr, 1,
+                   1, nullptr);
+}
+
+int wm_matmul_bwd(const float* g, const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* ga,
+                  int accumulate_a, float* gb, int accumulate_b) {
+    if (m < 0 || k < 0 || n < 0) return set_error(WM_ERR_INVALID, "wm_matmul_bwd: negative extent");
+    const int64_t k1 = std::max<int64_t>(k, 1), n1 = std::max<int64_t>(n, 1);
+    if (ga) WM_TRY(wm_gemm(0, 1, m, k, n, 1.0f, g, n1, b, n1, ga, k, accumulate_a, nullptr, 1, 1, nullptr));
+    if (gb) WM_TRY(wm_gemm(1, 0, k, n, m, 1.0f, a, k1, g, n1, gb, n, accumulate_b, nullptr, 1, 1, nullptr));
+    return WM_OK;
+}
+
+int wm_bmm(const float* a, const float* b, int64_t batch, int64_t m, int64_t k, int64_t n, float* c) {
+    if (batch < 0 || m < 0 || k < 0 || n < 0) return set_error(WM_ERR_INVALID, "wm_bmm: negative extent");
+    const int64_t st[6] = {m * k, 0, k * n, 0, m * n, 0};
+    return wm_gemm(0, 0, m, n, k, 1.0f, a, std::max<int64_t>(k, 1), b, std::max<int64_t>(n, 1), c, n, 0, nullptr,
+                   batch, 1, st);
+}
+
+int wm_bmm_bwd(const float* g, const float* a, const float* b, int64_t batch, int64_t m, int64_t k, int64_t n,
+               float* ga, int accumulate_a, float* gb, int accumulate_b) {
+    if (batch < 0 || m < 0 || k < 0 || n < 0) return set_error(WM_ERR_INVALID, "wm_bmm_bwd: negative extent");
+    const int64_t k1 = std::max<int64_t>(k, 1), n1 = std::max<int64_t>(n, 1);
+    if (ga) {
+        const int64_t st[6] = {m * n, 0, k * n, 0, m * k, 0};
+        WM_TRY(wm_gemm(0, 1, m, k, n, 1.0f, g, n1, b, n1, ga, k, accumulate_a, nullptr, batch, 1, st));
+    }
+    if (gb) {
+        const int64_t st[6] = {m * k, 0, m * n, 0, k * n, 0};
+        WM_TRY(wm_gemm(1, 0, k, n, m, 1.0f, a, k1, g, n1, gb, n, accumulate_b, nullptr, batch, 1, st));
+    }
+    return WM_OK;
+}
