@@ -1,9 +1,10 @@
 /*
  * wm_gemm.h -- C ABI of libwm_hip's fp32 matrix products on the MFMA
  * matrix cores: Tensor::matmul and Tensor::bmm (reference
- * core/tensor.cpp:783-895) with their backward, and the general strided
- * product the drop-in Linear and MultiHeadAttention modules are built on
- * (core/layer.cpp:13-15, :1103-1400).
+ * core/tensor.cpp:783-895) with their backward, Tensor::transpose
+ * (:2223-2248), and the general strided product the drop-in Linear and
+ * MultiHeadAttention modules are built on (core/layer.cpp:13-15,
+ * :1103-1437).
  *
  * Conventions are those of wm_hip.h: status codes, wm_last_error(), device
  * pointers to row-major fp32, one library stream.  Gradient outputs take an
@@ -65,6 +66,12 @@ int wm_bmm(const float* a, const float* b, int64_t batch, int64_t m, int64_t k, 
  * gb[p] (+)= a[p]^T @ g[p].                                                  */
 int wm_bmm_bwd(const float* g, const float* a, const float* b, int64_t batch, int64_t m, int64_t k, int64_t n,
                float* ga, int accumulate_a, float* gb, int accumulate_b);
+
+/* Tensor::transpose, core/tensor.cpp:2223-2248, and its closure:
+ *   out[c][r] (+)= x[r][c]  for x [rows, cols], out [cols, rows].
+ * The forward writes (accumulate 0); the closure adds the transposed
+ * gradient (accumulate 1).  x and out must not overlap.                      */
+int wm_transpose2d(const float* x, int64_t rows, int64_t cols, float* out, int accumulate);
 
 #ifdef __cplusplus
 }

@@ -1,8 +1,9 @@
 /*
- * wm_layers.h -- C ABI of libwm_hip's normalisation and attention-softmax
- * kernels: the reduction / softmax work inside whitematter's LayerNorm,
- * BatchNorm2d and MultiHeadAttention modules (reference core/layer.cpp),
- * which the reference writes as raw host loops that bypass its Tensor ops.
+ * wm_layers.h -- C ABI of libwm_hip's normalisation and attention kernels:
+ * the reduction / softmax work inside whitematter's LayerNorm, BatchNorm2d
+ * and MultiHeadAttention modules (reference core/layer.cpp), which the
+ * reference writes as raw host loops that bypass its Tensor ops, and the
+ * whole MultiHeadAttention forward and closure on top of them.
  *
  * Conventions are those of wm_hip.h: status codes, wm_last_error(), device
  * pointers to contiguous row-major fp32, one library stream, and for every
@@ -88,6 +89,35 @@ int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t row
  * cannot reproduce -- the distribution is the same, the bits are not).
  * The drop-in multiplies the input by this mask.                           */
 int wm_dropout_mask(float* mask, int64_t n, float p, uint64_t seed);
+
+/* MultiHeadAttention::forward(query, key, value, mask), core/layer.cpp:
+ * 1103-1280, with heads = num_heads, hd = embed / heads:
+ *   Q = q Wq^T + bq;  K = k Wk^T + bk;  V = v Wv^T + bv
+ *   attn[b, h] = softmax(Q_h K_h^T * (1 / sqrt(hd)) + mask[b or 0])
+ *   ctx[b, :, h] = attn[b, h] V_h;  out = ctx Wo^T + bo
+ * where X_h is the h-th hd-wide column block of X.  q [B, Sq, E]; k, v
+ * [B, Sk, E]; W* [E, E] (row = output feature); b* [E]; mask NULL or
+ * [mask_batches, 1, Sq, Sk] with mask_batches 1 or B.  Writes out [B, Sq, E]
+ * and the values the reference's closure captures: Q [B, Sq, E], K, V
+ * [B, Sk, E], attn [B, H, Sq, Sk] (the module's attn_weights), ctx
+ * [B, Sq, E].  Products on the matrix cores (include/wm_gemm.h), the mask
+ * and softmax by wm_attention_softmax_fwd.                                   */
+int wm_mha_fwd(const float* q, const float* k, const float* v, const float* mask, int64_t mask_batches,
+               const float* Wq, const float* Wk, const float* Wv, const float* Wo, const float* bq, const float* bk,
+               const float* bv, const float* bo, int64_t batch, int64_t seq_q, int64_t seq_k, int64_t embed,
+               int64_t heads, float* out, float* attn, float* Q, float* K, float* V, float* ctx);
+
+/* Its closure, core/layer.cpp:1299-1433, given dout = dL/dout and the
+ * captured Q, K, V, attn, ctx.  Every gradient is added to (+=), as the
+ * reference's loops do; the eight parameter gradients are always written
+ * (the reference does not test their requires_grad); gq, gk, gv may be NULL
+ * (that input does not require grad) and may be the same buffer (self
+ * attention: the V, K and Q projections add into it in that order).         */
+int wm_mha_bwd(const float* dout, const float* q, const float* k, const float* v, const float* Wq, const float* Wk,
+               const float* Wv, const float* Wo, const float* Q, const float* K, const float* V, const float* attn,
+               const float* ctx, int64_t batch, int64_t seq_q, int64_t seq_k, int64_t embed, int64_t heads,
+               float* gWq, float* gWk, float* gWv, float* gWo, float* gbq, float* gbk, float* gbv, float* gbo,
+               float* gq, float* gk, float* gv);
 
 #ifdef __cplusplus
 }

@@ -328,3 +328,71 @@ def gemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, c0, ldc, accumulate, bias=None,
     W.call("wm_gemm", int(ta), int(tb), m, n, k, C.c_float(alpha), da.vp, lda, db.vp, ldb, dc.vp, ldc,
            int(accumulate), W.ptr(dbias), batch, batch_inner, st)
     return dc.to_host()
+
+
+def mha_fwd(q, k, v, params, heads, mask=None):
+    """wm_mha_fwd; returns dict(out, attn, Q, K, V, ctx) as host arrays."""
+    B, Sq, E = q.shape
+    Sk = k.shape[1]
+    d_in = [dev(x) for x in (q, k, v)]
+    dm = dev(mask) if mask is not None else None
+    dp = [dev(np.asarray(p, np.float32)) for p in params]
+    outs = {"out": (B, Sq, E), "attn": (B, heads, Sq, Sk), "Q": (B, Sq, E), "K": (B, Sk, E), "V": (B, Sk, E),
+            "ctx": (B, Sq, E)}
+    dev_out = {n: W.DeviceArray(s) for n, s in outs.items()}
+    for d in dev_out.values():
+        d.fill(np.nan)
+    W.call("wm_mha_fwd", *[x.vp for x in d_in], W.ptr(dm), mask.shape[0] if mask is not None else 0,
+           *[p.vp for p in dp], B, Sq, Sk, E, heads, *[dev_out[n].vp for n in outs])
+    return {n: d.to_host() for n, d in dev_out.items()}
+
+
+def mha_bwd(dout, q, k, v, params, heads, saved, need=(True, True, True), alias=False, start=None):
+    """wm_mha_bwd adding into gradient buffers that start at `start[name]`
+    (default zeros); returns dict of host gradients (gq only, with alias)."""
+    B, Sq, E = q.shape
+    Sk = k.shape[1]
+    start = start or {}
+    shapes = {"gWq": (E, E), "gWk": (E, E), "gWv": (E, E), "gWo": (E, E), "gbq": (E,), "gbk": (E,), "gbv": (E,),
+              "gbo": (E,), "gq": q.shape, "gk": k.shape, "gv": v.shape}
+    bufs = {}
+    for n, s in shapes.items():
+        if n in ("gq", "gk", "gv"):
+            i = ("gq", "gk", "gv").index(n)
+            if not need[i] or (alias and n != "gq"):
+                continue
+        bufs[n] = dev(np.asarray(start.get(n, np.zeros(s, np.float32)), np.float32))
+    if alias:
+        for i, n in ((1, "gk"), (2, "gv")):
+            if need[i]:
+                bufs[n] = bufs["gq"]
+    ins = [dev(x) for x in (dout, q, k, v)] + [dev(np.asarray(p, np.float32)) for p in params[:4]]
+    sv = [dev(saved[n]) for n in ("Q", "K", "V", "attn", "ctx")]
+    W.call("wm_mha_bwd", *[x.vp for x in ins], *[x.vp for x in sv], B, Sq, Sk, E, heads,
+           *[W.ptr(bufs.get(n)) for n in shapes])
+    return {n: d.to_host() for n, d in bufs.items() if not (alias and n in ("gk", "gv"))}
+
+
+def mha_forward_scales(q, k, v, params, H, f):
+    """First-order error scales of Q, K, V, attn, ctx, out from the fp64
+    forward f: |x| |W|^T + |b| for projections; for a weight a_ij of a row
+    with score scales s_ij, a_ij * (s_ij + sum_j a_ij s_ij); the context and
+    output carry both their own sums of |terms| and their inputs' scales."""
+    Wq, Wk, Wv, Wo, bq, bk, bv, bo = [np.abs(np.asarray(p, np.float64)) for p in params]
+    B, Sq, E = q.shape
+    Sk = k.shape[1]
+    hd = E // H
+
+    def proj(x, Wa, ba):
+        return np.abs(x.astype(np.float64)) @ Wa.T + ba
+
+    sQ, sK, sV = proj(q, Wq, bq), proj(k, Wk, bk), proj(v, Wv, bv)
+    scale = 1.0 / np.sqrt(hd)
+    heads = lambda X, S: X.reshape(B, S, H, hd).transpose(0, 2, 1, 3)  # noqa: E731
+    s_sc = scale * (heads(sQ, Sq) @ heads(sK, Sk).transpose(0, 1, 3, 2))
+    a = f["attn"]
+    s_at = a * (s_sc + (a * s_sc).sum(-1, keepdims=True))
+    Vh, sVh = np.abs(heads(f["V"], Sk)), heads(sV, Sk)
+    s_ctx = (s_at @ Vh + a @ sVh + a @ Vh).transpose(0, 2, 1, 3).reshape(B, Sq, E)
+    s_out = s_ctx @ Wo.T + bo
+    return {"Q": sQ, "K": sK, "V": sV, "attn": s_at + 1e-30, "ctx": s_ctx, "out": s_out}

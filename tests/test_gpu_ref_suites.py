@@ -3,10 +3,10 @@ and tests/test_autograd.cpp in the reference), compiled unmodified against
 this build's drop-in Tensor (oracle/_ref/run_ref_suites, built by
 oracle/Makefile where the reference sources are present) and run on the GPU.
 
-Every test of the elementwise / broadcast / reduction / softmax path must
-pass.  The tests of ops outside this build (matmul, bmm, transpose, slice,
-permute, concat, stack) fail with the build's "not part of" exception and are
-listed here explicitly.
+Every test of the elementwise / broadcast / reduction / softmax path and of
+the matrix products (matmul, bmm, transpose) must pass.  The tests of ops
+outside this build (slice, permute, concat, stack) fail with the build's
+"not part of" exception and are listed here explicitly.
 """
 import os
 import re
@@ -17,8 +17,8 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "oracle", "_ref", "run_ref_suites")
 
-OUT_OF_SCOPE = {"matmul_2d", "matmul_batch", "transpose", "slice", "permute", "concat", "stack",
-                "matmul_grad", "transpose_grad"}
+OUT_OF_SCOPE = {"slice", "permute", "concat", "stack"}
+MATRIX_TESTS = {"matmul_2d", "matmul_batch", "transpose", "matmul_grad", "transpose_grad"}
 
 pytestmark = pytest.mark.gpu
 
@@ -35,6 +35,7 @@ def test_reference_suites_against_drop_in_tensor():
     assert not unexpected, f"hot-path reference tests failed: {unexpected}"
     for name, msg in failed.items():
         assert "not part of the MI355X" in msg, (name, msg)
+    assert MATRIX_TESTS <= passed, MATRIX_TESTS - passed
 
 
 OPTIM_BIN = os.path.join(ROOT, "oracle", "_ref", "run_ref_optim")
@@ -79,28 +80,31 @@ def test_reference_loss_suite_against_drop_in_losses():
 
 LAYERS_BIN = os.path.join(ROOT, "oracle", "_ref", "run_ref_layers")
 
-# Tests of modules whose forward needs matmul / conv / pool / gather kernels
-# this build does not have: they fail with the "not part of" exception.
+# Tests of modules whose forward needs conv / pool / gather / recurrent-gate
+# kernels this build does not have: they fail with the "not part of"
+# exception.
 LAYERS_OUT_OF_SCOPE = {
-    "linear_forward", "linear_gradient", "conv2d_forward", "conv2d_no_padding", "conv2d_stride",
+    "conv2d_forward", "conv2d_no_padding", "conv2d_stride",
     "conv_transpose2d_forward", "conv_transpose2d_upsample", "conv_transpose2d_gradient",
     "conv_transpose2d_output_padding", "conv_transpose2d_inverse_conv2d", "maxpool2d_forward", "avgpool2d_forward",
     "maxpool2d_values", "embedding_forward", "lstm_forward", "lstm_hidden_state", "lstm_variable_sequence_lengths",
     "lstm_seq_first", "lstm_initial_hidden_state", "lstm_gradient_flow", "lstm_output_values_bounded",
     "gru_forward", "gru_hidden_state", "gru_variable_sequence_lengths", "gru_seq_first", "gru_initial_hidden_state",
-    "gru_gradient_flow", "gru_output_continuity", "gru_deterministic", "mha_forward", "mha_cross",
-    "mha_causal_mask", "mha_with_mask", "mha_no_mask", "mha_attention_weights_sum", "mha_gradient_flow",
-    "mha_cross_gradient", "mha_single_head", "mha_variable_seq_len", "mha_numerical_stability",
-    "sequential_forward", "sequential_add", "mha_head_dim", "mha_causal_mask_structure", "lstm_forget_gate_bias"}
+    "gru_gradient_flow", "gru_output_continuity", "gru_deterministic", "lstm_forget_gate_bias"}
+# Linear, MultiHeadAttention and Sequential(Linear, ...) run on the matrix cores.
+LAYERS_MATRIX = {"linear_forward", "linear_gradient", "mha_forward", "mha_cross", "mha_causal_mask", "mha_with_mask",
+                 "mha_no_mask", "mha_attention_weights_sum", "mha_gradient_flow", "mha_cross_gradient",
+                 "mha_single_head", "mha_variable_seq_len", "mha_numerical_stability", "sequential_forward",
+                 "sequential_add", "mha_head_dim", "mha_causal_mask_structure"}
 
 
 @pytest.mark.skipif(not os.path.exists(LAYERS_BIN), reason="oracle/_ref/run_ref_layers not built")
 def test_reference_layer_suite_against_drop_in_modules():
     """tests/test_layers.cpp against the drop-in layer.h: the activation,
-    softmax, dropout, BatchNorm2d, LayerNorm, flatten, parameter-counting,
-    Sequential and summary tests pass; every failure is a module whose forward
-    needs a kernel outside this build and fails with the "not part of"
-    exception."""
+    softmax, dropout, BatchNorm2d, LayerNorm, Linear, MultiHeadAttention,
+    flatten, parameter-counting, Sequential and summary tests pass; every
+    failure is a module whose forward needs a kernel outside this build and
+    fails with the "not part of" exception."""
     r = subprocess.run([LAYERS_BIN], capture_output=True, text=True, timeout=300)
     out = r.stdout + r.stderr
     passed = set(re.findall(r"\[PASS\] (\S+)", out))
@@ -116,3 +120,4 @@ def test_reference_layer_suite_against_drop_in_modules():
     assert not unexpected, f"layer tests failed: {unexpected}"
     for name, msg in failed.items():
         assert "not part of the MI355X" in msg, (name, msg)
+    assert LAYERS_MATRIX <= passed, LAYERS_MATRIX - passed

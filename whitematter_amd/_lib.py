@@ -109,6 +109,10 @@ _SIGS = {
     "wm_matmul_bwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int],
     "wm_bmm": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
     "wm_bmm_bwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int],
+    "wm_transpose2d": [_vp, C.c_int64, C.c_int64, _vp, C.c_int],
+    # include/wm_layers.h (MultiHeadAttention)
+    "wm_mha_fwd": [_vp] * 4 + [C.c_int64] + [_vp] * 8 + [C.c_int64] * 5 + [_vp] * 6,
+    "wm_mha_bwd": [_vp] * 13 + [C.c_int64] * 5 + [_vp] * 11,
 }
 
 # enum wm_pointwise_loss

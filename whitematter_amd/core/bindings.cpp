@@ -125,6 +125,7 @@ PYBIND11_MODULE(_tensor, m) {
         .def("squeeze", &Tensor::squeeze, py::arg("dim") = -1)
         .def("unsqueeze", &Tensor::unsqueeze)
         .def("matmul", &Tensor::matmul)
+        .def("bmm", &Tensor::bmm)
         .def("transpose", &Tensor::transpose)
         .def("__add__", [](const TensorPtr& a, const TensorPtr& b) { return *a + b; })
         .def("__sub__", [](const TensorPtr& a, const TensorPtr& b) { return *a - b; })
@@ -194,6 +195,26 @@ PYBIND11_MODULE(_tensor, m) {
         .def_readwrite("beta", &BatchNorm2d::beta)
         .def_readwrite("running_mean", &BatchNorm2d::running_mean)
         .def_readwrite("running_var", &BatchNorm2d::running_var);
+    py::class_<Linear, Module>(m, "Linear")
+        .def(py::init<size_t, size_t>(), py::arg("in_features"), py::arg("out_features"))
+        .def_readwrite("weight", &Linear::weight)
+        .def_readwrite("bias", &Linear::bias);
+    py::class_<MultiHeadAttention, Module>(m, "MultiHeadAttention")
+        .def(py::init<size_t, size_t>(), py::arg("embed_dim"), py::arg("num_heads"))
+        .def("attend",
+             [](MultiHeadAttention& a, const TensorPtr& q, const TensorPtr& k, const TensorPtr& v,
+                const TensorPtr& mask) { return a.forward(q, k, v, mask); },
+             py::arg("query"), py::arg("key"), py::arg("value"), py::arg("mask") = TensorPtr())
+        .def_static("causal_mask", &MultiHeadAttention::causal_mask)
+        .def_readwrite("attn_weights", &MultiHeadAttention::attn_weights)
+        .def_readwrite("W_q", &MultiHeadAttention::W_q)
+        .def_readwrite("W_k", &MultiHeadAttention::W_k)
+        .def_readwrite("W_v", &MultiHeadAttention::W_v)
+        .def_readwrite("W_o", &MultiHeadAttention::W_o)
+        .def_readwrite("b_q", &MultiHeadAttention::b_q)
+        .def_readwrite("b_k", &MultiHeadAttention::b_k)
+        .def_readwrite("b_v", &MultiHeadAttention::b_v)
+        .def_readwrite("b_o", &MultiHeadAttention::b_o);
     py::class_<Dropout, Module>(m, "Dropout")
         .def(py::init<float>(), py::arg("p") = 0.5f)
         .def("train", &Dropout::train)

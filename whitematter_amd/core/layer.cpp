@@ -1,13 +1,13 @@
 // layer.cpp -- the drop-in modules (reference core/layer.cpp).
 //
-// LayerNorm and BatchNorm2d call include/wm_layers.h (forward and backward
-// closure on the device); Dropout draws its mask on the device; the
-// activations, Softmax / LogSoftmax, Flatten, Linear, the convolutions and
-// the pools are the reference's Tensor-op compositions (the last four reach
-// Tensor ops this build does not provide and throw there).  Embedding, LSTM,
-// GRU and MultiHeadAttention construct and count their parameters as the
-// reference does and throw from forward().  Summaries and parameter counting
-// are host bookkeeping, as in the reference.
+// LayerNorm, BatchNorm2d and MultiHeadAttention call include/wm_layers.h
+// (forward and backward closure on the device); Dropout draws its mask on the
+// device; the activations, Softmax / LogSoftmax, Flatten, Linear, the
+// convolutions and the pools are the reference's Tensor-op compositions (the
+// convolutions and pools reach Tensor ops this build does not provide and
+// throw there).  Embedding, LSTM and GRU construct and count their parameters
+// as the reference does and throw from forward().  Summaries and parameter
+// counting are host bookkeeping, as in the reference.
 #include "layer.h"
 
 #include <cmath>
@@ -19,6 +19,7 @@
 #include <string>
 
 #include "wm_hip.h"
+#include "wm_gemm.h"
 #include "wm_layers.h"
 
 namespace {
@@ -320,10 +321,77 @@ MultiHeadAttention::MultiHeadAttention(size_t embed_dim, size_t num_heads) : emb
 
 TensorPtr MultiHeadAttention::forward(const TensorPtr& input) { return forward(input, input, input, nullptr); }
 
-// The projections and both batched products are matmuls, which this build
-// does not have; the softmax between them is wm_attention_softmax_fwd/_bwd.
-TensorPtr MultiHeadAttention::forward(const TensorPtr&, const TensorPtr&, const TensorPtr&, const TensorPtr&) {
-    out_of_scope("MultiHeadAttention::forward");
+namespace {
+// A gradient buffer to add into: a known-zero buffer is cleared first, since
+// wm_mha_bwd only adds.
+float* grad_accum_target(const TensorPtr& t) {
+    int acc = 0;
+    float* g = grad_target(t, &acc);
+    if (!acc) ck(wm_fill(g, 0.0f, (int64_t)t->data.size()), "gradient clear");
+    return g;
+}
+}  // namespace
+
+// core/layer.cpp:1103-1437 as wm_mha_fwd / wm_mha_bwd.  The closure exists
+// only when an input requires grad (the reference's `track`), and then adds
+// into all eight parameter gradients; Q, K, V and the context stay on the
+// device for it, attn_weights is the stored attention.
+TensorPtr MultiHeadAttention::forward(const TensorPtr& query, const TensorPtr& key, const TensorPtr& value,
+                                      const TensorPtr& mask) {
+    if (query->shape.size() != 3 || key->shape.size() != 3 || value->shape.size() != 3)
+        throw std::invalid_argument("MultiHeadAttention: query, key and value must be 3-D");
+    if (query->shape[2] != embed_dim || key->shape[2] != embed_dim || value->shape[2] != embed_dim)
+        throw std::invalid_argument("MultiHeadAttention: last dimension must be embed_dim");
+    const size_t batch = query->shape[0], seq_q = query->shape[1], seq_k = key->shape[1];
+    if (key->shape[0] != batch || value->shape[0] != batch || value->shape[1] != seq_k)
+        throw std::invalid_argument("MultiHeadAttention: key / value shapes do not match the query");
+    int64_t mask_batches = 0;
+    if (mask) {
+        const auto& ms = mask->shape;
+        if (ms.size() != 4 || (ms[0] != 1 && ms[0] != batch) || ms[1] != 1 || ms[2] != seq_q || ms[3] != seq_k)
+            throw std::invalid_argument("MultiHeadAttention: mask must be [batch or 1, 1, seq_q, seq_k]");
+        mask_batches = (int64_t)ms[0];
+    }
+    const bool track = (query->requires_grad || key->requires_grad || value->requires_grad) && GradMode::is_enabled();
+    const int64_t B = (int64_t)batch, Sq = (int64_t)seq_q, Sk = (int64_t)seq_k, E = (int64_t)embed_dim,
+                  H = (int64_t)num_heads;
+    auto Q = std::make_shared<wm::DeviceVector>(batch * seq_q * embed_dim);
+    auto K = std::make_shared<wm::DeviceVector>(batch * seq_k * embed_dim);
+    auto V = std::make_shared<wm::DeviceVector>(batch * seq_k * embed_dim);
+    auto ctx = std::make_shared<wm::DeviceVector>(batch * seq_q * embed_dim);
+    auto attn = Tensor::create({batch, num_heads, seq_q, seq_k}, track);
+    auto output = Tensor::create({batch, seq_q, embed_dim}, track);
+    ck(wm_mha_fwd(query->data.dev(), key->data.dev(), value->data.dev(), mask ? mask->data.dev() : nullptr,
+                  mask_batches, W_q->data.dev(), W_k->data.dev(), W_v->data.dev(), W_o->data.dev(), b_q->data.dev(),
+                  b_k->data.dev(), b_v->data.dev(), b_o->data.dev(), B, Sq, Sk, E, H, output->data.dev_write(),
+                  attn->data.dev_write(), Q->dev_write(), K->dev_write(), V->dev_write(), ctx->dev_write()),
+       "MultiHeadAttention");
+    attn_weights = attn;
+    if (track) {
+        TensorPtr q = query, k = key, v = value, Wq = W_q, Wk = W_k, Wv = W_v, Wo = W_o, bq = b_q, bk = b_k, bv = b_v,
+                  bo = b_o, at = attn;
+        Tensor* out = output.get();
+        output->parents = {q, k, v, Wq, Wk, Wv, Wo, bq, bk, bv, bo};
+        output->grad_fn = [=]() {
+            float* gWq = grad_accum_target(Wq);
+            float* gWk = grad_accum_target(Wk);
+            float* gWv = grad_accum_target(Wv);
+            float* gWo = grad_accum_target(Wo);
+            float* gbq = grad_accum_target(bq);
+            float* gbk = grad_accum_target(bk);
+            float* gbv = grad_accum_target(bv);
+            float* gbo = grad_accum_target(bo);
+            float* gq = q->requires_grad ? grad_accum_target(q) : nullptr;
+            float* gk = k->requires_grad ? (k == q ? gq : grad_accum_target(k)) : nullptr;
+            float* gv = nullptr;
+            if (v->requires_grad) gv = v == q ? gq : v == k ? gk : grad_accum_target(v);
+            ck(wm_mha_bwd(out->grad.dev(), q->data.dev(), k->data.dev(), v->data.dev(), Wq->data.dev(),
+                          Wk->data.dev(), Wv->data.dev(), Wo->data.dev(), Q->dev(), K->dev(), V->dev(), at->data.dev(),
+                          ctx->dev(), B, Sq, Sk, E, H, gWq, gWk, gWv, gWo, gbq, gbk, gbv, gbo, gq, gk, gv),
+               "MultiHeadAttention backward");
+        };
+    }
+    return output;
 }
 
 std::vector<TensorPtr> MultiHeadAttention::parameters() { return {W_q, W_k, W_v, W_o, b_q, b_k, b_v, b_o}; }

@@ -5,18 +5,19 @@
 // so code written against it compiles unchanged.  What runs where:
 //   - LayerNorm and BatchNorm2d run the kernels of include/wm_layers.h
 //     (forward, running statistics, and a backward closure on the device);
-//   - ReLU, Sigmoid, Tanh, Softmax, LogSoftmax, Flatten are the same Tensor
-//     ops as in the reference, so they run on the device through tensor.h;
+//   - MultiHeadAttention runs wm_mha_fwd / wm_mha_bwd (projections and
+//     per-head products on the matrix cores, the attention softmax kernels);
+//   - Linear, ReLU, Sigmoid, Tanh, Softmax, LogSoftmax, Flatten are the same
+//     Tensor ops as in the reference (Linear: matmul then add), so they run
+//     on the device through tensor.h;
 //   - Dropout multiplies by a device-drawn mask (wm_dropout_mask);
-//   - Linear, Conv2d, ConvTranspose2d, MaxPool2d and AvgPool2d call the same
-//     Tensor ops as the reference (matmul, conv2d, pools), which this build's
-//     Tensor does not provide (they throw); Embedding, LSTM, GRU and
-//     MultiHeadAttention need matmul / gather kernels this build does not
-//     have and throw from forward().  Their constructors, parameters and
-//     summaries behave as the reference's, including the seeded
-//     initialisation (one std::mt19937(123) shared by all constructors).
-//     MultiHeadAttention's softmax itself is available as
-//     wm_attention_softmax_fwd / _bwd.
+//   - Conv2d, ConvTranspose2d, MaxPool2d and AvgPool2d call the same Tensor
+//     ops as the reference (conv2d, pools), which this build's Tensor does
+//     not provide (they throw); Embedding, LSTM and GRU need gather / gate
+//     kernels this build does not have and throw from forward().  Their
+//     constructors, parameters and summaries behave as the reference's,
+//     including the seeded initialisation (one std::mt19937(123) shared by
+//     all constructors).
 #ifndef LAYER_H
 #define LAYER_H
 

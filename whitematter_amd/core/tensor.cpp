@@ -10,6 +10,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "wm_gemm.h"
 #include "wm_hip.h"
 
 namespace {
@@ -464,12 +465,101 @@ TensorPtr Tensor::unsqueeze(int dim) const {
 }
 
 // ---------------------------------------------------------------------------
+// Matrix products on the matrix cores (include/wm_gemm.h): matmul :783-825,
+// bmm :827-895, transpose :2223-2248.  Shape mismatches throw
+// std::invalid_argument where the reference asserts.
+// ---------------------------------------------------------------------------
+
+TensorPtr Tensor::matmul(const TensorPtr& other) const {
+    if (shape.size() != 2 || other->shape.size() != 2) throw std::invalid_argument("matmul: operands must be 2-D");
+    if (shape[1] != other->shape[0]) throw std::invalid_argument("matmul: inner dimensions differ");
+    const int64_t m = (int64_t)shape[0], k = (int64_t)shape[1], n = (int64_t)other->shape[1];
+    const bool track = (requires_grad || other->requires_grad) && GradMode::is_enabled();
+    auto result = create({shape[0], other->shape[1]}, track);
+    ck(wm_matmul(data.dev(), other->data.dev(), m, k, n, result->data.dev_write()), "matmul");
+    if (track) {
+        auto self_ptr = const_cast<Tensor*>(this)->shared_from_this();
+        auto other_ptr = other;
+        Tensor* res = result.get();
+        result->parents = {self_ptr, other_ptr};
+        result->grad_fn = [self_ptr, other_ptr, res, m, k, n]() {
+            // One gradient at a time, so x.matmul(x) adds both into one buffer.
+            if (self_ptr->requires_grad) {
+                int acc = 0;
+                float* ga = grad_target(self_ptr, &acc);
+                ck(wm_matmul_bwd(res->grad.dev(), self_ptr->data.dev(), other_ptr->data.dev(), m, k, n, ga, acc,
+                                 nullptr, 0),
+                   "matmul backward");
+            }
+            if (other_ptr->requires_grad) {
+                int acc = 0;
+                float* gb = grad_target(other_ptr, &acc);
+                ck(wm_matmul_bwd(res->grad.dev(), self_ptr->data.dev(), other_ptr->data.dev(), m, k, n, nullptr, 0,
+                                 gb, acc),
+                   "matmul backward");
+            }
+        };
+    }
+    return result;
+}
+
+TensorPtr Tensor::bmm(const TensorPtr& other) const {
+    if (shape.size() != 3 || other->shape.size() != 3) throw std::invalid_argument("bmm requires 3D tensors");
+    if (shape[0] != other->shape[0]) throw std::invalid_argument("bmm: batch sizes must match");
+    if (shape[2] != other->shape[1]) throw std::invalid_argument("bmm: inner dimensions must match");
+    const int64_t batch = (int64_t)shape[0], m = (int64_t)shape[1], k = (int64_t)shape[2],
+                  n = (int64_t)other->shape[2];
+    const bool track = (requires_grad || other->requires_grad) && GradMode::is_enabled();
+    auto result = create({shape[0], shape[1], other->shape[2]}, track);
+    ck(wm_bmm(data.dev(), other->data.dev(), batch, m, k, n, result->data.dev_write()), "bmm");
+    if (track) {
+        auto self_ptr = const_cast<Tensor*>(this)->shared_from_this();
+        auto other_ptr = other;
+        Tensor* res = result.get();
+        result->parents = {self_ptr, other_ptr};
+        result->grad_fn = [self_ptr, other_ptr, res, batch, m, k, n]() {
+            if (self_ptr->requires_grad) {
+                int acc = 0;
+                float* ga = grad_target(self_ptr, &acc);
+                ck(wm_bmm_bwd(res->grad.dev(), self_ptr->data.dev(), other_ptr->data.dev(), batch, m, k, n, ga, acc,
+                              nullptr, 0),
+                   "bmm backward");
+            }
+            if (other_ptr->requires_grad) {
+                int acc = 0;
+                float* gb = grad_target(other_ptr, &acc);
+                ck(wm_bmm_bwd(res->grad.dev(), self_ptr->data.dev(), other_ptr->data.dev(), batch, m, k, n, nullptr,
+                              0, gb, acc),
+                   "bmm backward");
+            }
+        };
+    }
+    return result;
+}
+
+TensorPtr Tensor::transpose() const {
+    if (shape.size() != 2) throw std::invalid_argument("transpose: tensor must be 2-D");
+    const int64_t rows = (int64_t)shape[0], cols = (int64_t)shape[1];
+    const bool track = requires_grad && GradMode::is_enabled();
+    auto result = create({shape[1], shape[0]}, track);
+    ck(wm_transpose2d(data.dev(), rows, cols, result->data.dev_write(), 0), "transpose");
+    if (track) {
+        auto self_ptr = const_cast<Tensor*>(this)->shared_from_this();
+        Tensor* res = result.get();
+        result->parents = {self_ptr};
+        result->grad_fn = [self_ptr, res, rows, cols]() {
+            int acc = 0;
+            float* gx = grad_target(self_ptr, &acc);
+            ck(wm_transpose2d(res->grad.dev(), cols, rows, gx, acc), "transpose backward");
+        };
+    }
+    return result;
+}
+
+// ---------------------------------------------------------------------------
 // Outside this build
 // ---------------------------------------------------------------------------
 
-TensorPtr Tensor::matmul(const TensorPtr&) const { out_of_scope("matmul"); }
-TensorPtr Tensor::bmm(const TensorPtr&) const { out_of_scope("bmm"); }
-TensorPtr Tensor::transpose() const { out_of_scope("transpose"); }
 TensorPtr Tensor::slice(size_t, size_t, int) const { out_of_scope("slice"); }
 TensorPtr Tensor::conv2d(const TensorPtr&, const TensorPtr&, size_t, size_t) const { out_of_scope("conv2d"); }
 TensorPtr Tensor::conv_transpose2d(const TensorPtr&, const TensorPtr&, size_t, size_t, size_t) const {

@@ -265,6 +265,37 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
     }
 }
 
+// out[c][r] (+)= x[r][c] for x [rows, cols]: 64 x 64 tiles through LDS (65-
+// float pitch, so the column reads hit 64 different banks), 256 threads,
+// each moving 16 elements; reads and writes run along rows.
+constexpr int kTT = 64;
+
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                        float* __restrict__ out, int accumulate, int64_t tiles_c,
+                                                        int64_t ntiles) {
+    __shared__ float tile[kTT][kTT + 1];
+    const int tx = (int)threadIdx.x & 63, ty = (int)threadIdx.x >> 6;
+    for (int64_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+        const int64_t r0 = (t / tiles_c) * kTT, c0 = (t % tiles_c) * kTT;
+#pragma unroll
+        for (int i = 0; i < kTT / 4; ++i) {
+            const int64_t r = r0 + ty + 4 * i, c = c0 + tx;
+            if (r < rows && c < cols) tile[ty + 4 * i][tx] = x[r * cols + c];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kTT / 4; ++i) {
+            const int64_t c = c0 + ty + 4 * i, r = r0 + tx;
+            if (r < rows && c < cols) {
+                float* d = out + c * rows + r;
+                const float v = tile[tx][ty + 4 * i];
+                *d = accumulate ? *d + v : v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
     const int64_t tm = (P.m + kTile - 1) / kTile, tn = (P.n + kTile - 1) / kTile;
@@ -370,4 +401,18 @@ int wm_bmm_bwd(const float* g, const float* a, const float* b, int64_t batch, in
         WM_TRY(wm_gemm(1, 0, k, n, m, 1.0f, a, k1, g, n1, gb, n, accumulate_b, nullptr, batch, 1, st));
     }
     return WM_OK;
+}
+
+int wm_transpose2d(const float* x, int64_t rows, int64_t cols, float* out, int accumulate) {
+    if (rows < 0 || cols < 0) return set_error(WM_ERR_INVALID, "wm_transpose2d: negative extent");
+    if (rows == 0 || cols == 0) return WM_OK;
+    if (!x || !out) return set_error(WM_ERR_INVALID, "wm_transpose2d: null pointer");
+    if (x == out) return set_error(WM_ERR_INVALID, "wm_transpose2d: in-place transpose is not supported");
+    WM_CHECK_INIT();
+    const int64_t tiles_c = (cols + kTT - 1) / kTT;
+    const int64_t ntiles = ((rows + kTT - 1) / kTT) * tiles_c;
+    const unsigned grid = (unsigned)std::min<int64_t>(ntiles, (int64_t)num_cus() * 16);
+    hipLaunchKernelGGL(transpose_kernel, dim3(grid), dim3(256), 0, stream(), x, rows, cols, out, accumulate ? 1 : 0,
+                       tiles_c, ntiles);
+    return check_launch("wm_transpose2d");
 }
