@@ -521,6 +521,65 @@ def gemm_ops(n=8192, batch=64, t=1024, hd=128):
                        "elements": n * n + batch * t * t}
 
 
+def io_ops(n_floats=1 << 28):
+    """WMT tensor files (core/serialize.cpp:36-108) through the drop-in:
+    load_tensor of a 1 GiB file straight into HBM, save_tensor of the same
+    tensor from HBM, on a RAM-backed path (/dev/shm when present) so the
+    figure is the staging pipeline's (file-cache read, pinned copy, PCIe),
+    not a disk's.  Timed with events on the library stream around the whole
+    host-driven call; 'bytes' = the payload."""
+    from whitematter_amd import _tensor as T
+    d = "/dev/shm" if os.path.isdir("/dev/shm") and os.access("/dev/shm", os.W_OK) else "/tmp"
+    path = os.path.join(d, "wm_bench_io_%d.wmt" % os.getpid())
+    x = T.Tensor.from_array(synth.normal((n_floats,), synth.seed_for(12, 0)), requires_grad=True)
+    assert T.save_tensor(x, path)
+    holder = {}
+
+    def load():
+        holder["t"] = T.load_tensor(path)
+
+    def save():
+        assert T.save_tensor(x, path)
+
+    nb = n_floats * F32
+    ops = [Op("load_tensor", load, nb, "(host-driven copies)", n_floats),
+           Op("save_tensor", save, nb, "(host-driven copies)", n_floats)]
+    for op in ops:
+        op.host_io = True
+
+    class Cleanup:
+        def __del__(self):
+            try:
+                os.remove(path)
+            except OSError:
+                pass
+
+    return ops, [x, holder, Cleanup()], {
+        "workload": "io: WMT tensor file of %d fp32 (%d MiB) loaded into / saved from HBM through pinned "
+                    "double-buffered staging (include/wm_io.h), file on %s" % (n_floats, nb >> 20, d),
+        "elements": n_floats, "path": path}
+
+
+def cpu_baseline_io(path, reps=3):
+    """The reference's own load_tensor (oracle/_ref: ifstream read into a
+    std::vector, then Tensor::create's copy) on the same file, one thread."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    ref = oracle.reference()
+    if ref is None:
+        return None
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        t = ref.load_tensor(path)
+        ts.append(time.perf_counter() - t0)
+        n = int(np.prod(t.shape))
+        del t
+    sec = statistics.median(ts)
+    return {"value": round(n * F32 / sec / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": "the whole %d MiB file, median of %d loads" % (n * F32 >> 20, reps)}
+
+
 def traffic_for(op_name: str, config: str):
     """HBM bytes per launch of an op's main kernel, from the committed
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json,
@@ -535,7 +594,7 @@ def traffic_for(op_name: str, config: str):
         return None
 
 
-CONFIGS = {"gemm": gemm_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
+CONFIGS = {"gemm": gemm_ops, "io": io_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
            "norm": norm_ops}
 
 
@@ -597,9 +656,15 @@ def main():
             per_op[op.name].update({"TFLOPs": round(tf, 1), "pct_mfma_peak": round(100 * tf / PEAK_F32_MFMA_TFLOPS, 1),
                                     "flops": op.flops})
     mfma = all(op.flops for op in ops)
+    host_io = all(getattr(op, "host_io", False) for op in ops)
     dom = max(ops, key=lambda o: statistics.mean(o.ms))
     dom_ms = statistics.mean(dom.ms)
-    if mfma:
+    if host_io:
+        # host-driven file transfers: bounded by the file cache and PCIe, not by
+        # an HBM or matrix-core roofline
+        value = step_bytes / (step_ms * 1e-3) / 1e9
+        roofline = None
+    elif mfma:
         value = sum(op.flops for op in ops) / (step_ms * 1e-3) / 1e12
         dom_tf = dom.flops / (dom_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(dom_tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
@@ -630,6 +695,11 @@ def main():
     src.free(); dst.free()
 
     cpu = None
+    if not args.no_cpu and args.config == "io":
+        try:
+            cpu = cpu_baseline_io(workload["path"])
+        except Exception as e:  # the baseline is reported, never the target
+            cpu = {"value": None, "error": str(e)}
     if not args.no_cpu and args.config == "c2":
         try:
             cpu = cpu_baseline_c2(args.cpu_rows)

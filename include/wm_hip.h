@@ -45,7 +45,8 @@ enum wm_status {
     WM_ERR_INVALID = 1,     /* bad argument: shape mismatch, null pointer, ... */
     WM_ERR_HIP = 2,         /* HIP runtime error */
     WM_ERR_NOMEM = 3,       /* device allocation failed */
-    WM_ERR_UNSUPPORTED = 4  /* valid request this build does not implement */
+    WM_ERR_UNSUPPORTED = 4, /* valid request this build does not implement */
+    WM_ERR_IO = 5           /* a read / write callback delivered fewer bytes than asked */
 };
 
 /* Binary ops, core/tensor.cpp:897 (add), :981 (sub), :1063 (mul), :1147 (div),

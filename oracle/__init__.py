@@ -519,6 +519,9 @@ class RefTensor:
         self.L.wmref_get_data(self.h, _fp(out))
         return out.reshape(self.shape)
 
+    def requires_grad(self) -> bool:
+        return bool(self.L.wmref_requires_grad(self.h))
+
     def grad(self):
         out = np.empty(self.L.wmref_numel(self.h), np.float32)
         if not self.L.wmref_get_grad(self.h, _fp(out)):
@@ -607,6 +610,15 @@ class Reference:
         L.wmref_binary.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
         L.wmref_matmul.restype = C.c_void_p
         L.wmref_matmul.argtypes = [C.c_int, C.c_void_p, C.c_void_p]
+        L.wmref_requires_grad.argtypes = [C.c_void_p]
+        L.wmref_save_tensor.argtypes = [C.c_void_p, C.c_char_p]
+        L.wmref_load_tensor.argtypes = [C.c_char_p]
+        L.wmref_load_tensor.restype = C.c_void_p
+        for fn in ("wmref_save_model", "wmref_load_model", "wmref_save_optimizer", "wmref_load_optimizer"):
+            getattr(L, fn).argtypes = [C.c_void_p, C.c_char_p]
+        L.wmref_save_checkpoint.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.c_int, C.c_float, C.c_float]
+        L.wmref_load_checkpoint.argtypes = [C.c_char_p, C.c_void_p, C.c_void_p, C.POINTER(C.c_int),
+                                            C.POINTER(C.c_float), C.POINTER(C.c_float)]
         L.wmref_unary.argtypes = [C.c_int, C.c_void_p, C.c_float, C.c_float]
         L.wmref_reduce.argtypes = [C.c_int, C.c_void_p, C.c_int, C.c_int]
         L.wmref_softmax.argtypes = [C.c_int, C.c_void_p, C.c_int]
@@ -739,6 +751,35 @@ class Reference:
 
     def matmul(self, a: RefTensor, b: RefTensor) -> RefTensor:
         return RefTensor(self.L, self.L.wmref_matmul(0, a.h, b.h))
+
+    # core/serialize.h, the reference's own file writers and readers
+    def save_tensor(self, t: RefTensor, path: str) -> bool:
+        return bool(self.L.wmref_save_tensor(t.h, path.encode()))
+
+    def load_tensor(self, path: str) -> Optional[RefTensor]:
+        h = self.L.wmref_load_tensor(path.encode())
+        return RefTensor(self.L, h) if h else None
+
+    def save_model(self, m: "RefModule", path: str) -> bool:
+        return bool(self.L.wmref_save_model(m.h, path.encode()))
+
+    def load_model(self, m: "RefModule", path: str) -> bool:
+        return bool(self.L.wmref_load_model(m.h, path.encode()))
+
+    def save_optimizer(self, o, path: str) -> bool:
+        return bool(self.L.wmref_save_optimizer(o.h, path.encode()))
+
+    def load_optimizer(self, o, path: str) -> bool:
+        return bool(self.L.wmref_load_optimizer(o.h, path.encode()))
+
+    def save_checkpoint(self, path: str, m: "RefModule", o, epoch: int, loss: float = 0.0, acc: float = 0.0) -> bool:
+        return bool(self.L.wmref_save_checkpoint(path.encode(), m.h, o.h if o else None, epoch, loss, acc))
+
+    def load_checkpoint(self, path: str, m: "RefModule", o):
+        e, l_, a = C.c_int(), C.c_float(), C.c_float()
+        ok = self.L.wmref_load_checkpoint(path.encode(), m.h, o.h if o else None, C.byref(e), C.byref(l_),
+                                          C.byref(a))
+        return bool(ok), e.value, l_.value, a.value
 
     def bmm(self, a: RefTensor, b: RefTensor) -> RefTensor:
         return RefTensor(self.L, self.L.wmref_matmul(1, a.h, b.h))

@@ -19,6 +19,7 @@
 #include "optimizer.h"
 #include "loss.h"
 #include "layer.h"
+#include "serialize.h"
 
 #include <memory>
 
@@ -326,6 +327,34 @@ void* wmref_module_buffer(void* m, int which) {
     if (auto* bn = dynamic_cast<BatchNorm2d*>(mod)) return box(which == 0 ? bn->running_mean : bn->running_var);
     if (auto* a = dynamic_cast<MultiHeadAttention*>(mod)) return box(a->attn_weights);
     return nullptr;
+}
+
+// core/serialize.h: the reference's own WMT / WMM / WMO / checkpoint files.
+int wmref_save_tensor(void* h, const char* path) { return save_tensor(T(h), std::string(path)) ? 1 : 0; }
+
+void* wmref_load_tensor(const char* path) {
+    TensorPtr t = load_tensor(std::string(path));
+    return t ? box(t) : nullptr;
+}
+
+int wmref_save_model(void* m, const char* path) { return save_model(static_cast<Module*>(m), path) ? 1 : 0; }
+int wmref_load_model(void* m, const char* path) { return load_model(static_cast<Module*>(m), path) ? 1 : 0; }
+int wmref_save_optimizer(void* o, const char* path) {
+    return save_optimizer(static_cast<Optimizer*>(o), path) ? 1 : 0;
+}
+int wmref_load_optimizer(void* o, const char* path) {
+    return load_optimizer(static_cast<Optimizer*>(o), path) ? 1 : 0;
+}
+int wmref_save_checkpoint(const char* path, void* m, void* o, int epoch, float loss, float acc) {
+    return save_checkpoint(path, static_cast<Module*>(m), static_cast<Optimizer*>(o), epoch, loss, acc) ? 1 : 0;
+}
+int wmref_load_checkpoint(const char* path, void* m, void* o, int* epoch, float* loss, float* acc) {
+    Checkpoint info{0, 0.0f, 0.0f};
+    const bool ok = load_checkpoint(path, static_cast<Module*>(m), static_cast<Optimizer*>(o), info);
+    *epoch = info.epoch;
+    *loss = info.loss;
+    *acc = info.accuracy;
+    return ok ? 1 : 0;
 }
 
 // Causal mask, MultiHeadAttention::causal_mask.

@@ -34,6 +34,9 @@ REDUCE_OPS = {"sum": R_SUM, "mean": R_MEAN, "max": R_MAX, "min": R_MIN,
 
 _i64p = C.POINTER(C.c_int64)
 _vp = C.c_void_p
+# include/wm_io.h callbacks
+READ_FN = C.CFUNCTYPE(C.c_int64, C.c_void_p, C.c_void_p, C.c_int64)
+WRITE_FN = C.CFUNCTYPE(C.c_int64, C.c_void_p, C.c_void_p, C.c_int64)
 
 # name -> (restype, argtypes); every entry point returns int (status).
 _SIGS = {
@@ -110,6 +113,9 @@ _SIGS = {
     "wm_bmm": [_vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp],
     "wm_bmm_bwd": [_vp, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int, _vp, C.c_int],
     "wm_transpose2d": [_vp, C.c_int64, C.c_int64, _vp, C.c_int],
+    # include/wm_io.h
+    "wm_read_into_device": [READ_FN, _vp, _vp, C.c_int64],
+    "wm_write_from_device": [WRITE_FN, _vp, _vp, C.c_int64],
     # include/wm_layers.h (MultiHeadAttention)
     "wm_mha_fwd": [_vp] * 4 + [C.c_int64] + [_vp] * 8 + [C.c_int64] * 5 + [_vp] * 6,
     "wm_mha_bwd": [_vp] * 13 + [C.c_int64] * 5 + [_vp] * 11,

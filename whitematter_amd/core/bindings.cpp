@@ -12,6 +12,7 @@
 #include <pybind11/stl.h>
 
 #include "layer.h"
+#include "serialize.h"
 #include "loss.h"
 #include "optimizer.h"
 #include "tensor.h"
@@ -219,6 +220,25 @@ PYBIND11_MODULE(_tensor, m) {
         .def(py::init<float>(), py::arg("p") = 0.5f)
         .def("train", &Dropout::train)
         .def("eval", &Dropout::eval);
+
+    // WMT / WMM / WMO / checkpoint files (core/serialize.h), device-direct.
+    m.def("save_tensor", py::overload_cast<const TensorPtr&, const std::string&>(&save_tensor));
+    m.def("load_tensor", py::overload_cast<const std::string&>(&load_tensor));
+    m.def("save_model", [](Module* mod, const std::string& p) { return save_model(mod, p); });
+    m.def("load_model", [](Module* mod, const std::string& p) { return load_model(mod, p); });
+    m.def("save_optimizer", [](Optimizer* o, const std::string& p) { return save_optimizer(o, p); });
+    m.def("load_optimizer", [](Optimizer* o, const std::string& p) { return load_optimizer(o, p); });
+    m.def("save_checkpoint",
+          [](const std::string& p, Module* mod, Optimizer* o, int epoch, float loss, float acc) {
+              return save_checkpoint(p, mod, o, epoch, loss, acc);
+          },
+          py::arg("path"), py::arg("model"), py::arg("optimizer"), py::arg("epoch"), py::arg("loss") = 0.0f,
+          py::arg("accuracy") = 0.0f);
+    m.def("load_checkpoint", [](const std::string& p, Module* mod, Optimizer* o) {
+        Checkpoint info{0, 0.0f, 0.0f};
+        const bool ok = load_checkpoint(p, mod, o, info);
+        return py::make_tuple(ok, info.epoch, info.loss, info.accuracy);
+    });
 
     py::class_<LossFunction>(m, "LossFunction")
         .def("forward", &LossFunction::forward)
