@@ -189,9 +189,13 @@ def test_broadcast_ops_through_tensor(T):
         assert oracle.close_scaled(to.grad, gb, sb, 1e-5)[0], op
 
 
-def test_out_of_scope_ops_raise(T):
-    a = tensor(T, np.ones((2, 2), np.float32))
-    with pytest.raises(RuntimeError, match="not part of"):
-        a.matmul(a)
-    with pytest.raises(RuntimeError, match="not part of"):
-        a.transpose()
+def test_matrix_ops_through_the_api(T):
+    """matmul and transpose are in the build (matrix cores / a tiled copy);
+    the ops still outside it throw "not part of" (checked by the reference's
+    own suites in test_gpu_ref_suites.py)."""
+    x = np.float32([[1, 2], [3, 4]])
+    a = tensor(T, x)
+    assert np.array_equal(np.asarray(a.matmul(a).data).reshape(2, 2), x @ x)
+    assert np.array_equal(np.asarray(a.transpose().data).reshape(2, 2), x.T)
+    with pytest.raises(ValueError):
+        a.matmul(tensor(T, np.ones((3, 2), np.float32)))
