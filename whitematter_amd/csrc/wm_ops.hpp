@@ -110,12 +110,12 @@ __device__ __forceinline__ void binary_grads_n(const float (&g)[N], const float 
 #pragma unroll
         for (int j = 0; j < N; ++j) {
             p[j] = pow_grad_table(a[j], b[j], want_out, want_da, want_db);
-            fix |= pow_grad_needs_fix(a[j], b[j]);
+            fix |= pow_grad_needs_fix(a[j], b[j], p[j]);
         }
         if (fix) {
 #pragma unroll
             for (int j = 0; j < N; ++j)
-                if (pow_grad_needs_fix(a[j], b[j])) pow_grad_fix(a[j], b[j], want_out, want_da, want_db, p[j]);
+                if (pow_grad_needs_fix(a[j], b[j], p[j])) pow_grad_fix(a[j], b[j], want_out, want_da, want_db, p[j]);
         }
 #pragma unroll
         for (int j = 0; j < N; ++j) {

@@ -219,26 +219,46 @@ WM_HD inline float pow_f32(float x, float y) {
     return pow_needs_fix(x, y) ? powf(x, y) : pow_table(x, y);
 }
 
-// The three values pow's backward needs, sharing one log2|a|:
+// The three values pow's backward needs, sharing one log2|a| and one power
+// of two:
 //   out  = pow(a, b)            (the forward output, recomputed; d/db)
-//   pbm1 = pow(a, b - 1.0f)     (d/da = g * b * pbm1)
+//   pbm1 = pow(a, b - 1.0f)     (d/da = g * b * pbm1) = out * (1 / a)
 //   lga  = log(a)               (d/db = g * out * lga)
 // Only the requested ones are computed (the others are 0).  On the table
-// path out and pbm1 carry a relative error of ~2e-7 and lga is log(a)
-// rounded once from double (NaN for a < 0); pow_grad_fix replaces them with
-// powf / logf where pow_grad_needs_fix.
+// path out carries a relative error of ~2e-7, pbm1 ~3e-7 (the reciprocal
+// adds at most 1 ulp) and lga is log(a) rounded once from double (NaN for
+// a < 0).  The quotient is pow(a, b - 1) only while b - 1 is exact in
+// float, pow(a, b) stays in the normal range (or is the NaN of a negative
+// base) and 1 / a does too (|a| < 2^126); other lanes set `slow`, for
+// pow_grad_fix.
 struct PowGrad {
     float out, pbm1, lga;
+    bool slow;
 };
+
+WM_HD inline float recip_normal(float a) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return __builtin_amdgcn_rcpf(a);  // within 1 ulp for normal a with |a| < 2^126
+#else
+    return 1.0f / a;
+#endif
+}
 
 WM_HD inline PowGrad pow_grad_table(float a, float b, bool want_out, bool want_pbm1, bool want_lga) {
     using namespace powdetail;
-    PowGrad r = {0.0f, 0.0f, 0.0f};
+    PowGrad r = {0.0f, 0.0f, 0.0f, false};
     const double l2 = log2_normal(std::fabs(a));
-    if (want_out) r.out = apply_sign(a, b, exp2_grad((double)b * l2));
-    if (want_pbm1) {
-        const float bm1 = b - 1.0f;
-        r.pbm1 = apply_sign(a, bm1, exp2_grad((double)bm1 * l2));
+    if (want_out || want_pbm1) {
+        const float o = apply_sign(a, b, exp2_grad((double)b * l2));
+        if (want_out) r.out = o;
+        if (want_pbm1) {
+            r.pbm1 = o * recip_normal(a);
+            // The quotient needs b - 1 exact in float (it is not for |b|
+            // below ~2^-24 or at or above 2^24); then a NaN power (a < 0, b
+            // not an integer) is pow(a, b - 1) too.
+            const float bm1 = b - 1.0f;
+            r.slow = !(std::isnormal(o) || std::isnan(o)) || bm1 + 1.0f != b || !(std::fabs(a) < 0x1p126f);
+        }
     }
     if (want_lga) r.lga = a > 0.0f ? (float)(l2 * 0.6931471805599453) : NAN;
     return r;
@@ -248,7 +268,20 @@ WM_HD inline bool pow_grad_needs_fix(float a, float b) {
     return !powdetail::table_ok(a, b) || !powdetail::table_ok(a, b - 1.0f);
 }
 
+WM_HD inline bool pow_grad_needs_fix(float a, float b, const PowGrad& r) {
+    return r.slow || pow_grad_needs_fix(a, b);
+}
+
+// Operands outside the table path: all three from powf / logf.  A lane that
+// is only `slow` keeps out and lga and takes pow(a, b - 1) from the table
+// path's own power of two of (b - 1) log2|a|.
 WM_HD inline void pow_grad_fix(float a, float b, bool want_out, bool want_pbm1, bool want_lga, PowGrad& r) {
+    using namespace powdetail;
+    if (!pow_grad_needs_fix(a, b)) {
+        const float bm1 = b - 1.0f;
+        r.pbm1 = apply_sign(a, bm1, exp2_grad((double)bm1 * log2_normal(std::fabs(a))));
+        return;
+    }
     if (want_out) r.out = powf(a, b);
     if (want_pbm1) r.pbm1 = powf(a, b - 1.0f);
     if (want_lga) r.lga = logf(a);
@@ -256,7 +289,7 @@ WM_HD inline void pow_grad_fix(float a, float b, bool want_out, bool want_pbm1, 
 
 WM_HD inline PowGrad pow_grad_parts(float a, float b, bool want_out, bool want_pbm1, bool want_lga) {
     PowGrad r = pow_grad_table(a, b, want_out, want_pbm1, want_lga);
-    if (pow_grad_needs_fix(a, b)) pow_grad_fix(a, b, want_out, want_pbm1, want_lga, r);
+    if (pow_grad_needs_fix(a, b, r)) pow_grad_fix(a, b, want_out, want_pbm1, want_lga, r);
     return r;
 }
 
