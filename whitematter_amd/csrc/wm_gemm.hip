@@ -57,6 +57,7 @@ struct GemmParams {
     float alpha;
     int accumulate;
     int tiles_m, tiles_n;
+    int c_aligned;  // C and every problem's C start 16-byte aligned
 };
 
 // One operand's 128 x 32 tile per stage (rows of op(A), or columns of
@@ -175,6 +176,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
         a.init(P.a + po * P.sa0 + pi * P.sa1, P.lda, P.m, m0);
         b.init(P.b + po * P.sb0 + pi * P.sb1, P.ldb, P.n, n0);
         float* C = P.c + po * P.sc0 + pi * P.sc1;
+        const bool aligned_c = P.c_aligned != 0;
 
         f32x16 acc[2][2];
 #pragma unroll
@@ -237,30 +239,58 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
             __syncthreads();
         }
 
+        // Epilogue through LDS: each wave parks its 64 x 64 quarter (68-float
+        // pitch) in its own slice of the stage buffers, which the last barrier
+        // freed, then writes C as float4 rows, 16 lanes per 256-byte row span.
         // Accumulator element q of a 32 x 32 block sits at row
         // 8 * (q / 4) + 4 * half + q % 4, column r.
-        const float alpha = P.alpha;
-        const bool accum = P.accumulate != 0;
+        constexpr int kEp = 68;
+        float* ep = &lds[0][0][0] + wave * 64 * kEp;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int64_t row0 = m0 + wm * 64 + i * 32 + 4 * half;
-                const int64_t col = n0 + wn * 64 + j * 32 + r;
-                if (!interior && col >= P.n) continue;
-                const float bcol = P.bias ? P.bias[col] : 0.0f;
-                float* c0 = C + row0 * P.ldc + col;
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int dr = 8 * (q >> 2) + (q & 3);
-                    if (!interior && row0 + dr >= P.m) continue;
-                    float* dst = c0 + dr * P.ldc;
-                    float v = alpha * acc[i][j][q];
-                    if (accum) v = *dst + v;
-                    if (P.bias) v = v + bcol;
-                    *dst = v;
+                for (int q = 0; q < 16; ++q)
+                    ep[(i * 32 + 8 * (q >> 2) + 4 * half + (q & 3)) * kEp + j * 32 + r] = acc[i][j][q];
+        const float alpha = P.alpha;
+        const bool accum = P.accumulate != 0;
+        const int cq = (lane & 15) * 4;  // this lane's 4 columns within the quarter
+        const int64_t col = n0 + wn * 64 + cq;
+        const bool vec_c = interior && (P.ldc & 3) == 0 && aligned_c;
+        float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (P.bias) {
+            float bb[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bb[e] = (interior || col + e < P.n) ? P.bias[col + e] : 0.0f;
+            bias4 = make_float4(bb[0], bb[1], bb[2], bb[3]);
+        }
+#pragma unroll 4
+        for (int s4 = 0; s4 < 16; ++s4) {
+            const int rq = (lane >> 4) + 4 * s4;  // row within the quarter
+            const int64_t row = m0 + wm * 64 + rq;
+            const float4 a4 = *reinterpret_cast<const float4*>(ep + rq * kEp + cq);
+            float4 v = make_float4(alpha * a4.x, alpha * a4.y, alpha * a4.z, alpha * a4.w);
+            float* dst = C + row * P.ldc + col;
+            if (vec_c) {
+                if (accum) {
+                    const float4 old = *reinterpret_cast<const float4*>(dst);
+                    v = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+                }
+                if (P.bias) v = make_float4(v.x + bias4.x, v.y + bias4.y, v.z + bias4.z, v.w + bias4.w);
+                *reinterpret_cast<float4*>(dst) = v;
+            } else if (row < P.m) {
+                const float ve[4] = {v.x, v.y, v.z, v.w}, be[4] = {bias4.x, bias4.y, bias4.z, bias4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (col + e >= P.n) continue;
+                    float x = ve[e];
+                    if (accum) x = dst[e] + x;
+                    if (P.bias) x = x + be[e];
+                    dst[e] = x;
                 }
             }
+        }
         __syncthreads();  // the next problem's first stage reuses LDS buffer 0
     }
 }
@@ -305,6 +335,7 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     // The unchecked float4 loads need 16-byte aligned rows in both operands.
     const bool vec = P.lda % 4 == 0 && P.ldb % 4 == 0 && aligned16(P.a) && aligned16(P.b) &&
                      (P.batch == 1 || (P.sa0 % 4 == 0 && P.sa1 % 4 == 0 && P.sb0 % 4 == 0 && P.sb1 % 4 == 0));
+    P.c_aligned = aligned16(P.c) && (P.batch == 1 || (P.sc0 % 4 == 0 && P.sc1 % 4 == 0)) ? 1 : 0;
     dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch, 65535));
     hipStream_t s = stream();
 #define WM_GEMM(TA, TB, V) hipLaunchKernelGGL((gemm_kernel<TA, TB, V>), grid, dim3(kThreads), 0, s, P)
