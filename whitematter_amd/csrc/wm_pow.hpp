@@ -225,12 +225,13 @@ WM_HD inline float pow_f32(float x, float y) {
 //   pbm1 = pow(a, b - 1.0f)     (d/da = g * b * pbm1) = out * (1 / a)
 //   lga  = log(a)               (d/db = g * out * lga)
 // Only the requested ones are computed (the others are 0).  On the table
-// path out carries a relative error of ~2e-7, pbm1 ~3e-7 (the reciprocal
-// adds at most 1 ulp) and lga is log(a) rounded once from double (NaN for
-// a < 0).  The quotient is pow(a, b - 1) only while b - 1 is exact in
-// float, pow(a, b) stays in the normal range (or is the NaN of a negative
-// base) and 1 / a does too (|a| < 2^126); other lanes set `slow`, for
-// pow_grad_fix.
+// path out carries a relative error of ~2e-7 and pbm1 ~3e-7 against the
+// exact pow(a, b - 1) (the reciprocal adds at most 1 ulp); the reference's
+// pow(a, b - 1.0f) rounds the exponent to float first, which moves it by up
+// to |ln a| 2^-24 < 5.3e-6 relative (see below).  lga is log(a) rounded once
+// from double (NaN for a < 0).  The quotient stands for pow(a, b - 1) while |b| < 2^24, pow(a, b)
+// stays in the normal range (or is the NaN of a negative base) and 1 / a
+// does too (|a| < 2^126); other lanes set `slow`, for pow_grad_fix.
 struct PowGrad {
     float out, pbm1, lga;
     bool slow;
@@ -253,11 +254,17 @@ WM_HD inline PowGrad pow_grad_table(float a, float b, bool want_out, bool want_p
         if (want_out) r.out = o;
         if (want_pbm1) {
             r.pbm1 = o * recip_normal(a);
-            // The quotient needs b - 1 exact in float (it is not for |b|
-            // below ~2^-24 or at or above 2^24); then a NaN power (a < 0, b
-            // not an integer) is pow(a, b - 1) too.
+            // pow(a, b - 1.0f) takes b - 1 rounded to float.  Below |b| =
+            // 2^24 that rounding is non-zero only for |b - 1| < 2 (|b| beyond
+            // that keeps b - 1 exact) and then at most 2^-24, which changes
+            // the power by at most |ln a| 2^-24 < 5.3e-6 relative (normal a);
+            // from 2^24 up it can drop the "- 1" altogether, so those lanes
+            // are slow.  A NaN power (a < 0, b not an integer) is
+            // pow(a, b - 1) too unless b - 1 rounded to an integer (|b| below
+            // 2^-25).
             const float bm1 = b - 1.0f;
-            r.slow = !(std::isnormal(o) || std::isnan(o)) || bm1 + 1.0f != b || !(std::fabs(a) < 0x1p126f);
+            const bool ok = std::isnormal(o) || (std::isnan(o) && std::rint(bm1) != bm1);
+            r.slow = !ok || !(std::fabs(b) < 0x1p24f) || !(std::fabs(a) < 0x1p126f);
         }
     }
     if (want_lga) r.lga = a > 0.0f ? (float)(l2 * 0.6931471805599453) : NAN;
