@@ -157,3 +157,11 @@ def test_matmul_large_vs_float64(wm, shape):
     a, b = rng_normal((m, k), 50), rng_uniform((k, n), 51, -1.0, 1.0)
     a64, b64 = a.astype(np.float64), b.astype(np.float64)
     close(matmul(a, b), a64 @ b64, np.abs(a64) @ np.abs(b64))
+
+
+def test_bmm_more_problems_than_one_grid_dimension(wm):
+    """70,000 tiny problems: more than the 65,535 the launch's second grid
+    dimension holds, so workgroups walk the batch in strides."""
+    P, m, k, n = 70000, 2, 3, 5
+    a, b = rng_normal((P, m, k), 60), rng_normal((P, k, n), 61)
+    close(matmul(a, b), o64.bmm(a, b), oab.bmm(a, b))
