@@ -521,6 +521,48 @@ def gemm_ops(n=8192, batch=64, t=1024, hd=128):
                        "elements": n * n + batch * t * t}
 
 
+def mha_ops(B=8, S=1024, E=1024, H=16):
+    """MultiHeadAttention forward and closure (wm_mha_fwd / wm_mha_bwd) at a
+    transformer shape: self attention over [B, S, E] with H heads and a
+    causal mask.  flops = the products (projections 4 * 2 B S E^2, scores and
+    attn V 2 * 2 B H S^2 hd; the closure twice that); the attention softmax
+    and the bias column sums ride along in the same time."""
+    hd = E // H
+    x = W.DeviceArray.from_host(synth.normal((B, S, E), synth.seed_for(13, 0)))
+    params = [W.DeviceArray.from_host(synth.normal((E, E), synth.seed_for(13, 1 + i), 0.0, E ** -0.5))
+              for i in range(4)]
+    params += [W.DeviceArray.from_host(synth.normal((E,), synth.seed_for(13, 5 + i), 0.0, 0.1)) for i in range(4)]
+    mask = W.DeviceArray.from_host(np.where(np.triu(np.ones((S, S)), 1) > 0, -1e9, 0).astype(np.float32))
+    out, ctx = W.DeviceArray((B, S, E)), W.DeviceArray((B, S, E))
+    Q, K, V = (W.DeviceArray((B, S, E)) for _ in range(3))
+    attn = W.DeviceArray((B, H, S, S))
+    dout = W.DeviceArray.from_host(synth.normal((B, S, E), synth.seed_for(13, 9)))
+    grads = [W.DeviceArray((E, E)) for _ in range(4)] + [W.DeviceArray((E,)) for _ in range(4)]
+    gx = W.DeviceArray((B, S, E))
+    for gbuf in grads + [gx]:
+        gbuf.fill(0.0)
+    pv = [p.vp for p in params]
+
+    def fwd():
+        W.call("wm_mha_fwd", x.vp, x.vp, x.vp, mask.vp, 1, *pv, B, S, S, E, H, out.vp, attn.vp, Q.vp, K.vp, V.vp,
+               ctx.vp)
+
+    def bwd():
+        W.call("wm_mha_bwd", dout.vp, x.vp, x.vp, x.vp, *pv[:4], Q.vp, K.vp, V.vp, attn.vp, ctx.vp, B, S, S, E, H,
+               *[gb.vp for gb in grads], gx.vp, gx.vp, gx.vp)
+
+    fwd()
+    f_fl = 4 * 2 * B * S * E * E + 2 * 2 * B * H * S * S * hd
+    att = B * H * S * S * F32
+    ops = [Op("mha fwd", fwd, 4 * B * S * E * F32 + 3 * att, "gemm_kernel", B * S * E, f_fl),
+           Op("mha bwd", bwd, 6 * B * S * E * F32 + 4 * att, "gemm_kernel", B * S * E, 2 * f_fl)]
+    keep = [x, mask, out, ctx, Q, K, V, attn, dout, gx] + params + grads
+    return ops, keep, {"workload": "mha: MultiHeadAttention self attention x[%d,%d,%d], %d heads (hd %d), causal "
+                                   "mask; forward and closure (parameter gradients accumulated, one input gradient "
+                                   "for q = k = v)" % (B, S, E, H, hd),
+                       "elements": B * S * E}
+
+
 def io_ops(n_floats=1 << 28):
     """WMT tensor files (core/serialize.cpp:36-108) through the drop-in:
     load_tensor of a 1 GiB file straight into HBM, save_tensor of the same
@@ -594,7 +636,7 @@ def traffic_for(op_name: str, config: str):
         return None
 
 
-CONFIGS = {"gemm": gemm_ops, "io": io_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
+CONFIGS = {"gemm": gemm_ops, "mha": mha_ops, "io": io_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
            "norm": norm_ops}
 
 

@@ -39,12 +39,16 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kTile = 128;      // C tile rows and columns per workgroup
+constexpr int kTile = 128;      // C tile rows per workgroup (columns: BN = 128 or 64)
 constexpr int kBK = 32;         // k per stage
 constexpr int kPitchK = kBK + 4;      // LDS [row][k] pitch (floats)
-constexpr int kPitchR = kTile + 2;    // LDS [k][row] pitch (floats)
-constexpr int kThreads = 256;   // 4 waves as 2 x 2, each 64 x 64 of C
-constexpr int kOperandFloats = kTile * kPitchK > kBK * kPitchR ? kTile * kPitchK : kBK * kPitchR;
+constexpr int kThreads = 256;   // 4 waves as 2 x 2, each 64 x BN/2 of C
+// LDS [k][row] pitch for an operand tile of R rows: R + 2 keeps a
+// quarter-wave's 4-byte reads on distinct banks and puts the two half-waves'
+// rows (16 k apart) on opposite halves of the banks (16 (R + 2) = 32 mod 64).
+template <int R>
+constexpr int pitch_r() { return R + 2; }
+constexpr int kOperandFloats = kTile * kPitchK > kBK * (kTile + 2) ? kTile * kPitchK : kBK * (kTile + 2);
 
 struct GemmParams {
     const float* a;
@@ -60,17 +64,22 @@ struct GemmParams {
     int c_aligned;  // C and every problem's C start 16-byte aligned
 };
 
-// One operand's 128 x 32 tile per stage (rows of op(A), or columns of
-// op(B), by k).  KC: element (r, kk) at base[r * ld + kk], else at
-// base[kk * ld + r].  Each thread moves four float4s:
-//   KC:  slot i = row t/8 + 32 i, k 4 (t % 8) .. + 3      -> LDS [row][k]
-//   !KC: slot i = k t/32 + 8 i, rows 4 (t % 32) .. + 3     -> LDS [k][row]
-template <bool KC>
+// One operand's R x 32 tile per stage (R = 128 or 64 rows of op(A), or
+// columns of op(B), by k).  KC: element (r, kk) at base[r * ld + kk], else
+// at base[kk * ld + r].  Each thread moves NS = R / 32 float4s:
+//   KC:  slot i = row t/8 + 32 i, k 4 (t % 8) .. + 3          -> LDS [row][k]
+//   !KC: slot i = k t/L + (256/L) i, rows 4 (t % L) .. + 3,    -> LDS [k][row]
+//        with L = R / 4 lanes across the rows
+template <bool KC, int R>
 struct Operand {
+    static constexpr int NS = R / 32;
+    static constexpr int L = R / 4;
+    static constexpr int KSTEP = kThreads / L;  // k rows per slot (!KC)
+    static constexpr int PR = pitch_r<R>();
     const float* base;
     int64_t ld, rows, r0;
     int64_t lane_off;  // this thread's first element relative to (r0, k0 = 0)
-    float4 v[4];
+    float4 v[NS];
 
     __device__ __forceinline__ void init(const float* b, int64_t ld_, int64_t rows_, int64_t r0_) {
         const int t = (int)threadIdx.x;
@@ -78,27 +87,27 @@ struct Operand {
         ld = ld_;
         rows = rows_;
         r0 = r0_;
-        lane_off = KC ? (r0 + t / 8) * ld + 4 * (t % 8) : (int64_t)(t / 32) * ld + r0 + 4 * (t % 32);
+        lane_off = KC ? (r0 + t / 8) * ld + 4 * (t % 8) : (int64_t)(t / L) * ld + r0 + 4 * (t % L);
     }
 
     // Interior tile, whole stage inside k, 16-byte aligned rows.
     __device__ __forceinline__ void load_fast(int64_t k0) {
         const float* p = base + lane_off + (KC ? k0 : k0 * ld);
-        const int64_t step = KC ? 32 * ld : 8 * ld;
+        const int64_t step = KC ? 32 * ld : KSTEP * ld;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const float4*>(p + i * step);
+        for (int i = 0; i < NS; ++i) v[i] = *reinterpret_cast<const float4*>(p + i * step);
     }
 
     // Any tile: element by element, reading only inside rows x kdim.
     __device__ __forceinline__ void load_edge(int64_t kdim, int64_t k0) {
         const int t = (int)threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NS; ++i) {
             float e[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int64_t r = KC ? r0 + t / 8 + 32 * i : r0 + 4 * (t % 32) + j;
-                const int64_t kk = KC ? k0 + 4 * (t % 8) + j : k0 + t / 32 + 8 * i;
+                const int64_t r = KC ? r0 + t / 8 + 32 * i : r0 + 4 * (t % L) + j;
+                const int64_t kk = KC ? k0 + 4 * (t % 8) + j : k0 + t / L + KSTEP * i;
                 e[j] = (r < rows && kk < kdim) ? (KC ? base[r * ld + kk] : base[kk * ld + r]) : 0.0f;
             }
             v[i] = make_float4(e[0], e[1], e[2], e[3]);
@@ -108,11 +117,11 @@ struct Operand {
     __device__ __forceinline__ void store(float* lds) const {
         const int t = (int)threadIdx.x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NS; ++i) {
             if constexpr (KC) {
                 *reinterpret_cast<float4*>(lds + (t / 8 + 32 * i) * kPitchK + 4 * (t % 8)) = v[i];
             } else {
-                float* q = lds + (t / 32 + 8 * i) * kPitchR + 4 * (t % 32);
+                float* q = lds + (t / L + KSTEP * i) * PR + 4 * (t % L);
                 *reinterpret_cast<float2*>(q) = make_float2(v[i].x, v[i].y);
                 *reinterpret_cast<float2*>(q + 2) = make_float2(v[i].z, v[i].w);
             }
@@ -124,8 +133,8 @@ struct Operand {
         if constexpr (KC) {
             return *reinterpret_cast<const float4*>(lds + row * kPitchK + kk);
         } else {
-            return make_float4(lds[kk * kPitchR + row], lds[(kk + 1) * kPitchR + row], lds[(kk + 2) * kPitchR + row],
-                               lds[(kk + 3) * kPitchR + row]);
+            return make_float4(lds[kk * PR + row], lds[(kk + 1) * PR + row], lds[(kk + 2) * PR + row],
+                               lds[(kk + 3) * PR + row]);
         }
     }
 };
@@ -143,8 +152,9 @@ __device__ __forceinline__ void tile_of(int t, int tiles_m, int tiles_n, int& tm
     tn = in / rows;
 }
 
-template <bool TA, bool TB, bool VEC>
+template <bool TA, bool TB, bool VEC, int BN>
 __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
+    constexpr int JB = BN / 64;  // 32-column blocks per wave (each wave: 64 x BN/2)
     __shared__ __attribute__((aligned(16))) float lds[2][2][kOperandFloats];  // [stage][A, B]
 
     const int ntiles = P.tiles_m * P.tiles_n;
@@ -154,8 +164,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
     if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
     int tm, tn;
     tile_of(t, P.tiles_m, P.tiles_n, tm, tn);
-    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
-    const bool interior = VEC && m0 + kTile <= P.m && n0 + kTile <= P.n;
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * BN;
+    const bool interior = VEC && m0 + kTile <= P.m && n0 + BN <= P.n;
 
     const int lane = (int)threadIdx.x & 63;
     const int wave = (int)threadIdx.x >> 6;
@@ -166,8 +176,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
 
     // op(A) row r, k kk: A[r * lda + kk] (TA = 0) or A[kk * lda + r].
     // op(B) column r, k kk: B[kk * ldb + r] (TB = 0) or B[r * ldb + kk].
-    using OpA = Operand<!TA>;
-    using OpB = Operand<TB>;
+    using OpA = Operand<!TA, kTile>;
+    using OpB = Operand<TB, BN>;
 
     for (int64_t p = blockIdx.y; p < P.batch; p += gridDim.y) {
         const int64_t po = p / P.batch_inner, pi = p - po * P.batch_inner;
@@ -178,11 +188,11 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
         float* C = P.c + po * P.sc0 + pi * P.sc1;
         const bool aligned_c = P.c_aligned != 0;
 
-        f32x16 acc[2][2];
+        f32x16 acc[2][JB];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < JB; ++j)
 #pragma unroll
                 for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
@@ -217,15 +227,15 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
 #pragma unroll
             for (int kq = 0; kq < 4; ++kq) {
                 const int kk = 16 * half + 4 * kq;
-                float4 av[2], bv[2];
+                float4 av[2], bv[JB];
 #pragma unroll
                 for (int i = 0; i < 2; ++i) av[i] = OpA::frag(As, wm * 64 + i * 32 + r, kk);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) bv[j] = OpB::frag(Bs, wn * 64 + j * 32 + r, kk);
+                for (int j = 0; j < JB; ++j) bv[j] = OpB::frag(Bs, wn * (BN / 2) + j * 32 + r, kk);
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < JB; ++j) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
@@ -239,24 +249,26 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
             __syncthreads();
         }
 
-        // Epilogue through LDS: each wave parks its 64 x 64 quarter (68-float
-        // pitch) in its own slice of the stage buffers, which the last barrier
-        // freed, then writes C as float4 rows, 16 lanes per 256-byte row span.
+        // Epilogue through LDS: each wave parks its 64 x BN/2 quarter (4 floats
+        // of row padding) in its own slice of the stage buffers, which the
+        // last barrier freed, then writes C as float4 rows: LPR lanes per row
+        // of the quarter, RPP rows per pass.
         // Accumulator element q of a 32 x 32 block sits at row
         // 8 * (q / 4) + 4 * half + q % 4, column r.
-        constexpr int kEp = 68;
+        constexpr int kEp = BN / 2 + 4;
+        constexpr int LPR = BN / 8, RPP = 64 / LPR;
         float* ep = &lds[0][0][0] + wave * 64 * kEp;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < JB; ++j)
 #pragma unroll
                 for (int q = 0; q < 16; ++q)
                     ep[(i * 32 + 8 * (q >> 2) + 4 * half + (q & 3)) * kEp + j * 32 + r] = acc[i][j][q];
         const float alpha = P.alpha;
         const bool accum = P.accumulate != 0;
-        const int cq = (lane & 15) * 4;  // this lane's 4 columns within the quarter
-        const int64_t col = n0 + wn * 64 + cq;
+        const int cq = (lane % LPR) * 4;  // this lane's 4 columns within the quarter
+        const int64_t col = n0 + wn * (BN / 2) + cq;
         const bool vec_c = interior && (P.ldc & 3) == 0 && aligned_c;
         float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
         if (P.bias) {
@@ -266,8 +278,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
             bias4 = make_float4(bb[0], bb[1], bb[2], bb[3]);
         }
 #pragma unroll 4
-        for (int s4 = 0; s4 < 16; ++s4) {
-            const int rq = (lane >> 4) + 4 * s4;  // row within the quarter
+        for (int s4 = 0; s4 < 64 / RPP; ++s4) {
+            const int rq = lane / LPR + RPP * s4;  // row within the quarter
             const int64_t row = m0 + wm * 64 + rq;
             const float4 a4 = *reinterpret_cast<const float4*>(ep + rq * kEp + cq);
             float4 v = make_float4(alpha * a4.x, alpha * a4.y, alpha * a4.z, alpha * a4.w);
@@ -328,7 +340,11 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict_
 
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
-    const int64_t tm = (P.m + kTile - 1) / kTile, tn = (P.n + kTile - 1) / kTile;
+    // 64-wide column tiles for narrow products (attention's per-head products
+    // with hd = 64), 128-wide otherwise.
+    const bool narrow = P.n <= 64;
+    const int64_t bn = narrow ? 64 : 128;
+    const int64_t tm = (P.m + kTile - 1) / kTile, tn = (P.n + bn - 1) / bn;
     if (tm * tn > (int64_t)0x7fffffff) return set_error(WM_ERR_INVALID, "wm_gemm: too many tiles");
     P.tiles_m = (int)tm;
     P.tiles_n = (int)tn;
@@ -338,7 +354,11 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     P.c_aligned = aligned16(P.c) && (P.batch == 1 || (P.sc0 % 4 == 0 && P.sc1 % 4 == 0)) ? 1 : 0;
     dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch, 65535));
     hipStream_t s = stream();
-#define WM_GEMM(TA, TB, V) hipLaunchKernelGGL((gemm_kernel<TA, TB, V>), grid, dim3(kThreads), 0, s, P)
+#define WM_GEMM(TA, TB, V)                                                                   \
+    do {                                                                                     \
+        if (narrow) hipLaunchKernelGGL((gemm_kernel<TA, TB, V, 64>), grid, dim3(kThreads), 0, s, P); \
+        else hipLaunchKernelGGL((gemm_kernel<TA, TB, V, 128>), grid, dim3(kThreads), 0, s, P);       \
+    } while (0)
     if (vec) {
         if (!ta && !tb) WM_GEMM(false, false, true);
         else if (!ta && tb) WM_GEMM(false, true, true);
