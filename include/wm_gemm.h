@@ -13,7 +13,9 @@
  *
  * Arithmetic: products and sums in fp32 on v_mfma_f32_32x32x2_f32 (no
  * reduced-precision inputs).  The reference adds each product to its fp32
- * accumulator in k order; the matrix cores add them in another order, so the
+ * accumulator in k order; the matrix cores add them in another order (and a
+ * product with fewer output tiles than CUs and a long k adds the partial
+ * products of its k slices in a second pass, in fixed slice order), so the
  * results agree with the reference within fp32 summation error (tested
  * against an fp64 restatement relative to sum_k |a_ik * b_kj|), not bit for
  * bit.  Products of small integers, whose partial sums are exact in fp32,

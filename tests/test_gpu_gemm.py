@@ -165,3 +165,54 @@ def test_bmm_more_problems_than_one_grid_dimension(wm):
     P, m, k, n = 70000, 2, 3, 5
     a, b = rng_normal((P, m, k), 60), rng_normal((P, k, n), 61)
     close(matmul(a, b), o64.bmm(a, b), oab.bmm(a, b))
+
+
+@pytest.mark.parametrize("trans", [(0, 0), (0, 1), (1, 0), (1, 1)], ids=lambda t: "NT"[t[0]] + "NT"[t[1]])
+@pytest.mark.parametrize("mnk", [(70, 130, 5000), (256, 256, 8192), (200, 40, 3000), (1, 1, 1024)], ids=str)
+@pytest.mark.parametrize("pad", [0, 3])
+def test_gemm_split_k(wm, trans, mnk, pad):
+    """Few output tiles and a long k: the product runs as k slices whose
+    partial products a second pass adds (ragged last slice, narrow tiles,
+    unaligned rows, accumulate and bias in the second pass)."""
+    ta, tb = trans
+    m, n, k = mnk
+    A, B = rng_normal((m, k), 34), rng_normal((k, n), 35)
+    C0, bias = rng_normal((m, n), 36), rng_normal((n,), 37)
+    sa, sb = op_store(A, ta, (m if ta else k) + pad), op_store(B, tb, (k if tb else n) + pad)
+    ldc = n + pad
+    c0 = np.full((m, ldc), 7.0, np.float32)
+    c0[:, :n] = C0
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    alpha = 0.375
+    got = gemm(ta, tb, m, n, k, alpha, sa, sa.shape[1], sb, sb.shape[1], c0, ldc, True, bias)
+    close(got[:, :n], alpha * (A64 @ B64) + C0 + bias, alpha * (np.abs(A64) @ np.abs(B64)) + np.abs(C0) +
+          np.abs(bias))
+    assert np.all(got[:, n:] == 7.0)
+    got = gemm(ta, tb, m, n, k, 1.0, sa, sa.shape[1], sb, sb.shape[1], c0, ldc, False)
+    close(got[:, :n], A64 @ B64, np.abs(A64) @ np.abs(B64))
+
+
+def test_gemm_split_k_two_level_batch(wm):
+    """Per-head weight-gradient-shaped products (hd x hd over a long k) on
+    [rows, H * hd] activations: split k across a two-level batch."""
+    B, R, H, hd = 2, 2100, 3, 64
+    E = H * hd
+    X, G = rng_normal((B, R, E), 38), rng_normal((B, R, E), 39)
+    out = np.full((B, H, hd, hd), np.nan, np.float32)
+    got = gemm(1, 0, hd, hd, R, 1.0, X, E, G, E, out, hd, False, None, B * H, H,
+               (R * E, hd, R * E, hd, H * hd * hd, hd * hd))
+    Xh = X.astype(np.float64).reshape(B, R, H, hd).transpose(0, 2, 3, 1)
+    Gh = G.astype(np.float64).reshape(B, R, H, hd).transpose(0, 2, 1, 3)
+    close(got, Xh @ Gh, np.abs(Xh) @ np.abs(Gh))
+
+
+def test_matmul_weight_gradient_split_k(wm):
+    """matmul's closure for a Linear-shaped product: gb = a^T g over 8192
+    rows (split k) and ga = g b^T (not split), against float64."""
+    m, k, n = 8192, 512, 256
+    a, b, g = rng_normal((m, k), 62), rng_normal((k, n), 63), rng_normal((m, n), 64)
+    gb0 = rng_normal((k, n), 65)
+    ga, gb = matmul_bwd(g, a, b, None, gb0)
+    a64, b64, g64 = a.astype(np.float64), b.astype(np.float64), g.astype(np.float64)
+    close(ga, g64 @ b64.T, np.abs(g64) @ np.abs(b64).T)
+    close(gb, gb0 + a64.T @ g64, np.abs(gb0) + np.abs(a64).T @ np.abs(g64))

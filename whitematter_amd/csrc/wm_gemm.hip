@@ -27,6 +27,11 @@
 // C or the last k stage take an element-wise path that reads only inside
 // the operands and zero-fills the rest.
 //
+// A launch with fewer tiles than CUs and a long k (a weight gradient
+// x^T dY: small m x n, k = every row of the batch) splits k into slices:
+// each slice's product goes to a workspace and a second pass adds the slices
+// in fixed order, scales and accumulates into C.
+//
 // Sums are fp32 in the matrix cores' order (see include/wm_gemm.h).
 #include "wm_common.hpp"
 
@@ -62,6 +67,10 @@ struct GemmParams {
     int accumulate;
     int tiles_m, tiles_n;
     int c_aligned;  // C and every problem's C start 16-byte aligned
+    // Split k: each problem runs as kslices products over k slices of ksplit
+    // (a multiple of kBK); slice s writes its own C at + s * sck.
+    int kslices;
+    int64_t ksplit, sck;
 };
 
 // One operand's R x 32 tile per stage (R = 128 or 64 rows of op(A), or
@@ -171,21 +180,25 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
     const int wave = (int)threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, r = lane & 31;
-    const int nk = (int)((P.k + kBK - 1) / kBK);
-    const int nk_fast = interior ? (int)(P.k / kBK) : 0;  // stages that take the unchecked loads
 
     // op(A) row r, k kk: A[r * lda + kk] (TA = 0) or A[kk * lda + r].
     // op(B) column r, k kk: B[kk * ldb + r] (TB = 0) or B[r * ldb + kk].
     using OpA = Operand<!TA, kTile>;
     using OpB = Operand<TB, BN>;
 
-    for (int64_t p = blockIdx.y; p < P.batch; p += gridDim.y) {
-        const int64_t po = p / P.batch_inner, pi = p - po * P.batch_inner;
+    const int64_t nprob = P.batch * P.kslices;
+    for (int64_t p = blockIdx.y; p < nprob; p += gridDim.y) {
+        const int64_t pb = p / P.kslices, ks = p - pb * P.kslices;
+        const int64_t po = pb / P.batch_inner, pi = pb - po * P.batch_inner;
+        const int64_t kb = ks * P.ksplit;  // first k of this slice
+        const int64_t kdim = min(P.ksplit, P.k - kb);
+        const int nk = (int)((kdim + kBK - 1) / kBK);
+        const int nk_fast = interior ? (int)(kdim / kBK) : 0;  // stages that take the unchecked loads
         OpA a;
         OpB b;
-        a.init(P.a + po * P.sa0 + pi * P.sa1, P.lda, P.m, m0);
-        b.init(P.b + po * P.sb0 + pi * P.sb1, P.ldb, P.n, n0);
-        float* C = P.c + po * P.sc0 + pi * P.sc1;
+        a.init(P.a + po * P.sa0 + pi * P.sa1 + (TA ? kb * P.lda : kb), P.lda, P.m, m0);
+        b.init(P.b + po * P.sb0 + pi * P.sb1 + (TB ? kb : kb * P.ldb), P.ldb, P.n, n0);
+        float* C = P.c + po * P.sc0 + pi * P.sc1 + ks * P.sck;
         const bool aligned_c = P.c_aligned != 0;
 
         f32x16 acc[2][JB];
@@ -201,8 +214,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
                 a.load_fast(0);
                 b.load_fast(0);
             } else {
-                a.load_edge(P.k, 0);
-                b.load_edge(P.k, 0);
+                a.load_edge(kdim, 0);
+                b.load_edge(kdim, 0);
             }
             a.store(lds[0][0]);
             b.store(lds[0][1]);
@@ -218,8 +231,8 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
                     a.load_fast(k0);
                     b.load_fast(k0);
                 } else {
-                    a.load_edge(P.k, k0);
-                    b.load_edge(P.k, k0);
+                    a.load_edge(kdim, k0);
+                    b.load_edge(kdim, k0);
                 }
             }
             const float* As = lds[cur][0];
@@ -338,6 +351,80 @@ __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict_
     }
 }
 
+// Split-k second pass: C_p = alpha * sum_s part[p][s] (+ C_p) (+ bias) for
+// the kslices partial products of each problem (part: [batch][kslices][m][n],
+// contiguous), the slices added in order 0, 1, ... so the result does not
+// depend on scheduling.  One thread per 4 consecutive columns of a row.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ part, int kslices, int64_t m,
+                                                            int64_t n, int64_t batch, int64_t batch_inner, float* c,
+                                                            int64_t ldc, int64_t sc0, int64_t sc1, float alpha,
+                                                            int accumulate, const float* __restrict__ bias,
+                                                            int c_vec) {
+    const int64_t nq = (n + 3) / 4;
+    const int64_t items = batch * m * nq;
+    const int64_t mn = m * n;
+    const bool part_vec = (n & 3) == 0;
+    for (int64_t it = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; it < items;
+         it += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = it / nq, j0 = 4 * (it - row * nq);
+        const int64_t pb = row / m, i = row - pb * m;
+        const float* src = part + pb * kslices * mn + i * n + j0;
+        const int cnt = (int)min<int64_t>(4, n - j0);
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < kslices; ++s, src += mn) {
+            if (part_vec) {
+                const float4 v = *reinterpret_cast<const float4*>(src);
+                acc[0] += v.x;
+                acc[1] += v.y;
+                acc[2] += v.z;
+                acc[3] += v.w;
+            } else {
+                for (int e = 0; e < cnt; ++e) acc[e] += src[e];
+            }
+        }
+        const int64_t po = pb / batch_inner, pi = pb - po * batch_inner;
+        float* dst = c + po * sc0 + pi * sc1 + i * ldc + j0;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = alpha * acc[e];
+        if (c_vec && cnt == 4) {
+            if (accumulate) {
+                const float4 old = *reinterpret_cast<const float4*>(dst);
+                v[0] = old.x + v[0];
+                v[1] = old.y + v[1];
+                v[2] = old.z + v[2];
+                v[3] = old.w + v[3];
+            }
+            if (bias) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = v[e] + bias[j0 + e];
+            }
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            for (int e = 0; e < cnt; ++e) {
+                float x = v[e];
+                if (accumulate) x = dst[e] + x;
+                if (bias) x = x + bias[j0 + e];
+                dst[e] = x;
+            }
+        }
+    }
+}
+
+// Slices per problem for a launch of `work` workgroups (tiles x problems)
+// over a k extent of k: a launch that leaves most of the chip idle (fewer
+// workgroups than CUs; two fit on each) and has a long k is cut into k
+// slices so the workgroups of one pass cover the chip, each slice at least
+// kMinSlice long.  1 = no split.
+constexpr int64_t kMinSlice = 256;
+
+int64_t choose_kslices(int64_t work, int64_t k) {
+    const int64_t cus = num_cus();
+    if (work >= cus || k < 4 * kMinSlice) return 1;
+    const int64_t s = std::max<int64_t>(2, 2 * cus / work);
+    return std::min<int64_t>(s, k / kMinSlice);
+}
+
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
     // 64-wide column tiles for narrow products (attention's per-head products
@@ -352,8 +439,36 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     const bool vec = P.lda % 4 == 0 && P.ldb % 4 == 0 && aligned16(P.a) && aligned16(P.b) &&
                      (P.batch == 1 || (P.sa0 % 4 == 0 && P.sa1 % 4 == 0 && P.sb0 % 4 == 0 && P.sb1 % 4 == 0));
     P.c_aligned = aligned16(P.c) && (P.batch == 1 || (P.sc0 % 4 == 0 && P.sc1 % 4 == 0)) ? 1 : 0;
-    dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch, 65535));
     hipStream_t s = stream();
+
+    // Split k: the partial products go to a workspace [batch][kslices][m][n]
+    // (unscaled, overwritten), and a second pass adds them into C.
+    int64_t kslices = choose_kslices(tm * tn * P.batch, P.k);
+    Workspace part(0);
+    GemmParams F = P;  // the final C, for the second pass
+    if (kslices > 1) {
+        const int64_t slice = ((P.k + kslices - 1) / kslices + kBK - 1) / kBK * kBK;
+        kslices = (P.k + slice - 1) / slice;
+        const int64_t mn = P.m * P.n;
+        part.p = ws_alloc((size_t)(P.batch * kslices * mn) * sizeof(float));
+        if (!part.p) return set_error(WM_ERR_NOMEM, "wm_gemm: split-k workspace");
+        P.ksplit = slice;
+        P.kslices = (int)kslices;
+        P.c = part.as<float>();
+        P.ldc = P.n;
+        P.sc0 = P.batch_inner * kslices * mn;
+        P.sc1 = kslices * mn;
+        P.sck = mn;
+        P.alpha = 1.0f;
+        P.accumulate = 0;
+        P.bias = nullptr;
+        P.c_aligned = (P.n & 3) == 0 ? 1 : 0;
+    } else {
+        P.ksplit = P.k;
+        P.kslices = 1;
+        P.sck = 0;
+    }
+    dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch * P.kslices, 65535));
 #define WM_GEMM(TA, TB, V)                                                                   \
     do {                                                                                     \
         if (narrow) hipLaunchKernelGGL((gemm_kernel<TA, TB, V, 64>), grid, dim3(kThreads), 0, s, P); \
@@ -371,6 +486,14 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
         else WM_GEMM(true, true, false);
     }
 #undef WM_GEMM
+    if (P.kslices > 1) {
+        WM_TRY(check_launch("wm_gemm"));
+        const bool c_vec = F.c_aligned && (F.ldc & 3) == 0;
+        const int64_t items = F.batch * F.m * ((F.n + 3) / 4);
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(items, 256)), dim3(256), 0, s, part.as<float>(),
+                           P.kslices, F.m, F.n, F.batch, F.batch_inner, F.c, F.ldc, F.sc0, F.sc1, F.alpha,
+                           F.accumulate, F.bias, c_vec ? 1 : 0);
+    }
     return check_launch("wm_gemm");
 }
 
