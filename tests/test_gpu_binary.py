@@ -32,6 +32,7 @@ SHAPES = [
     ((1,), (37,)),                   # scalar on the left
     ((5, 7, 64), (7, 1)),            # middle-dim broadcast
     ((8, 2048), (8, 2048)),
+    ((5, 70000), (5, 1)),            # column vector, few long rows: split into chunks
     ((0, 16), (16,)),                # empty
 ]
 
