@@ -34,7 +34,10 @@ def params_for(E, seed):
 
 CASES = [(2, 5, 5, 8, 2, None), (1, 4, 6, 12, 3, "batch"), (2, 6, 6, 16, 4, "causal"), (1, 3, 3, 8, 1, None),
          (2, 64, 64, 64, 4, "causal"), (1, 33, 47, 96, 3, "batch"), (2, 128, 128, 128, 8, None),
-         (1, 200, 130, 64, 2, None), (2, 256, 256, 256, 8, "causal")]
+         (1, 200, 130, 64, 2, None), (2, 256, 256, 256, 8, "causal"),
+         # ragged query blocks against longer key rows (softmax tiles of 2, 4
+         # and more than 8 float4 per thread)
+         (1, 37, 300, 32, 1, "causal"), (2, 40, 700, 64, 2, "batch"), (1, 20, 1100, 32, 2, None)]
 
 
 def case_inputs(case, seed):
