@@ -39,16 +39,16 @@ __device__ __forceinline__ bool strictly_better(float x, float v) {
 // order within one thread.
 // Branch-free: an empty state takes any non-NaN element (or a NaN at
 // position 0); a non-empty one only a strictly better element.
-template <bool MAXOP>
-__device__ __forceinline__ void scan_push(float& v, int64_t& i, float x, int64_t k) {
+template <bool MAXOP, class I>
+__device__ __forceinline__ void scan_push(float& v, I& i, float x, I k) {
     const bool take = strictly_better<MAXOP>(x, v) || (i == kEmpty && (!__builtin_isnan(x) || k == 0));
     v = take ? x : v;
     i = take ? k : i;
 }
 
 // Combine two states over disjoint position sets (any order).
-template <bool MAXOP>
-__device__ __forceinline__ void combine(float& v, int64_t& i, float v2, int64_t i2) {
+template <bool MAXOP, class I>
+__device__ __forceinline__ void combine(float& v, I& i, float v2, I i2) {
     if (i2 == kEmpty) return;
     if (i == 0 && __builtin_isnan(v)) return;                 // NaN first element wins
     if (i2 == 0 && __builtin_isnan(v2)) { v = v2; i = i2; return; }
@@ -223,7 +223,10 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
 // four times smaller for the same parallelism.  Items are (o, chunk, inner
 // tile) triples, tile fastest; every thread of a workgroup walks the same
 // items, so the barriers are uniform.
-template <int OP, bool VEC>
+// IdxT: the positions a thread tracks (int32_t whenever n fits, which
+// halves the compare-and-select work of the max family); partials and
+// results are int64_t.
+template <int OP, bool VEC, class IdxT>
 __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __restrict__ x, int64_t outer, int64_t n,
                                                               int64_t inner, int64_t chunk, int64_t K,
                                                               float* __restrict__ val, int64_t* __restrict__ idx,
@@ -232,7 +235,7 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
     constexpr int W = VEC ? 4 : 1;
     constexpr int NW = kBlock / 64;
     __shared__ float lv[NW][64 * W];
-    __shared__ int64_t li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
+    __shared__ IdxT li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t tile_elems = (int64_t)64 * W;
     const int64_t tiles = (inner + tile_elems - 1) / tile_elems;
@@ -248,9 +251,9 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
         const int64_t r0 = min(k1, k0 + w * q), r1 = min(k1, r0 + q);
         const float* xp = x + o * n * inner + i0;
         float v[W];
-        int64_t pos[W];
+        IdxT pos[W];
 #pragma unroll
-        for (int j = 0; j < W; ++j) { v[j] = 0.f; pos[j] = kEmpty; }
+        for (int j = 0; j < W; ++j) { v[j] = 0.f; pos[j] = (IdxT)kEmpty; }
         if (i0 < inner) {
             int64_t p = r0;
             for (; p + 3 < r1; p += 4) {
@@ -269,7 +272,7 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 #pragma unroll
                     for (int j = 0; j < W; ++j) {
                         if constexpr (KIND == 0) v[j] += a[u][j];
-                        else scan_push<KIND == 1>(v[j], pos[j], a[u][j], p + u);
+                        else scan_push<KIND == 1>(v[j], pos[j], a[u][j], (IdxT)(p + u));
                     }
             }
             for (; p < r1; ++p) {
@@ -283,7 +286,7 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 #pragma unroll
                 for (int j = 0; j < W; ++j) {
                     if constexpr (KIND == 0) v[j] += a[j];
-                    else scan_push<KIND == 1>(v[j], pos[j], a[j], p);
+                    else scan_push<KIND == 1>(v[j], pos[j], a[j], (IdxT)p);
                 }
             }
         }
@@ -300,7 +303,7 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
                 const int64_t i = i0 + j;
                 if (i >= inner) break;
                 float tv = lv[0][lane * W + j];
-                int64_t ti = kEmpty;
+                IdxT ti = (IdxT)kEmpty;
                 if constexpr (KIND == 0) {
                     tv = (tv + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
                 } else {
@@ -495,12 +498,13 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
     Workspace wi(K > 1 && KIND != 0 ? (size_t)(outer * K * inner) * sizeof(int64_t) : 0);
     if (K > 1 && (!wv.p || (KIND != 0 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
     dim3 grid(grid_for(outer * K * tiles, 1, 32));
-    if (vec)
-        hipLaunchKernelGGL((reduce_cols_kernel<OP, true>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val,
-                           idx, wv.as<float>(), wi.as<int64_t>());
-    else
-        hipLaunchKernelGGL((reduce_cols_kernel<OP, false>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K,
-                           val, idx, wv.as<float>(), wi.as<int64_t>());
+#define WM_RC(V, I)                                                                                          \
+    hipLaunchKernelGGL((reduce_cols_kernel<OP, V, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val, \
+                       idx, wv.as<float>(), wi.as<int64_t>())
+    const bool narrow = n <= (int64_t)INT32_MAX;
+    if (vec) { if (narrow) WM_RC(true, int32_t); else WM_RC(true, int64_t); }
+    else { if (narrow) WM_RC(false, int32_t); else WM_RC(false, int64_t); }
+#undef WM_RC
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
         hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0,
