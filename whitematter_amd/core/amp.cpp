@@ -1,0 +1,116 @@
+// amp.cpp -- the device parts of the drop-in amp.h: HalfTensor's
+// conversions, GradScaler::unscale, check_gradients_finite and
+// clip_grad_norm_amp (reference core/amp.h:125-147, :256-286, :293-327),
+// through libwm_hip's C ABI.
+#include "amp.h"
+
+#include <cmath>
+#include <stdexcept>
+#include <string>
+
+#include "wm_hip.h"
+#include "wm_optim.h"
+
+namespace {
+
+void check(int rc, const char* what) {
+    if (rc != WM_OK) throw std::runtime_error(std::string("whitematter_amd ") + what + ": " + wm_last_error());
+}
+
+// Device scratch for the fp16 halves of one conversion.
+struct HalfBuffer {
+    void* p = nullptr;
+    explicit HalfBuffer(size_t n) { check(wm_alloc(&p, n * sizeof(uint16_t)), "HalfTensor: device buffer"); }
+    ~HalfBuffer() { if (p) wm_free(p); }
+    HalfBuffer(const HalfBuffer&) = delete;
+    HalfBuffer& operator=(const HalfBuffer&) = delete;
+    uint16_t* get() const { return static_cast<uint16_t*>(p); }
+};
+
+// The gradients that hold values: a gradient that is empty or known to be
+// all zeros is skipped (scaling zeros leaves zeros, and zeros are finite).
+void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs, std::vector<int64_t>& sizes) {
+    for (const auto& p : params) {
+        if (!p || p->grad.empty() || p->grad.known_zero()) continue;
+        ptrs.push_back(p->grad.dev_rw());
+        sizes.push_back((int64_t)p->grad.size());
+    }
+}
+
+}  // namespace
+
+// core/amp.h:125-147
+bool GradScaler::unscale(Optimizer* optimizer) {
+    if (!enabled_) return true;
+    const float inv_scale = 1.0f / scale_;
+    std::vector<float*> ptrs;
+    std::vector<int64_t> sizes;
+    live_grads(optimizer->params, ptrs, sizes);
+    int found = 0;
+    check(wm_grad_unscale((int)ptrs.size(), ptrs.data(), sizes.data(), inv_scale, &found), "GradScaler::unscale");
+    found_inf_or_nan_ = found != 0;
+    return !found_inf_or_nan_;
+}
+
+// core/amp.h:263-267
+HalfTensor::HalfTensor(const TensorPtr& tensor) : shape(tensor->shape) {
+    const size_t n = tensor->data.size();
+    data.resize(n);
+    if (n == 0) return;
+    HalfBuffer h(n);
+    check(wm_f32_to_f16_rtz(h.get(), tensor->data.dev(), (int64_t)n), "HalfTensor");
+    check(wm_d2h(data.data(), h.get(), n * sizeof(uint16_t)), "HalfTensor");
+}
+
+// core/amp.h:270-274
+TensorPtr HalfTensor::to_float(bool requires_grad) const {
+    auto result = Tensor::create(shape, requires_grad);
+    if (result->data.size() != data.size()) result->data.resize(data.size());
+    if (data.empty()) return result;
+    HalfBuffer h(data.size());
+    check(wm_h2d(h.get(), data.data(), data.size() * sizeof(uint16_t)), "HalfTensor::to_float");
+    check(wm_f16_to_f32(result->data.dev_write(), h.get(), (int64_t)data.size()), "HalfTensor::to_float");
+    return result;
+}
+
+// core/amp.h:293-300: every element finite.  The device pass multiplies by
+// 1.0f (exact) up to the first non-finite element and reports whether there
+// is one; the values are unchanged.
+bool check_gradients_finite(const std::vector<TensorPtr>& params) {
+    std::vector<float*> ptrs;
+    std::vector<int64_t> sizes;
+    live_grads(params, ptrs, sizes);
+    int found = 0;
+    check(wm_grad_unscale((int)ptrs.size(), ptrs.data(), sizes.data(), 1.0f, &found), "check_gradients_finite");
+    return found == 0;
+}
+
+// core/amp.h:303-327: norm of g / scale over all gradients; when
+// max_norm / (norm + 1e-6f) < 1 every gradient (still scaled) is multiplied
+// by that coefficient.
+float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, float scale) {
+    const float inv_scale = 1.0f / scale;
+    std::vector<float*> ptrs;
+    std::vector<int64_t> sizes;
+    live_grads(params, ptrs, sizes);
+    float sumsq = 0.0f;
+    if (!ptrs.empty()) {
+        void* d = nullptr;
+        check(wm_alloc(&d, sizeof(float)), "clip_grad_norm_amp");
+        int rc = wm_fill(static_cast<float*>(d), 0.0f, 1);
+        if (rc == WM_OK)
+            rc = wm_grad_sumsq_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()), sizes.data(),
+                                     static_cast<float*>(d));
+        if (rc == WM_OK) rc = wm_d2h(&sumsq, d, sizeof(float));
+        wm_free(d);
+        check(rc, "clip_grad_norm_amp");
+    }
+    // sum of (g * inv_scale)^2 = inv_scale^2 * sum of g^2 (exact for a
+    // power-of-two scale, within the sums contract otherwise)
+    const float total_norm = std::sqrt(sumsq * inv_scale * inv_scale);
+    const float clip_coef = max_norm / (total_norm + 1e-6f);
+    if (clip_coef < 1.0f)
+        for (size_t k = 0; k < ptrs.size(); ++k)
+            check(wm_unary(WM_SCALE, ptrs[k], ptrs[k], sizes[k], clip_coef, 0.0f), "clip_grad_norm_amp");
+    return total_norm;
+}

@@ -11,6 +11,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include "amp.h"
 #include "layer.h"
 #include "serialize.h"
 #include "loss.h"
@@ -172,6 +173,48 @@ PYBIND11_MODULE(_tensor, m) {
              py::arg("weight_decay") = 0.0f)
         .def("state", [states](const RMSprop& o, size_t i) { return states(o.v, o.buffer, i); });
     m.def("clip_grad_norm_", [](std::vector<TensorPtr> ps, float max_norm) { clip_grad_norm_(ps, max_norm); });
+
+    // Mixed precision (amp.h): fp16 storage and loss scaling.
+    m.def("float_to_half", &float_to_half);
+    m.def("half_to_float", &half_to_float);
+    m.def("to_half", [](py::array_t<float, py::array::c_style | py::array::forcecast> x) {
+        std::vector<float> v(x.data(), x.data() + x.size());
+        const std::vector<uint16_t> h = to_half(v);
+        py::array_t<uint16_t> out(h.size());
+        if (!h.empty()) std::memcpy(out.mutable_data(), h.data(), h.size() * sizeof(uint16_t));
+        return out;
+    });
+    m.def("from_half", [](py::array_t<uint16_t, py::array::c_style | py::array::forcecast> x) {
+        std::vector<uint16_t> v(x.data(), x.data() + x.size());
+        const std::vector<float> f = from_half(v);
+        py::array_t<float> out(f.size());
+        if (!f.empty()) std::memcpy(out.mutable_data(), f.data(), f.size() * sizeof(float));
+        return out;
+    });
+    py::class_<HalfTensor>(m, "HalfTensor")
+        .def(py::init<const TensorPtr&>())
+        .def_property_readonly("data", [](const HalfTensor& h) {
+            py::array_t<uint16_t> a(h.data.size());
+            if (!h.data.empty()) std::memcpy(a.mutable_data(), h.data.data(), h.data.size() * sizeof(uint16_t));
+            return a;
+        })
+        .def_readonly("shape", &HalfTensor::shape)
+        .def("to_float", &HalfTensor::to_float, py::arg("requires_grad") = false)
+        .def("size", &HalfTensor::size)
+        .def("memory_saved", &HalfTensor::memory_saved);
+    py::class_<GradScaler>(m, "GradScaler")
+        .def(py::init<float, float, float, int, bool>(), py::arg("init_scale") = 65536.0f,
+             py::arg("growth_factor") = 2.0f, py::arg("backoff_factor") = 0.5f, py::arg("growth_interval") = 2000,
+             py::arg("enabled") = true)
+        .def("get_scale", &GradScaler::get_scale)
+        .def("scale", py::overload_cast<const TensorPtr&>(&GradScaler::scale, py::const_))
+        .def("unscale", &GradScaler::unscale)
+        .def("step", &GradScaler::step, py::arg("optimizer"), py::arg("already_unscaled") = false)
+        .def("update", &GradScaler::update)
+        .def("growth_tracker", &GradScaler::growth_tracker)
+        .def("set_scale", &GradScaler::set_scale);
+    m.def("check_gradients_finite", &check_gradients_finite);
+    m.def("clip_grad_norm_amp", &clip_grad_norm_amp, py::arg("params"), py::arg("max_norm"), py::arg("scale") = 1.0f);
     m.def("clip_grad_value_", [](std::vector<TensorPtr> ps, float c) { clip_grad_value_(ps, c); });
     m.def("get_grad_norm", &get_grad_norm);
 
