@@ -302,8 +302,11 @@ def opt_ops():
         Op("AdamW step", adam, N * 28, "multi_update_kernel<wm::Upd<1, true", N),
         Op("SGD momentum step", sgd, N * 20, "multi_update_kernel<wm::Upd<0, true", N),
         Op("RMSprop step", rms, N * 20, "multi_update_kernel<wm::Upd<2, false, false", N),
-        Op("clip_grad_norm_", clip, N * 12, "multi_sumsq_kernel", N),
-        Op("GradScaler unscale", unscale, N * 12, "multi_first_bad_kernel", N),
+        # algorithmic bytes: every gradient read once and written once (8 per
+        # element); both ops read the gradients twice (the norm, or the first
+        # non-finite position, must be known before any write), so they move 12
+        Op("clip_grad_norm_", clip, N * 8, "multi_sumsq_kernel", N),
+        Op("GradScaler unscale", unscale, N * 8, "multi_first_bad_kernel", N),
     ]
     return ops, P + G + S1 + S2 + [total], {
         "workload": "opt: %d parameter tensors, %d parameters (GPT-2-small shapes), fp32 params / grads / "
