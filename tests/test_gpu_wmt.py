@@ -220,3 +220,59 @@ def test_checkpoint_without_optimizer_and_mismatch(wm, tmp_path):
     data[4] = 2  # version 2
     write(bad, bytes(data))
     assert not t.load_checkpoint(bad, m2, None)[0]
+
+
+def test_checkpoint_state_rules_and_messages(wm, tmp_path, capfd):
+    """Checkpoints take optimizer state as it comes (core/serialize.cpp:
+    459-500): state of the other kind is skipped with a warning and the load
+    succeeds, an unknown kind tag is ignored, and a short state buffer list
+    is not compared.  WMO files refuse the same cases (:255-312) with the
+    reference's messages."""
+    t = T()
+    lin = t.Linear(6, 4)
+    params = [np.asarray(p.data).reshape(p.shape) for p in lin.parameters()]
+    vel = [rng_normal(p.shape, 200 + i).reshape(-1) for i, p in enumerate(params)]
+    sgd = wmt.sgd_block(0.25, 0.5, vel)
+    adam = wmt.adam_block(0.01, 0.9, 0.999, 1e-8, 3, vel, vel)
+    capfd.readouterr()
+    # Adam state into an SGD optimizer: skipped with a warning, load succeeds
+    p = str(tmp_path / "a.ckpt")
+    write(p, wmt.checkpoint_file(4, 0.75, 0.5, params, adam))
+    opt = t.SGD(lin.parameters(), 0.1, 0.9)
+    ok, epoch, loss, acc = t.load_checkpoint(p, lin, opt)
+    err = capfd.readouterr().err
+    assert ok and epoch == 4 and "Warning: Checkpoint has Adam state but optimizer is not Adam, skipping" in err
+    assert opt.lr == np.float32(0.1)
+    # an unknown kind tag is ignored
+    write(p, wmt.checkpoint_file(4, 0.75, 0.5, params, struct_u32(7)))
+    assert t.load_checkpoint(p, lin, opt)[0]
+    # the checkpoint reads each buffer's own size whatever count the file states
+    bad_count = bytearray(sgd)
+    bad_count[12] = 9  # the velocity count word
+    write(p, wmt.checkpoint_file(4, 0.75, 0.5, params, bytes(bad_count)))
+    assert t.load_checkpoint(p, lin, opt)[0]
+    assert opt.lr == np.float32(0.25) and opt.momentum == np.float32(0.5)
+    for i in range(len(params)):
+        assert np.array_equal(opt.state(i)[0].reshape(-1), vel[i])
+    # the same block in a WMO file is refused on the count, with its message
+    q = str(tmp_path / "o.wmo")
+    capfd.readouterr()
+    write(q, wmt.optimizer_file(bytes(bad_count)))
+    assert not t.load_optimizer(opt, q)
+    assert "Error: Velocity buffer count mismatch" in capfd.readouterr().err
+    write(q, wmt.optimizer_file(adam))
+    assert not t.load_optimizer(opt, q)
+    assert "Error: File contains Adam state but optimizer is not Adam" in capfd.readouterr().err
+    write(q, wmt.optimizer_file(struct_u32(7)))
+    assert not t.load_optimizer(opt, q)
+    assert "Error: Unknown optimizer type in file: 7" in capfd.readouterr().err
+    # a size mismatch in the WMO file refuses too
+    short = [v[:-1] for v in vel]
+    write(q, wmt.optimizer_file(wmt.sgd_block(0.25, 0.5, short)))
+    assert not t.load_optimizer(opt, q)
+    assert "Error: Velocity buffer size mismatch" in capfd.readouterr().err
+
+
+def struct_u32(v):
+    import struct
+    return struct.pack("<I", v)

@@ -155,6 +155,7 @@ PYBIND11_MODULE(_tensor, m) {
     py::class_<SGD, Optimizer>(m, "SGD")
         .def(py::init<const std::vector<TensorPtr>&, float, float>(), py::arg("params"), py::arg("lr"),
              py::arg("momentum") = 0.0f)
+        .def_readwrite("momentum", &SGD::momentum)
         .def("state", [states](const SGD& o, size_t i) { return states(o.velocity, {}, i); });
     py::class_<Adam, Optimizer>(m, "Adam")
         .def(py::init<const std::vector<TensorPtr>&, float, float, float, float>(), py::arg("params"),
