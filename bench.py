@@ -52,7 +52,8 @@ class Op:
     def __init__(self, name, launch, nbytes, kernel, elems, flops=None):
         self.name, self.launch, self.bytes, self.kernel, self.elems = name, launch, nbytes, kernel, elems
         self.flops = flops  # set for matrix-core ops: their roofline is TFLOP/s, not HBM
-        self.ms = []
+        self.ms = []   # event basis: markers before and after the op on the library stream
+        self.kms = []  # kernel basis: first kernel's start to last kernel's end (wm_span_*)
 
 
 # ---------------------------------------------------------------------------
@@ -667,11 +668,18 @@ def main():
     def run_op(op, timed):
         flush.fill(1.0)
         if timed:
+            W.call("wm_span_begin")
             W.call("wm_timer_start")
         op.launch()
         if timed:
-            ms = W.C.c_float()
+            ms, kms, nk = W.C.c_float(), W.C.c_float(), W.C.c_int()
             W.call("wm_timer_stop", W.C.byref(ms))
+            if getattr(op, "host_io", False):
+                W.lib().wm_span_end(W.C.byref(kms), W.C.byref(nk))  # no kernels: host-driven copies
+                op.kms.append(ms.value)
+            else:
+                W.call("wm_span_end", W.C.byref(kms), W.C.byref(nk))
+                op.kms.append(kms.value)
             op.ms.append(ms.value)
 
     for _ in range(args.warmup):
@@ -694,6 +702,7 @@ def main():
         step_bytes += op.bytes
         gbps = op.bytes / (ms * 1e-3) / 1e9
         per_op[op.name] = {"ms": round(ms, 4), "ms_median": round(statistics.median(op.ms), 4),
+                           "ms_kernel_median": round(statistics.median(op.kms), 4),
                            "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
                            "Gelem_per_s": round(op.elems / (ms * 1e-3) / 1e9, 2), "bytes": op.bytes}
         if op.flops:

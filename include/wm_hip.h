@@ -104,6 +104,15 @@ int wm_device_cus(int* cus);
 /* Events on the library stream bracketing enqueued work. */
 int wm_timer_start(void);
 int wm_timer_stop(float* elapsed_ms);
+/* Kernel timing: between wm_span_begin and wm_span_end, each kernel the
+   library launches (up to 64) carries a start and a stop event bound to its
+   own dispatch.  wm_span_end waits for the last one and gives the sum of the
+   kernels' durations (*kernel_ms: what a kernel trace shows, without the
+   marker packets wm_timer_* put around the work) and, if span_ms is not
+   null, the time from the first kernel's start to the last one's end.
+   It fails if no kernel ran. */
+int wm_span_begin(void);
+int wm_span_end(float* kernel_ms, float* span_ms, int* kernels);
 /* Plain streaming copy kernel, used to calibrate rocprof byte counters. */
 int wm_copy_kernel(float* dst, const float* src, int64_t n);
 

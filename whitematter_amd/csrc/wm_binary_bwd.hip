@@ -399,7 +399,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
     if (a_full && b_full) {
         if (numel % 4 == 0 && aligned) {
             int64_t n4 = numel / 4;
-            hipLaunchKernelGGL(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock * 4, 32)), dim3(kBlock), 0, st, g, a, b, o,
+            launch_kernel(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock * 4, 32)), dim3(kBlock), 0, st, g, a, b, o,
                                ga, acc_a, gb, acc_b, n4);
             return check_launch("wm_binary_bwd(flat)");
         }
@@ -428,14 +428,14 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
             if (gV && !ws.p) return set_error(WM_ERR_NOMEM, "wm_binary_bwd: workspace");
             dim3 grid((unsigned)col_tiles, (unsigned)K);
             if (vb)
-                hipLaunchKernelGGL((bwd_colsum_kernel<OP, true>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
+                launch_kernel((bwd_colsum_kernel<OP, true>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
                                    ws.as<float>(), R, C, rpc);
             else
-                hipLaunchKernelGGL((bwd_colsum_kernel<OP, false>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
+                launch_kernel((bwd_colsum_kernel<OP, false>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
                                    ws.as<float>(), R, C, rpc);
             WM_TRY(check_launch("wm_binary_bwd(colsum)"));
             if (gV) {
-                hipLaunchKernelGGL(colsum_finalize_kernel, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st,
+                launch_kernel(colsum_finalize_kernel, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st,
                                    ws.as<float>(), gV, accV, K, C);
                 WM_TRY(check_launch("wm_binary_bwd(colsum finalize)"));
             }
@@ -456,14 +456,14 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
             const bool vec = C % 4 == 0 && aligned;
             dim3 grid(grid_for(R * K, kBlock / 64, 32));
 #define WM_RS(VBv, VECv)                                                                                          \
-    hipLaunchKernelGGL((bwd_rowsum_kernel<OP, VBv, VECv>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF, gV, accV, \
+    launch_kernel((bwd_rowsum_kernel<OP, VBv, VECv>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF, gV, accV, \
                        ws.as<float>(), R, C, chunk, K)
             if (vb) { if (vec) WM_RS(true, true); else WM_RS(true, false); }
             else { if (vec) WM_RS(false, true); else WM_RS(false, false); }
 #undef WM_RS
             WM_TRY(check_launch("wm_binary_bwd(rowsum)"));
             if (gV && K > 1) {
-                hipLaunchKernelGGL(rowsum_finalize_kernel, dim3(grid_for(R, 1, 8)), dim3(kBlock), 0, st,
+                launch_kernel(rowsum_finalize_kernel, dim3(grid_for(R, 1, 8)), dim3(kBlock), 0, st,
                                    ws.as<float>(), gV, accV, R, K);
                 WM_TRY(check_launch("wm_binary_bwd(rowsum finalize)"));
             }
@@ -480,12 +480,12 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
         so *= size[k];
     }
     if (ga) {
-        hipLaunchKernelGGL((bwd_generic_kernel<OP, false>), dim3(grid_for(na, kBlock)), dim3(kBlock), 0, st, g, a, b,
+        launch_kernel((bwd_generic_kernel<OP, false>), dim3(grid_for(na, kBlock)), dim3(kBlock), 0, st, g, a, b,
                            o, ga, acc_a, na, d);
         WM_TRY(check_launch("wm_binary_bwd(generic a)"));
     }
     if (gb) {
-        hipLaunchKernelGGL((bwd_generic_kernel<OP, true>), dim3(grid_for(nb, kBlock)), dim3(kBlock), 0, st, g, a, b,
+        launch_kernel((bwd_generic_kernel<OP, true>), dim3(grid_for(nb, kBlock)), dim3(kBlock), 0, st, g, a, b,
                            o, gb, acc_b, nb, d);
         WM_TRY(check_launch("wm_binary_bwd(generic b)"));
     }

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <cstdint>
 #include <cstddef>
 #include <cmath>
@@ -43,6 +44,21 @@ int upload_async(void* dev_dst, const void* host_src, size_t bytes);
 
 // Check the launch that was just enqueued.
 int check_launch(const char* what);
+
+// Events for the next launch: both null unless a kernel span is open
+// (wm_span_begin); then the span's first launch gets the start event and
+// every launch the stop event.
+void span_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel of the library is launched through here: a plain launch, or
+// one whose dispatch carries the open kernel span's events.
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+                          Args... args) {
+    hipEvent_t e0, e1;
+    span_events(&e0, &e1);
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, e0, e1, 0u, args...);
+}
 
 #define WM_TRY(expr)                 \
     do {                             \

@@ -413,7 +413,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     // Same shape (or both fully contiguous after folding): flat float4 walk.
     if (nd == 1 && ia == 1 && ib == 1 && (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         int64_t n4 = inner / 4;
-        hipLaunchKernelGGL(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
+        launch_kernel(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
                            out, a, b, n4);
         return check_launch("wm_binary(flat)");
     }
@@ -438,7 +438,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         }
         if (nd == 1) stream_a = stream_b = 1;
 #define WM_ROWS(AI, BI, V) \
-    hipLaunchKernelGGL((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
+    launch_kernel((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
                        stream_a, stream_b)
         if (vec) {
             if (ia && ib) WM_ROWS(1, 1, true);
@@ -457,7 +457,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     FullDims d;
     d.nd = nd;
     for (int i = 0; i < nd; ++i) { d.size[i] = L.size[i]; d.sa[i] = L.sa[i]; d.sb[i] = L.sb[i]; }
-    hipLaunchKernelGGL(binary_generic_kernel<OP>, dim3(grid_for(L.numel, kBlock)), dim3(kBlock), 0, s, out, a, b,
+    launch_kernel(binary_generic_kernel<OP>, dim3(grid_for(L.numel, kBlock)), dim3(kBlock), 0, s, out, a, b,
                        L.numel, d);
     return check_launch("wm_binary(generic)");
 }
@@ -466,10 +466,10 @@ template <int OP>
 int launch_unary(float* out, const float* x, int64_t n, float p0, float p1) {
     hipStream_t s = stream();
     if (aligned16(out) && aligned16(x)) {
-        hipLaunchKernelGGL(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
+        launch_kernel(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
                            out, x, n, p0, p1);
     } else {
-        hipLaunchKernelGGL(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
+        launch_kernel(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
                            p0, p1);
     }
     return check_launch("wm_unary");
@@ -486,11 +486,11 @@ int launch_unary_bwd(const float* g, const float* x, const float* o, float* gx, 
     bool vec = aligned16(g) && aligned16(gx) && (!RX || aligned16(x)) && (!RO || aligned16(o));
     dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll, 32)), grid_s(grid_for(n, kBlock));
     if (vec) {
-        if (acc) hipLaunchKernelGGL((unary_bwd_kernel<OP, true>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
-        else hipLaunchKernelGGL((unary_bwd_kernel<OP, false>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        if (acc) launch_kernel((unary_bwd_kernel<OP, true>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        else launch_kernel((unary_bwd_kernel<OP, false>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
     } else {
-        if (acc) hipLaunchKernelGGL((unary_bwd_scalar_kernel<OP, true>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
-        else hipLaunchKernelGGL((unary_bwd_scalar_kernel<OP, false>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        if (acc) launch_kernel((unary_bwd_scalar_kernel<OP, true>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
+        else launch_kernel((unary_bwd_scalar_kernel<OP, false>), grid_s, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
     }
     return check_launch("wm_unary_bwd");
 }
@@ -521,10 +521,10 @@ int wm_fill(float* out, float value, int64_t n) {
     if (!out) return set_error(WM_ERR_INVALID, "wm_fill: null pointer");
     WM_CHECK_INIT();
     if (aligned16(out) && n % 4 == 0) {
-        hipLaunchKernelGGL(fill_vec_kernel, dim3(grid_for(n / 4, kBlock, 64)), dim3(kBlock), 0, stream(), out,
+        launch_kernel(fill_vec_kernel, dim3(grid_for(n / 4, kBlock, 64)), dim3(kBlock), 0, stream(), out,
                            value, n / 4);
     } else {
-        hipLaunchKernelGGL(fill_scalar_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, stream(), out, value, n);
+        launch_kernel(fill_scalar_kernel, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, stream(), out, value, n);
     }
     return check_launch("wm_fill");
 }
@@ -536,7 +536,7 @@ int wm_copy_kernel(float* dst, const float* src, int64_t n) {
     if (n % 4 || !aligned16(dst) || !aligned16(src))
         return set_error(WM_ERR_INVALID, "wm_copy_kernel: needs 16-byte aligned buffers and n % 4 == 0");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll, 32)), dim3(kBlock), 0, stream(), dst,
+    launch_kernel(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll, 32)), dim3(kBlock), 0, stream(), dst,
                        src, n / 4);
     return check_launch("wm_copy_kernel");
 }
@@ -548,7 +548,7 @@ int wm_f32_to_f16_rtz(uint16_t* out, const float* x, int64_t n) {
     if (!aligned16(x) || ((uintptr_t)out & 7u))
         return set_error(WM_ERR_INVALID, "wm_f32_to_f16_rtz: x must be 16-byte and out 8-byte aligned");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    launch_kernel(f32_to_f16_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
     return check_launch("wm_f32_to_f16_rtz");
 }
 
@@ -559,7 +559,7 @@ int wm_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
     if (!aligned16(out) || ((uintptr_t)x & 7u))
         return set_error(WM_ERR_INVALID, "wm_f16_to_f32: out must be 16-byte and x 8-byte aligned");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(f16_to_f32_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    launch_kernel(f16_to_f32_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
     return check_launch("wm_f16_to_f32");
 }
 

@@ -241,10 +241,10 @@ int wm_epilogue_f16_fwd(uint16_t* out, float* mean, const uint16_t* h, const uin
     const bool vec = cols % 8 == 0 && aligned16(h) && aligned16(res) && aligned16(g) && (!out || aligned16(out));
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 16));
     if (vec)
-        hipLaunchKernelGGL(epilogue_fwd_kernel<true>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
+        launch_kernel(epilogue_fwd_kernel<true>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
                            cols, lo, hi);
     else
-        hipLaunchKernelGGL(epilogue_fwd_kernel<false>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
+        launch_kernel(epilogue_fwd_kernel<false>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
                            cols, lo, hi);
     return check_launch("wm_epilogue_f16_fwd");
 }
@@ -273,14 +273,14 @@ int wm_epilogue_f16_bwd(const float* dm, const uint16_t* h, const uint16_t* res,
     if (gg && !ws.p) return set_error(WM_ERR_NOMEM, "wm_epilogue_f16_bwd: workspace");
     dim3 grid((unsigned)col_tiles, (unsigned)K);
     if (vec)
-        hipLaunchKernelGGL(epilogue_bwd_kernel<true>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres,
+        launch_kernel(epilogue_bwd_kernel<true>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres,
                            acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
     else
-        hipLaunchKernelGGL(epilogue_bwd_kernel<false>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h,
+        launch_kernel(epilogue_bwd_kernel<false>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h,
                            gres, acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
     WM_TRY(check_launch("wm_epilogue_f16_bwd"));
     if (gg) {
-        hipLaunchKernelGGL(epilogue_gsum_kernel, dim3(grid_for(cols, 64, 8)), dim3(kBlock), 0, stream(),
+        launch_kernel(epilogue_gsum_kernel, dim3(grid_for(cols, 64, 8)), dim3(kBlock), 0, stream(),
                            ws.as<float>(), gg, acc_g, K, cols);
         WM_TRY(check_launch("wm_epilogue_f16_bwd(gsum)"));
     }

@@ -471,8 +471,8 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     dim3 grid((unsigned)(tm * tn), (unsigned)std::min<int64_t>(P.batch * P.kslices, 65535));
 #define WM_GEMM(TA, TB, V)                                                                   \
     do {                                                                                     \
-        if (narrow) hipLaunchKernelGGL((gemm_kernel<TA, TB, V, 64>), grid, dim3(kThreads), 0, s, P); \
-        else hipLaunchKernelGGL((gemm_kernel<TA, TB, V, 128>), grid, dim3(kThreads), 0, s, P);       \
+        if (narrow) launch_kernel((gemm_kernel<TA, TB, V, 64>), grid, dim3(kThreads), 0, s, P); \
+        else launch_kernel((gemm_kernel<TA, TB, V, 128>), grid, dim3(kThreads), 0, s, P);       \
     } while (0)
     if (vec) {
         if (!ta && !tb) WM_GEMM(false, false, true);
@@ -490,7 +490,7 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
         WM_TRY(check_launch("wm_gemm"));
         const bool c_vec = F.c_aligned && (F.ldc & 3) == 0;
         const int64_t items = F.batch * F.m * ((F.n + 3) / 4);
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid_for(items, 256)), dim3(256), 0, s, part.as<float>(),
+        launch_kernel(splitk_reduce_kernel, dim3(grid_for(items, 256)), dim3(256), 0, s, part.as<float>(),
                            P.kslices, F.m, F.n, F.batch, F.batch_inner, F.c, F.ldc, F.sc0, F.sc1, F.alpha,
                            F.accumulate, F.bias, c_vec ? 1 : 0);
     }
@@ -586,7 +586,7 @@ int wm_transpose2d(const float* x, int64_t rows, int64_t cols, float* out, int a
     const int64_t tiles_c = (cols + kTT - 1) / kTT;
     const int64_t ntiles = ((rows + kTT - 1) / kTT) * tiles_c;
     const unsigned grid = (unsigned)std::min<int64_t>(ntiles, (int64_t)num_cus() * 16);
-    hipLaunchKernelGGL(transpose_kernel, dim3(grid), dim3(256), 0, stream(), x, rows, cols, out, accumulate ? 1 : 0,
+    launch_kernel(transpose_kernel, dim3(grid), dim3(256), 0, stream(), x, rows, cols, out, accumulate ? 1 : 0,
                        tiles_c, ntiles);
     return check_launch("wm_transpose2d");
 }

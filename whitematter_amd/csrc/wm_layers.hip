@@ -242,16 +242,16 @@ int colsum_parts(const float* part, int64_t parts, int64_t n, float* out, int ac
     hipStream_t st = stream();
     const dim3 cg((unsigned)((n + 63) / 64));
     if (parts <= 64) {
-        hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, part, parts, n, out, acc);
+        launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, part, parts, n, out, acc);
         return check_launch(what);
     }
     const int64_t chunk = 64, parts2 = (parts + chunk - 1) / chunk;
     Workspace w2((size_t)(parts2 * n) * sizeof(float));
     if (!w2.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
-    hipLaunchKernelGGL(colsum_stage_kernel, dim3(cg.x, (unsigned)parts2), dim3(256), 0, st, part, parts, n, chunk,
+    launch_kernel(colsum_stage_kernel, dim3(cg.x, (unsigned)parts2), dim3(256), 0, st, part, parts, n, chunk,
                        w2.as<float>());
     WM_TRY(check_launch(what));
-    hipLaunchKernelGGL(colsum_parts_kernel, cg, dim3(256), 0, st, w2.as<float>(), parts2, n, out, acc);
+    launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, w2.as<float>(), parts2, n, out, acc);
     return check_launch(what);
 }
 
@@ -761,17 +761,17 @@ int launch_ln_fwd(const float* x, const float* gamma, const float* beta, int64_t
     const bool vec = n % 4 == 0 && aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
     if (tc.nt == 0) {
         dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 2));
-        hipLaunchKernelGGL(ln_fwd_long_kernel, grid, dim3(1024), 0, st, x, gamma, beta, rows, n, eps, y, mean, inv);
+        launch_kernel(ln_fwd_long_kernel, grid, dim3(1024), 0, st, x, gamma, beta, rows, n, eps, y, mean, inv);
         return check_launch("wm_layernorm_fwd(long)");
     }
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * ln_waves(tc.nt) * 2));
 #define WM_LNF(NTv, IT)                                                                                         \
     if (tc.nt == NTv && tc.items == IT) {                                                                       \
         if (vec)                                                                                                \
-            hipLaunchKernelGGL((ln_fwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, x, gamma, beta, rows, n, \
+            launch_kernel((ln_fwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, x, gamma, beta, rows, n, \
                                eps, y, mean, inv);                                                              \
         else                                                                                                    \
-            hipLaunchKernelGGL((ln_fwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, x, gamma, beta, rows,   \
+            launch_kernel((ln_fwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, x, gamma, beta, rows,   \
                                n, eps, y, mean, inv);                                                           \
         return check_launch("wm_layernorm_fwd");                                                                \
     }
@@ -788,7 +788,7 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
     if (tc.nt == 0) {
         if (gx) {
             dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 2));
-            hipLaunchKernelGGL(ln_bwd_long_kernel, grid, dim3(1024), 0, st, g, x, gamma, mean, inv, rows, n, gx,
+            launch_kernel(ln_bwd_long_kernel, grid, dim3(1024), 0, st, g, x, gamma, mean, inv, rows, n, gx,
                                acc_x);
             WM_TRY(check_launch("wm_layernorm_bwd(long)"));
         }
@@ -798,7 +798,7 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
         Workspace wg(dgamma ? (size_t)(chunks * n) * sizeof(float) : 0);
         Workspace wb(dbeta ? (size_t)(chunks * n) * sizeof(float) : 0);
         if ((dgamma && !wg.p) || (dbeta && !wb.p)) return set_error(WM_ERR_NOMEM, "wm_layernorm_bwd: workspace");
-        hipLaunchKernelGGL(ln_param_parts_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)chunks), dim3(256), 0,
+        launch_kernel(ln_param_parts_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)chunks), dim3(256), 0,
                            st, g, x, mean, inv, rows, n, rpc, wg.as<float>(), wb.as<float>());
         WM_TRY(check_launch("wm_layernorm_bwd(params)"));
         if (dgamma) WM_TRY(colsum_parts(wg.as<float>(), chunks, n, dgamma, acc_g, "wm_layernorm_bwd(colsum)"));
@@ -818,10 +818,10 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
 #define WM_LNB(NTv, IT)                                                                                         \
     if (!launched && tc.nt == NTv && tc.items == IT) {                                                          \
         if (vec)                                                                                                \
-            hipLaunchKernelGGL((ln_bwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, g, x, gamma, mean, inv,  \
+            launch_kernel((ln_bwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, g, x, gamma, mean, inv,  \
                                rows, n, gx, acc_x, wg.as<float>(), wb.as<float>());                             \
         else                                                                                                    \
-            hipLaunchKernelGGL((ln_bwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, g, x, gamma, mean, inv, \
+            launch_kernel((ln_bwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, g, x, gamma, mean, inv, \
                                rows, n, gx, acc_x, wg.as<float>(), wb.as<float>());                             \
         launched = true;                                                                                        \
     }
@@ -903,17 +903,17 @@ int wm_batchnorm2d_fwd(const float* x, const float* gamma, const float* beta, fl
     if (training && !part.p) return set_error(WM_ERR_NOMEM, "wm_batchnorm2d_fwd: workspace");
     const dim3 grid((unsigned)gm.chunks, (unsigned)channels);
     if (training) {
-        if (vec) hipLaunchKernelGGL(bn_stats_kernel<true>, grid, dim3(256), 0, st, x, gm, part.as<double>());
-        else hipLaunchKernelGGL(bn_stats_kernel<false>, grid, dim3(256), 0, st, x, gm, part.as<double>());
+        if (vec) launch_kernel(bn_stats_kernel<true>, grid, dim3(256), 0, st, x, gm, part.as<double>());
+        else launch_kernel(bn_stats_kernel<false>, grid, dim3(256), 0, st, x, gm, part.as<double>());
         WM_TRY(check_launch("wm_batchnorm2d_fwd(stats)"));
     }
-    hipLaunchKernelGGL(bn_stats_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
+    launch_kernel(bn_stats_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
                        part.as<double>(), channels, gm.chunks, n, eps, momentum, training, running_mean, running_var,
                        mean, inv_std);
     WM_TRY(check_launch("wm_batchnorm2d_fwd(finalize)"));
     if (n == 0) return WM_OK;
-    if (vec) hipLaunchKernelGGL(bn_apply_kernel<true>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
-    else hipLaunchKernelGGL(bn_apply_kernel<false>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
+    if (vec) launch_kernel(bn_apply_kernel<true>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
+    else launch_kernel(bn_apply_kernel<false>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
     return check_launch("wm_batchnorm2d_fwd(apply)");
 }
 
@@ -933,20 +933,20 @@ int wm_batchnorm2d_bwd(const float* g, const float* x, const float* gamma, const
     Workspace coef((size_t)channels * sizeof(float2));
     if (!part.p || !coef.p) return set_error(WM_ERR_NOMEM, "wm_batchnorm2d_bwd: workspace");
     const dim3 grid((unsigned)gm.chunks, (unsigned)channels);
-    if (vec) hipLaunchKernelGGL(bn_bwd_sums_kernel<true>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
-    else hipLaunchKernelGGL(bn_bwd_sums_kernel<false>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
+    if (vec) launch_kernel(bn_bwd_sums_kernel<true>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
+    else launch_kernel(bn_bwd_sums_kernel<false>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
     WM_TRY(check_launch("wm_batchnorm2d_bwd(sums)"));
-    hipLaunchKernelGGL(bn_bwd_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
+    launch_kernel(bn_bwd_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
                        part.as<double>(), channels, gm.chunks, n, gamma, inv_std, dgamma, acc_gamma, dbeta, acc_beta,
                        coef.as<float2>());
     WM_TRY(check_launch("wm_batchnorm2d_bwd(finalize)"));
     if (!gx || n == 0) return WM_OK;
     const float nf = (float)n;
     if (vec)
-        hipLaunchKernelGGL(bn_bwd_apply_kernel<true>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
+        launch_kernel(bn_bwd_apply_kernel<true>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
                            coef.as<float2>(), gm, nf, gx, acc_x);
     else
-        hipLaunchKernelGGL(bn_bwd_apply_kernel<false>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
+        launch_kernel(bn_bwd_apply_kernel<false>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
                            coef.as<float2>(), gm, nf, gx, acc_x);
     return check_launch("wm_batchnorm2d_bwd(apply)");
 }
@@ -967,17 +967,17 @@ int wm_attention_softmax_fwd(const float* scores, const float* mask, int64_t mas
     const bool vec = tk % 4 == 0 && aligned16(scores) && aligned16(attn) && (!mask || aligned16(mask));
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
     if (tc.nt == 0) {
-        hipLaunchKernelGGL(attn_softmax_fwd_long_kernel, grid, dim3(1024), 0, st, scores, mask, mstride, heads * tq,
+        launch_kernel(attn_softmax_fwd_long_kernel, grid, dim3(1024), 0, st, scores, mask, mstride, heads * tq,
                            tq, rows, tk, attn);
         return check_launch("wm_attention_softmax_fwd(long)");
     }
 #define WM_ASF(NTv, IT)                                                                                          \
     if (tc.nt == NTv && tc.items == IT) {                                                                        \
         if (vec)                                                                                                 \
-            hipLaunchKernelGGL((attn_softmax_fwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, scores, mask,   \
+            launch_kernel((attn_softmax_fwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, scores, mask,   \
                                mstride, heads * tq, tq, rows, tk, attn);                                         \
         else                                                                                                     \
-            hipLaunchKernelGGL((attn_softmax_fwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, scores, mask,  \
+            launch_kernel((attn_softmax_fwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, scores, mask,  \
                                mstride, heads * tq, tq, rows, tk, attn);                                         \
         return check_launch("wm_attention_softmax_fwd");                                                         \
     }
@@ -997,16 +997,16 @@ int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t row
     const bool vec = tk % 4 == 0 && aligned16(attn) && aligned16(d_attn) && aligned16(d_scores);
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
     if (tc.nt == 0) {
-        hipLaunchKernelGGL(attn_softmax_bwd_long_kernel, grid, dim3(1024), 0, st, attn, d_attn, rows, tk, d_scores);
+        launch_kernel(attn_softmax_bwd_long_kernel, grid, dim3(1024), 0, st, attn, d_attn, rows, tk, d_scores);
         return check_launch("wm_attention_softmax_bwd(long)");
     }
 #define WM_ASB(NTv, IT)                                                                                         \
     if (tc.nt == NTv && tc.items == IT) {                                                                       \
         if (vec)                                                                                                \
-            hipLaunchKernelGGL((attn_softmax_bwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, attn, d_attn,  \
+            launch_kernel((attn_softmax_bwd_kernel<NTv, IT, true>), grid, dim3(NTv), 0, st, attn, d_attn,  \
                                rows, tk, d_scores);                                                             \
         else                                                                                                    \
-            hipLaunchKernelGGL((attn_softmax_bwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, attn, d_attn, \
+            launch_kernel((attn_softmax_bwd_kernel<NTv, IT, false>), grid, dim3(NTv), 0, st, attn, d_attn, \
                                rows, tk, d_scores);                                                             \
         return check_launch("wm_attention_softmax_bwd");                                                        \
     }
@@ -1022,7 +1022,7 @@ int wm_dropout_mask(float* mask, int64_t n, float p, uint64_t seed) {
     if (!mask) return set_error(WM_ERR_INVALID, "wm_dropout_mask: null pointer");
     WM_CHECK_INIT();
     const float scale = 1.0f / (1.0f - p);  // core/layer.cpp:55
-    hipLaunchKernelGGL(dropout_mask_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream(), mask, n, p, scale, seed);
+    launch_kernel(dropout_mask_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream(), mask, n, p, scale, seed);
     return check_launch("wm_dropout_mask");
 }
 

@@ -440,16 +440,16 @@ constexpr int64_t kChunk = 16384;
 int sum_to_loss(const float* v, int64_t n, int64_t stride, float sign, float denom, float* out, const char* what) {
     hipStream_t st = stream();
     if (n <= kDirect) {
-        hipLaunchKernelGGL(sum_finalize_kernel, dim3(1), dim3(1024), 0, st, v, n, stride, sign, denom, out);
+        launch_kernel(sum_finalize_kernel, dim3(1), dim3(1024), 0, st, v, n, stride, sign, denom, out);
         return check_launch(what);
     }
     const int64_t parts = (n + kChunk - 1) / kChunk;
     Workspace ws((size_t)parts * sizeof(float));
     if (!ws.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
-    hipLaunchKernelGGL(sum_chunks_kernel, dim3((unsigned)parts), dim3(256), 0, st, v, n, stride, kChunk,
+    launch_kernel(sum_chunks_kernel, dim3((unsigned)parts), dim3(256), 0, st, v, n, stride, kChunk,
                        ws.as<float>());
     WM_TRY(check_launch(what));
-    hipLaunchKernelGGL(sum_finalize_kernel, dim3(1), dim3(1024), 0, st, ws.as<float>(), parts, (int64_t)1, sign,
+    launch_kernel(sum_finalize_kernel, dim3(1), dim3(1024), 0, st, ws.as<float>(), parts, (int64_t)1, sign,
                        denom, out);
     return check_launch(what);
 }
@@ -468,16 +468,16 @@ int launch_head_fwd(const float* x, const float* labels, int64_t rows, int64_t c
         dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
         bool launched = false;
         if (tc.nt == 0) {
-            hipLaunchKernelGGL(head_fwd_long_kernel<FOCAL>, grid, dim3(1024), 0, st, x, labels, rows, cols, stats);
+            launch_kernel(head_fwd_long_kernel<FOCAL>, grid, dim3(1024), 0, st, x, labels, rows, cols, stats);
             launched = true;
         }
 #define WM_HF(NTv, IT)                                                                                          \
     if (!launched && tc.nt == NTv && tc.items == IT) {                                                          \
         if (vec)                                                                                                \
-            hipLaunchKernelGGL((head_fwd_kernel<NTv, IT, true, FOCAL>), grid, dim3(NTv), 0, st, x, labels, rows, \
+            launch_kernel((head_fwd_kernel<NTv, IT, true, FOCAL>), grid, dim3(NTv), 0, st, x, labels, rows, \
                                cols, stats);                                                                    \
         else                                                                                                    \
-            hipLaunchKernelGGL((head_fwd_kernel<NTv, IT, false, FOCAL>), grid, dim3(NTv), 0, st, x, labels,    \
+            launch_kernel((head_fwd_kernel<NTv, IT, false, FOCAL>), grid, dim3(NTv), 0, st, x, labels,    \
                                rows, cols, stats);                                                              \
         launched = true;                                                                                        \
     }
@@ -487,7 +487,7 @@ int launch_head_fwd(const float* x, const float* labels, int64_t rows, int64_t c
         if (!launched) return set_error(WM_ERR_INVALID, std::string(what) + ": no tile");
         WM_TRY(check_launch(what));
         if (FOCAL) {
-            hipLaunchKernelGGL(focal_rows_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, st, stats, rows, gamma,
+            launch_kernel(focal_rows_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, st, stats, rows, gamma,
                                alpha);
             WM_TRY(check_launch(what));
         }
@@ -505,10 +505,10 @@ int launch_head_bwd(const float* x, const float* labels, const float* stats, con
     const bool vec = cols % 4 == 0 && aligned16(gx) && (MODE == kOneHot || aligned16(x));
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 8));
     if (vec)
-        hipLaunchKernelGGL((head_bwd_kernel<MODE, true>), grid, dim3(256), 0, stream(), x, labels, stats, loss_grad,
+        launch_kernel((head_bwd_kernel<MODE, true>), grid, dim3(256), 0, stream(), x, labels, stats, loss_grad,
                            gx, acc, rows, cols, alpha);
     else
-        hipLaunchKernelGGL((head_bwd_kernel<MODE, false>), grid, dim3(256), 0, stream(), x, labels, stats,
+        launch_kernel((head_bwd_kernel<MODE, false>), grid, dim3(256), 0, stream(), x, labels, stats,
                            loss_grad, gx, acc, rows, cols, alpha);
     return check_launch(what);
 }
@@ -520,10 +520,10 @@ int launch_pw_fwd(const float* x, const float* y, int64_t n, float p0, float p1,
     Workspace ws((size_t)grid * sizeof(float));
     if (!ws.p) return set_error(WM_ERR_NOMEM, "wm_pointwise_loss_fwd: workspace");
     if (vec)
-        hipLaunchKernelGGL((pw_fwd_kernel<KIND, true>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1,
+        launch_kernel((pw_fwd_kernel<KIND, true>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1,
                            ws.as<float>());
     else
-        hipLaunchKernelGGL((pw_fwd_kernel<KIND, false>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1,
+        launch_kernel((pw_fwd_kernel<KIND, false>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1,
                            ws.as<float>());
     WM_TRY(check_launch("wm_pointwise_loss_fwd"));
     return sum_to_loss(ws.as<float>(), grid, 1, 1.0f, denom, loss, "wm_pointwise_loss_fwd");
@@ -535,10 +535,10 @@ int launch_pw_bwd(const float* x, const float* y, int64_t n, float p0, float p1,
     const bool vec = aligned16(x) && aligned16(y) && aligned16(gx);
     const unsigned grid = grid_for((n + 3) / 4, 256 * kUnroll, 4);
     if (vec)
-        hipLaunchKernelGGL((pw_bwd_kernel<KIND, true>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1, denom,
+        launch_kernel((pw_bwd_kernel<KIND, true>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1, denom,
                            loss_grad, gx, acc);
     else
-        hipLaunchKernelGGL((pw_bwd_kernel<KIND, false>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1, denom,
+        launch_kernel((pw_bwd_kernel<KIND, false>), dim3(grid), dim3(256), 0, stream(), x, y, n, p0, p1, denom,
                            loss_grad, gx, acc);
     return check_launch("wm_pointwise_loss_bwd");
 }
@@ -585,7 +585,7 @@ int wm_nll_fwd(const float* pred, const float* labels, int64_t rows, int64_t cla
     Workspace terms((size_t)std::max<int64_t>(rows, 1) * sizeof(float));
     if (!terms.p) return set_error(WM_ERR_NOMEM, "wm_nll_fwd: workspace");
     if (rows > 0) {
-        hipLaunchKernelGGL(nll_gather_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), pred, labels, rows,
+        launch_kernel(nll_gather_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), pred, labels, rows,
                            classes, terms.as<float>());
         WM_TRY(check_launch("wm_nll_fwd"));
     }
@@ -599,7 +599,7 @@ int wm_nll_bwd(const float* labels, const float* loss_grad, float* grad, int acc
     if (!loss_grad) return set_error(WM_ERR_INVALID, "wm_nll_bwd: null loss_grad");
     WM_CHECK_INIT();
     if (accumulate) {
-        hipLaunchKernelGGL(nll_scatter_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), labels, loss_grad,
+        launch_kernel(nll_scatter_kernel, dim3(grid_for(rows, 256)), dim3(256), 0, stream(), labels, loss_grad,
                            grad, rows, classes);
         return check_launch("wm_nll_bwd");
     }

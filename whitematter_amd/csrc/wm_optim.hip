@@ -156,10 +156,10 @@ int launch_update(float* p, const float* g, float* s1, float* s2, int64_t n, con
     const bool vec = n % 4 == 0 && aligned16(p) && aligned16(g) && (NS < 1 || aligned16(s1)) &&
                      (NS < 2 || aligned16(s2));
     if (vec)
-        hipLaunchKernelGGL(update_vec_kernel<U>, dim3(grid_for(n / 4, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
+        launch_kernel(update_vec_kernel<U>, dim3(grid_for(n / 4, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
                            s1, s2, n / 4, upd);
     else
-        hipLaunchKernelGGL(update_scalar_kernel<U>, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
+        launch_kernel(update_scalar_kernel<U>, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), p, g,
                            s1, s2, n, upd);
     return check_launch(what);
 }
@@ -521,7 +521,7 @@ int launch_multi(int count, float* const* p, const float* const* g, float* const
     MultiTable t;
     WM_TRY(t.build(count, p, g, s1, s2, n, U::NS, what));
     if (t.chunks == 0) return WM_OK;
-    hipLaunchKernelGGL(multi_update_kernel<U>, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+    launch_kernel(multi_update_kernel<U>, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
                        t.chunks, upd);
     return check_launch(what);
 }
@@ -597,9 +597,9 @@ int wm_grad_sumsq_accumulate(const float* g, int64_t n, float* total) {
     const int nb = (int)std::min<int64_t>(grid_for(n / 4 + 1, kBlock, 4), kMaxPart);
     Workspace ws((size_t)nb * sizeof(float));
     if (!ws.p) return set_error(WM_ERR_NOMEM, "wm_grad_sumsq_accumulate: workspace");
-    hipLaunchKernelGGL(sumsq_partial_kernel, dim3(nb), dim3(kBlock), 0, stream(), g, n, ws.as<float>());
+    launch_kernel(sumsq_partial_kernel, dim3(nb), dim3(kBlock), 0, stream(), g, n, ws.as<float>());
     WM_TRY(check_launch("wm_grad_sumsq_accumulate"));
-    hipLaunchKernelGGL(sumsq_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), ws.as<float>(), nb, total);
+    launch_kernel(sumsq_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), ws.as<float>(), nb, total);
     return check_launch("wm_grad_sumsq_accumulate(finalize)");
 }
 
@@ -608,7 +608,7 @@ int wm_clip_grad_norm_scale(float* g, int64_t n, const float* total_sumsq, float
     if (n == 0) return WM_OK;
     if (!g || !total_sumsq) return set_error(WM_ERR_INVALID, "wm_clip_grad_norm_scale: null pointer");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(clip_norm_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n, total_sumsq,
+    launch_kernel(clip_norm_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n, total_sumsq,
                        max_norm);
     return check_launch("wm_clip_grad_norm_scale");
 }
@@ -618,7 +618,7 @@ int wm_clip_grad_value(float* g, int64_t n, float clip_value) {
     if (n == 0) return WM_OK;
     if (!g) return set_error(WM_ERR_INVALID, "wm_clip_grad_value: null pointer");
     WM_CHECK_INIT();
-    hipLaunchKernelGGL(clip_value_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n,
+    launch_kernel(clip_value_kernel, dim3(grid_for(n, kBlock, 16)), dim3(kBlock), 0, stream(), g, n,
                        clip_value);
     return check_launch("wm_clip_grad_value");
 }
@@ -640,16 +640,16 @@ int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float 
     // 1. the first non-finite scaled position in parameter order
     Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
     if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
-    hipLaunchKernelGGL(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+    launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
                        t.chunks, inv_scale, first.as<int64_t>());
     WM_TRY(check_launch("wm_grad_unscale(find)"));
-    hipLaunchKernelGGL(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
+    launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
                        t.chunks, first.as<int64_t>(), where.as<int64_t>());
     WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
     int64_t cut[2] = {0, 0};
     WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
     // 2. scale everything before it (everything when there is none)
-    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
                        2, nullptr, inv_scale, (int)cut[0], cut[1]);
     WM_TRY(check_launch("wm_grad_unscale(scale)"));
     *found_inf = cut[0] < t.count() ? 1 : 0;
@@ -706,10 +706,10 @@ int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, floa
     if (t.chunks == 0) return wm_fill(total, 0.0f, 1);
     Workspace part((size_t)t.chunks * sizeof(float));
     if (!part.p) return set_error(WM_ERR_NOMEM, "wm_grad_sumsq_multi: workspace");
-    hipLaunchKernelGGL(multi_sumsq_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+    launch_kernel(multi_sumsq_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
                        t.chunks, part.as<float>());
     WM_TRY(check_launch("wm_grad_sumsq_multi"));
-    hipLaunchKernelGGL(multi_sum_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<float>(), t.chunks,
+    launch_kernel(multi_sum_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<float>(), t.chunks,
                        total, 0);
     return check_launch("wm_grad_sumsq_multi(finalize)");
 }
@@ -720,7 +720,7 @@ int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, 
     MultiTable t;
     WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_norm_scale_multi"));
     if (t.chunks == 0) return WM_OK;
-    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
                        0, total_sumsq, max_norm, 0, (int64_t)0);
     return check_launch("wm_clip_grad_norm_scale_multi");
 }
@@ -729,7 +729,7 @@ int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float
     MultiTable t;
     WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_value_multi"));
     if (t.chunks == 0) return WM_OK;
-    hipLaunchKernelGGL(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
                        1, nullptr, clip_value, 0, (int64_t)0);
     return check_launch("wm_clip_grad_value_multi");
 }

@@ -470,14 +470,14 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
         const bool vec = (n % 4 == 0) && aligned16(x);
         dim3 grid(grid_for(outer * K, kBlock / 64, 32));
         if (vec)
-            hipLaunchKernelGGL((reduce_rows_kernel<OP, true>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
+            launch_kernel((reduce_rows_kernel<OP, true>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
                                idx, wv.as<float>(), wi.as<int64_t>());
         else
-            hipLaunchKernelGGL((reduce_rows_kernel<OP, false>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
+            launch_kernel((reduce_rows_kernel<OP, false>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
                                idx, wv.as<float>(), wi.as<int64_t>());
         WM_TRY(check_launch("wm_reduce(rows)"));
         if (K > 1) {
-            hipLaunchKernelGGL(reduce_rows_finalize_kernel<OP>, dim3(grid_for(outer, 1, 8)), dim3(kBlock), 0, st,
+            launch_kernel(reduce_rows_finalize_kernel<OP>, dim3(grid_for(outer, 1, 8)), dim3(kBlock), 0, st,
                                wv.as<float>(), wi.as<int64_t>(), outer, K, n, val, idx);
             WM_TRY(check_launch("wm_reduce(rows finalize)"));
         }
@@ -499,7 +499,7 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
     if (K > 1 && (!wv.p || (KIND != 0 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
     dim3 grid(grid_for(outer * K * tiles, 1, 32));
 #define WM_RC(V, I)                                                                                          \
-    hipLaunchKernelGGL((reduce_cols_kernel<OP, V, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val, \
+    launch_kernel((reduce_cols_kernel<OP, V, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val, \
                        idx, wv.as<float>(), wi.as<int64_t>())
     const bool narrow = n <= (int64_t)INT32_MAX;
     if (vec) { if (narrow) WM_RC(true, int32_t); else WM_RC(true, int64_t); }
@@ -507,7 +507,7 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
 #undef WM_RC
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
-        hipLaunchKernelGGL(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0,
+        launch_kernel(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0,
                            st, wv.as<float>(), wi.as<int64_t>(), outer, K, inner, n, val, idx);
         WM_TRY(check_launch("wm_reduce(cols finalize)"));
     }
@@ -561,23 +561,23 @@ int wm_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int
         if (vec4) {
             dim3 grid(grid_for(total / 4, kBlock, 16));
             if (inner == 1) {
-                if (accumulate) hipLaunchKernelGGL((reduce_bwd_sum_vec_kernel<true, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
-                else hipLaunchKernelGGL((reduce_bwd_sum_vec_kernel<false, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                if (accumulate) launch_kernel((reduce_bwd_sum_vec_kernel<true, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                else launch_kernel((reduce_bwd_sum_vec_kernel<false, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
             } else {
-                if (accumulate) hipLaunchKernelGGL((reduce_bwd_sum_vec_kernel<true, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
-                else hipLaunchKernelGGL((reduce_bwd_sum_vec_kernel<false, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                if (accumulate) launch_kernel((reduce_bwd_sum_vec_kernel<true, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                else launch_kernel((reduce_bwd_sum_vec_kernel<false, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
             }
         } else {
             dim3 grid(grid_for(total, kBlock, 16));
-            if (accumulate) hipLaunchKernelGGL((reduce_bwd_sum_kernel<true>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner);
-            else hipLaunchKernelGGL((reduce_bwd_sum_kernel<false>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner);
+            if (accumulate) launch_kernel((reduce_bwd_sum_kernel<true>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner);
+            else launch_kernel((reduce_bwd_sum_kernel<false>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner);
         }
         return check_launch("wm_reduce_bwd(sum)");
     }
     if (op == WM_R_MAX || op == WM_R_MIN) {
         if (!idx) return set_error(WM_ERR_INVALID, "wm_reduce_bwd: max/min backward needs the saved indices");
         if (!accumulate) WM_TRY(wm_fill(gx, 0.f, total));
-        hipLaunchKernelGGL(reduce_bwd_scatter_kernel, dim3(grid_for(outer * inner, kBlock, 8)), dim3(kBlock), 0, st, g,
+        launch_kernel(reduce_bwd_scatter_kernel, dim3(grid_for(outer * inner, kBlock, 8)), dim3(kBlock), 0, st, g,
                            idx, gx, outer, n, inner);
         return check_launch("wm_reduce_bwd(scatter)");
     }

@@ -26,8 +26,18 @@ struct DeviceState {
     int cus = 0;
 };
 
+// An open kernel span (wm_span_begin .. wm_span_end): one (start, stop)
+// event pair per launch, bound to that launch's own dispatch.
+constexpr int kSpanMax = 64;
+struct Span {
+    bool open = false;
+    int launches = 0;
+    hipEvent_t start[kSpanMax] = {}, stop[kSpanMax] = {};
+};
+
 std::mutex g_mu;
 DeviceState g_dev;
+Span g_span;
 thread_local std::string g_err;
 
 // Size classes: 512 B granularity below 1 MiB, 2 MiB granularity above.
@@ -138,6 +148,21 @@ static bool pool_free(void* p) {
 
 void* ws_alloc(size_t bytes) { return pool_alloc(bytes); }
 void ws_free(void* p) { (void)pool_free(p); }
+
+void span_events(hipEvent_t* start, hipEvent_t* stop) {
+    if (!g_span.open) {
+        *start = *stop = nullptr;
+        return;
+    }
+    if (g_span.launches >= kSpanMax) {  // counted, not timed; wm_span_end reports it
+        *start = *stop = nullptr;
+        ++g_span.launches;
+        return;
+    }
+    *start = g_span.start[g_span.launches];
+    *stop = g_span.stop[g_span.launches];
+    ++g_span.launches;
+}
 
 int check_launch(const char* what) {
     hipError_t e = hipGetLastError();
@@ -286,6 +311,40 @@ int wm_timer_stop(float* elapsed_ms) {
     if (e == hipSuccess) e = hipEventSynchronize(g_dev.ev_stop);
     if (e == hipSuccess) e = hipEventElapsedTime(elapsed_ms, g_dev.ev_start, g_dev.ev_stop);
     if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string("wm_timer_stop: ") + hipGetErrorString(e));
+    return WM_OK;
+}
+
+int wm_span_begin(void) {
+    WM_CHECK_INIT();
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < kSpanMax && e == hipSuccess; ++i) {
+        if (!g_span.start[i]) e = hipEventCreate(&g_span.start[i]);
+        if (e == hipSuccess && !g_span.stop[i]) e = hipEventCreate(&g_span.stop[i]);
+    }
+    if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string("wm_span_begin: ") + hipGetErrorString(e));
+    g_span.open = true;
+    g_span.launches = 0;
+    return WM_OK;
+}
+
+int wm_span_end(float* kernel_ms, float* span_ms, int* kernels) {
+    if (!kernel_ms) return set_error(WM_ERR_INVALID, "wm_span_end: null pointer");
+    if (!g_span.open) return set_error(WM_ERR_INVALID, "wm_span_end: no open span");
+    g_span.open = false;
+    const int n = g_span.launches;
+    if (kernels) *kernels = n;
+    if (n == 0) return set_error(WM_ERR_INVALID, "wm_span_end: no kernel ran in the span");
+    if (n > kSpanMax) return set_error(WM_ERR_INVALID, "wm_span_end: more launches than the span times");
+    hipError_t e = hipEventSynchronize(g_span.stop[n - 1]);
+    float total = 0.f;
+    for (int i = 0; i < n && e == hipSuccess; ++i) {
+        float ms = 0.f;
+        e = hipEventElapsedTime(&ms, g_span.start[i], g_span.stop[i]);
+        total += ms;
+    }
+    if (e == hipSuccess && span_ms) e = hipEventElapsedTime(span_ms, g_span.start[0], g_span.stop[n - 1]);
+    if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string("wm_span_end: ") + hipGetErrorString(e));
+    *kernel_ms = total;
     return WM_OK;
 }
 

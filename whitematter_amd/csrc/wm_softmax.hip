@@ -164,13 +164,13 @@ int launch_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
     // Several rows per CU in flight; the grid-stride loop covers the rest.
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
     if (tc.nt == 0) {
-        hipLaunchKernelGGL(softmax_fwd_long_kernel<LOG>, grid, dim3(1024), 0, st, out, x, rows, cols);
+        launch_kernel(softmax_fwd_long_kernel<LOG>, grid, dim3(1024), 0, st, out, x, rows, cols);
         return check_launch("wm_softmax_fwd(long)");
     }
 #define WM_SF(NTv, IT)                                                                                        \
     if (tc.nt == NTv && tc.items == IT) {                                                                     \
-        if (vec) hipLaunchKernelGGL((softmax_fwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
-        else hipLaunchKernelGGL((softmax_fwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
+        if (vec) launch_kernel((softmax_fwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
+        else launch_kernel((softmax_fwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, out, x, rows, cols); \
         return check_launch("wm_softmax_fwd");                                                                \
     }
     WM_SF(64, 1) WM_SF(64, 2) WM_SF(64, 4) WM_SF(64, 8)
@@ -186,13 +186,13 @@ int launch_softmax_bwd(const float* g, const float* out, float* gx, int acc, int
     const bool vec = cols % 4 == 0 && aligned16(g) && aligned16(out) && aligned16(gx);
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
     if (tc.nt == 0) {
-        hipLaunchKernelGGL(softmax_bwd_long_kernel<LOG>, grid, dim3(1024), 0, st, g, out, gx, acc, rows, cols);
+        launch_kernel(softmax_bwd_long_kernel<LOG>, grid, dim3(1024), 0, st, g, out, gx, acc, rows, cols);
         return check_launch("wm_softmax_bwd(long)");
     }
 #define WM_SB(NTv, IT)                                                                                              \
     if (tc.nt == NTv && tc.items == IT) {                                                                           \
-        if (vec) hipLaunchKernelGGL((softmax_bwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
-        else hipLaunchKernelGGL((softmax_bwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
+        if (vec) launch_kernel((softmax_bwd_kernel<NTv, IT, true, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
+        else launch_kernel((softmax_bwd_kernel<NTv, IT, false, LOG>), grid, dim3(NTv), 0, st, g, out, gx, acc, rows, cols); \
         return check_launch("wm_softmax_bwd");                                                                      \
     }
     WM_SB(64, 1) WM_SB(64, 2) WM_SB(64, 4) WM_SB(64, 8)

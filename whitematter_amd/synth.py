@@ -13,6 +13,9 @@ need multi-GiB temporaries.
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -39,25 +42,44 @@ def _u53(z: np.ndarray) -> np.ndarray:
     return ((z >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
 
 
+def _chunks(n: int, fill) -> None:
+    """Run fill(start, count) over n elements in _CHUNK pieces.  The
+    generator is a counter stream, so the pieces are independent; large
+    tensors spread them over threads (numpy releases the GIL in these
+    element-wise passes), and the bytes do not depend on the thread count."""
+    starts = range(0, n, _CHUNK)
+    workers = min(len(starts), 16, os.cpu_count() or 1)
+    if workers <= 1:
+        for s in starts:
+            fill(s, min(_CHUNK, n - s))
+        return
+    with ThreadPoolExecutor(workers) as ex:
+        list(ex.map(lambda s: fill(s, min(_CHUNK, n - s)), starts))
+
+
 def normal(shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
     n = int(np.prod(shape)) if len(shape) else 1
     out = np.empty(n, np.float32)
-    for s in range(0, n, _CHUNK):
-        c = min(_CHUNK, n - s)
+
+    def fill(s, c):
         z = _splitmix(seed, 2 * s, 2 * c)
         u1, u2 = _u53(z[0::2]), _u53(z[1::2])
         v = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
         out[s:s + c] = (mean + std * v).astype(np.float32)
+
+    _chunks(n, fill)
     return out.reshape(shape)
 
 
 def uniform(shape, seed: int, lo: float, hi: float) -> np.ndarray:
     n = int(np.prod(shape)) if len(shape) else 1
     out = np.empty(n, np.float32)
-    for s in range(0, n, _CHUNK):
-        c = min(_CHUNK, n - s)
+
+    def fill(s, c):
         u24 = (_splitmix(seed, s, c) >> np.uint64(40)).astype(np.float64) * (1.0 / 16777216.0)
         out[s:s + c] = (lo + (hi - lo) * u24).astype(np.float32)
+
+    _chunks(n, fill)
     return out.reshape(shape)
 
 
@@ -69,12 +91,12 @@ def quantize(x: np.ndarray, step_inv: float = 64.0) -> np.ndarray:
 def spikes(x: np.ndarray, seed: int, p: float = 0.01, value: float = 20.0) -> np.ndarray:
     """Set an independent Bernoulli(p) subset of x to +value."""
     flat = x.reshape(-1).copy()
-    n = flat.size
-    for s in range(0, n, _CHUNK):
-        c = min(_CHUNK, n - s)
+
+    def fill(s, c):
         u = (_splitmix(seed ^ 0x5B1CE, s, c) >> np.uint64(40)).astype(np.float64) * (1.0 / 16777216.0)
-        m = u < p
-        flat[s:s + c][m] = np.float32(value)
+        flat[s:s + c][u < p] = np.float32(value)
+
+    _chunks(flat.size, fill)
     return flat.reshape(x.shape)
 
 
