@@ -1,32 +1,54 @@
 """Benchmark of the MI355X Tensor elementwise / broadcast / reduction path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all]
 
 Metric: achieved HBM GB/s (% of MI355X peak) per op, and the
-speedup over the host-CPU reference path.  A "step" is one pass of the
+speedup over the host-CPU reference path.  A "step" is one pass of a
 configuration's ops, forward and backward, over inputs already resident in
-HBM.  Each op is timed with HIP events recorded on the library stream (the
-stream every kernel is launched on); a 512 MiB fill runs between ops (outside
-the timed region) so no op starts with its inputs in L2 / Infinity Cache.
+HBM; a 512 MiB fill runs before every op (untimed) so no op starts with its
+inputs in L2 / Infinity Cache.
+
+Each op is timed twice per step, in separate launches:
+  kernel basis  the durations of the op's kernels, from start / stop events
+                bound to each kernel's own dispatch (wm_span_*): what a
+                rocprofv3 kernel trace shows; the figure every GB/s and
+                roofline fraction below is computed from (median of K steps);
+  event basis   events recorded on the library stream before and after the
+                op (wm_timer_*): adds the marker packets' latency, reported
+                beside it (mean and median).
 
 Bytes are ALGORITHMIC: every distinct input read once (broadcast operands at
 their real size), every output written once, read + write for every gradient
 accumulated with "+=".  pow's backward recomputes pow(a, b) instead of
 reading the saved output, so its bytes are the recompute figure.
 
-The default workload is config 2: A[8192,8192]
-with r[1,8192] and c[8192,1]; A+r, A*c, A/r, A->pow(c), forward and backward.
-``value`` is the step's total algorithmic bytes over its total kernel time.
-Other configs (--config c1/c3/c4/c5) print the same line for that workload.
+The default run (--config all) measures the five BASELINE configurations and
+the config-5 chain as a Tensor-API caller issues it:
+  c2     (headline) A[8192,8192] with r[1,8192],
+         c[8192,1]; A+r, A*c, A/r, A->pow(c), fwd + bwd;
+  c1     y = relu(a + b).sum(1).sum(), fwd + bwd (L2-resident, launch-bound);
+  c3     X[16384,4096] sum/mean/max/min/argmax/argmin over dims 0 and 1, full
+         sum, max backward;
+  c4     logits[8192,32000] softmax / log_softmax fwd + bwd;
+  c5     the fused fp16-storage epilogue (C ABI) fwd + bwd;
+  c5api  the same computation through the drop-in Tensor API: HalfTensor
+         to_float, add, mul, clamp, tanh_, reshape, mean, reshape, and each
+         closure of the backward.
+The top-level value / roofline / cpu_baseline are c2's; "configs" holds one
+record per configuration with its own per-op figures, roofline and CPU
+baseline.  --config NAME runs one configuration (also opt, loss, norm, gemm,
+mha, io).
 
 The CPU baseline is the reference's own core/tensor.cpp (oracle/_ref, built
 with the reference's flags) -- or, where that is not built, the oracle's
-restatement compiled with the same flags -- timed single-threaded on one host
-core over a row slice of the same workload.
+restatement compiled with the same flags -- timed single-threaded on one
+host core over a bounded row sample of the same workload, scaled to the full
+size (the sample is stated in each record).
 """
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -53,7 +75,8 @@ class Op:
         self.name, self.launch, self.bytes, self.kernel, self.elems = name, launch, nbytes, kernel, elems
         self.flops = flops  # set for matrix-core ops: their roofline is TFLOP/s, not HBM
         self.ms = []   # event basis: markers before and after the op on the library stream
-        self.kms = []  # kernel basis: first kernel's start to last kernel's end (wm_span_*)
+        self.kms = []  # kernel basis: the op's kernel durations summed (wm_span_*)
+        self.kparts = []  # the same, kernel by kernel
 
 
 # ---------------------------------------------------------------------------
@@ -236,6 +259,71 @@ def c5_ops(b=32, t=1024, c=4096):
                     "(grads fp32, accumulated)" % (b, t, c, c), "elements": N}
 
 
+def c5api_ops(b=32, t=1024, c=4096):
+    """Config 5 as a caller of the drop-in Tensor API issues it (core/amp.h
+    HalfTensor, core/tensor.h ops): every op materialises its fp32 output, as
+    the reference's do, and every closure is timed on its own after the
+    upstream gradient dm is injected (y->grad = dm; y->grad_fn(), SURVEY's
+    injection rule).  Intermediate gradients start known-zero each step, so
+    each closure's first contribution is written without a read."""
+    from whitematter_amd import _tensor as T
+    h, res, g, dm = synth.config5(b, t, c)
+    rows = b * t
+    N = rows * c
+    hh = T.HalfTensor(T.Tensor.from_array(h))
+    rr = T.HalfTensor(T.Tensor.from_array(res))
+    del h, res
+    gt = T.Tensor.from_array(g, requires_grad=True)
+    dmt = T.Tensor.from_array(dm)
+    st = {}
+
+    def to_float_h():
+        gt.zero_grad()
+        st.clear()
+        st["hf"] = hh.to_float(True)
+
+    def fwd(name, fn):
+        def run():
+            st[name] = fn()
+        return run
+
+    def bwd(name, inject=False):
+        def run():
+            x = st[name]
+            if inject:
+                x.set_grad_from(dmt)
+            x.call_grad_fn()
+        return run
+
+    f4 = N * F32
+    ops = [
+        Op("HalfTensor.to_float(h)", to_float_h, N * 2 + f4, "f16_to_f32_kernel", N),
+        Op("HalfTensor.to_float(res)", fwd("rf", lambda: rr.to_float(True)), N * 2 + f4, "f16_to_f32_kernel", N),
+        Op("add fwd", fwd("t1", lambda: st["hf"].add(st["rf"])), 3 * f4, "binary_flat_kernel", N),
+        Op("mul(g) fwd", fwd("t2", lambda: st["t1"].mul(gt)), 2 * f4 + c * F32, "binary_rows_kernel", N),
+        Op("clamp fwd", fwd("t3", lambda: st["t2"].clamp(-4.0, 4.0)), 2 * f4, "unary_fwd_kernel", N),
+        Op("tanh_ fwd", fwd("t4", lambda: st["t3"].tanh_()), 2 * f4, "unary_fwd_kernel", N),
+        Op("reshape fwd", fwd("t5", lambda: st["t4"].reshape([rows, c])), 2 * f4, "copy", N),
+        Op("mean(1) fwd", fwd("m", lambda: st["t5"].mean(1, True)), f4 + rows * F32, "reduce_rows_kernel", N),
+        Op("reshape(m) fwd", fwd("m3", lambda: st["m"].reshape([b, t, 1])), 2 * rows * F32, "copy", rows),
+        # backward: dm injected into m3, then each node's closure in order
+        Op("reshape(m) bwd", bwd("m3", inject=True), 3 * rows * F32, "copy", rows),
+        Op("mean(1) bwd", bwd("m"), rows * F32 + f4, "reduce_bwd_sum_vec_kernel", N),
+        Op("reshape bwd", bwd("t5"), 2 * f4, "copy", N),
+        Op("tanh_ bwd", bwd("t4"), 3 * f4, "unary_bwd_kernel", N),
+        Op("clamp bwd", bwd("t3"), 3 * f4, "unary_bwd_kernel", N),
+        # G, a (t1), the g vector; t1.grad written; g.grad read + written
+        Op("mul(g) bwd", bwd("t2"), 3 * f4 + 3 * c * F32, "bwd_colsum_kernel", N),
+        Op("add bwd", bwd("t1"), 3 * f4, "bwd_flat_kernel", N),
+    ]
+    return ops, [hh, rr, gt, dmt, st], {
+        "workload": "c5api: the c5 chain through the drop-in Tensor API: HalfTensor(h), HalfTensor(res) "
+                    "[%d,%d,%d] fp16 -> to_float(requires_grad) -> add -> mul(g[%d]) -> clamp(-4,4) -> tanh_ -> "
+                    "reshape([%d,%d]) -> mean(1, keepdim) -> reshape([%d,%d,1]); backward closures with dm "
+                    "injected; fp32 intermediates as the Tensor API materialises them" % (b, t, c, c, rows, c, b, t),
+        "elements": N}
+
+
 def gpt2_small_shapes():
     """Parameter shapes of a GPT-2-small-sized model (124M parameters): the
     tensor list an optimizer step walks (many small bias / norm vectors next
@@ -318,64 +406,247 @@ def opt_ops():
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline (reference core/tensor.cpp through oracle/_ref, 1 core)
+# CPU baselines: the reference's core/tensor.cpp (oracle/_ref) on 1 host core
 # ---------------------------------------------------------------------------
 
-def cpu_baseline_c2(sample_rows=1024, cols=8192, reps=3):
+class _OneCore:
+    """Pin this process to one host core for the duration (the reference's
+    hot-path ops are single-threaded: no OpenMP on the path)."""
+
+    def __enter__(self):
+        self.cpus = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {min(self.cpus)})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.cpus)
+
+
+def _reference():
     sys.path.insert(0, ROOT)
     import oracle
-    A, c, r, G = synth.config2(8192, cols)
-    A, c, G = A[:sample_rows], c[:sample_rows], G[:sample_rows]
     ref = oracle.reference()
-    kind = "reference" if ref is not None else "port"
-    N = sample_rows * cols
+    if ref is None:
+        raise RuntimeError("oracle/_ref is not built (the reference build needs /root/reference at build time)")
+    return ref
+
+
+def _timed(fn):
+    t0 = time.perf_counter()
+    out = fn()
+    return out, time.perf_counter() - t0
+
+
+def _cpu_record(samples, ncpus, sample, reps):
+    """samples: op name -> (list of sample seconds, scale to the full workload,
+    full-workload algorithmic bytes).  Per-op figures are the median sample
+    time scaled to the full workload."""
+    per_ms, per_gbps, tot_t, tot_b = {}, {}, 0.0, 0
+    for name, (ts, scale, nbytes) in samples.items():
+        t = statistics.median(ts) * scale
+        per_ms[name] = round(t * 1e3, 3)
+        per_gbps[name] = round(nbytes / t / 1e9, 4)
+        tot_t += t
+        tot_b += nbytes
+    return {"value": round(tot_b / tot_t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"{sample}; median of {reps} after 1 warm-up unless stated; per-op times scaled to the full "
+                      f"workload; single-threaded on 1 of {ncpus} host cores",
+            "per_op_ms_full": per_ms, "per_op_GBps": per_gbps}
+
+
+def cpu_baseline_c1(reps=3):
+    ref = _reference()
+    a, b = synth.config1()
+    rows, cols = a.shape
+    N = rows * cols
     big = N * F32
-    total_bytes = 0
-    times = {}
-    cpu0 = os.sched_getaffinity(0)
-    core = min(cpu0)
-    os.sched_setaffinity(0, {core})
-    try:
-        for name, op, other in (("A+r", "add", r), ("A*c", "mul", c), ("A/r", "div", r), ("A^c", "pow", c)):
-            vb = other.size * F32
+    bytes_ = {"add fwd": 2 * big + cols * F32, "relu fwd": 2 * big, "sum(1) fwd": big + rows * F32,
+              "sum() fwd": rows * F32 + F32, "sum() bwd": F32 + rows * F32, "sum(1) bwd": rows * F32 + big,
+              "relu bwd": 3 * big, "add bwd": big + 2 * big + 2 * cols * F32}
+    ts = {k: [] for k in bytes_}
+    with _OneCore() as oc:
+        for rep in range(reps + 1):
+            ta, tb = ref.tensor(a, True), ref.tensor(b, True)
+            t, d0 = _timed(lambda: ref.binary("add", ta, tb))
+            r, d1 = _timed(lambda: ref.unary("relu", t))
+            s1, d2 = _timed(lambda: ref.reduce("sum", r, 1, False))
+            y, d3 = _timed(lambda: ref.reduce("sum", s1, -1, False))
+            y.set_grad(np.ones(1, np.float32))
+            _, d4 = _timed(y.call_grad_fn)
+            _, d5 = _timed(s1.call_grad_fn)
+            _, d6 = _timed(r.call_grad_fn)
+            _, d7 = _timed(t.call_grad_fn)
+            if rep:
+                for k, d in zip(bytes_, (d0, d1, d2, d3, d4, d5, d6, d7)):
+                    ts[k].append(d)
+        ncpu = len(oc.cpus)
+    return _cpu_record({k: (ts[k], 1, bytes_[k]) for k in bytes_}, ncpu, "the whole of config 1", reps)
+
+
+def cpu_baseline_c2(sample_rows=1024, cols=8192, reps=3):
+    ref = _reference()
+    rows_full = 8192
+    A, c, r, G = synth.config2(sample_rows, cols)  # the first sample_rows rows of A, c and G
+    scale = rows_full / sample_rows
+    N = rows_full * cols
+    big = N * F32
+    samples = {}
+    with _OneCore() as oc:
+        for name, op, other, vec in (("A+r", "add", r, cols), ("A*c", "mul", c, rows_full), ("A/r", "div", r, cols),
+                                     ("A^c", "pow", c, rows_full)):
+            vb = vec * F32
             fb = 2 * big + vb
             bb = 3 * big + 2 * vb if op == "add" else 4 * big + 3 * vb
             tf, tb = [], []
             for rep in range(reps + 1):
-                if kind == "reference":
-                    ta, to = ref.tensor(A, True), ref.tensor(other, True)
-                    t0 = time.perf_counter()
-                    y = ref.binary(op, ta, to)
-                    t1 = time.perf_counter()
+                ta, to = ref.tensor(A, True), ref.tensor(other, True)
+                y, d0 = _timed(lambda: ref.binary(op, ta, to))
+                y.set_grad(G)
+                _, d1 = _timed(y.call_grad_fn)
+                if rep:
+                    tf.append(d0)
+                    tb.append(d1)
+                del y, ta, to
+            samples[name + " fwd"] = (tf, scale, fb)
+            samples[name + " bwd"] = (tb, scale, bb)
+        ncpu = len(oc.cpus)
+    return _cpu_record(samples, ncpu, f"A[{sample_rows},{cols}] row slice of config 2 (1/{int(scale)} of A), same ops",
+                       reps)
+
+
+def cpu_baseline_c3(sample_rows=2048, cols=4096, reps=3):
+    ref = _reference()
+    rows_full = 16384
+    X = synth.quantize(synth.normal((sample_rows, cols), synth.seed_for(3, 0)))  # first rows of config 3's X
+    scale = rows_full / sample_rows
+    N = rows_full * cols
+    big = N * F32
+    samples = {}
+    with _OneCore() as oc:
+        tx = ref.tensor(X, False)
+        for dim in (0, 1):
+            nout = cols if dim == 0 else rows_full
+            for name in ("sum", "mean", "max", "min", "argmax", "argmin"):
+                ts = []
+                for rep in range(reps + 1):
+                    _, d = _timed(lambda: ref.reduce(name, tx, dim, False))
+                    if rep:
+                        ts.append(d)
+                samples[f"{name} dim{dim}"] = (ts, scale, big + nout * F32)
+        ts = []
+        for rep in range(reps + 1):
+            _, d = _timed(lambda: ref.reduce("sum", tx, -1, False))
+            if rep:
+                ts.append(d)
+        samples["sum full"] = (ts, scale, big + F32)
+        # max backward: the closure routes g to the first winner (O(outputs))
+        tg = ref.tensor(X, True)
+        for dim in (0, 1):
+            nout = cols if dim == 0 else sample_rows
+            g = synth.normal((nout,), synth.seed_for(3, 5 + dim))
+            ts = []
+            for rep in range(reps + 1):
+                m = ref.reduce("max", tg, dim, False)
+                m.set_grad(g)
+                _, d = _timed(m.call_grad_fn)
+                if rep:
+                    ts.append(d)
+            full_out = cols if dim == 0 else rows_full
+            samples[f"max dim{dim} bwd"] = (ts, 1 if dim == 0 else scale, full_out * (F32 + 8 + 2 * F32))
+        ncpu = len(oc.cpus)
+    return _cpu_record(samples, ncpu, f"X[{sample_rows},{cols}] row slice of config 3 (1/{int(scale)} of X), same ops",
+                       reps)
+
+
+def cpu_baseline_c4(sample_rows=64, jac_rows=2, cols=32000, reps=3):
+    """softmax / log_softmax forward and log_softmax backward on 64 rows; the
+    softmax backward (the reference's explicit Jacobian, O(cols^2) per row)
+    on 2 rows, one run: extrapolated by rows."""
+    ref = _reference()
+    rows_full = 8192
+    L = synth.spikes(synth.normal((sample_rows, cols), synth.seed_for(4, 0), 0.0, 3.0), synth.seed_for(4, 1))
+    G = synth.normal((sample_rows, cols), synth.seed_for(4, 2))
+    N = rows_full * cols
+    big = N * F32
+    samples = {}
+    with _OneCore() as oc:
+        for log in (False, True):
+            nm = "log_softmax" if log else "softmax"
+            tf, tb = [], []
+            for rep in range(reps + 1):
+                tx = ref.tensor(L, True)
+                y, d = _timed(lambda: ref.softmax(tx, log))
+                if rep:
+                    tf.append(d)
+                if log:
                     y.set_grad(G)
-                    t2 = time.perf_counter()
-                    y.call_grad_fn()
-                    t3 = time.perf_counter()
-                    del y, ta, to
-                else:
-                    o = oracle.get("port")
-                    t0 = time.perf_counter()
-                    out = o.binary(op, A, other)
-                    t1 = time.perf_counter()
-                    t2 = time.perf_counter()
-                    o.binary_bwd(op, G, A, other, out)
-                    t3 = time.perf_counter()
-                if rep > 0:
-                    tf.append(t1 - t0)
-                    tb.append(t3 - t2)
-            times[name + " fwd"] = (statistics.median(tf), fb)
-            times[name + " bwd"] = (statistics.median(tb), bb)
-            total_bytes += fb + bb
-    finally:
-        os.sched_setaffinity(0, cpu0)
-    total_t = sum(t for t, _ in times.values())
-    value = total_bytes / total_t / 1e9
-    return {"value": round(value, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"A[{sample_rows},{cols}] row slice of config 2 (1/{8192 // sample_rows} of A), same ops "
-                      f"fwd+bwd, median of {reps} after 1 warm-up, single-threaded on 1 of "
-                      f"{len(cpu0)} host cores",
-            "per_op_ms": {k: round(t * 1e3, 3) for k, (t, _) in times.items()},
-            "per_op_GBps": {k: round(b / t / 1e9, 4) for k, (t, b) in times.items()}}
+                    _, d = _timed(y.call_grad_fn)
+                    if rep:
+                        tb.append(d)
+            samples[nm + " fwd"] = (tf, rows_full / sample_rows, 2 * big)
+            if log:
+                samples[nm + " bwd"] = (tb, rows_full / sample_rows, 4 * big)
+        tx = ref.tensor(L[:jac_rows], True)
+        y = ref.softmax(tx, False)
+        y.set_grad(G[:jac_rows])
+        _, d = _timed(y.call_grad_fn)
+        samples["softmax bwd"] = ([d], rows_full / jac_rows, 4 * big)
+        ncpu = len(oc.cpus)
+    rec = _cpu_record(samples, ncpu, f"logits[{sample_rows},{cols}] row slice of config 4 (softmax bwd: "
+                                     f"{jac_rows} rows, one run, extrapolated x{rows_full // jac_rows})", reps)
+    rec["extrapolated"] = ["softmax bwd"]
+    return rec
+
+
+def cpu_baseline_c5api(sample_rows=256, c=4096, reps=3):
+    """The config-5 chain through the reference's Tensor API on the first
+    sample_rows rows (t = 0 .. sample_rows - 1 of batch 0)."""
+    ref = _reference()
+    rows_full = 32 * 1024
+    h = synth.normal((1, sample_rows, c), synth.seed_for(5, 0))
+    res = synth.normal((1, sample_rows, c), synth.seed_for(5, 1))
+    g = synth.uniform((c,), synth.seed_for(5, 2), 0.8, 1.2)
+    dm = synth.normal((1, sample_rows, 1), synth.seed_for(5, 3))
+    h16, r16 = ref.f32_to_f16(h), ref.f32_to_f16(res)
+    scale = rows_full / sample_rows
+    N = rows_full * c
+    f4 = N * F32
+    bytes_ = {"HalfTensor.to_float(h)": N * 2 + f4, "HalfTensor.to_float(res)": N * 2 + f4, "add fwd": 3 * f4,
+              "mul(g) fwd": 2 * f4 + c * F32, "clamp fwd": 2 * f4, "tanh_ fwd": 2 * f4, "reshape fwd": 2 * f4,
+              "mean(1) fwd": f4 + rows_full * F32, "reshape(m) fwd": 2 * rows_full * F32,
+              "reshape(m) bwd": 3 * rows_full * F32, "mean(1) bwd": rows_full * F32 + f4, "reshape bwd": 2 * f4,
+              "tanh_ bwd": 3 * f4, "clamp bwd": 3 * f4, "mul(g) bwd": 3 * f4 + 3 * c * F32, "add bwd": 3 * f4}
+    ts = {k: [] for k in bytes_}
+    with _OneCore() as oc:
+        for rep in range(reps + 1):
+            d = {}
+            hf, d["HalfTensor.to_float(h)"] = _timed(lambda: ref.tensor(ref.f16_to_f32(h16), True))
+            rf, d["HalfTensor.to_float(res)"] = _timed(lambda: ref.tensor(ref.f16_to_f32(r16), True))
+            gt = ref.tensor(g, True)
+            t1, d["add fwd"] = _timed(lambda: ref.binary("add", hf, rf))
+            t2, d["mul(g) fwd"] = _timed(lambda: ref.binary("mul", t1, gt))
+            t3, d["clamp fwd"] = _timed(lambda: ref.unary("clamp", t2, -4.0, 4.0))
+            t4, d["tanh_ fwd"] = _timed(lambda: ref.unary("tanh", t3))
+            t5, d["reshape fwd"] = _timed(lambda: ref.reshape(t4, (sample_rows, c)))
+            m, d["mean(1) fwd"] = _timed(lambda: ref.reduce("mean", t5, 1, True))
+            m3, d["reshape(m) fwd"] = _timed(lambda: ref.reshape(m, (1, sample_rows, 1)))
+            m3.set_grad(dm)
+            for name, node in (("reshape(m) bwd", m3), ("mean(1) bwd", m), ("reshape bwd", t5), ("tanh_ bwd", t4),
+                               ("clamp bwd", t3), ("mul(g) bwd", t2), ("add bwd", t1)):
+                _, d[name] = _timed(node.call_grad_fn)
+            if rep:
+                for k in bytes_:
+                    ts[k].append(d[k])
+            del hf, rf, gt, t1, t2, t3, t4, t5, m, m3
+        ncpu = len(oc.cpus)
+    # the (m) reshapes and their closure move rows-sized vectors: scale by rows too
+    return _cpu_record({k: (ts[k], scale, bytes_[k]) for k in bytes_}, ncpu,
+                       f"h, res[1,{sample_rows},{c}] (the first {sample_rows} of 32768 rows of config 5) through "
+                       f"the same chain, the (h, res) fp16 bits made by the reference's float_to_half", reps)
+
+
+CPU_BASELINES = {"c1": cpu_baseline_c1, "c2": cpu_baseline_c2, "c3": cpu_baseline_c3, "c4": cpu_baseline_c4,
+                 "c5api": cpu_baseline_c5api}
 
 
 # ---------------------------------------------------------------------------
@@ -640,8 +911,140 @@ def traffic_for(op_name: str, config: str):
         return None
 
 
-CONFIGS = {"gemm": gemm_ops, "mha": mha_ops, "io": io_ops, "c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "opt": opt_ops, "loss": loss_ops,
-           "norm": norm_ops}
+CONFIGS = {"c1": c1_ops, "c2": c2_ops, "c3": c3_ops, "c4": c4_ops, "c5": c5_ops, "c5api": c5api_ops, "opt": opt_ops,
+           "loss": loss_ops, "norm": norm_ops, "gemm": gemm_ops, "mha": mha_ops, "io": io_ops}
+# --config all: the headline first, then the rest
+ALL = ["c2", "c1", "c3", "c4", "c5", "c5api"]
+
+
+def run_config(name, args, flush, want_cpu):
+    """Build one configuration, time its ops (kernel and event bases, one
+    flush before every launch), and return its record."""
+    ops, keep, workload = CONFIGS[name]()
+
+    def launch(op, basis):
+        flush.fill(1.0)
+        if basis is None:
+            op.launch()
+            return
+        if basis == "kernel":
+            W.call("wm_span_begin")
+            op.launch()
+            kms, nk = W.C.c_float(), W.C.c_int()
+            rc = W.lib().wm_span_end(W.C.byref(kms), None, W.C.byref(nk))
+            if rc != 0 and nk.value == 0:
+                return  # no kernel (host-driven copies): the event basis only
+            W.check(rc, "wm_span_end (%s)" % op.name)
+            op.kms.append(kms.value)
+            op.nk = nk.value
+            per = []
+            for i in range(nk.value):
+                km = W.C.c_float()
+                W.call("wm_span_kernel", i, W.C.byref(km))
+                per.append(km.value)
+            op.kparts.append(per)
+        else:
+            W.call("wm_timer_start")
+            op.launch()
+            ms = W.C.c_float()
+            W.call("wm_timer_stop", W.C.byref(ms))
+            op.ms.append(ms.value)
+
+    for _ in range(args.warmup):
+        for op in ops:
+            launch(op, None)
+    W.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for op in ops:
+            launch(op, "kernel")
+        for op in ops:
+            launch(op, "event")
+    W.sync()
+    wall = time.perf_counter() - t0
+
+    cpu = None
+    if want_cpu:
+        try:
+            if name == "io":
+                cpu = cpu_baseline_io(workload["path"])
+            elif name in CPU_BASELINES:
+                cpu = CPU_BASELINES[name]()
+        except Exception as e:  # the baseline is reported, never the target
+            cpu = {"value": None, "error": str(e)}
+
+    per_op, step_ms, step_bytes, step_flops = {}, 0.0, 0, 0
+    host_io = all(getattr(op, "host_io", False) for op in ops)
+    mfma = all(op.flops for op in ops)
+    for op in ops:
+        km = statistics.median(op.kms) if op.kms else statistics.median(op.ms)
+        step_ms += km
+        step_bytes += op.bytes
+        step_flops += op.flops or 0
+        gbps = op.bytes / (km * 1e-3) / 1e9
+        d = {"ms": round(km, 4), "ms_event_mean": round(statistics.mean(op.ms), 4),
+             "ms_event_median": round(statistics.median(op.ms), 4), "GBps": round(gbps, 1),
+             "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "Gelem_per_s": round(op.elems / (km * 1e-3) / 1e9, 2),
+             "bytes": op.bytes}
+        if op.kms:
+            d["kernels"] = getattr(op, "nk", None)
+            if d["kernels"] and d["kernels"] > 1 and all(len(k) == d["kernels"] for k in op.kparts):
+                d["ms_by_kernel"] = [round(statistics.median(k[i] for k in op.kparts), 4) for i in range(d["kernels"])]
+            d["GBps_event_mean"] = round(op.bytes / (statistics.mean(op.ms) * 1e-3) / 1e9, 1)
+        if op.flops:
+            tf = op.flops / (km * 1e-3) / 1e12
+            d.update({"TFLOPs": round(tf, 1), "pct_mfma_peak": round(100 * tf / PEAK_F32_MFMA_TFLOPS, 1),
+                      "flops": op.flops})
+        if cpu and cpu.get("per_op_ms_full", {}).get(op.name):
+            d["speedup_vs_cpu"] = round(cpu["per_op_ms_full"][op.name] / km, 1)
+        per_op[op.name] = d
+
+    dom = max(ops, key=lambda o: statistics.median(o.kms) if o.kms else statistics.median(o.ms))
+    dom_ms = per_op[dom.name]["ms"]
+    if host_io:
+        # host-driven file transfers: bounded by the file cache and PCIe, not by
+        # an HBM or matrix-core roofline
+        value, unit, roofline = step_bytes / (step_ms * 1e-3) / 1e9, "GB/s", None
+    elif mfma:
+        value, unit = step_flops / (step_ms * 1e-3) / 1e12, "TFLOP/s"
+        dom_tf = dom.flops / (dom_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(dom_tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(dom_tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": traffic_for(dom.name, name),
+                    "kernel": dom.kernel, "op": dom.name, "algorithmic_flops": dom.flops, "ms": dom_ms}
+    else:
+        value, unit = step_bytes / (step_ms * 1e-3) / 1e9, "GB/s"
+        dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.name, name),
+                    "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes, "ms": dom_ms}
+    peak = PEAK_F32_MFMA_TFLOPS if mfma else PEAK_GBPS
+    rec = {"workload": workload["workload"], "elements": workload.get("elements"), "value": round(value, 1),
+           "unit": unit, "pct_of_peak": round(100 * value / peak, 1) if not host_io else None,
+           "ms_per_step": round(step_ms, 4), "roofline": roofline, "cpu_baseline": cpu, "ops": per_op,
+           "wall_s_timed_loop": round(wall, 3)}
+    if cpu and cpu.get("value") and not mfma:
+        rec["speedup_vs_cpu_step"] = round(value / cpu["value"], 1)
+    del ops, keep
+    gc.collect()
+    return rec
+
+
+def copy_calibration(flush):
+    """The 1 GiB streaming copy kernel: the practical read + write ceiling."""
+    n_copy = 1 << 28
+    src, dst = W.DeviceArray((n_copy,)), W.DeviceArray((n_copy,))
+    src.fill(2.0)
+    ks = []
+    for _ in range(3):
+        flush.fill(1.0)
+        W.call("wm_span_begin")
+        W.call("wm_copy_kernel", dst.vp, src.vp, n_copy)
+        k = W.C.c_float()
+        W.call("wm_span_end", W.C.byref(k), None, None)
+        ks.append(k.value)
+    src.free()
+    dst.free()
+    return round(2 * n_copy * F32 / (statistics.median(ks) * 1e-3) / 1e9, 1)
 
 
 def main():
@@ -649,10 +1052,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="all", choices=["all"] + sorted(CONFIGS))
     ap.add_argument("--flush-mib", type=int, default=512)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -662,134 +1064,41 @@ def main():
 
     W.call("wm_init", 0)
     cus = W.device_cus()
-    ops, keep, workload = CONFIGS[args.config]()
     flush = W.DeviceArray((args.flush_mib * (1 << 20) // 4,))
-
-    def run_op(op, timed):
-        flush.fill(1.0)
-        if timed:
-            W.call("wm_span_begin")
-            W.call("wm_timer_start")
-        op.launch()
-        if timed:
-            ms, kms, nk = W.C.c_float(), W.C.c_float(), W.C.c_int()
-            W.call("wm_timer_stop", W.C.byref(ms))
-            if getattr(op, "host_io", False):
-                W.lib().wm_span_end(W.C.byref(kms), W.C.byref(nk))  # no kernels: host-driven copies
-                op.kms.append(ms.value)
-            else:
-                W.call("wm_span_end", W.C.byref(kms), W.C.byref(nk))
-                op.kms.append(kms.value)
-            op.ms.append(ms.value)
-
-    for _ in range(args.warmup):
-        for op in ops:
-            run_op(op, False)
-    W.sync()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        for op in ops:
-            run_op(op, True)
-    W.sync()
-    wall = time.perf_counter() - t0
-
-    per_op = {}
-    step_ms = 0.0
-    step_bytes = 0
-    for op in ops:
-        ms = statistics.mean(op.ms)
-        step_ms += ms
-        step_bytes += op.bytes
-        gbps = op.bytes / (ms * 1e-3) / 1e9
-        per_op[op.name] = {"ms": round(ms, 4), "ms_median": round(statistics.median(op.ms), 4),
-                           "ms_kernel_median": round(statistics.median(op.kms), 4),
-                           "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
-                           "Gelem_per_s": round(op.elems / (ms * 1e-3) / 1e9, 2), "bytes": op.bytes}
-        if op.flops:
-            tf = op.flops / (ms * 1e-3) / 1e12
-            per_op[op.name].update({"TFLOPs": round(tf, 1), "pct_mfma_peak": round(100 * tf / PEAK_F32_MFMA_TFLOPS, 1),
-                                    "flops": op.flops})
-    mfma = all(op.flops for op in ops)
-    host_io = all(getattr(op, "host_io", False) for op in ops)
-    dom = max(ops, key=lambda o: statistics.mean(o.ms))
-    dom_ms = statistics.mean(dom.ms)
-    if host_io:
-        # host-driven file transfers: bounded by the file cache and PCIe, not by
-        # an HBM or matrix-core roofline
-        value = step_bytes / (step_ms * 1e-3) / 1e9
-        roofline = None
-    elif mfma:
-        value = sum(op.flops for op in ops) / (step_ms * 1e-3) / 1e12
-        dom_tf = dom.flops / (dom_ms * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "achieved": round(dom_tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(dom_tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": traffic_for(dom.name, args.config),
-                    "kernel": dom.kernel, "op": dom.name, "algorithmic_flops": dom.flops,
-                    "avg_ms": round(dom_ms, 4)}
-    else:
-        value = step_bytes / (step_ms * 1e-3) / 1e9
-        dom_gbps = dom.bytes / (dom_ms * 1e-3) / 1e9
-        roofline = {"bound": "hbm", "achieved": round(dom_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(dom_gbps / PEAK_GBPS, 4), "traffic": traffic_for(dom.name, args.config),
-                    "kernel": dom.kernel, "op": dom.name, "algorithmic_bytes": dom.bytes,
-                    "avg_ms": round(dom_ms, 4)}
-
-    # calibration copy kernel (its own launches, after the timed region)
-    n_copy = 1 << 28  # 1 GiB
-    src = W.DeviceArray((n_copy,)); dst = W.DeviceArray((n_copy,))
-    src.fill(2.0)
-    cms = []
-    for _ in range(3):
-        flush.fill(1.0)
-        W.call("wm_timer_start")
-        W.call("wm_copy_kernel", dst.vp, src.vp, n_copy)
-        ms = W.C.c_float()
-        W.call("wm_timer_stop", W.C.byref(ms))
-        cms.append(ms.value)
-    copy_gbps = 2 * n_copy * F32 / (statistics.median(cms) * 1e-3) / 1e9
-    src.free(); dst.free()
-
-    cpu = None
-    if not args.no_cpu and args.config == "io":
-        try:
-            cpu = cpu_baseline_io(workload["path"])
-        except Exception as e:  # the baseline is reported, never the target
-            cpu = {"value": None, "error": str(e)}
-    if not args.no_cpu and args.config == "c2":
-        try:
-            cpu = cpu_baseline_c2(args.cpu_rows)
-        except Exception as e:  # the baseline is reported, never the target
-            cpu = {"value": None, "error": str(e)}
-    if cpu and cpu.get("value"):
-        for name, d in per_op.items():
-            t = cpu.get("per_op_ms", {}).get(name)
-            if t:
-                # CPU ms scaled from the row sample to the full workload
-                scale = 8192 / args.cpu_rows
-                d["speedup_vs_cpu"] = round(t * scale / d["ms"], 1)
-
+    names = ALL if args.config == "all" else [args.config]
+    recs = {}
+    for nm in names:
+        print(f"bench.py: {nm} ...", file=sys.stderr, flush=True)
+        recs[nm] = run_config(nm, args, flush, not args.no_cpu)
+    head = recs[names[0]]
+    mfma = head["unit"] == "TFLOP/s"
     line = {
         "metric": METRIC_MFMA if mfma else METRIC,
-        "value": round(value, 1),
-        "unit": "TFLOP/s" if mfma else "GB/s",
+        "value": head["value"],
+        "unit": head["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded splitmix64 -> Box-Muller fp64 -> fp32, BASELINE config recipe)",
-        "config": dict(workload, pct_of_peak=round(100 * value / (PEAK_F32_MFMA_TFLOPS if mfma else PEAK_GBPS), 1),
-                       cus=cus,
-                       timing="HIP events on the library stream per op; 512 MiB flush between ops "
-                              "(untimed); ms_per_step = sum of op kernel times",
-                       wall_s_timed_loop=round(wall, 3)),
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "ops": per_op,
-        "copy_kernel_GBps": round(copy_gbps, 1),
+        "config": {"workload": head["workload"], "elements": head["elements"], "pct_of_peak": head["pct_of_peak"],
+                   "cus": cus,
+                   "timing": "kernel basis: per-dispatch start/stop events (the kernels' own durations, as a "
+                             "kernel trace shows), median of the timed steps; event basis (markers around the op "
+                             "on the library stream) in separate launches, reported beside; 512 MiB flush before "
+                             "every launch (untimed); ms_per_step = sum of the ops' kernel-basis medians",
+                   "configs_run": names},
+        "roofline": head["roofline"],
+        "cpu_baseline": head["cpu_baseline"],
+        "ops": head["ops"],
+        "copy_kernel_GBps": copy_calibration(flush),
     }
+    if len(names) > 1:
+        line["configs"] = {nm: recs[nm] for nm in names[1:]}
     print(json.dumps(line), flush=True)
 
 

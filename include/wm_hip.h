@@ -113,6 +113,8 @@ int wm_timer_stop(float* elapsed_ms);
    It fails if no kernel ran. */
 int wm_span_begin(void);
 int wm_span_end(float* kernel_ms, float* span_ms, int* kernels);
+/* Duration of the i-th kernel (0-based) of the last span wm_span_end closed. */
+int wm_span_kernel(int i, float* ms);
 /* Plain streaming copy kernel, used to calibrate rocprof byte counters. */
 int wm_copy_kernel(float* dst, const float* src, int64_t n);
 

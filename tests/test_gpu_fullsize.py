@@ -226,3 +226,95 @@ def test_c5_epilogue(wm):
     close(gr.to_host(), dt, np.abs(dt))
     dgt = du * t.astype(np.float64)
     close(gg.to_host(), dgt.sum(axis=0), np.abs(dgt).sum(axis=0))
+
+
+def _f16_bounds_check(out16, w64, ulps=2):
+    """out16 (fp16 bits) is the truncating fp16 of some fp32 value within
+    `ulps` fp32 ulps of w64 (the fp32 contract of tanh, then the reference's
+    float_to_half).  Truncation toward zero is monotone, so that holds iff
+    out16 lies between the truncations of the interval's two ends."""
+    o32 = oracle.get("f32")
+    w32 = w64.astype(np.float32)
+    lo, hi = w32.copy(), w32.copy()
+    for _ in range(ulps):
+        lo = np.nextafter(lo, np.float32(-np.inf))
+        hi = np.nextafter(hi, np.float32(np.inf))
+    f = o32.f16_to_f32
+    got = f(out16)
+    assert np.all((got >= f(o32.f32_to_f16(lo))) & (got <= f(o32.f32_to_f16(hi))))
+
+
+def test_c5_epilogue_forward_against_fp64(wm):
+    """The fused forward's fp16 output against fp64 tanh directly (not the
+    GPU's own unary tanh): within the 2-ulp contract before truncation."""
+    rows, cols, lo, hi = 32 * 1024, 4096, -4.0, 4.0
+    o32 = oracle.get("f32")
+    h16 = o32.f32_to_f16(normal((rows, cols), 511))
+    r16 = o32.f32_to_f16(normal((rows, cols), 512))
+    g = uniform((cols,), 513, 0.8, 1.2)
+    dh, dr, dg_ = (W.DeviceArray.from_host(a) for a in (h16, r16, g))
+    out = W.DeviceArray((rows, cols), np.uint16)
+    mean = W.DeviceArray((rows,))
+    W.call("wm_epilogue_f16_fwd", out.vp, mean.vp, dh.vp, dr.vp, dg_.vp, rows, cols, W.C.c_float(lo),
+           W.C.c_float(hi))
+    v = np.clip((o32.f16_to_f32(h16) + o32.f16_to_f32(r16)) * g, np.float32(lo), np.float32(hi))
+    _f16_bounds_check(out.to_host(), np.tanh(v.astype(np.float64)))
+
+
+def test_c5_tensor_api_chain(wm):
+    """Config 5 as a caller of the drop-in Tensor API writes it (core/amp.h
+    HalfTensor :256-286, then core/tensor.cpp add :897, mul :1063 (row
+    broadcast of g), clamp :1524, tanh_ :1302, reshape :2250, mean :1709,
+    reshape), at full size, forward and every closure of the backward with
+    the upstream gradient injected at the root (SURVEY's injection rule).
+    Forward: fp16 storage bit-exact, add / mul / clamp bit-exact IEEE fp32,
+    tanh within 2 ulp of fp64, the mean within the sums contract; backward:
+    every gradient within 1e-5 of the fp64 closed form (the mean's gradient
+    unscaled, S6; clamp passes only strictly inside, S11)."""
+    from whitematter_amd import _tensor as T
+    B, S, C, lo, hi = 32, 1024, 4096, -4.0, 4.0
+    rows = B * S
+    o32 = oracle.get("f32")
+    h = normal((B, S, C), 521)
+    res = normal((B, S, C), 522)
+    g = uniform((C,), 523, 0.8, 1.2)
+    dm = normal((B, S, 1), 524)
+    hh, rr = T.HalfTensor(T.Tensor.from_array(h)), T.HalfTensor(T.Tensor.from_array(res))
+    h16, r16 = o32.f32_to_f16(h), o32.f32_to_f16(res)
+    del h, res
+    assert np.array_equal(np.asarray(hh.data).reshape(B, S, C), h16)
+    assert np.array_equal(np.asarray(rr.data).reshape(B, S, C), r16)
+    gt = T.Tensor.from_array(g, requires_grad=True)
+    hf, rf = hh.to_float(True), rr.to_float(True)
+    t1 = hf.add(rf)
+    t2 = t1.mul(gt)
+    t3 = t2.clamp(lo, hi)
+    t4 = t3.tanh_()
+    t5 = t4.reshape([rows, C])
+    m = t5.mean(1, True)
+    m3 = m.reshape([B, S, 1])
+    assert list(m3.shape) == [B, S, 1]
+    # forward
+    a = o32.f16_to_f32(h16) + o32.f16_to_f32(r16)
+    assert np.array_equal(np.asarray(t1.data), a)
+    b = a * g
+    assert np.array_equal(np.asarray(t2.data), b)
+    c = np.minimum(np.maximum(b, np.float32(lo)), np.float32(hi))
+    assert np.array_equal(np.asarray(t3.data), c)
+    w = np.asarray(t4.data)
+    u = oracle.ulp_vs_f64(w, np.tanh(c.astype(np.float64)))
+    assert float(np.nanmax(u)) <= 2.0
+    w64 = w.astype(np.float64).reshape(rows, C)
+    close(np.asarray(m3.data).reshape(rows), w64.sum(axis=1) / C, np.abs(w64).sum(axis=1) / C)
+    # backward: dm injected at the root, then every closure in order
+    m3.run_grad_fn(dm)
+    for node in (m, t5, t4, t3, t2, t1):
+        node.call_grad_fn()
+    dw = np.broadcast_to(dm.astype(np.float64).reshape(rows, 1), (rows, C)).reshape(B, S, C)
+    du = np.where((b > lo) & (b < hi), dw * (1.0 - w.astype(np.float64) ** 2), 0.0)
+    del w64, dw
+    dt = du * g.astype(np.float64)
+    close(np.asarray(hf.grad), dt, np.abs(dt))
+    close(np.asarray(rf.grad), dt, np.abs(dt))
+    dgt = (du * a.astype(np.float64)).reshape(rows, C)
+    close(np.asarray(gt.grad), dgt.sum(axis=0), np.abs(dgt).sum(axis=0))

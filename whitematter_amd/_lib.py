@@ -53,6 +53,7 @@ _SIGS = {
     "wm_timer_stop": [C.POINTER(C.c_float)],
     "wm_span_begin": [],
     "wm_span_end": [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_int)],
+    "wm_span_kernel": [C.c_int, C.POINTER(C.c_float)],
     "wm_copy_kernel": [_vp, _vp, C.c_int64],
     "wm_fill": [_vp, C.c_float, C.c_int64],
     "wm_f32_to_f16_rtz": [_vp, _vp, C.c_int64],

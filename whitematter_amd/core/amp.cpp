@@ -17,16 +17,6 @@ void check(int rc, const char* what) {
     if (rc != WM_OK) throw std::runtime_error(std::string("whitematter_amd ") + what + ": " + wm_last_error());
 }
 
-// Device scratch for the fp16 halves of one conversion.
-struct HalfBuffer {
-    void* p = nullptr;
-    explicit HalfBuffer(size_t n) { check(wm_alloc(&p, n * sizeof(uint16_t)), "HalfTensor: device buffer"); }
-    ~HalfBuffer() { if (p) wm_free(p); }
-    HalfBuffer(const HalfBuffer&) = delete;
-    HalfBuffer& operator=(const HalfBuffer&) = delete;
-    uint16_t* get() const { return static_cast<uint16_t*>(p); }
-};
-
 // The gradients that hold values: a gradient that is empty or known to be
 // all zeros is skipped (scaling zeros leaves zeros, and zeros are finite).
 void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs, std::vector<int64_t>& sizes) {
@@ -55,11 +45,9 @@ bool GradScaler::unscale(Optimizer* optimizer) {
 // core/amp.h:263-267
 HalfTensor::HalfTensor(const TensorPtr& tensor) : shape(tensor->shape) {
     const size_t n = tensor->data.size();
-    data.resize(n);
+    data = wm::HalfVector(n);
     if (n == 0) return;
-    HalfBuffer h(n);
-    check(wm_f32_to_f16_rtz(h.get(), tensor->data.dev(), (int64_t)n), "HalfTensor");
-    check(wm_d2h(data.data(), h.get(), n * sizeof(uint16_t)), "HalfTensor");
+    check(wm_f32_to_f16_rtz(data.dev_write(), tensor->data.dev(), (int64_t)n), "HalfTensor");
 }
 
 // core/amp.h:270-274
@@ -67,9 +55,7 @@ TensorPtr HalfTensor::to_float(bool requires_grad) const {
     auto result = Tensor::create(shape, requires_grad);
     if (result->data.size() != data.size()) result->data.resize(data.size());
     if (data.empty()) return result;
-    HalfBuffer h(data.size());
-    check(wm_h2d(h.get(), data.data(), data.size() * sizeof(uint16_t)), "HalfTensor::to_float");
-    check(wm_f16_to_f32(result->data.dev_write(), h.get(), (int64_t)data.size()), "HalfTensor::to_float");
+    check(wm_f16_to_f32(result->data.dev_write(), data.dev(), (int64_t)data.size()), "HalfTensor::to_float");
     return result;
 }
 

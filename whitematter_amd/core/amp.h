@@ -190,7 +190,9 @@ private:
 
 class HalfTensor {
 public:
-    std::vector<uint16_t> data;
+    // The fp16 bits live in HBM; wm::HalfVector keeps std::vector<uint16_t>'s
+    // API (size(), data(), operator[], conversion to std::vector) for callers.
+    wm::HalfVector data;
     std::vector<size_t> shape;
 
     HalfTensor() = default;

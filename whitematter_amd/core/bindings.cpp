@@ -93,6 +93,10 @@ PYBIND11_MODULE(_tensor, m) {
                  t.grad = from_numpy(g);
                  if (t.grad_fn) t.grad_fn();
              })
+        // This node's closure alone, on the gradient it holds.
+        .def("call_grad_fn", [](Tensor& t) { if (t.grad_fn) t.grad_fn(); })
+        // The gradient as a device copy of another tensor's values.
+        .def("set_grad_from", [](Tensor& t, const TensorPtr& src) { t.grad = src->data; })
         .def("add", &Tensor::add)
         .def("sub", &Tensor::sub)
         .def("mul", py::overload_cast<const TensorPtr&>(&Tensor::mul, py::const_))

@@ -266,4 +266,138 @@ bool DeviceVector::operator==(const DeviceVector& o) const {
     return std::equal(a, a + n_, b);
 }
 
+// ---- HalfVector -----------------------------------------------------------
+
+HalfVector::HalfVector(size_type n) : n_(n) {
+    if (n_ == 0) return;
+    ensure_dev_alloc();
+    host_valid_ = false;  // neither copy holds values until the first write
+    dev_valid_ = true;
+}
+
+HalfVector::HalfVector(const std::vector<uint16_t>& v) : n_(v.size()), h_(v) { dev_valid_ = n_ == 0; }
+
+HalfVector::HalfVector(const HalfVector& o) : n_(o.n_) {
+    if (n_ == 0) return;
+    if (o.dev_valid_) {
+        ensure_dev_alloc();
+        ck(wm_d2d(d_, o.d_, n_ * sizeof(uint16_t)), "HalfVector copy");
+        host_valid_ = false;
+    } else {
+        h_ = o.h_;
+        dev_valid_ = false;
+    }
+}
+
+HalfVector::HalfVector(HalfVector&& o) noexcept
+    : n_(o.n_), d_(o.d_), h_(std::move(o.h_)), host_valid_(o.host_valid_), dev_valid_(o.dev_valid_) {
+    o.n_ = 0;
+    o.d_ = nullptr;
+    o.host_valid_ = o.dev_valid_ = true;
+}
+
+HalfVector::~HalfVector() { release(); }
+
+HalfVector& HalfVector::operator=(const HalfVector& o) {
+    if (this == &o) return *this;
+    HalfVector tmp(o);
+    return *this = std::move(tmp);
+}
+
+HalfVector& HalfVector::operator=(HalfVector&& o) noexcept {
+    if (this == &o) return *this;
+    release();
+    n_ = o.n_;
+    d_ = o.d_;
+    h_ = std::move(o.h_);
+    host_valid_ = o.host_valid_;
+    dev_valid_ = o.dev_valid_;
+    o.n_ = 0;
+    o.d_ = nullptr;
+    o.host_valid_ = o.dev_valid_ = true;
+    return *this;
+}
+
+HalfVector& HalfVector::operator=(const std::vector<uint16_t>& v) { return *this = HalfVector(v); }
+
+void HalfVector::release() {
+    if (d_) {
+        wm_free(d_);
+        d_ = nullptr;
+    }
+}
+
+void HalfVector::ensure_dev_alloc() const {
+    if (d_ || n_ == 0) return;
+    void* p = nullptr;
+    ck(wm_alloc(&p, n_ * sizeof(uint16_t)), "HalfVector allocation");
+    d_ = static_cast<uint16_t*>(p);
+}
+
+void HalfVector::sync_host() const {
+    if (n_ == 0 || host_valid_) return;
+    h_.resize(n_);
+    ck(wm_d2h(h_.data(), d_, n_ * sizeof(uint16_t)), "HalfVector device->host");
+    host_valid_ = true;
+}
+
+const uint16_t* HalfVector::data() const {
+    sync_host();
+    return h_.data();
+}
+
+uint16_t* HalfVector::data() {
+    sync_host();
+    dev_valid_ = n_ == 0;  // the caller may write through the pointer
+    return h_.data();
+}
+
+const uint16_t* HalfVector::dev() const {
+    if (n_ == 0) return nullptr;
+    ensure_dev_alloc();
+    if (!dev_valid_) {
+        ck(wm_h2d(d_, h_.data(), n_ * sizeof(uint16_t)), "HalfVector host->device");
+        dev_valid_ = true;
+    }
+    return d_;
+}
+
+uint16_t* HalfVector::dev_write() {
+    if (n_ == 0) return nullptr;
+    ensure_dev_alloc();
+    dev_valid_ = true;
+    host_valid_ = false;
+    return d_;
+}
+
+void HalfVector::resize(size_type n, uint16_t value) {
+    if (n == n_) return;
+    sync_host();
+    h_.resize(n, value);
+    release();
+    n_ = n;
+    host_valid_ = true;
+    dev_valid_ = n_ == 0;
+}
+
+void HalfVector::clear() {
+    release();
+    h_.clear();
+    n_ = 0;
+    host_valid_ = dev_valid_ = true;
+}
+
+HalfVector::operator std::vector<uint16_t>() const {
+    sync_host();
+    return std::vector<uint16_t>(h_.begin(), h_.begin() + (std::ptrdiff_t)n_);
+}
+
+bool HalfVector::operator==(const HalfVector& o) const {
+    if (n_ != o.n_) return false;
+    if (n_ == 0) return true;
+    const uint16_t* a = data();
+    const uint16_t* b = o.data();
+    return std::equal(a, a + n_, b);
+}
+
 }  // namespace wm

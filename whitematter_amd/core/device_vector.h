@@ -22,6 +22,7 @@
 #pragma once
 
 #include <cstddef>
+#include <cstdint>
 #include <initializer_list>
 #include <vector>
 
@@ -105,6 +106,59 @@ private:
     mutable bool host_valid_ = true;       // h_ holds the current values
     mutable bool dev_valid_ = true;        // d_ holds the current values
     bool zero_ = false;                    // logically all zeros (neither copy needs to be valid)
+};
+
+// fp16 bit patterns (uint16_t) with std::vector<uint16_t>'s API and the
+// same coherence rules as DeviceVector (no known-zero state): the storage of
+// HalfTensor::data (core/amp.h:258), so fp16 tensors stay in HBM and
+// converting them to fp32 is one device pass.
+class HalfVector {
+public:
+    using value_type = uint16_t;
+    using size_type = std::size_t;
+    using iterator = uint16_t*;
+    using const_iterator = const uint16_t*;
+
+    HalfVector() = default;
+    explicit HalfVector(size_type n);  // device storage of n elements, contents unset until written
+    HalfVector(const std::vector<uint16_t>& v);  // NOLINT: implicit, like a vector copy
+    HalfVector(const HalfVector& o);
+    HalfVector(HalfVector&& o) noexcept;
+    ~HalfVector();
+    HalfVector& operator=(const HalfVector& o);
+    HalfVector& operator=(HalfVector&& o) noexcept;
+    HalfVector& operator=(const std::vector<uint16_t>& v);
+
+    size_type size() const { return n_; }
+    bool empty() const { return n_ == 0; }
+    uint16_t* data();
+    const uint16_t* data() const;
+    uint16_t& operator[](size_type i) { return data()[i]; }
+    const uint16_t& operator[](size_type i) const { return data()[i]; }
+    iterator begin() { return data(); }
+    iterator end() { return data() + n_; }
+    const_iterator begin() const { return data(); }
+    const_iterator end() const { return data() + n_; }
+    void resize(size_type n, uint16_t value = 0);
+    void clear();
+    operator std::vector<uint16_t>() const;  // NOLINT: implicit, copies to the host
+    bool operator==(const HalfVector& o) const;
+
+    // Device pointer to current values (uploads a stale device copy).
+    const uint16_t* dev() const;
+    // Device pointer for a full overwrite: no upload, host mirror goes stale.
+    uint16_t* dev_write();
+
+private:
+    void ensure_dev_alloc() const;
+    void sync_host() const;
+    void release();
+
+    size_type n_ = 0;
+    mutable uint16_t* d_ = nullptr;
+    mutable std::vector<uint16_t> h_;
+    mutable bool host_valid_ = true;
+    mutable bool dev_valid_ = true;
 };
 
 }  // namespace wm

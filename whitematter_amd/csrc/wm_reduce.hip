@@ -57,15 +57,6 @@ __device__ __forceinline__ void combine(float& v, I& i, float v2, I i2) {
     }
 }
 
-template <bool MAXOP>
-__device__ __forceinline__ void wave_combine(float& v, int64_t& i) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        float v2 = __shfl_xor(v, off, 64);
-        int64_t i2 = __shfl_xor(i, off, 64);
-        combine<MAXOP>(v, i, v2, i2);
-    }
-}
 
 // Reduction kinds: 0 = sum/mean, 1 = max family, 2 = min family.
 __host__ __device__ constexpr int kind_of(int op) {
@@ -73,136 +64,332 @@ __host__ __device__ constexpr int kind_of(int op) {
 }
 
 // Write the final result of one output slot.
-template <int OP>
-__device__ __forceinline__ void write_result(float* val, int64_t* idx, int64_t slot, float v, int64_t i, int64_t n) {
+template <int OP, class I>
+__device__ __forceinline__ void write_result(float* val, int64_t* idx, int64_t slot, float v, I i, int64_t n) {
     if constexpr (OP == WM_R_SUM) { val[slot] = v; }
     else if constexpr (OP == WM_R_MEAN) { val[slot] = v / (float)n; }
     else if constexpr (OP == WM_R_MAX || OP == WM_R_MIN) {
         if (val) val[slot] = v;
-        if (idx) idx[slot] = i;
+        if (idx) idx[slot] = (int64_t)i;
     } else {
         if (val) val[slot] = (float)i;
-        if (idx) idx[slot] = i;
+        if (idx) idx[slot] = (int64_t)i;
     }
+}
+
+// ---------------------------------------------------------------------------
+// A thread's scan over its piece of a slice
+// ---------------------------------------------------------------------------
+//
+// scan_fast folds with the reference's strict compare alone, starting from
+// v = -inf (max) / +inf (min) and an empty position.  That takes every
+// element the empty-state rule of scan_push takes except a first non-NaN
+// element equal to -inf (+inf): a piece whose state is still empty after
+// the loop (all its elements NaN or that infinity) is re-scanned with
+// scan_push (scan_fix below).  A NaN at position 0 of the slice wins the
+// whole scan; the thread whose piece starts there loads that element before
+// its loop and, after the loop, replaces its state with it if it is a NaN
+// (scan_start).
+template <bool MAXOP>
+__device__ __forceinline__ float scan_init() { return MAXOP ? -__builtin_inff() : __builtin_inff(); }
+
+template <bool MAXOP, class I>
+__device__ __forceinline__ void scan_fast(float& v, I& i, float x, I k) {
+    const bool take = strictly_better<MAXOP>(x, v);
+    v = take ? x : v;
+    i = take ? k : i;
+}
+
+template <bool MAXOP, class I>
+__device__ __forceinline__ void scan_start(float& v, I& i, float x0) {
+    if (__builtin_isnan(x0)) { v = x0; i = 0; }
+}
+
+// Positions [p0, p1) of one slice, element p at base[p * stride]; returns
+// the state (value, position).  Out of line: it is the rare path.
+template <class I>
+struct ScanState {
+    float v;
+    I i;
+};
+
+template <bool MAXOP, class I>
+__device__ __noinline__ ScanState<I> scan_fix(const float* base, int64_t stride, int64_t p0, int64_t p1) {
+    float v = 0.f;
+    I i = (I)kEmpty;
+    for (int64_t p = p0; p < p1; ++p) scan_push<MAXOP>(v, i, base[p * stride], (I)p);
+    return {v, i};
+}
+
+template <bool MAXOP, class I>
+__device__ __forceinline__ void wave_combine_t(float& v, I& i) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float v2 = __shfl_xor(v, off, 64);
+        I i2 = __shfl_xor(i, off, 64);
+        combine<MAXOP>(v, i, v2, i2);
+    }
+}
+
+// The state (v, pos) of a chunk as an unsigned 64-bit key whose order is
+// the scan's preference between chunks.  The high word is the value in an
+// order-preserving encoding (inverted for min; -0 and +0 encode alike, as
+// they compare equal).  The low word ranks lower positions higher on equal
+// values: with 32-bit positions it holds 2^31 - 1 - pos above one bit for
+// the sign of a zero, so the key decodes back to (value, pos) with no load;
+// with 64-bit positions it holds ~k for chunk k (chunks are in position
+// order), and the second pass reads the winning chunk's saved position.  A
+// NaN at position 0 (which wins the whole scan) is the largest key, an empty
+// state 0.
+template <bool MAXOP>
+__device__ __forceinline__ uint32_t order_word(float v) {
+    const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return MAXOP ? o : ~o;
+}
+
+template <bool MAXOP, class I>
+__device__ __forceinline__ uint64_t chunk_key(float v, I pos, uint32_t k) {
+    if (pos == (I)kEmpty) return 0ull;
+    if (pos == 0 && __builtin_isnan(v)) return ~0ull;
+    uint32_t lo;
+    if constexpr (sizeof(I) == 4) {
+        const uint32_t zsign = v == 0.f ? (__float_as_uint(v) >> 31) : 0u;
+        lo = ((0x7FFFFFFFu - (uint32_t)pos) << 1) | zsign;
+    } else {
+        lo = ~k;
+    }
+    return ((uint64_t)order_word<MAXOP>(v) << 32) | lo;
+}
+
+// Decode a winning key: its position (32-bit positions) or chunk (64-bit)
+// and, for 32-bit positions, its value.  The NaN-at-0 key's value is read
+// from the input by the caller (its payload is not in the key).
+template <bool MAXOP>
+__device__ __forceinline__ float key_value(uint64_t key) {
+    uint32_t o = (uint32_t)(key >> 32);
+    if (!MAXOP) o = ~o;
+    uint32_t b = (o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o;
+    if (b == 0u && (key & 1u)) b = 0x80000000u;  // -0
+    return __uint_as_float(b);
+}
+
+__device__ __forceinline__ int64_t key_pos32(uint64_t key) { return 0x7FFFFFFF - (int64_t)(((uint32_t)key >> 1) & 0x7FFFFFFFu); }
+__device__ __forceinline__ int64_t key_chunk(uint64_t key) { return (int64_t)(uint32_t)~(uint32_t)key; }
+
+// The result slot's (value, position) from its winning key; x_at(pos) reads
+// the input element at pos of the slot.
+template <bool MAXOP, class I, class XAt>
+__device__ __forceinline__ void decode_winner(uint64_t key, const I* pi_slot, int64_t pi_stride, XAt x_at, float& v,
+                                              I& pos) {
+    if constexpr (sizeof(I) == 4) {
+        if (key == ~0ull) {
+            pos = 0;
+            v = x_at(0);
+        } else {
+            pos = (I)key_pos32(key);
+            v = key_value<MAXOP>(key);
+        }
+    } else {
+        pos = pi_slot[key_chunk(key) * pi_stride];
+        v = x_at(pos);
+    }
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint64_t o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    return k;
 }
 
 // ---------------------------------------------------------------------------
 // inner == 1: rows
 // ---------------------------------------------------------------------------
 
-// One wave per (row, chunk).  Partials (value, position) go to pv/pi when the
-// row is split (K > 1), else the result is written directly.  Each lane keeps
-// four 128-bit loads in flight and folds them in increasing position order.
-template <int OP, bool VEC>
-__global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __restrict__ x, int64_t rows, int64_t n,
-                                                              int64_t chunk, int64_t K, float* __restrict__ val,
-                                                              int64_t* __restrict__ idx, float* __restrict__ pv,
-                                                              int64_t* __restrict__ pi) {
-    constexpr int KIND = kind_of(OP);
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
-    const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
-    for (int64_t item = wave; item < rows * K; item += nwaves) {
-        const int64_t r = item / K;
-        const int64_t k = item - r * K;
-        const int64_t c0 = k * chunk;
-        const int64_t c1 = min(n, c0 + chunk);
-        const float* xr = x + r * n;
-        float v = 0.f;
-        int64_t pos = kEmpty;
-        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (VEC) {
-            int64_t c = c0 + lane * 4;
-            for (; c + 3 * 256 < c1; c += 4 * 256) {
-                float4 a[4];
+// A wave's scan of row positions [c0, c1) (c0 a multiple of 4 when VEC).
+// Each lane keeps four 128-bit loads in flight and folds them in increasing
+// position order; the lanes are combined with DPP / shuffles.  Every lane
+// returns the wave's state.
+template <int KIND, bool VEC, class I>
+__device__ __forceinline__ void wave_scan_row(const float* __restrict__ xr, int64_t c0, int64_t c1, int lane,
+                                              float& v_out, I& pos_out) {
+    constexpr bool MX = KIND == 1;
+    float v = KIND == 0 ? 0.f : scan_init<MX>();
+    I pos = (I)kEmpty;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    // Position 0's element, loaded now and looked at after the loop, so no
+    // lane waits for it before its first stream load.
+    const bool has0 = KIND != 0 && c0 == 0 && lane == 0 && c1 > 0;
+    const float x0 = has0 ? xr[0] : 0.f;
+    if constexpr (VEC) {
+        int64_t c = c0 + lane * 4;
+        for (; c + 3 * 256 < c1; c += 4 * 256) {
+            float4 a[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) a[u] = ld_stream(xr + c + u * 256);
+            for (int u = 0; u < 4; ++u) a[u] = ld_stream(xr + c + u * 256);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if constexpr (KIND == 0) {
-                        s.x += a[u].x; s.y += a[u].y; s.z += a[u].z; s.w += a[u].w;
-                    } else {
-                        const int64_t p = c + u * 256;
-                        scan_push<KIND == 1>(v, pos, a[u].x, p);
-                        scan_push<KIND == 1>(v, pos, a[u].y, p + 1);
-                        scan_push<KIND == 1>(v, pos, a[u].z, p + 2);
-                        scan_push<KIND == 1>(v, pos, a[u].w, p + 3);
-                    }
-                }
-            }
-            for (; c < c1; c += 256) {
-                float4 a0 = ld_stream(xr + c);
+            for (int u = 0; u < 4; ++u) {
                 if constexpr (KIND == 0) {
-                    s.x += a0.x; s.y += a0.y; s.z += a0.z; s.w += a0.w;
+                    s.x += a[u].x; s.y += a[u].y; s.z += a[u].z; s.w += a[u].w;
                 } else {
-                    scan_push<KIND == 1>(v, pos, a0.x, c);
-                    scan_push<KIND == 1>(v, pos, a0.y, c + 1);
-                    scan_push<KIND == 1>(v, pos, a0.z, c + 2);
-                    scan_push<KIND == 1>(v, pos, a0.w, c + 3);
+                    const I p = (I)(c + u * 256);
+                    scan_fast<MX>(v, pos, a[u].x, p);
+                    scan_fast<MX>(v, pos, a[u].y, (I)(p + 1));
+                    scan_fast<MX>(v, pos, a[u].z, (I)(p + 2));
+                    scan_fast<MX>(v, pos, a[u].w, (I)(p + 3));
                 }
-            }
-        } else {
-            for (int64_t c = c0 + lane; c < c1; c += 64) {
-                float a0 = ld_stream1(xr + c);
-                if constexpr (KIND == 0) s.x += a0;
-                else scan_push<KIND == 1>(v, pos, a0, c);
             }
         }
-        if constexpr (KIND == 0) v = wave_sum((s.x + s.y) + (s.z + s.w));
-        else wave_combine<KIND == 1>(v, pos);
-        if (lane == 0) {
-            if (K == 1) write_result<OP>(val, idx, r, v, pos, n);
-            else {
-                pv[r * K + k] = v;
-                if (KIND != 0) pi[r * K + k] = pos;
+        for (; c < c1; c += 256) {
+            float4 a0 = ld_stream(xr + c);
+            if constexpr (KIND == 0) {
+                s.x += a0.x; s.y += a0.y; s.z += a0.z; s.w += a0.w;
+            } else {
+                scan_fast<MX>(v, pos, a0.x, (I)c);
+                scan_fast<MX>(v, pos, a0.y, (I)(c + 1));
+                scan_fast<MX>(v, pos, a0.z, (I)(c + 2));
+                scan_fast<MX>(v, pos, a0.w, (I)(c + 3));
+            }
+        }
+        if constexpr (KIND != 0) {
+            // this lane's positions: c0 + 4 lane + 256 j + {0..3}
+            if (__builtin_expect(pos == (I)kEmpty, 0)) {
+                float fv = 0.f;
+                I fi = (I)kEmpty;
+                for (int64_t q = c0 + lane * 4; q < c1; q += 256)
+                    for (int64_t e = q; e < q + 4 && e < c1; ++e) scan_push<MX>(fv, fi, xr[e], (I)e);
+                v = fv;
+                pos = fi;
+            }
+        }
+    } else {
+        for (int64_t c = c0 + lane; c < c1; c += 64) {
+            float a0 = ld_stream1(xr + c);
+            if constexpr (KIND == 0) s.x += a0;
+            else scan_fast<MX>(v, pos, a0, (I)c);
+        }
+        if constexpr (KIND != 0) {
+            if (__builtin_expect(pos == (I)kEmpty, 0)) {
+                float fv = 0.f;
+                I fi = (I)kEmpty;
+                for (int64_t c = c0 + lane; c < c1; c += 64) scan_push<MX>(fv, fi, xr[c], (I)c);
+                v = fv;
+                pos = fi;
             }
         }
     }
+    if constexpr (KIND != 0) {
+        if (has0) scan_start<MX>(v, pos, x0);
+    }
+    if constexpr (KIND == 0) v = wave_sum((s.x + s.y) + (s.z + s.w));
+    else wave_combine_t<MX>(v, pos);
+    v_out = v;
+    pos_out = pos;
 }
 
-// Second pass for split rows: one block per row, chunks combined in a fixed
-// tree (block_sum or the (value, position) combine).
-template <int OP>
-__global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const float* __restrict__ pv,
-                                                                       const int64_t* __restrict__ pi, int64_t rows,
+// Two shapes of launch, chosen by K (uniform):
+//   K == 1  one wave per row: the wave's state is the row's result;
+//   K  > 1  one workgroup per (row, chunk of `chunk` positions): the four
+//           waves take consecutive quarters of the chunk and their states
+//           are combined in wave order through LDS; the workgroup's state is
+//           the chunk's partial, which reduce_rows_finalize_kernel combines.
+template <int OP, bool VEC, class I>
+__global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __restrict__ x, int64_t rows, int64_t n,
+                                                              int64_t chunk, int64_t K, float* __restrict__ val,
+                                                              int64_t* __restrict__ idx, float* __restrict__ pv,
+                                                              uint64_t* __restrict__ pk, I* __restrict__ pi) {
+    constexpr int KIND = kind_of(OP);
+    constexpr bool MX = KIND == 1;
+    constexpr int NW = kBlock / 64;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (K == 1) {
+        const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+        const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
+        for (int64_t r = wave; r < rows; r += nwaves) {
+            float v;
+            I pos;
+            wave_scan_row<KIND, VEC, I>(x + r * n, 0, n, lane, v, pos);
+            if (lane == 0) write_result<OP>(val, idx, r, v, pos, n);
+        }
+        return;
+    }
+    __shared__ float lv[NW];
+    __shared__ I li[NW];
+    for (int64_t item = blockIdx.x; item < rows * K; item += gridDim.x) {
+        const int64_t r = item / K, k = item - r * K;
+        const int64_t c0 = k * chunk, c1 = min(n, c0 + chunk);
+        const int64_t q = chunk / NW;  // a multiple of 256
+        const int64_t a0 = min(c1, c0 + w * q), a1 = min(c1, a0 + q);
+        float v;
+        I pos;
+        wave_scan_row<KIND, VEC, I>(x + r * n, a0, a1, lane, v, pos);
+        if (lane == 0) { lv[w] = v; li[w] = pos; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float tv = lv[0];
+            I ti = li[0];
+            if constexpr (KIND == 0) {
+                tv = (lv[0] + lv[1]) + (lv[2] + lv[3]);
+            } else {
+#pragma unroll
+                for (int ww = 1; ww < NW; ++ww) combine<MX>(tv, ti, lv[ww], li[ww]);
+            }
+            if constexpr (KIND == 0) {
+                pv[r * K + k] = tv;
+            } else {
+                pk[r * K + k] = chunk_key<MX>(tv, ti, (uint32_t)k);
+                if constexpr (sizeof(I) == 8) pi[r * K + k] = ti;
+            }
+        }
+        __syncthreads();  // LDS is reused by the next item
+    }
+}
+
+// Second pass for split rows: one workgroup per row; thread t folds chunks
+// t, t + 256, ... in increasing order (sums) or takes the largest key (the
+// max family), then a fixed block tree.
+template <int OP, class I>
+__global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const float* __restrict__ x,
+                                                                       const float* __restrict__ pv,
+                                                                       const uint64_t* __restrict__ pk,
+                                                                       const I* __restrict__ pi, int64_t rows,
                                                                        int64_t K, int64_t n, float* __restrict__ val,
                                                                        int64_t* __restrict__ idx) {
     constexpr int KIND = kind_of(OP);
-    __shared__ float lv[kBlock / 64];
-    __shared__ int64_t li[kBlock / 64];
+    constexpr int NW = kBlock / 64;
+    __shared__ float lv[NW];
+    __shared__ uint64_t lk[NW];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         if constexpr (KIND == 0) {
-            float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            int64_t k = threadIdx.x;
-            for (; k + 7 * kBlock < K; k += 8 * kBlock) {
+            float a[4] = {0.f, 0.f, 0.f, 0.f};
+            int64_t kk = threadIdx.x;
+            for (; kk + 3 * kBlock < K; kk += 4 * kBlock) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) a[j] += pv[r * K + k + j * kBlock];
+                for (int j = 0; j < 4; ++j) a[j] += pv[r * K + kk + j * kBlock];
             }
-            for (int j = 0; k < K; k += kBlock, ++j) a[j & 7] += pv[r * K + k];
-            float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-            s = block_sum<kBlock>(s, lv);
-            if (threadIdx.x == 0) write_result<OP>(val, idx, r, s, 0, n);
+            for (int j = 0; kk < K; kk += kBlock, ++j) a[j & 3] += pv[r * K + kk];
+            const float t = block_sum<kBlock>((a[0] + a[1]) + (a[2] + a[3]), lv);
+            if (threadIdx.x == 0) write_result<OP>(val, idx, r, t, (I)0, n);
         } else {
-            float v = 0.f;
-            int64_t pos = kEmpty;
-            int64_t k = threadIdx.x;
-            for (; k + 7 * kBlock < K; k += 8 * kBlock) {
-                float bv[8];
-                int64_t bi[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) { bv[j] = pv[r * K + k + j * kBlock]; bi[j] = pi[r * K + k + j * kBlock]; }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) combine<KIND == 1>(v, pos, bv[j], bi[j]);
+            uint64_t best = 0;
+            for (int64_t kk = threadIdx.x; kk < K; kk += kBlock) {
+                const uint64_t c = pk[r * K + kk];
+                best = c > best ? c : best;
             }
-            for (; k < K; k += kBlock) combine<KIND == 1>(v, pos, pv[r * K + k], pi[r * K + k]);
-            wave_combine<KIND == 1>(v, pos);
-            if ((threadIdx.x & 63) == 0) { lv[threadIdx.x >> 6] = v; li[threadIdx.x >> 6] = pos; }
+            best = wave_max_u64(best);
+            if (lane == 0) lk[w] = best;
             __syncthreads();
             if (threadIdx.x == 0) {
-                float bv = lv[0];
-                int64_t bi = li[0];
-                for (int w = 1; w < kBlock / 64; ++w) combine<KIND == 1>(bv, bi, lv[w], li[w]);
-                write_result<OP>(val, idx, r, bv, bi, n);
+#pragma unroll
+                for (int ww = 1; ww < NW; ++ww) best = lk[ww] > best ? lk[ww] : best;
+                float v;
+                I pos;
+                decode_winner<KIND == 1>(best, pi + r * K, 1, [&](int64_t p) { return x[r * n + p]; }, v, pos);
+                write_result<OP>(val, idx, r, v, pos, n);
             }
         }
         __syncthreads();
@@ -216,50 +403,82 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
 // Lane l of each wave owns W adjacent inner positions (W = 4 with 128-bit
 // loads) of output row o, so a wave reads 64*W contiguous floats per position
 // of n.  The workgroup's 4 waves take four contiguous quarters of the chunk
-// [k0, k1) of n, each walking its quarter in increasing order with four loads
-// in flight; the four wave results are combined in wave order through LDS.
-// Splitting the chunk inside the workgroup (rather than over more
-// workgroups) keeps the number of partial results, and so the second pass,
-// four times smaller for the same parallelism.  Items are (o, chunk, inner
-// tile) triples, tile fastest; every thread of a workgroup walks the same
-// items, so the barriers are uniform.
-// IdxT: the positions a thread tracks (int32_t whenever n fits, which
-// halves the compare-and-select work of the max family); partials and
-// results are int64_t.
-template <int OP, bool VEC, class IdxT>
+// [k0, k1) of n, each walking its quarter in increasing order with U loads
+// in flight; the four wave states are combined in wave order through LDS.
+// Items are (o, chunk, inner tile) triples, tile fastest; every thread of a
+// workgroup walks the same items, so the barriers are uniform.
+//
+// With K > 1 chunks the workgroup's state is a partial (value and I-typed
+// position per column) that reduce_cols_finalize_kernel combines.
+template <int OP, bool VEC, class I>
 __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __restrict__ x, int64_t outer, int64_t n,
                                                               int64_t inner, int64_t chunk, int64_t K,
                                                               float* __restrict__ val, int64_t* __restrict__ idx,
-                                                              float* __restrict__ pv, int64_t* __restrict__ pi) {
+                                                              float* __restrict__ pv, uint64_t* __restrict__ pk,
+                                                              I* __restrict__ pi) {
     constexpr int KIND = kind_of(OP);
+    constexpr bool MX = KIND == 1;
     constexpr int W = VEC ? 4 : 1;
     constexpr int NW = kBlock / 64;
+    constexpr int U = VEC ? 8 : 4;
     __shared__ float lv[NW][64 * W];
-    __shared__ IdxT li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
+    __shared__ I li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t tile_elems = (int64_t)64 * W;
     const int64_t tiles = (inner + tile_elems - 1) / tile_elems;
     const int64_t items = outer * K * tiles;
+
+    // The four wave states (v, pos) -> wave 0 lanes hold the workgroup's
+    // state of their W columns.
+    auto lds_combine = [&](float (&v)[W], I (&pos)[W]) {
+        __syncthreads();  // earlier LDS reads are done
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            lv[w][lane * W + j] = v[j];
+            if constexpr (KIND != 0) li[w][lane * W + j] = pos[j];
+        }
+        __syncthreads();
+        if (w == 0) {
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                if constexpr (KIND == 0) {
+                    v[j] = (lv[0][lane * W + j] + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
+                } else {
+                    v[j] = lv[0][lane * W + j];
+                    pos[j] = li[0][lane * W + j];
+#pragma unroll
+                    for (int ww = 1; ww < NW; ++ww) combine<MX>(v[j], pos[j], lv[ww][lane * W + j], li[ww][lane * W + j]);
+                }
+            }
+        }
+    };
+
     for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
         const int64_t t = item % tiles;
         const int64_t ok = item / tiles;
         const int64_t k = ok % K;
         const int64_t o = ok / K;
         const int64_t i0 = t * tile_elems + (int64_t)lane * W;
+        const bool live = i0 < inner;
         const int64_t k0 = k * chunk, k1 = min(n, k0 + chunk);
         const int64_t q = (k1 - k0 + NW - 1) / NW;
         const int64_t r0 = min(k1, k0 + w * q), r1 = min(k1, r0 + q);
         const float* xp = x + o * n * inner + i0;
         float v[W];
-        IdxT pos[W];
+        I pos[W];
 #pragma unroll
-        for (int j = 0; j < W; ++j) { v[j] = 0.f; pos[j] = (IdxT)kEmpty; }
-        if (i0 < inner) {
+        for (int j = 0; j < W; ++j) { v[j] = KIND == 0 ? 0.f : scan_init<MX>(); pos[j] = (I)kEmpty; }
+        if (live) {
+            // Row 0's elements, loaded now and looked at after the loop.
+            const bool has0 = KIND != 0 && r0 == 0 && r1 > 0;
+            float x0[W];
+#pragma unroll
+            for (int j = 0; j < W; ++j) x0[j] = has0 ? xp[j] : 0.f;
             int64_t p = r0;
-            for (; p + 3 < r1; p += 4) {
-                float a[4][W];
+            for (; p + (U - 1) < r1; p += U) {
+                float a[U][W];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < U; ++u) {
                     if constexpr (VEC) {
                         float4 qv = ld_stream(xp + (p + u) * inner);
                         a[u][0] = qv.x; a[u][1] = qv.y; a[u][2] = qv.z; a[u][3] = qv.w;
@@ -268,11 +487,11 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u)
+                for (int u = 0; u < U; ++u)
 #pragma unroll
                     for (int j = 0; j < W; ++j) {
                         if constexpr (KIND == 0) v[j] += a[u][j];
-                        else scan_push<KIND == 1>(v[j], pos[j], a[u][j], (IdxT)(p + u));
+                        else scan_fast<MX>(v[j], pos[j], a[u][j], (I)(p + u));
                     }
             }
             for (; p < r1; ++p) {
@@ -286,35 +505,41 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 #pragma unroll
                 for (int j = 0; j < W; ++j) {
                     if constexpr (KIND == 0) v[j] += a[j];
-                    else scan_push<KIND == 1>(v[j], pos[j], a[j], (IdxT)p);
+                    else scan_fast<MX>(v[j], pos[j], a[j], (I)p);
+                }
+            }
+            if constexpr (KIND != 0) {
+#pragma unroll
+                for (int j = 0; j < W; ++j) {
+                    if (__builtin_expect(pos[j] == (I)kEmpty && r0 < r1, 0)) {
+                        const ScanState<I> f = scan_fix<MX, I>(xp + j, inner, r0, r1);
+                        v[j] = f.v;
+                        pos[j] = f.i;
+                    }
+                    if (has0) scan_start<MX>(v[j], pos[j], x0[j]);
                 }
             }
         }
-        __syncthreads();  // the previous item's LDS reads are done
+        lds_combine(v, pos);
+        if (K == 1) {
+            if (w == 0) {
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            lv[w][lane * W + j] = v[j];
-            if constexpr (KIND != 0) li[w][lane * W + j] = pos[j];
+                for (int j = 0; j < W; ++j)
+                    if (i0 + j < inner) write_result<OP>(val, idx, o * inner + i0 + j, v[j], pos[j], n);
+            }
+            continue;
         }
-        __syncthreads();
         if (w == 0) {
 #pragma unroll
             for (int j = 0; j < W; ++j) {
-                const int64_t i = i0 + j;
-                if (i >= inner) break;
-                float tv = lv[0][lane * W + j];
-                IdxT ti = (IdxT)kEmpty;
-                if constexpr (KIND == 0) {
-                    tv = (tv + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
-                } else {
-                    ti = li[0][lane * W + j];
-#pragma unroll
-                    for (int ww = 1; ww < NW; ++ww) combine<KIND == 1>(tv, ti, lv[ww][lane * W + j], li[ww][lane * W + j]);
-                }
-                if (K == 1) write_result<OP>(val, idx, o * inner + i, tv, ti, n);
-                else {
-                    pv[(o * K + k) * inner + i] = tv;
-                    if (KIND != 0) pi[(o * K + k) * inner + i] = ti;
+                if (i0 + j < inner) {
+                    const int64_t at = (o * K + k) * inner + i0 + j;
+                    if constexpr (KIND == 0) {
+                        pv[at] = v[j];
+                    } else {
+                        pk[at] = chunk_key<MX>(v[j], pos[j], (uint32_t)k);
+                        if constexpr (sizeof(I) == 8) pi[at] = pos[j];
+                    }
                 }
             }
         }
@@ -322,68 +547,79 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
 }
 
 // Second pass for split columns.  A workgroup owns 16 adjacent output slots
-// and its 256 threads form 16 groups of 16 lanes: group g combines chunks
-// k = g, g + 16, g + 32, ... of its lane's slot in increasing k, and the 16
-// group results are combined in group order through LDS.  Small slot tiles
-// spread the pass over many workgroups; it is latency-bound otherwise.
-template <int OP>
-__global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const float* __restrict__ pv,
-                                                                       const int64_t* __restrict__ pi, int64_t outer,
+// and its 256 threads form 16 groups of 16 lanes: group g folds chunks
+// k = g, g + 16, g + 32, ... of its lane's slot (all its loads issued
+// first) -- sums in increasing k, the max family by the largest key -- and
+// the 16 group results are combined in group order through LDS.  Small
+// slot tiles spread the pass over many workgroups, so each thread waits for
+// one round of loads.
+template <int OP, class I>
+__global__ void __launch_bounds__(kBlock) reduce_cols_finalize_kernel(const float* __restrict__ x,
+                                                                       const float* __restrict__ pv,
+                                                                       const uint64_t* __restrict__ pk,
+                                                                       const I* __restrict__ pi, int64_t outer,
                                                                        int64_t K, int64_t inner, int64_t n,
                                                                        float* __restrict__ val,
                                                                        int64_t* __restrict__ idx) {
     constexpr int KIND = kind_of(OP);
     constexpr int S = 16;          // slots per workgroup
     constexpr int G = kBlock / S;  // groups
-    __shared__ float lv[G][S];
-    __shared__ int64_t li[KIND != 0 ? G : 1][S];
+    __shared__ float lv[KIND == 0 ? G : 1][S];
+    __shared__ uint64_t lk[KIND != 0 ? G : 1][S];
     const int c = threadIdx.x & (S - 1), g = threadIdx.x / S;
     const int64_t total = outer * inner;
     for (int64_t s0 = (int64_t)blockIdx.x * S; s0 < total; s0 += (int64_t)gridDim.x * S) {
         const int64_t s = s0 + c;
-        float rv = 0.f;
-        int64_t ri = kEmpty;
-        if (s < total) {
-            const int64_t o = s / inner, i = s - o * inner;
-            const float* pvs = pv + o * K * inner + i;
-            if constexpr (KIND == 0) {
-                int64_t k = g;
-                for (; k + 3 * G < K; k += 4 * G) {
-                    float b[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) b[u] = pvs[(k + u * G) * inner];
-                    rv = ((rv + b[0]) + b[1]) + (b[2] + b[3]);
-                }
-                for (; k < K; k += G) rv += pvs[k * inner];
-            } else {
-                const int64_t* pis = pi + o * K * inner + i;
+        const int64_t o = s / inner, i = s - o * inner;
+        if constexpr (KIND == 0) {
+            float rv = 0.f;
+            if (s < total) {
+                const float* pvs = pv + o * K * inner + i;
                 int64_t k = g;
                 for (; k + 3 * G < K; k += 4 * G) {
                     float bv[4];
-                    int64_t bi[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) { bv[u] = pvs[(k + u * G) * inner]; bi[u] = pis[(k + u * G) * inner]; }
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) combine<KIND == 1>(rv, ri, bv[u], bi[u]);
+                    for (int u = 0; u < 4; ++u) bv[u] = pvs[(k + u * G) * inner];
+                    rv = ((rv + bv[0]) + bv[1]) + (bv[2] + bv[3]);
                 }
-                for (; k < K; k += G) combine<KIND == 1>(rv, ri, pvs[k * inner], pis[k * inner]);
+                for (; k < K; k += G) rv += pvs[k * inner];
             }
-        }
-        lv[g][c] = rv;
-        if constexpr (KIND != 0) li[g][c] = ri;
-        __syncthreads();
-        if (g == 0 && s < total) {
-            float tv = lv[0][c];
-            int64_t ti = kEmpty;
-            if constexpr (KIND == 0) {
+            lv[g][c] = rv;
+            __syncthreads();
+            if (g == 0 && s < total) {
+                float tv = lv[0][c];
 #pragma unroll
                 for (int gg = 1; gg < G; ++gg) tv += lv[gg][c];
-            } else {
-                ti = li[0][c];
-#pragma unroll
-                for (int gg = 1; gg < G; ++gg) combine<KIND == 1>(tv, ti, lv[gg][c], li[gg][c]);
+                write_result<OP>(val, idx, s, tv, (I)0, n);
             }
-            write_result<OP>(val, idx, s, tv, ti, n);
+        } else {
+            uint64_t best = 0;
+            if (s < total) {
+                const uint64_t* pks = pk + o * K * inner + i;
+                int64_t k = g;
+                for (; k + 3 * G < K; k += 4 * G) {
+                    uint64_t b[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) b[u] = pks[(k + u * G) * inner];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) best = b[u] > best ? b[u] : best;
+                }
+                for (; k < K; k += G) {
+                    const uint64_t b = pks[k * inner];
+                    best = b > best ? b : best;
+                }
+            }
+            lk[g][c] = best;
+            __syncthreads();
+            if (g == 0 && s < total) {
+#pragma unroll
+                for (int gg = 1; gg < G; ++gg) best = lk[gg][c] > best ? lk[gg][c] : best;
+                float v;
+                I pos;
+                decode_winner<KIND == 1>(best, pi + o * K * inner + i, inner,
+                                         [&](int64_t p) { return x[(o * n + p) * inner + i]; }, v, pos);
+                write_result<OP>(val, idx, s, v, pos, n);
+            }
         }
         __syncthreads();
     }
@@ -452,37 +688,53 @@ __global__ void __launch_bounds__(kBlock) reduce_bwd_scatter_kernel(const float*
 // host
 // ---------------------------------------------------------------------------
 
-template <int OP>
-int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+template <int OP, class I>
+int launch_rows(const float* x, int64_t rows, int64_t n, float* val, int64_t* idx) {
     constexpr int KIND = kind_of(OP);
     hipStream_t st = stream();
+    const bool vec = (n % 4 == 0) && aligned16(x);
+    // Enough rows: one wave per row.  Few long rows (a full reduction is one
+    // row): each row in chunks of whole workgroups, ~8 workgroups per CU,
+    // then a second pass over the chunk partials.
     const int64_t target_waves = (int64_t)num_cus() * 32;
-    if (inner == 1) {
-        int64_t K = 1;
-        if (outer < target_waves) K = std::min<int64_t>((target_waves + outer - 1) / outer, (n + 4095) / 4096);
+    int64_t K = 1, chunk = n;
+    if (rows < target_waves) {
+        const int64_t target_wgs = (int64_t)num_cus() * 8;
+        K = std::min<int64_t>((target_wgs + rows - 1) / rows, (n + 4095) / 4096);
         K = std::max<int64_t>(K, 1);
-        int64_t chunk = (n + K - 1) / K;
-        chunk = (chunk + 255) / 256 * 256;
-        K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
-        Workspace wv(K > 1 ? (size_t)(outer * K) * sizeof(float) : 0);
-        Workspace wi(K > 1 && KIND != 0 ? (size_t)(outer * K) * sizeof(int64_t) : 0);
-        if (K > 1 && (!wv.p || (KIND != 0 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
-        const bool vec = (n % 4 == 0) && aligned16(x);
-        dim3 grid(grid_for(outer * K, kBlock / 64, 32));
-        if (vec)
-            launch_kernel((reduce_rows_kernel<OP, true>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
-                               idx, wv.as<float>(), wi.as<int64_t>());
-        else
-            launch_kernel((reduce_rows_kernel<OP, false>), grid, dim3(kBlock), 0, st, x, outer, n, chunk, K, val,
-                               idx, wv.as<float>(), wi.as<int64_t>());
-        WM_TRY(check_launch("wm_reduce(rows)"));
         if (K > 1) {
-            launch_kernel(reduce_rows_finalize_kernel<OP>, dim3(grid_for(outer, 1, 8)), dim3(kBlock), 0, st,
-                               wv.as<float>(), wi.as<int64_t>(), outer, K, n, val, idx);
-            WM_TRY(check_launch("wm_reduce(rows finalize)"));
+            chunk = (n + K - 1) / K;
+            chunk = (chunk + 1023) / 1024 * 1024;  // four wave quarters of whole 256-float strides
+            K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
         }
-        return WM_OK;
     }
+    if (K == 1) {
+        dim3 grid(grid_for(rows, kBlock / 64, 32));
+        if (vec) launch_kernel((reduce_rows_kernel<OP, true, I>), grid, dim3(kBlock), 0, st, x, rows, n, n, (int64_t)1,
+                               val, idx, (float*)nullptr, (uint64_t*)nullptr, (I*)nullptr);
+        else launch_kernel((reduce_rows_kernel<OP, false, I>), grid, dim3(kBlock), 0, st, x, rows, n, n, (int64_t)1,
+                           val, idx, (float*)nullptr, (uint64_t*)nullptr, (I*)nullptr);
+        return check_launch("wm_reduce(rows)");
+    }
+    Workspace wv(KIND == 0 ? (size_t)(rows * K) * sizeof(float) : 0);
+    Workspace wk(KIND != 0 ? (size_t)(rows * K) * sizeof(uint64_t) : 0);
+    Workspace wi(KIND != 0 && sizeof(I) == 8 ? (size_t)(rows * K) * sizeof(I) : 0);
+    if (KIND == 0 ? !wv.p : (!wk.p || (sizeof(I) == 8 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
+    dim3 grid(grid_for(rows * K, 1, 8));
+    if (vec) launch_kernel((reduce_rows_kernel<OP, true, I>), grid, dim3(kBlock), 0, st, x, rows, n, chunk, K, val,
+                           idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+    else launch_kernel((reduce_rows_kernel<OP, false, I>), grid, dim3(kBlock), 0, st, x, rows, n, chunk, K, val, idx,
+                       wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+    WM_TRY(check_launch("wm_reduce(rows)"));
+    launch_kernel((reduce_rows_finalize_kernel<OP, I>), dim3(grid_for(rows, 1, 8)), dim3(kBlock), 0, st, x,
+                  wv.as<float>(), wk.as<uint64_t>(), wi.as<I>(), rows, K, n, val, idx);
+    return check_launch("wm_reduce(rows finalize)");
+}
+
+template <int OP, class I>
+int launch_cols(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+    constexpr int KIND = kind_of(OP);
+    hipStream_t st = stream();
     const bool vec = (inner % 4 == 0) && aligned16(x);
     const int64_t tile = (int64_t)64 * (vec ? 4 : 1);
     const int64_t tiles = (inner + tile - 1) / tile;
@@ -494,24 +746,35 @@ int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float
     K = std::max<int64_t>(std::min<int64_t>(K, 4096), 1);
     const int64_t chunk = (n + K - 1) / K;
     K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
-    Workspace wv(K > 1 ? (size_t)(outer * K * inner) * sizeof(float) : 0);
-    Workspace wi(K > 1 && KIND != 0 ? (size_t)(outer * K * inner) * sizeof(int64_t) : 0);
-    if (K > 1 && (!wv.p || (KIND != 0 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
+    const size_t parts = K > 1 ? (size_t)(outer * K * inner) : 0;
+    Workspace wv(KIND == 0 ? parts * sizeof(float) : 0);
+    Workspace wk(KIND != 0 ? parts * sizeof(uint64_t) : 0);
+    Workspace wi(KIND != 0 && sizeof(I) == 8 ? parts * sizeof(I) : 0);
+    if (parts && (KIND == 0 ? !wv.p : (!wk.p || (sizeof(I) == 8 && !wi.p))))
+        return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
     dim3 grid(grid_for(outer * K * tiles, 1, 32));
-#define WM_RC(V, I)                                                                                          \
-    launch_kernel((reduce_cols_kernel<OP, V, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K, val, \
-                       idx, wv.as<float>(), wi.as<int64_t>())
-    const bool narrow = n <= (int64_t)INT32_MAX;
-    if (vec) { if (narrow) WM_RC(true, int32_t); else WM_RC(true, int64_t); }
-    else { if (narrow) WM_RC(false, int32_t); else WM_RC(false, int64_t); }
-#undef WM_RC
+    if (vec) launch_kernel((reduce_cols_kernel<OP, true, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K,
+                           val, idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+    else launch_kernel((reduce_cols_kernel<OP, false, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K,
+                       val, idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
-        launch_kernel(reduce_cols_finalize_kernel<OP>, dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0,
-                           st, wv.as<float>(), wi.as<int64_t>(), outer, K, inner, n, val, idx);
+        launch_kernel((reduce_cols_finalize_kernel<OP, I>), dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0, st,
+                      x, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>(), outer, K, inner, n, val, idx);
         WM_TRY(check_launch("wm_reduce(cols finalize)"));
     }
     return WM_OK;
+}
+
+// Positions are tracked as 32-bit integers whenever the reduced extent fits
+// (half the compare-and-select work and partial bytes of 64-bit ones).
+template <int OP>
+int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+    const bool narrow = n <= (int64_t)INT32_MAX;
+    if (inner == 1)
+        return narrow ? launch_rows<OP, int32_t>(x, outer, n, val, idx) : launch_rows<OP, int64_t>(x, outer, n, val, idx);
+    return narrow ? launch_cols<OP, int32_t>(x, outer, n, inner, val, idx)
+                  : launch_cols<OP, int64_t>(x, outer, n, inner, val, idx);
 }
 
 }  // namespace wm
