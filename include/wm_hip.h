@@ -115,6 +115,9 @@ int wm_span_begin(void);
 int wm_span_end(float* kernel_ms, float* span_ms, int* kernels);
 /* Duration of the i-th kernel (0-based) of the last span wm_span_end closed. */
 int wm_span_kernel(int i, float* ms);
+/* Device blocks the library's pool has handed out so far (wm_alloc and
+   internal workspace); a test of an entry point that allocates nothing. */
+int wm_pool_handouts(int64_t* count);
 /* Plain streaming copy kernel, used to calibrate rocprof byte counters. */
 int wm_copy_kernel(float* dst, const float* src, int64_t n);
 
@@ -184,6 +187,21 @@ int wm_unary_bwd(int op, const float* g, const float* x, const float* out,
  * (:2096-2134). */
 int wm_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner,
               float* val, int64_t* idx);
+
+/* wm_reduce without allocating: no counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
+ * and errors as wm_reduce, and the same kernels; the chunk partials of a
+ * split reduction live in a fixed 8 MiB device array per GPU (held until the
+ * process ends) instead of the library's pool, so no device memory is taken
+ * from the pool or the driver.  A reduction whose partials exceed 8 MiB
+ * fails with WM_ERR_UNSUPPORTED (wm_reduce handles it).  Every call on one
+ * GPU shares the array: this library orders its calls on its one stream, and
+ * work that overlaps a call on another stream (a replayed graph) races on it.
+ * Call wm_init first: the first call on a device looks up the array's
+ * address (no allocation). */
+int wm_reduce_noalloc(int op, const float* x, int64_t outer, int64_t n, int64_t inner,
+                      float* val, int64_t* idx);
 
 /* Backward of wm_reduce for SUM/MEAN (gx[o,k,i] (+)= g[o,i]; the reference's
  * mean reuses sum's closure, so no 1/n, :1709-1721) and MAX/MIN

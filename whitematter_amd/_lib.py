@@ -54,6 +54,7 @@ _SIGS = {
     "wm_span_begin": [],
     "wm_span_end": [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_int)],
     "wm_span_kernel": [C.c_int, C.POINTER(C.c_float)],
+    "wm_pool_handouts": [C.POINTER(C.c_int64)],
     "wm_copy_kernel": [_vp, _vp, C.c_int64],
     "wm_fill": [_vp, C.c_float, C.c_int64],
     "wm_f32_to_f16_rtz": [_vp, _vp, C.c_int64],
@@ -65,6 +66,7 @@ _SIGS = {
     "wm_unary": [C.c_int, _vp, _vp, C.c_int64, C.c_float, C.c_float],
     "wm_unary_bwd": [C.c_int, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_float, C.c_float],
     "wm_reduce": [C.c_int, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, _vp],
+    "wm_reduce_noalloc": [C.c_int, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, _vp],
     "wm_reduce_bwd": [C.c_int, _vp, _vp, C.c_int64, C.c_int64, C.c_int64, _vp, C.c_int],
     "wm_softmax_fwd": [_vp, _vp, C.c_int64, C.c_int64],
     "wm_log_softmax_fwd": [_vp, _vp, C.c_int64, C.c_int64],

@@ -22,6 +22,8 @@ int set_error(int status, const std::string& msg);
 int ensure_init();
 hipStream_t stream();
 int num_cus();
+// The device the library runs on (wm_init's, or 0).
+int device();
 
 // Stream-ordered workspace from the caching allocator.  Freed blocks go back
 // to the pool immediately: every kernel runs on the one library stream, so a

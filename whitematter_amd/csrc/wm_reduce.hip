@@ -20,6 +20,9 @@
 #include "wm_common.hpp"
 
 #include <algorithm>
+#include <memory>
+#include <mutex>
+#include <unordered_map>
 
 namespace wm {
 
@@ -688,8 +691,53 @@ __global__ void __launch_bounds__(kBlock) reduce_bwd_scatter_kernel(const float*
 // host
 // ---------------------------------------------------------------------------
 
+// Where a launch's chunk partials live: blocks from the library's pool
+// (base == null), or a fixed region of `cap` bytes (the allocation-free
+// entry point's scratch array).
+struct PartialArena {
+    char* base = nullptr;
+    size_t cap = 0;
+};
+
+// The partial arrays of one launch: floats for sums, order keys (+ 64-bit
+// positions when positions are wide) for the max family.
+struct Partials {
+    Workspace wv, wk, wi;
+    float* pv = nullptr;
+    uint64_t* pk = nullptr;
+    void* pi = nullptr;
+    Partials(size_t fbytes, size_t kbytes, size_t ibytes, bool pool)
+        : wv(pool ? fbytes : 0), wk(pool ? kbytes : 0), wi(pool ? ibytes : 0) {}
+};
+
+template <int KIND, class I>
+int take_partials(size_t parts, const PartialArena& arena, std::unique_ptr<Partials>& P) {
+    const size_t fb = KIND == 0 ? parts * sizeof(float) : 0;
+    const size_t kb = KIND != 0 ? parts * sizeof(uint64_t) : 0;
+    const size_t ib = KIND != 0 && sizeof(I) == 8 ? parts * sizeof(I) : 0;
+    P.reset(new Partials(fb, kb, ib, arena.base == nullptr));
+    if (parts == 0) return WM_OK;
+    if (!arena.base) {
+        if ((fb && !P->wv.p) || (kb && !P->wk.p) || (ib && !P->wi.p))
+            return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
+        P->pv = P->wv.as<float>();
+        P->pk = P->wk.as<uint64_t>();
+        P->pi = P->wi.p;
+        return WM_OK;
+    }
+    const size_t first = (fb + kb + 255) / 256 * 256;
+    if (first + ib > arena.cap)
+        return set_error(WM_ERR_UNSUPPORTED, "wm_reduce_noalloc: this reduction needs " + std::to_string(first + ib) +
+                                                 " bytes of partials; the scratch array holds " +
+                                                 std::to_string(arena.cap) + " (use wm_reduce)");
+    P->pv = reinterpret_cast<float*>(arena.base);
+    P->pk = reinterpret_cast<uint64_t*>(arena.base);
+    P->pi = ib ? arena.base + first : nullptr;
+    return WM_OK;
+}
+
 template <int OP, class I>
-int launch_rows(const float* x, int64_t rows, int64_t n, float* val, int64_t* idx) {
+int launch_rows(const float* x, int64_t rows, int64_t n, float* val, int64_t* idx, const PartialArena& arena) {
     constexpr int KIND = kind_of(OP);
     hipStream_t st = stream();
     const bool vec = (n % 4 == 0) && aligned16(x);
@@ -716,23 +764,23 @@ int launch_rows(const float* x, int64_t rows, int64_t n, float* val, int64_t* id
                            val, idx, (float*)nullptr, (uint64_t*)nullptr, (I*)nullptr);
         return check_launch("wm_reduce(rows)");
     }
-    Workspace wv(KIND == 0 ? (size_t)(rows * K) * sizeof(float) : 0);
-    Workspace wk(KIND != 0 ? (size_t)(rows * K) * sizeof(uint64_t) : 0);
-    Workspace wi(KIND != 0 && sizeof(I) == 8 ? (size_t)(rows * K) * sizeof(I) : 0);
-    if (KIND == 0 ? !wv.p : (!wk.p || (sizeof(I) == 8 && !wi.p))) return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
+    std::unique_ptr<Partials> P;
+    WM_TRY((take_partials<KIND, I>((size_t)(rows * K), arena, P)));
+    I* pi = static_cast<I*>(P->pi);
     dim3 grid(grid_for(rows * K, 1, 8));
     if (vec) launch_kernel((reduce_rows_kernel<OP, true, I>), grid, dim3(kBlock), 0, st, x, rows, n, chunk, K, val,
-                           idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+                           idx, P->pv, P->pk, pi);
     else launch_kernel((reduce_rows_kernel<OP, false, I>), grid, dim3(kBlock), 0, st, x, rows, n, chunk, K, val, idx,
-                       wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+                       P->pv, P->pk, pi);
     WM_TRY(check_launch("wm_reduce(rows)"));
-    launch_kernel((reduce_rows_finalize_kernel<OP, I>), dim3(grid_for(rows, 1, 8)), dim3(kBlock), 0, st, x,
-                  wv.as<float>(), wk.as<uint64_t>(), wi.as<I>(), rows, K, n, val, idx);
+    launch_kernel((reduce_rows_finalize_kernel<OP, I>), dim3(grid_for(rows, 1, 8)), dim3(kBlock), 0, st, x, P->pv,
+                  P->pk, pi, rows, K, n, val, idx);
     return check_launch("wm_reduce(rows finalize)");
 }
 
 template <int OP, class I>
-int launch_cols(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+int launch_cols(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx,
+                const PartialArena& arena) {
     constexpr int KIND = kind_of(OP);
     hipStream_t st = stream();
     const bool vec = (inner % 4 == 0) && aligned16(x);
@@ -746,21 +794,18 @@ int launch_cols(const float* x, int64_t outer, int64_t n, int64_t inner, float* 
     K = std::max<int64_t>(std::min<int64_t>(K, 4096), 1);
     const int64_t chunk = (n + K - 1) / K;
     K = std::max<int64_t>(1, (n + chunk - 1) / chunk);
-    const size_t parts = K > 1 ? (size_t)(outer * K * inner) : 0;
-    Workspace wv(KIND == 0 ? parts * sizeof(float) : 0);
-    Workspace wk(KIND != 0 ? parts * sizeof(uint64_t) : 0);
-    Workspace wi(KIND != 0 && sizeof(I) == 8 ? parts * sizeof(I) : 0);
-    if (parts && (KIND == 0 ? !wv.p : (!wk.p || (sizeof(I) == 8 && !wi.p))))
-        return set_error(WM_ERR_NOMEM, "wm_reduce: workspace");
+    std::unique_ptr<Partials> P;
+    WM_TRY((take_partials<KIND, I>(K > 1 ? (size_t)(outer * K * inner) : 0, arena, P)));
+    I* pi = static_cast<I*>(P->pi);
     dim3 grid(grid_for(outer * K * tiles, 1, 32));
     if (vec) launch_kernel((reduce_cols_kernel<OP, true, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K,
-                           val, idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+                           val, idx, P->pv, P->pk, pi);
     else launch_kernel((reduce_cols_kernel<OP, false, I>), grid, dim3(kBlock), 0, st, x, outer, n, inner, chunk, K,
-                       val, idx, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>());
+                       val, idx, P->pv, P->pk, pi);
     WM_TRY(check_launch("wm_reduce(cols)"));
     if (K > 1) {
         launch_kernel((reduce_cols_finalize_kernel<OP, I>), dim3(grid_for(outer * inner, 16, 8)), dim3(kBlock), 0, st,
-                      x, wv.as<float>(), wk.as<uint64_t>(), wi.as<I>(), outer, K, inner, n, val, idx);
+                      x, P->pv, P->pk, pi, outer, K, inner, n, val, idx);
         WM_TRY(check_launch("wm_reduce(cols finalize)"));
     }
     return WM_OK;
@@ -769,12 +814,47 @@ int launch_cols(const float* x, int64_t outer, int64_t n, int64_t inner, float* 
 // Positions are tracked as 32-bit integers whenever the reduced extent fits
 // (half the compare-and-select work and partial bytes of 64-bit ones).
 template <int OP>
-int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+int launch_reduce(const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx,
+                  const PartialArena& arena) {
     const bool narrow = n <= (int64_t)INT32_MAX;
     if (inner == 1)
-        return narrow ? launch_rows<OP, int32_t>(x, outer, n, val, idx) : launch_rows<OP, int64_t>(x, outer, n, val, idx);
-    return narrow ? launch_cols<OP, int32_t>(x, outer, n, inner, val, idx)
-                  : launch_cols<OP, int64_t>(x, outer, n, inner, val, idx);
+        return narrow ? launch_rows<OP, int32_t>(x, outer, n, val, idx, arena)
+                      : launch_rows<OP, int64_t>(x, outer, n, val, idx, arena);
+    return narrow ? launch_cols<OP, int32_t>(x, outer, n, inner, val, idx, arena)
+                  : launch_cols<OP, int64_t>(x, outer, n, inner, val, idx, arena);
+}
+
+// The allocation-free entry point's partials: a file-scope device array (no
+// counterpart in the reference), one copy per GPU the library runs on, held
+// until the process ends.  Host code uses the address hipGetSymbolAddress
+// gives for the current device, never the array's name.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::unordered_map<int, void*> g_scratch_at;  // device -> its copy of scratch
+
+// The address of `scratch` on the library's device, looked up once per device
+// with that device current.
+int scratch_address(void** out) {
+    const int dev = device();
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_at.find(dev);
+    if (it != g_scratch_at.end()) {
+        *out = it->second;
+        return WM_OK;
+    }
+    int prev = -1;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess && prev != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev >= 0 && prev != dev) (void)hipSetDevice(prev);
+    if (e != hipSuccess || !p)
+        return set_error(WM_ERR_HIP, std::string("wm_reduce_noalloc: scratch address: ") + hipGetErrorString(e));
+    g_scratch_at[dev] = p;
+    *out = p;
+    return WM_OK;
 }
 
 }  // namespace wm
@@ -783,32 +863,49 @@ using namespace wm;
 
 extern "C" {
 
-int wm_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
-    if (outer < 0 || n < 0 || inner < 0) return set_error(WM_ERR_INVALID, "wm_reduce: negative extent");
-    if (op < WM_R_SUM || op > WM_R_ARGMIN) return set_error(WM_ERR_INVALID, "wm_reduce: unknown op");
+static int reduce_entry(const char* name, int op, const float* x, int64_t outer, int64_t n, int64_t inner,
+                        float* val, int64_t* idx, bool noalloc) {
+    const std::string nm(name);
+    if (outer < 0 || n < 0 || inner < 0) return set_error(WM_ERR_INVALID, nm + ": negative extent");
+    if (op < WM_R_SUM || op > WM_R_ARGMIN) return set_error(WM_ERR_INVALID, nm + ": unknown op");
     if (outer == 0 || inner == 0) return WM_OK;
     if (n == 0) {
         // An empty sum is 0 and an empty mean 0/0 (the reference's loops do
         // nothing, then divide); max/min/arg* would read data[0] there.
         if (op == WM_R_SUM || op == WM_R_MEAN) {
-            if (!val) return set_error(WM_ERR_INVALID, "wm_reduce: null output");
+            if (!val) return set_error(WM_ERR_INVALID, nm + ": null output");
             WM_CHECK_INIT();
             return wm_fill(val, op == WM_R_SUM ? 0.f : __builtin_nanf(""), outer * inner);
         }
-        return set_error(WM_ERR_INVALID, "wm_reduce: empty reduction axis");
+        return set_error(WM_ERR_INVALID, nm + ": empty reduction axis");
     }
-    if (!x) return set_error(WM_ERR_INVALID, "wm_reduce: null input");
-    if ((op == WM_R_SUM || op == WM_R_MEAN) && !val) return set_error(WM_ERR_INVALID, "wm_reduce: null output");
-    if (op >= WM_R_MAX && !val && !idx) return set_error(WM_ERR_INVALID, "wm_reduce: no output requested");
+    if (!x) return set_error(WM_ERR_INVALID, nm + ": null input");
+    if ((op == WM_R_SUM || op == WM_R_MEAN) && !val) return set_error(WM_ERR_INVALID, nm + ": null output");
+    if (op >= WM_R_MAX && !val && !idx) return set_error(WM_ERR_INVALID, nm + ": no output requested");
     WM_CHECK_INIT();
-    switch (op) {
-        case WM_R_SUM: return launch_reduce<WM_R_SUM>(x, outer, n, inner, val, idx);
-        case WM_R_MEAN: return launch_reduce<WM_R_MEAN>(x, outer, n, inner, val, idx);
-        case WM_R_MAX: return launch_reduce<WM_R_MAX>(x, outer, n, inner, val, idx);
-        case WM_R_MIN: return launch_reduce<WM_R_MIN>(x, outer, n, inner, val, idx);
-        case WM_R_ARGMAX: return launch_reduce<WM_R_ARGMAX>(x, outer, n, inner, val, idx);
-        default: return launch_reduce<WM_R_ARGMIN>(x, outer, n, inner, val, idx);
+    PartialArena arena;
+    if (noalloc) {
+        void* p = nullptr;
+        WM_TRY(scratch_address(&p));
+        arena.base = static_cast<char*>(p);
+        arena.cap = kScratchBytes;
     }
+    switch (op) {
+        case WM_R_SUM: return launch_reduce<WM_R_SUM>(x, outer, n, inner, val, idx, arena);
+        case WM_R_MEAN: return launch_reduce<WM_R_MEAN>(x, outer, n, inner, val, idx, arena);
+        case WM_R_MAX: return launch_reduce<WM_R_MAX>(x, outer, n, inner, val, idx, arena);
+        case WM_R_MIN: return launch_reduce<WM_R_MIN>(x, outer, n, inner, val, idx, arena);
+        case WM_R_ARGMAX: return launch_reduce<WM_R_ARGMAX>(x, outer, n, inner, val, idx, arena);
+        default: return launch_reduce<WM_R_ARGMIN>(x, outer, n, inner, val, idx, arena);
+    }
+}
+
+int wm_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+    return reduce_entry("wm_reduce", op, x, outer, n, inner, val, idx, false);
+}
+
+int wm_reduce_noalloc(int op, const float* x, int64_t outer, int64_t n, int64_t inner, float* val, int64_t* idx) {
+    return reduce_entry("wm_reduce_noalloc", op, x, outer, n, inner, val, idx, true);
 }
 
 int wm_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int64_t n, int64_t inner, float* gx,

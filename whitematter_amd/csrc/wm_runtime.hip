@@ -108,10 +108,16 @@ int ensure_init() {
 }
 
 hipStream_t stream() { return g_dev.stream; }
+int device() { return g_dev.device >= 0 ? g_dev.device : 0; }
 int num_cus() { return g_dev.cus > 0 ? g_dev.cus : 256; }
+
+// Blocks the pool has handed out (wm_alloc and workspace), for tests that
+// check an entry point allocates nothing.
+static int64_t g_handouts = 0;
 
 static void* pool_alloc(size_t bytes) {
     std::lock_guard<std::mutex> lk(g_mu);
+    ++g_handouts;
     size_t cls = size_class(bytes);
     auto it = g_pool.free_blocks.find(cls);
     if (it != g_pool.free_blocks.end()) {
@@ -326,6 +332,13 @@ int wm_timer_stop(float* elapsed_ms) {
     if (e == hipSuccess) e = hipEventSynchronize(g_dev.ev_stop);
     if (e == hipSuccess) e = hipEventElapsedTime(elapsed_ms, g_dev.ev_start, g_dev.ev_stop);
     if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string("wm_timer_stop: ") + hipGetErrorString(e));
+    return WM_OK;
+}
+
+int wm_pool_handouts(int64_t* count) {
+    if (!count) return set_error(WM_ERR_INVALID, "wm_pool_handouts: null pointer");
+    std::lock_guard<std::mutex> lk(g_mu);
+    *count = g_handouts;
     return WM_OK;
 }
 
