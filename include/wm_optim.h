@@ -86,12 +86,20 @@ int wm_clip_grad_value(float* g, int64_t n, float clip_value);
  * (the stopping position decides what is written). */
 int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float inv_scale, int* found_inf);
 
+/* check_gradients_finite, core/amp.h:293-300: *all_finite (host) = 1 when
+ * every element of every listed gradient is finite, else 0.  Read-only: one
+ * search launch over the list (and its finalize), then one synchronisation
+ * for the answer. */
+int wm_grads_finite_multi(int count, const float* const* g, const int64_t* n, int* all_finite);
+
 /* ---- multi-tensor variants ----------------------------------------------
  * The same updates over a whole parameter list in one launch: host arrays of
  * `count` device pointers (one per parameter tensor) and sizes; zero-size
  * entries are skipped.  Each element gets exactly the single-tensor update,
  * so results equal calling the single-tensor entry point per tensor in list
- * order.  The list's descriptor table is uploaded on the library stream
+ * order -- also when entries share arrays (a parameter listed twice): the
+ * list is cut into runs whose written arrays overlap nothing else in the
+ * run, one launch per run, in list order.  The list's descriptor table is uploaded on the library stream
  * through pinned staging; the call does not wait for the GPU.  This is what
  * the drop-in optimizers' step() uses: a model's many small parameter tensors
  * would otherwise cost one kernel launch each.                             */
@@ -109,6 +117,10 @@ int wm_rmsprop_step_multi(int count, float* const* p, const float* const* g, flo
 /* get_grad_norm's sum of squares over a gradient list: *total (device) =
  * sum over every element of every tensor, a fixed-order two-pass sum.      */
 int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, float* total);
+/* clip_grad_norm_amp's sum of squares, core/amp.h:303-312: sum of (g * mul)^2
+ * with each element scaled before it is squared (mul = 1 / scale), so still-
+ * scaled gradients do not overflow the sum the way g^2 * mul^2 would. */
+int wm_grad_sumsq_scaled_multi(int count, const float* const* g, const int64_t* n, float mul, float* total);
 
 /* clip_grad_norm_'s scaling and clip_grad_value_ over a gradient list.      */
 int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, const float* total_sumsq,

@@ -136,3 +136,43 @@ def test_reference_amp_program_against_drop_in():
     assert r.returncode == 0, out[-2000:]
     assert len(re.findall(r"^\s+PASSED", out, re.M)) == 5 and "FAILED" not in out, out[-2000:]
     assert "All tests completed!" in out
+
+
+def test_clip_grad_norm_amp_large_scaled_gradients(T):
+    """Each element is scaled before it is squared (core/amp.h:306-312): with
+    scale 2^32 and an unscaled norm near 1e10, g^2 alone would overflow fp32,
+    the reference's sum does not."""
+    rng = np.random.default_rng(6)
+    scale = 2.0 ** 32
+    grads = [(rng.standard_normal(n) * 3e7 * scale).astype(np.float32) for n in (100000, 4097)]
+    assert np.isfinite(np.concatenate(grads)).all()
+    ps = params_with_grads(T, grads)
+    norm = T.clip_grad_norm_amp(ps, 1.0, scale)
+    inv = np.float32(1.0) / np.float32(scale)
+    g64 = np.concatenate([g * inv for g in grads]).astype(np.float64)
+    ref = np.sqrt((g64 * g64).sum())
+    assert np.isfinite(norm) and abs(norm - ref) <= 1e-5 * ref
+    coef = np.float32(1.0) / (np.float32(norm) + np.float32(1e-6))
+    for p, g in zip(ps, grads):
+        assert np.array_equal(np.asarray(p.grad), g * coef)
+
+
+def test_unscale_with_zero_scale_reports_overflow(T):
+    """inv_scale = 1 / 0 = inf makes every product non-finite, zeros included
+    (0 * inf = NaN): the reference reports an overflow as soon as any
+    parameter has a gradient, even an all-zero one, and changes nothing."""
+    z = tensor(T, np.zeros(16, np.float32), True)           # known-zero gradient
+    opt = T.SGD([z], 0.1)
+    scaler = T.GradScaler(1.0, 2.0, 0.5, 3)
+    scaler.set_scale(0.0)
+    assert not scaler.unscale(opt)
+    assert not np.asarray(z.grad).any()
+
+
+def test_check_gradients_finite_leaves_device_values(T):
+    """The finite check is read-only: values are unchanged afterwards,
+    including a huge finite value that any rescaling would disturb."""
+    g = np.float32([3e38, -1.5, 0.0, 7.0] * 256)
+    ps = params_with_grads(T, [g])
+    assert T.check_gradients_finite(ps)
+    assert np.array_equal(np.asarray(ps[0].grad), g)

@@ -231,3 +231,69 @@ def test_multi_norm_clip_value(wm):
         mine = g * coef
         o32.clip_grad_value(mine, 0.5)
         assert oracle.bit_equal(d_.get(), mine)
+
+
+@pytest.mark.parametrize("kind,hp", CONFIGS, ids=lambda v: v if isinstance(v, str) else "-".join(map(str, v.values())))
+def test_multi_duplicated_parameter(wm, kind, hp):
+    """A parameter listed twice (one module added to a list twice) is
+    updated twice, one update after the other, each listing with its own
+    state, as the reference's loop over the list does
+    (core/optimizer.cpp:22-138); the multi-tensor launch must not let two
+    workgroups update it at once."""
+    lr, a, b, c, d = hp["lr"], hp.get("a", 0.0), hp.get("b", 0.0), hp.get("c", 0.0), hp.get("d", 0.0)
+    n0, n1 = 70001, 4096
+    p0 = rng(11).standard_normal(n0).astype(np.float32)
+    p1 = rng(12).standard_normal(n1).astype(np.float32)
+    # list: [p0, p1, p0] with separate state per listing
+    mine_p = [p0.copy(), p1.copy()]
+    states = [[np.zeros(n, np.float32), np.zeros(n, np.float32)] for n in (n0, n1, n0)]
+    dp = [Slot(p0), Slot(p1)]
+    ds = [[Slot(s[0]), Slot(s[1])] for s in states]
+    for t in range(1, 3):
+        g0 = (rng(20 + t).standard_normal(n0)).astype(np.float32)
+        g1 = (rng(30 + t).standard_normal(n1)).astype(np.float32)
+        dg = [Slot(g0), Slot(g1)]
+        P, _p = _ptrs([dp[0], dp[1], dp[0]])
+        G, _g = _ptrs([dg[0], dg[1], dg[0]])
+        S1, _s1 = _ptrs([x[0] for x in ds])
+        S2, _s2 = _ptrs([x[1] for x in ds])
+        ns, _ns = W.i64_array([n0, n1, n0])
+        if kind == "sgd":
+            W.call("wm_sgd_step_multi", 3, P, G, S1 if a > 0 else None, ns, lr, a)
+        elif kind == "adam":
+            W.call("wm_adam_step_multi", 3, P, G, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t))
+        elif kind == "adamw":
+            W.call("wm_adamw_step_multi", 3, P, G, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t), d)
+        else:
+            W.call("wm_rmsprop_step_multi", 3, P, G, S1, S2 if c > 0 else None, ns, lr, a, b, c, d)
+        for which, g, st in ((0, g0, states[0]), (1, g1, states[1]), (0, g0, states[2])):
+            oracle_step(kind, hp, mine_p[which], g, st[0], st[1], t)
+        assert oracle.bit_equal(dp[0].get(), mine_p[0]), (kind, t)
+        assert oracle.bit_equal(dp[1].get(), mine_p[1]), (kind, t)
+
+
+def test_multi_duplicated_gradient_clip_and_unscale(wm):
+    """clip_grad_value_ / clip_grad_norm_'s scaling and GradScaler::unscale
+    over a list holding one gradient twice: applied twice in list order."""
+    n = 50000
+    g = (rng(40).standard_normal(n) * 3).astype(np.float32)
+    d = Slot(g)
+    G, _g = _ptrs([d, d])
+    ns, _ns = W.i64_array([n, n])
+    W.call("wm_clip_grad_value_multi", 2, G, ns, 0.5)
+    mine = g.copy()
+    o32.clip_grad_value(mine, 0.5)
+    o32.clip_grad_value(mine, 0.5)
+    assert oracle.bit_equal(d.get(), mine)
+    total = W.DeviceArray.from_host(np.float32([400.0]))
+    W.call("wm_clip_grad_norm_scale_multi", 2, G, ns, total.vp, 2.0)
+    coef = np.float32(2.0) / (np.sqrt(np.float32(400.0)) + np.float32(1e-6))
+    mine = (mine * coef) * coef
+    assert oracle.bit_equal(d.get(), mine)
+    found = C.c_int(-1)
+    inv = np.float32(1.0) / np.float32(4.0)
+    W.call("wm_grad_unscale", 2, G, ns, float(inv), C.byref(found))
+    assert found.value == 0
+    assert oracle.bit_equal(d.get(), (mine * inv) * inv)

@@ -89,6 +89,8 @@ _SIGS = {
     "wm_adamw_step_multi": [C.c_int, _vp, _vp, _vp, _vp, _vp] + [C.c_float] * 7,
     "wm_rmsprop_step_multi": [C.c_int, _vp, _vp, _vp, _vp, _vp] + [C.c_float] * 5,
     "wm_grad_sumsq_multi": [C.c_int, _vp, _vp, _vp],
+    "wm_grad_sumsq_scaled_multi": [C.c_int, _vp, _vp, C.c_float, _vp],
+    "wm_grads_finite_multi": [C.c_int, _vp, _vp, C.POINTER(C.c_int)],
     "wm_clip_grad_norm_scale_multi": [C.c_int, _vp, _vp, _vp, C.c_float],
     "wm_clip_grad_value_multi": [C.c_int, _vp, _vp, C.c_float],
     # include/wm_loss.h

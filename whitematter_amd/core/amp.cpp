@@ -5,6 +5,7 @@
 #include "amp.h"
 
 #include <cmath>
+#include <limits>
 #include <stdexcept>
 #include <string>
 
@@ -18,13 +19,24 @@ void check(int rc, const char* what) {
 }
 
 // The gradients that hold values: a gradient that is empty or known to be
-// all zeros is skipped (scaling zeros leaves zeros, and zeros are finite).
-void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs, std::vector<int64_t>& sizes) {
+// all zeros is skipped (scaling zeros by a finite factor leaves zeros, and
+// zeros are finite).  `write` hands out pointers for in-place updates (the
+// host mirrors go stale), otherwise read-only ones.
+void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs, std::vector<int64_t>& sizes,
+                bool write = true) {
     for (const auto& p : params) {
         if (!p || p->grad.empty() || p->grad.known_zero()) continue;
-        ptrs.push_back(p->grad.dev_rw());
+        ptrs.push_back(write ? p->grad.dev_rw() : const_cast<float*>(p->grad.dev()));
         sizes.push_back((int64_t)p->grad.size());
     }
+}
+
+// Whether any listed parameter has a non-empty gradient (known-zero ones
+// included).
+bool any_grad(const std::vector<TensorPtr>& params) {
+    for (const auto& p : params)
+        if (p && !p->grad.empty()) return true;
+    return false;
 }
 
 }  // namespace
@@ -33,6 +45,13 @@ void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs,
 bool GradScaler::unscale(Optimizer* optimizer) {
     if (!enabled_) return true;
     const float inv_scale = 1.0f / scale_;
+    if (!std::isfinite(inv_scale)) {
+        // Every product is then non-finite, zeros included (0 * inf, x * NaN):
+        // the reference stops at the first element of the first non-empty
+        // gradient, having changed nothing.
+        found_inf_or_nan_ = any_grad(optimizer->params);
+        return !found_inf_or_nan_;
+    }
     std::vector<float*> ptrs;
     std::vector<int64_t> sizes;
     live_grads(optimizer->params, ptrs, sizes);
@@ -59,16 +78,15 @@ TensorPtr HalfTensor::to_float(bool requires_grad) const {
     return result;
 }
 
-// core/amp.h:293-300: every element finite.  The device pass multiplies by
-// 1.0f (exact) up to the first non-finite element and reports whether there
-// is one; the values are unchanged.
+// core/amp.h:293-300: every element finite; a read-only device search.
 bool check_gradients_finite(const std::vector<TensorPtr>& params) {
     std::vector<float*> ptrs;
     std::vector<int64_t> sizes;
-    live_grads(params, ptrs, sizes);
-    int found = 0;
-    check(wm_grad_unscale((int)ptrs.size(), ptrs.data(), sizes.data(), 1.0f, &found), "check_gradients_finite");
-    return found == 0;
+    live_grads(params, ptrs, sizes, false);
+    int all = 1;
+    check(wm_grads_finite_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()), sizes.data(), &all),
+          "check_gradients_finite");
+    return all != 0;
 }
 
 // core/amp.h:303-327: norm of g / scale over all gradients; when
@@ -85,15 +103,19 @@ float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, f
         check(wm_alloc(&d, sizeof(float)), "clip_grad_norm_amp");
         int rc = wm_fill(static_cast<float*>(d), 0.0f, 1);
         if (rc == WM_OK)
-            rc = wm_grad_sumsq_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()), sizes.data(),
-                                     static_cast<float*>(d));
+            rc = wm_grad_sumsq_scaled_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()),
+                                            sizes.data(), inv_scale, static_cast<float*>(d));
         if (rc == WM_OK) rc = wm_d2h(&sumsq, d, sizeof(float));
         wm_free(d);
         check(rc, "clip_grad_norm_amp");
     }
-    // sum of (g * inv_scale)^2 = inv_scale^2 * sum of g^2 (exact for a
-    // power-of-two scale, within the sums contract otherwise)
-    const float total_norm = std::sqrt(sumsq * inv_scale * inv_scale);
+    // Known-zero gradients were skipped; with a non-finite inv_scale their
+    // zeros would add 0 * inf (or 0 * NaN) = NaN to the reference's sum.
+    if (!std::isfinite(inv_scale))
+        for (const auto& p : params)
+            if (p && !p->grad.empty() && p->grad.known_zero()) sumsq = std::numeric_limits<float>::quiet_NaN();
+    // each element scaled before it is squared, as the reference does
+    const float total_norm = std::sqrt(sumsq);
     const float clip_coef = max_norm / (total_norm + 1e-6f);
     if (clip_coef < 1.0f)
         for (size_t k = 0; k < ptrs.size(); ++k)

@@ -368,9 +368,10 @@ __global__ void __launch_bounds__(kBlock) multi_map_kernel(const MultiEntry* __r
     }
 }
 
-// part[c] = sum of squares of chunk c.
+// part[c] = sum of (x * mul)^2 over chunk c (mul = 1 is exact: the plain
+// sum of squares).
 __global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* __restrict__ tab, int count,
-                                                              int64_t chunks, float* __restrict__ part) {
+                                                              int64_t chunks, float mul, float* __restrict__ part) {
     __shared__ float lds[kBlock / 64];
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const MultiEntry e = tab[find_entry(tab, count, c)];
@@ -382,11 +383,15 @@ __global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* _
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
             for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
                 const float4 v = ld_stream(e.p + i);
-                s += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                const float a = v.x * mul, b = v.y * mul, c2 = v.z * mul, d = v.w * mul;
+                s += a * a + b * b + c2 * c2 + d * d;
             }
             tail = end4;
         }
-        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) s += e.p[i] * e.p[i];
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) {
+            const float a = e.p[i] * mul;
+            s += a * a;
+        }
         s = block_sum<kBlock>(s, lds);
         if (threadIdx.x == 0) part[c] = s;
         __syncthreads();
@@ -510,6 +515,59 @@ struct MultiTable {
     unsigned grid() const { return grid_for(chunks, 1, 8); }
 };
 
+// Consecutive runs of list positions in which no array written by one
+// tensor overlaps an array of another (a parameter listed twice, state
+// buffers shared between entries).  Each run is one launch and the runs go
+// in list order, so such a tensor is updated once per listing, one update
+// after the other, as the reference's loop over the list does; read-only
+// arrays (gradients of an update) may overlap each other freely.
+std::vector<std::pair<int, int>> independent_runs(int count, float* const* p, const float* const* g,
+                                                  float* const* s1, float* const* s2, const int64_t* n, int ns) {
+    struct Range {
+        uintptr_t lo, hi;
+        int pos;
+        bool written;
+    };
+    std::vector<Range> r;
+    r.reserve((size_t)count * 4);
+    auto add = [&](const void* a, int k, bool w) {
+        if (a) r.push_back({(uintptr_t)a, (uintptr_t)a + (uintptr_t)n[k] * sizeof(float), k, w});
+    };
+    for (int k = 0; k < count; ++k) {
+        if (n[k] <= 0) continue;
+        add(p[k], k, true);
+        if (g) add(g[k], k, false);
+        if (ns > 0 && s1) add(s1[k], k, true);
+        if (ns > 1 && s2) add(s2[k], k, true);
+    }
+    std::sort(r.begin(), r.end(), [](const Range& a, const Range& b) { return a.lo < b.lo; });
+    // last[j]: the latest earlier list position whose arrays conflict with j's
+    std::vector<int> last(count, -1);
+    std::vector<const Range*> open;
+    for (const Range& x : r) {
+        size_t keep = 0;
+        for (const Range* o : open) {
+            if (o->hi <= x.lo) continue;  // ended before x starts
+            open[keep++] = o;
+            if (o->pos != x.pos && (o->written || x.written)) {
+                const int a = std::min(o->pos, x.pos), b = std::max(o->pos, x.pos);
+                last[b] = std::max(last[b], a);
+            }
+        }
+        open.resize(keep);
+        open.push_back(&x);
+    }
+    std::vector<std::pair<int, int>> runs;
+    int start = 0;
+    for (int j = 1; j < count; ++j)
+        if (last[j] >= start) {
+            runs.emplace_back(start, j);
+            start = j;
+        }
+    runs.emplace_back(start, count);
+    return runs;
+}
+
 template <class U>
 int launch_multi(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
                  const int64_t* n, const U& upd, const char* what) {
@@ -518,12 +576,17 @@ int launch_multi(int count, float* const* p, const float* const* g, float* const
     if (!p || !g || !n || (U::NS > 0 && !s1) || (U::NS > 1 && !s2))
         return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
     WM_CHECK_INIT();
-    MultiTable t;
-    WM_TRY(t.build(count, p, g, s1, s2, n, U::NS, what));
-    if (t.chunks == 0) return WM_OK;
-    launch_kernel(multi_update_kernel<U>, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                       t.chunks, upd);
-    return check_launch(what);
+    for (const auto& run : independent_runs(count, p, g, s1, s2, n, U::NS)) {
+        const int b = run.first;
+        MultiTable t;
+        WM_TRY(t.build(run.second - b, p + b, g + b, s1 ? s1 + b : nullptr, s2 ? s2 + b : nullptr, n + b, U::NS,
+                       what));
+        if (t.chunks == 0) continue;
+        launch_kernel(multi_update_kernel<U>, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                      t.chunks, upd);
+        WM_TRY(check_launch(what));
+    }
+    return WM_OK;
 }
 
 static int check_n(int64_t n, const char* what) {
@@ -634,25 +697,34 @@ int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float 
     for (int k = 0; k < count; ++k)
         if (!gl[k]) nl[k] = 0;  // a missing gradient is skipped like an empty one
     WM_CHECK_INIT();
-    MultiTable t;
-    WM_TRY(t.build(count, gl.data(), nullptr, nullptr, nullptr, nl.data(), 0, "wm_grad_unscale"));
-    if (t.chunks == 0) return WM_OK;
-    // 1. the first non-finite scaled position in parameter order
-    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
-    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
-    launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                       t.chunks, inv_scale, first.as<int64_t>());
-    WM_TRY(check_launch("wm_grad_unscale(find)"));
-    launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                       t.chunks, first.as<int64_t>(), where.as<int64_t>());
-    WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
-    int64_t cut[2] = {0, 0};
-    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
-    // 2. scale everything before it (everything when there is none)
-    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
-                       2, nullptr, inv_scale, (int)cut[0], cut[1]);
-    WM_TRY(check_launch("wm_grad_unscale(scale)"));
-    *found_inf = cut[0] < t.count() ? 1 : 0;
+    // Runs of gradients that do not overlap, in list order: a gradient listed
+    // twice is scaled (and searched) twice, one pass after the other.
+    for (const auto& run : independent_runs(count, gl.data(), nullptr, nullptr, nullptr, nl.data(), 0)) {
+        const int b = run.first;
+        MultiTable t;
+        WM_TRY(t.build(run.second - b, gl.data() + b, nullptr, nullptr, nullptr, nl.data() + b, 0,
+                       "wm_grad_unscale"));
+        if (t.chunks == 0) continue;
+        // 1. the first non-finite scaled position in parameter order
+        Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
+        if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grad_unscale: workspace");
+        launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                      t.chunks, inv_scale, first.as<int64_t>());
+        WM_TRY(check_launch("wm_grad_unscale(find)"));
+        launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                      t.chunks, first.as<int64_t>(), where.as<int64_t>());
+        WM_TRY(check_launch("wm_grad_unscale(find finalize)"));
+        int64_t cut[2] = {0, 0};
+        WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
+        // 2. scale everything before it (everything when there is none)
+        launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                      2, nullptr, inv_scale, (int)cut[0], cut[1]);
+        WM_TRY(check_launch("wm_grad_unscale(scale)"));
+        if (cut[0] < t.count()) {
+            *found_inf = 1;
+            return WM_OK;
+        }
+    }
     return WM_OK;
 }
 
@@ -699,39 +771,76 @@ static int multi_grads(int count, const float* const* g, const int64_t* n, Multi
     return t.build(count, const_cast<float* const*>(g), nullptr, nullptr, nullptr, n, 0, what);
 }
 
-int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, float* total) {
-    if (!total) return set_error(WM_ERR_INVALID, "wm_grad_sumsq_multi: null total");
+static int sumsq_multi(int count, const float* const* g, const int64_t* n, float mul, float* total, const char* what) {
+    if (!total) return set_error(WM_ERR_INVALID, std::string(what) + ": null total");
     MultiTable t;
-    WM_TRY(multi_grads(count, g, n, t, "wm_grad_sumsq_multi"));
+    WM_TRY(multi_grads(count, g, n, t, what));
     if (t.chunks == 0) return wm_fill(total, 0.0f, 1);
     Workspace part((size_t)t.chunks * sizeof(float));
-    if (!part.p) return set_error(WM_ERR_NOMEM, "wm_grad_sumsq_multi: workspace");
-    launch_kernel(multi_sumsq_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                       t.chunks, part.as<float>());
-    WM_TRY(check_launch("wm_grad_sumsq_multi"));
-    launch_kernel(multi_sum_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<float>(), t.chunks,
-                       total, 0);
-    return check_launch("wm_grad_sumsq_multi(finalize)");
+    if (!part.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
+    launch_kernel(multi_sumsq_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks, mul,
+                  part.as<float>());
+    WM_TRY(check_launch(what));
+    launch_kernel(multi_sum_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), part.as<float>(), t.chunks, total, 0);
+    return check_launch(what);
+}
+
+int wm_grad_sumsq_multi(int count, const float* const* g, const int64_t* n, float* total) {
+    return sumsq_multi(count, g, n, 1.0f, total, "wm_grad_sumsq_multi");
+}
+
+int wm_grad_sumsq_scaled_multi(int count, const float* const* g, const int64_t* n, float mul, float* total) {
+    return sumsq_multi(count, g, n, mul, total, "wm_grad_sumsq_scaled_multi");
+}
+
+int wm_grads_finite_multi(int count, const float* const* g, const int64_t* n, int* all_finite) {
+    if (!all_finite) return set_error(WM_ERR_INVALID, "wm_grads_finite_multi: null all_finite");
+    *all_finite = 1;
+    MultiTable t;
+    WM_TRY(multi_grads(count, g, n, t, "wm_grads_finite_multi"));
+    if (t.chunks == 0) return WM_OK;
+    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
+    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grads_finite_multi: workspace");
+    launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                  1.0f, first.as<int64_t>());
+    WM_TRY(check_launch("wm_grads_finite_multi"));
+    launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                  t.chunks, first.as<int64_t>(), where.as<int64_t>());
+    WM_TRY(check_launch("wm_grads_finite_multi(finalize)"));
+    int64_t cut[2] = {0, 0};
+    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
+    *all_finite = cut[0] < t.count() ? 0 : 1;
+    return WM_OK;
+}
+
+// An in-place map over a gradient list, one launch per run of gradients that
+// do not overlap (a gradient listed twice is mapped twice, in list order).
+static int map_grads(int count, float* const* g, const int64_t* n, int mode, const float* total, float arg,
+                     const char* what) {
+    if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
+    if (count > 0 && (!g || !n)) return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
+    if (count == 0) return WM_OK;
+    WM_CHECK_INIT();
+    for (const auto& run : independent_runs(count, g, nullptr, nullptr, nullptr, n, 0)) {
+        const int b = run.first;
+        MultiTable t;
+        WM_TRY(t.build(run.second - b, g + b, nullptr, nullptr, nullptr, n + b, 0, what));
+        if (t.chunks == 0) continue;
+        launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                      mode, total, arg, 0, (int64_t)0);
+        WM_TRY(check_launch(what));
+    }
+    return WM_OK;
 }
 
 int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, const float* total_sumsq,
                                   float max_norm) {
     if (!total_sumsq) return set_error(WM_ERR_INVALID, "wm_clip_grad_norm_scale_multi: null total");
-    MultiTable t;
-    WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_norm_scale_multi"));
-    if (t.chunks == 0) return WM_OK;
-    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
-                       0, total_sumsq, max_norm, 0, (int64_t)0);
-    return check_launch("wm_clip_grad_norm_scale_multi");
+    return map_grads(count, g, n, 0, total_sumsq, max_norm, "wm_clip_grad_norm_scale_multi");
 }
 
 int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float clip_value) {
-    MultiTable t;
-    WM_TRY(multi_grads(count, g, n, t, "wm_clip_grad_value_multi"));
-    if (t.chunks == 0) return WM_OK;
-    launch_kernel(multi_map_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
-                       1, nullptr, clip_value, 0, (int64_t)0);
-    return check_launch("wm_clip_grad_value_multi");
+    return map_grads(count, g, n, 1, nullptr, clip_value, "wm_clip_grad_value_multi");
 }
 
 }  // extern "C"
