@@ -53,12 +53,14 @@ def test_f32_to_f16_branches(wm):
     assert np.array_equal(f32_to_f16_gpu(x), oracle.get("f32").f32_to_f16(x))
 
 
-def run_fused(h16, r16, g, dm, acc=None):
+def run_fused(h16, r16, g, dm, acc=None, lo=None, hi=None):
+    lo = LO if lo is None else lo
+    hi = HI if hi is None else hi
     rows, cols = h16.shape
     dh, dr, dg_, ddm = dev(h16), dev(r16), dev(g), dev(dm)
     out = W.DeviceArray((rows, cols), np.uint16)
     m = W.DeviceArray((rows,))
-    W.call("wm_epilogue_f16_fwd", out.vp, m.vp, dh.vp, dr.vp, dg_.vp, rows, cols, C.c_float(LO), C.c_float(HI))
+    W.call("wm_epilogue_f16_fwd", out.vp, m.vp, dh.vp, dr.vp, dg_.vp, rows, cols, C.c_float(lo), C.c_float(hi))
     if acc is None:
         gh, gr, gg = W.DeviceArray((rows, cols)), W.DeviceArray((rows, cols)), W.DeviceArray((cols,))
         for d in (gh, gr, gg):
@@ -68,7 +70,7 @@ def run_fused(h16, r16, g, dm, acc=None):
         gh, gr, gg = dev(acc[0]), dev(acc[1]), dev(acc[2])
         flags = (1, 1, 1)
     W.call("wm_epilogue_f16_bwd", ddm.vp, dh.vp, dr.vp, dg_.vp, gh.vp, flags[0], gr.vp, flags[1], gg.vp, flags[2],
-           rows, cols, C.c_float(LO), C.c_float(HI))
+           rows, cols, C.c_float(lo), C.c_float(hi))
     return out.to_host(), m.to_host(), gh.to_host(), gr.to_host(), gg.to_host()
 
 
@@ -76,19 +78,21 @@ def tanh_gpu(v):
     return W.unary(W.TANH, dev(v)).to_host()
 
 
-def reference_chain(h16, r16, g, dm):
+def reference_chain(h16, r16, g, dm, lo=None, hi=None):
     """fp32 forward intermediates (exact ops), the GPU's fp32 tanh, and the
     fp64 backward chain of the reference closures."""
+    lo = LO if lo is None else lo
+    hi = HI if hi is None else hi
     o32 = oracle.get("f32")
     h = o32.f16_to_f32(h16)
     r = o32.f16_to_f32(r16)
     t = o32.binary("add", h, r)
     u = o32.binary("mul", t, g)
-    v = o32.unary("clamp", u, LO, HI)
+    v = o32.unary("clamp", u, lo, hi)
     w = tanh_gpu(v)                                  # pinned by test_gpu_unary
     w64 = w.astype(np.float64)
     dv = dm.astype(np.float64)[:, None] * (1.0 - w64 * w64)
-    du = np.where((u > LO) & (u < HI), dv, 0.0)
+    du = np.where((u > lo) & (u < hi), dv, 0.0)
     dt = du * g.astype(np.float64)[None, :]
     dg = (du * t.astype(np.float64)).sum(axis=0)
     dg_scale = np.abs(du * t.astype(np.float64)).sum(axis=0)
@@ -97,9 +101,13 @@ def reference_chain(h16, r16, g, dm):
     return w, mean, mean_scale, dt, dg, dg_scale
 
 
+# (-4, 4): the bounds for which the kernels clamp with the hardware min /
+# max; a zero bound takes the compare-and-select path
+@pytest.mark.parametrize("bounds", [(-4.0, 4.0), (0.0, 4.0), (-1.5, -0.0)], ids=str)
 @pytest.mark.parametrize("shape", [(64, 4096), (37, 1000), (5, 13), (1, 8), (300, 256)])
 @pytest.mark.parametrize("accumulate", [False, True])
-def test_fused_epilogue(wm, shape, accumulate):
+def test_fused_epilogue(wm, shape, accumulate, bounds):
+    lo, hi = bounds
     rows, cols = shape
     h = synth.normal(shape, synth.seed_for(5, 0))
     r = synth.normal(shape, synth.seed_for(5, 1))
@@ -110,8 +118,8 @@ def test_fused_epilogue(wm, shape, accumulate):
     acc = None
     if accumulate:
         acc = (synth.normal(shape, 91), synth.normal(shape, 92), synth.normal((cols,), 93))
-    out16, m, gh, gr, gg = run_fused(h16, r16, g, dm, acc)
-    w, mean, mean_scale, dt, dg, dg_scale = reference_chain(h16, r16, g, dm)
+    out16, m, gh, gr, gg = run_fused(h16, r16, g, dm, acc, lo, hi)
+    w, mean, mean_scale, dt, dg, dg_scale = reference_chain(h16, r16, g, dm, lo, hi)
     # forward: out is the truncating fp16 of the fp32 tanh value, bit for bit
     assert np.array_equal(out16, o32.f32_to_f16(w))
     assert oracle.close_scaled(m, mean, mean_scale, 1e-5)[0]

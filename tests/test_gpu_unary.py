@@ -11,6 +11,7 @@ import pytest
 
 import oracle
 from gpu_helpers import rng_normal, rng_uniform, unary_bwd, unary_fwd
+from whitematter_amd import _lib as W
 
 pytestmark = pytest.mark.gpu
 
@@ -90,3 +91,16 @@ def test_unary_backward_boundaries(wm):
     assert a.tolist() == [0, 0, 1, -1, -1, 1, 1]
     c = unary_bwd("clamp", g, x, unary_fwd("clamp", x, -0.75, 1.25), p0=-0.75, p1=1.25)
     assert c.tolist() == [1, 1, 1, 0, 0, 0, 1]
+
+
+def test_tanh_dense_within_2ulp(wm):
+    """tanh_ (core/tensor.cpp:1307) on every 17th fp32 bit pattern of
+    [-10, 10], both sides of the kernel's switch at |x| = 1 included:
+    within 2 ulp of fp64 tanh everywhere (beyond 10 it is +-1)."""
+    x = np.arange(0, 0x41200001, 17, dtype=np.uint32).view(np.float32)
+    for sign in (np.float32(1), np.float32(-1)):
+        xs = x * sign
+        got = W.unary(W.TANH, W.DeviceArray.from_host(xs)).to_host()
+        u = oracle.ulp_vs_f64(got, np.tanh(xs.astype(np.float64)))
+        assert float(u.max()) <= 2.0, float(xs[int(np.argmax(u))])
+        assert np.array_equal(np.signbit(got), np.signbit(xs))

@@ -33,35 +33,49 @@ struct Chain {
     float t, u, w;
 };
 
+// FC: lo and hi are neither zero nor NaN.  Then the hardware min / max give
+// the reference's clamp bit for bit: fminf(u, hi) is u below hi, hi above
+// it, hi for a NaN u (as (u < hi) ? u : hi is), and a tie returns the same
+// bits either way since hi is not a signed zero; likewise fmaxf(lo, m).
+template <bool FC>
 __device__ __forceinline__ Chain chain(float h, float r, float g, float lo, float hi) {
     Chain c;
     c.t = h + r;
     c.u = c.t * g;
-    float m = (c.u < hi) ? c.u : hi;       // std::min(hi, u)
-    float v = (lo < m) ? m : lo;           // std::max(lo, .)
-    c.w = tanhf(v);
+    float v;
+    if constexpr (FC) {
+        v = fmaxf(lo, fminf(c.u, hi));
+    } else {
+        const float m = (c.u < hi) ? c.u : hi;  // std::min(hi, u)
+        v = (lo < m) ? m : lo;                  // std::max(lo, .)
+    }
+    c.w = tanh_fast(v);
     return c;
 }
 
-// Forward: one workgroup per row; each thread takes 8 consecutive columns per
-// step (16 bytes of each fp16 input).  VEC: cols % 8 == 0 and 16-byte aligned.
-template <bool VEC>
+// Forward: one wave per row.  With 128-bit accesses lane l takes 8
+// consecutive columns at 512 j + 8 l for j = 0, 1, ..., so every load and
+// store instruction of a wave covers 1 KB of one fp16 row; U steps of loads
+// are issued before any is used.  The row mean is a DPP / shuffle wave sum:
+// no barrier anywhere.  VEC: cols % 8 == 0 and 16-byte aligned.
+template <bool VEC, bool FC>
 __global__ void __launch_bounds__(kBlock) epilogue_fwd_kernel(uint16_t* __restrict__ out, float* __restrict__ mean,
                                                                const uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ res,
                                                                const float* __restrict__ g, int64_t rows,
                                                                int64_t cols, float lo, float hi) {
-    __shared__ float lds[kBlock / 64];
-    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    constexpr int U = 4;
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
+    for (int64_t r = wave; r < rows; r += nwaves) {
         const uint16_t* hr = h + r * cols;
         const uint16_t* rr = res + r * cols;
         uint16_t* orow = out ? out + r * cols : nullptr;
         float s = 0.f;
         if constexpr (VEC) {
-#pragma unroll 2
-            for (int64_t c = (int64_t)threadIdx.x * 8; c < cols; c += kBlock * 8) {
-                const float4 hq = ld_stream(reinterpret_cast<const float*>(hr + c));
-                const float4 rq = ld_stream(reinterpret_cast<const float*>(rr + c));
+            // one step: 8 columns at c from each input, 8 outputs
+            auto step = [&](float4 hq, float4 rq, int64_t c) {
                 const float4 g0 = *reinterpret_cast<const float4*>(g + c);
                 const float4 g1 = *reinterpret_cast<const float4*>(g + c + 4);
                 const uint32_t hw[4] = {__float_as_uint(hq.x), __float_as_uint(hq.y), __float_as_uint(hq.z),
@@ -69,28 +83,56 @@ __global__ void __launch_bounds__(kBlock) epilogue_fwd_kernel(uint16_t* __restri
                 const uint32_t rw[4] = {__float_as_uint(rq.x), __float_as_uint(rq.y), __float_as_uint(rq.z),
                                         __float_as_uint(rq.w)};
                 const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+                float wv[8];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    wv[2 * k] = chain<FC>(h2f(hw[k] & 0xFFFFu), h2f(rw[k] & 0xFFFFu), gv[2 * k], lo, hi).w;
+                    wv[2 * k + 1] = chain<FC>(h2f(hw[k] >> 16), h2f(rw[k] >> 16), gv[2 * k + 1], lo, hi).w;
+                }
+                const float t = ((wv[0] + wv[1]) + (wv[2] + wv[3])) + ((wv[4] + wv[5]) + (wv[6] + wv[7]));
+                s += t;
+                // tanh gives [-1, 1] or NaN, and the hardware's packed
+                // truncating conversion is the reference's float_to_half for
+                // every finite |x| < 65536: only a NaN (t is NaN iff some w
+                // is) takes the bit formula
                 uint32_t ow[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    Chain lo_c = chain(h2f(hw[k] & 0xFFFFu), h2f(rw[k] & 0xFFFFu), gv[2 * k], lo, hi);
-                    Chain hi_c = chain(h2f(hw[k] >> 16), h2f(rw[k] >> 16), gv[2 * k + 1], lo, hi);
-                    s += lo_c.w + hi_c.w;
-                    ow[k] = float2_to_half2_bits_rtz(lo_c.w, hi_c.w);
+                    typedef __fp16 wm_h2 __attribute__((ext_vector_type(2)));
+                    ow[k] = __builtin_bit_cast(uint32_t, (wm_h2)__builtin_amdgcn_cvt_pkrtz(wv[2 * k], wv[2 * k + 1]));
+                }
+                if (__builtin_isnan(t)) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) ow[k] = float2_to_half2_bits_rtz(wv[2 * k], wv[2 * k + 1]);
                 }
                 if (orow)
                     st_stream(reinterpret_cast<float*>(orow + c),
                               make_float4(__uint_as_float(ow[0]), __uint_as_float(ow[1]), __uint_as_float(ow[2]),
                                           __uint_as_float(ow[3])));
+            };
+            int64_t c = (int64_t)lane * 8;
+            for (; c + (U - 1) * 512 < cols; c += U * 512) {
+                float4 hq[U], rq[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    hq[u] = ld_stream(reinterpret_cast<const float*>(hr + c + u * 512));
+                    rq[u] = ld_stream(reinterpret_cast<const float*>(rr + c + u * 512));
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) step(hq[u], rq[u], c + u * 512);
             }
+            for (; c < cols; c += 512)
+                step(ld_stream(reinterpret_cast<const float*>(hr + c)), ld_stream(reinterpret_cast<const float*>(rr + c)),
+                     c);
         } else {
-            for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
-                Chain ch = chain(h2f(hr[c]), h2f(rr[c]), g[c], lo, hi);
+            for (int64_t c = lane; c < cols; c += 64) {
+                const Chain ch = chain<FC>(h2f(hr[c]), h2f(rr[c]), g[c], lo, hi);
                 s += ch.w;
                 if (orow) orow[c] = (uint16_t)f2h(ch.w);
             }
         }
-        s = block_sum<kBlock>(s, lds);
-        if (threadIdx.x == 0) mean[r] = s / (float)cols;
+        s = wave_sum(s);
+        if (lane == 0) mean[r] = s / (float)cols;
     }
 }
 
@@ -111,7 +153,7 @@ __device__ __forceinline__ void load_half4(const uint16_t* p, float* out) {
     out[3] = half_bits_to_float(q.y >> 16);
 }
 
-template <bool VEC>
+template <bool VEC, bool FC>
 __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __restrict__ dm,
                                                                const uint16_t* __restrict__ h,
                                                                const uint16_t* __restrict__ res,
@@ -155,7 +197,7 @@ __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __res
         float dt[W];
 #pragma unroll
         for (int j = 0; j < W; ++j) {
-            Chain ch = chain(hv[j], rv[j], gv[j], lo, hi);
+            Chain ch = chain<FC>(hv[j], rv[j], gv[j], lo, hi);
             const float dv = dw * (1.0f - ch.w * ch.w);
             const float du = (ch.u > lo && ch.u < hi) ? dv : 0.0f;
             dt[j] = du * gv[j];
@@ -200,30 +242,43 @@ __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __res
     }
 }
 
-// gg[c] (+)= sum_k part[k, c]: 64 columns per workgroup, 4 waves over k.
-__global__ void __launch_bounds__(kBlock) epilogue_gsum_kernel(const float* __restrict__ part, float* __restrict__ gg,
-                                                                int acc, int64_t K, int64_t C) {
-    __shared__ float lds[4][64];
+// gg[c] (+)= sum_k part[k, c]: 64 columns per workgroup of 16 waves; wave
+// w folds k = w, w + 16, ... (four loads in flight per lane), and the 16
+// wave sums are added in wave order through LDS (a fixed order).
+constexpr int kSumBlock = 1024;
+__global__ void __launch_bounds__(kSumBlock) epilogue_gsum_kernel(const float* __restrict__ part,
+                                                                   float* __restrict__ gg, int acc, int64_t K,
+                                                                   int64_t C) {
+    constexpr int NW = kSumBlock / 64;
+    __shared__ float lds[NW][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     for (int64_t c0 = (int64_t)blockIdx.x * 64; c0 < C; c0 += (int64_t)gridDim.x * 64) {
         const int64_t c = c0 + lane;
         float s[4] = {0.f, 0.f, 0.f, 0.f};
         if (c < C) {
             int64_t k = w;
-            for (; k + 12 < K; k += 16) {
+            for (; k + 3 * NW < K; k += 4 * NW) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) s[j] += part[(k + 4 * j) * C + c];
+                for (int j = 0; j < 4; ++j) s[j] += part[(k + j * NW) * C + c];
             }
-            for (int j = 0; k < K; k += 4, ++j) s[j & 3] += part[k * C + c];
+            for (int j = 0; k < K; k += NW, ++j) s[j & 3] += part[k * C + c];
         }
         lds[w][lane] = (s[0] + s[1]) + (s[2] + s[3]);
         __syncthreads();
         if (w == 0 && c < C) {
-            const float t = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+            float t = lds[0][lane];
+#pragma unroll
+            for (int ww = 1; ww < NW; ++ww) t += lds[ww][lane];
             gg[c] = acc ? gg[c] + t : t;
         }
         __syncthreads();
     }
+}
+
+// The clamp bounds for which the hardware min / max reproduce the
+// reference's compare-and-select clamp (see chain).
+inline bool clamp_is_minmax(float lo, float hi) {
+    return lo != 0.f && hi != 0.f && !std::isnan(lo) && !std::isnan(hi);
 }
 
 }  // namespace wm
@@ -239,13 +294,14 @@ int wm_epilogue_f16_fwd(uint16_t* out, float* mean, const uint16_t* h, const uin
     if (!mean || !h || !res || !g) return set_error(WM_ERR_INVALID, "wm_epilogue_f16_fwd: null pointer");
     WM_CHECK_INIT();
     const bool vec = cols % 8 == 0 && aligned16(h) && aligned16(res) && aligned16(g) && (!out || aligned16(out));
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 16));
-    if (vec)
-        launch_kernel(epilogue_fwd_kernel<true>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
-                           cols, lo, hi);
-    else
-        launch_kernel(epilogue_fwd_kernel<false>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows,
-                           cols, lo, hi);
+    dim3 grid(grid_for(rows, kBlock / 64, 16));
+    const bool fc = clamp_is_minmax(lo, hi);
+#define WM_EPI_FWD(V, F)                                                                                       \
+    launch_kernel(epilogue_fwd_kernel<V, F>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows, cols, lo, \
+                  hi)
+    if (vec) { if (fc) WM_EPI_FWD(true, true); else WM_EPI_FWD(true, false); }
+    else { if (fc) WM_EPI_FWD(false, true); else WM_EPI_FWD(false, false); }
+#undef WM_EPI_FWD
     return check_launch("wm_epilogue_f16_fwd");
 }
 
@@ -265,23 +321,26 @@ int wm_epilogue_f16_bwd(const float* dm, const uint16_t* h, const uint16_t* res,
                      (!gres || aligned16(gres));
     const int64_t W = vec ? 8 : 1;
     const int64_t col_tiles = (cols + kBlock * W - 1) / (kBlock * W);
-    int64_t K = std::min<int64_t>(((int64_t)num_cus() * 8 + col_tiles - 1) / col_tiles, (rows + 15) / 16);
+    // ~2 workgroups per CU: each thread folds its columns' dg partials over
+    // rows / K rows, and the second pass reads K partials per column
+    int64_t K = std::min<int64_t>(((int64_t)num_cus() * 4 + col_tiles - 1) / col_tiles, (rows + 15) / 16);
     K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
     const int64_t rpc = (rows + K - 1) / K;
     K = (rows + rpc - 1) / rpc;
     Workspace ws(gg ? (size_t)(K * cols) * sizeof(float) : 0);
     if (gg && !ws.p) return set_error(WM_ERR_NOMEM, "wm_epilogue_f16_bwd: workspace");
     dim3 grid((unsigned)col_tiles, (unsigned)K);
-    if (vec)
-        launch_kernel(epilogue_bwd_kernel<true>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres,
-                           acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
-    else
-        launch_kernel(epilogue_bwd_kernel<false>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h,
-                           gres, acc_res, ws.as<float>(), rows, cols, rpc, lo, hi);
+    const bool fc = clamp_is_minmax(lo, hi);
+#define WM_EPI_BWD(V, F)                                                                                     \
+    launch_kernel(epilogue_bwd_kernel<V, F>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres, \
+                  acc_res, ws.as<float>(), rows, cols, rpc, lo, hi)
+    if (vec) { if (fc) WM_EPI_BWD(true, true); else WM_EPI_BWD(true, false); }
+    else { if (fc) WM_EPI_BWD(false, true); else WM_EPI_BWD(false, false); }
+#undef WM_EPI_BWD
     WM_TRY(check_launch("wm_epilogue_f16_bwd"));
     if (gg) {
-        launch_kernel(epilogue_gsum_kernel, dim3(grid_for(cols, 64, 8)), dim3(kBlock), 0, stream(),
-                           ws.as<float>(), gg, acc_g, K, cols);
+        launch_kernel(epilogue_gsum_kernel, dim3(grid_for(cols, 64, 8)), dim3(kSumBlock), 0, stream(),
+                      ws.as<float>(), gg, acc_g, K, cols);
         WM_TRY(check_launch("wm_epilogue_f16_bwd(gsum)"));
     }
     return WM_OK;

@@ -163,7 +163,7 @@ template <int OP>
 __device__ __forceinline__ float unary_fwd(float x, float p0, float p1) {
     if constexpr (OP == WM_RELU) return x > 0.0f ? x : 0.0f;            // simd_relu :139-158
     else if constexpr (OP == WM_SIGMOID) return 1.0f / (1.0f + expf(-x)); // :1286
-    else if constexpr (OP == WM_TANH) return tanhf(x);                  // :1307
+    else if constexpr (OP == WM_TANH) return tanh_fast(x);              // :1307
     else if constexpr (OP == WM_LOG)                                    // :1328
         // The +1e-8f is the reference's fp32 add; the log itself is taken in
         // double and rounded once, which keeps it within 1 ulp (logf's
