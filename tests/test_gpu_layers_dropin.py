@@ -108,6 +108,32 @@ def test_dropout_mask_matches_generator_and_rules(wm):
     assert np.all(got[keep] == np.float32(1) / (np.float32(1) - np.float32(p)))
 
 
+# Published SplitMix64 outputs: state 1234567's first five (the Rosetta Code
+# SplitMix64 task) and state 0's first.  Output k of state s is
+# mix(s + k * golden); the mask's element i draws mix(seed + i + golden).
+_SM64_GOLDEN = 0x9E3779B97F4A7C15
+_SM64_KATS = [(1234567, k + 1, v) for k, v in enumerate(
+    [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431, 16408922859458223821])] + \
+    [(0, 1, 0xE220A8397B1DCDAF)]
+
+
+@pytest.mark.parametrize("state,k,value", _SM64_KATS)
+def test_dropout_mask_generator_known_answers(wm, state, k, value):
+    """Element `offset` keeps its value iff u > p with u the top 24 bits of
+    the published output: p = u drops it, p one float below u keeps it."""
+    from whitematter_amd import _lib as W
+    offset = 70001
+    n = offset + 1
+    seed = (state + k * _SM64_GOLDEN - _SM64_GOLDEN - offset) % (1 << 64)
+    u = np.float32((value >> 40) * 2.0 ** -24)
+    below = np.nextafter(u, np.float32(-1))
+    m = W.DeviceArray((n,))
+    W.call("wm_dropout_mask", m.vp, n, W.C.c_float(float(u)), seed)
+    assert m.to_host()[offset] == 0.0
+    W.call("wm_dropout_mask", m.vp, n, W.C.c_float(float(below)), seed)
+    assert m.to_host()[offset] == np.float32(1) / (np.float32(1) - below)
+
+
 def test_dropin_dropout_forward_backward(wm):
     t = T()
     x = rng_normal((32, 64), 12)

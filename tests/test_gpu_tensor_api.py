@@ -199,3 +199,20 @@ def test_matrix_ops_through_the_api(T):
     assert np.array_equal(np.asarray(a.transpose().data).reshape(2, 2), x.T)
     with pytest.raises(ValueError):
         a.matmul(tensor(T, np.ones((3, 2), np.float32)))
+
+
+def test_host_pointer_contract(tmp_path):
+    """The drop-in's host-pointer contract,
+    through the reference's class API in C++: a non-const data() / begin()
+    pointer is valid until the next device operation on the vector."""
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    wm = os.path.join(root, "whitematter_amd")
+    exe = str(tmp_path / "host_pointer_contract")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(wm, "core"), "-I", os.path.join(root, "include"),
+                    os.path.join(root, "tests", "cpp", "host_pointer_contract.cpp"), "-L", wm, "-lwm_tensor",
+                    "-lwm_hip", "-Wl,-rpath," + wm, "-o", exe], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0 and "CONTRACT HOLDS" in r.stdout, r.stdout + r.stderr

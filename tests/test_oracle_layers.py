@@ -298,3 +298,30 @@ def test_attention_softmax_finite_differences():
     idx = list(range(s.size))
     num = fd(lambda z: (o64.attention_softmax(z) * f32(w)).sum(), s, idx, 1e-3)
     assert np.allclose(num, ds.flat[idx], rtol=1e-4, atol=1e-6)
+
+
+# Published SplitMix64 outputs (Vigna's generator): the sequence for state
+# 1234567 (6457827717110365317, ...; the Rosetta Code SplitMix64 task) and
+# the first output for state 0.  Output k of state s is mix(s + k * golden).
+_SM64_GOLDEN = 0x9E3779B97F4A7C15
+_SM64_KATS = [(1234567, k + 1, v) for k, v in enumerate(
+    [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431, 16408922859458223821])] + \
+    [(0, 1, 0xE220A8397B1DCDAF)]
+
+
+@pytest.mark.parametrize("offset", [0, 5, 1000003])
+@pytest.mark.parametrize("state,k,value", _SM64_KATS)
+def test_dropout_mask_generator_known_answers(state, k, value, offset):
+    """The dropout mask draws u = top 24 bits of mix(seed + i + golden) for
+    element i and keeps the element when u > p (core/layer.cpp:59).  Choosing
+    seed so that seed + i + golden is the state of a published output pins
+    the mix and the counter: with p = u the element is dropped (u > u is
+    false), with p one float below u it is kept, so u equals those 24 bits."""
+    o32 = oracle.get("f32")
+    n = offset + 1
+    seed = (state + k * _SM64_GOLDEN - _SM64_GOLDEN - offset) % (1 << 64)
+    u = np.float32((value >> 40) * 2.0 ** -24)
+    drop = o32.dropout_mask(n, u, seed)
+    keep = o32.dropout_mask(n, np.nextafter(u, np.float32(-1)), seed)
+    assert drop[offset] == 0.0
+    assert keep[offset] == np.float32(1.0) / (np.float32(1.0) - np.nextafter(u, np.float32(-1)))
