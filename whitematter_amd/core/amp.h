@@ -9,16 +9,22 @@
 //       inf), fp16 -> fp32 exact.
 //   HalfTensor (:256-286)
 //       the conversion runs on the device (wm_f32_to_f16_rtz /
-//       wm_f16_to_f32, the same formulas), so only the 2-byte halves cross
-//       PCIe; `data` stays a host std::vector<uint16_t> as in the reference.
+//       wm_f16_to_f32, the same formulas) and the halves stay in HBM:
+//       `data` is a wm::HalfVector with std::vector<uint16_t>'s API, whose
+//       host copy is made only when a caller reads it.
 //   GradScaler (:96-204)
-//       unscale() is one multi-tensor device pass (wm_grad_unscale) with the
-//       reference's semantics: gradients are multiplied by 1 / scale in
-//       parameter order up to the first product that is not finite, which
-//       and everything after it stay as they were.
+//       unscale() (wm_grad_unscale) has the reference's semantics:
+//       gradients are multiplied by 1 / scale in parameter order up to the
+//       first product that is not finite, which and everything after it stay
+//       as they were.  On the device that is a read-only search for that
+//       first product, a 16-byte copy of its position to the host, then one
+//       scaling pass over what precedes it.
 //   AmpContext, AutocastGuard (:210-250)   host state, unchanged.
 //   check_gradients_finite, clip_grad_norm_amp (:293-327)
-//       device scans over the gradients (no host copy).
+//       check_gradients_finite is one read-only device search (no
+//       gradient is written); clip_grad_norm_amp is one sum-of-squares pass
+//       over g / scale and, when it clips, one scaling pass.  Only the flag
+//       or the norm crosses to the host.
 #ifndef AMP_H
 #define AMP_H
 
@@ -217,7 +223,7 @@ public:
 // Mixed precision training utilities
 // =============================================================================
 
-// True when every gradient element is finite (a device scan).
+// True when every gradient element is finite (a read-only device search).
 bool check_gradients_finite(const std::vector<TensorPtr>& params);
 
 // Global norm of the gradients divided by `scale`; when max_norm / (norm +
