@@ -1030,21 +1030,26 @@ def run_config(name, args, flush, want_cpu):
 
 
 def copy_calibration(flush):
-    """The 1 GiB streaming copy kernel: the practical read + write ceiling."""
+    """The 1 GiB copy kernels, streaming (the practical read + write ceiling)
+    and cached: GB/s of each.  Under rocprofv3 --pmc their dispatches are the
+    byte counters' calibration (1 GiB read + 1 GiB written each)."""
     n_copy = 1 << 28
     src, dst = W.DeviceArray((n_copy,)), W.DeviceArray((n_copy,))
     src.fill(2.0)
-    ks = []
-    for _ in range(3):
-        flush.fill(1.0)
-        W.call("wm_span_begin")
-        W.call("wm_copy_kernel", dst.vp, src.vp, n_copy)
-        k = W.C.c_float()
-        W.call("wm_span_end", W.C.byref(k), None, None)
-        ks.append(k.value)
+    out = {}
+    for entry in ("wm_copy_kernel", "wm_copy_kernel_cached"):
+        ks = []
+        for _ in range(3):
+            flush.fill(1.0)
+            W.call("wm_span_begin")
+            W.call(entry, dst.vp, src.vp, n_copy)
+            k = W.C.c_float()
+            W.call("wm_span_end", W.C.byref(k), None, None)
+            ks.append(k.value)
+        out[entry] = round(2 * n_copy * F32 / (statistics.median(ks) * 1e-3) / 1e9, 1)
     src.free()
     dst.free()
-    return round(2 * n_copy * F32 / (statistics.median(ks) * 1e-3) / 1e9, 1)
+    return out
 
 
 def main():
@@ -1095,8 +1100,11 @@ def main():
         "roofline": head["roofline"],
         "cpu_baseline": head["cpu_baseline"],
         "ops": head["ops"],
-        "copy_kernel_GBps": copy_calibration(flush),
+        "copy_kernel_GBps": None,
     }
+    copies = copy_calibration(flush)
+    line["copy_kernel_GBps"] = copies["wm_copy_kernel"]
+    line["copy_kernel_cached_GBps"] = copies["wm_copy_kernel_cached"]
     if len(names) > 1:
         line["configs"] = {nm: recs[nm] for nm in names[1:]}
     print(json.dumps(line), flush=True)

@@ -118,8 +118,12 @@ int wm_span_kernel(int i, float* ms);
 /* Device blocks the library's pool has handed out so far (wm_alloc and
    internal workspace); a test of an entry point that allocates nothing. */
 int wm_pool_handouts(int64_t* count);
-/* Plain streaming copy kernel, used to calibrate rocprof byte counters. */
+/* Plain streaming copy kernel (non-temporal loads and stores), used to
+   calibrate rocprof byte counters and as the practical HBM ceiling. */
 int wm_copy_kernel(float* dst, const float* src, int64_t n);
+/* The same copy with ordinary cached loads and stores: calibrates the byte
+   counters for kernels that read through the caches. */
+int wm_copy_kernel_cached(float* dst, const float* src, int64_t n);
 
 /* ---- fill / conversions ------------------------------------------------- */
 

@@ -104,3 +104,15 @@ def test_tanh_dense_within_2ulp(wm):
         u = oracle.ulp_vs_f64(got, np.tanh(xs.astype(np.float64)))
         assert float(u.max()) <= 2.0, float(xs[int(np.argmax(u))])
         assert np.array_equal(np.signbit(got), np.signbit(xs))
+
+
+@pytest.mark.parametrize("entry", ["wm_copy_kernel", "wm_copy_kernel_cached"])
+def test_calibration_copies_are_copies(wm, entry):
+    """The two calibration copy kernels (streaming and cached accesses)
+    copy every element, and refuse a size that is not a multiple of 4."""
+    n = (1 << 20) + 4
+    x = rng_normal((n,), 17)
+    src, dst = W.DeviceArray.from_host(x), W.DeviceArray((n,))
+    W.call(entry, dst.vp, src.vp, n)
+    assert oracle.bit_equal(dst.to_host(), x)
+    assert getattr(W.lib(), entry)(dst.vp, src.vp, n - 1) != 0

@@ -56,6 +56,7 @@ _SIGS = {
     "wm_span_kernel": [C.c_int, C.POINTER(C.c_float)],
     "wm_pool_handouts": [C.POINTER(C.c_int64)],
     "wm_copy_kernel": [_vp, _vp, C.c_int64],
+    "wm_copy_kernel_cached": [_vp, _vp, C.c_int64],
     "wm_fill": [_vp, C.c_float, C.c_int64],
     "wm_f32_to_f16_rtz": [_vp, _vp, C.c_int64],
     "wm_f16_to_f32": [_vp, _vp, C.c_int64],

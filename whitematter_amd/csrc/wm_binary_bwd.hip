@@ -26,6 +26,7 @@ int make_bcast_layout_public(const int64_t* as, int an, const int64_t* bs, int b
                              int64_t* sa, int64_t* sb, int64_t& numel);
 
 constexpr int kBlock = 256;
+constexpr int kSlotsFlat = 1;  // float4s per thread in bwd_flat_kernel
 
 // ---------------------------------------------------------------------------
 // flat: same shape
@@ -41,8 +42,10 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
     const bool need_b = (ga && da_reads_b<OP>()) || (gb && db_reads_b<OP>()) || (gb && db_reads_out<OP>() && !o);
     const bool need_o = gb && db_reads_out<OP>() && o;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    // kSlots float4 per thread per step (kBlock apart), loads first.
-    constexpr int kSlots = 4;
+    // One float4 per thread on a grid that covers the tensor: measured 71 ->
+    // 79 % of the HBM peak against 4 float4s per thread on 32 workgroups
+    // per CU (the loop stays grid-stride for very large tensors).
+    constexpr int kSlots = kSlotsFlat;
     const int64_t stride = (int64_t)gridDim.x * kBlock * kSlots;
     for (int64_t i0 = (int64_t)blockIdx.x * kBlock * kSlots + threadIdx.x; i0 < n4; i0 += stride) {
         float4 vg[kSlots], va[kSlots], vb[kSlots], vo[kSlots], oa[kSlots], ob[kSlots];
@@ -399,7 +402,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
     if (a_full && b_full) {
         if (numel % 4 == 0 && aligned) {
             int64_t n4 = numel / 4;
-            launch_kernel(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock * 4, 32)), dim3(kBlock), 0, st, g, a, b, o,
+            launch_kernel(bwd_flat_kernel<OP>, dim3(grid_for(n4, kBlock * kSlotsFlat, 1 << 12)), dim3(kBlock), 0, st, g, a, b, o,
                                ga, acc_a, gb, acc_b, n4);
             return check_launch("wm_binary_bwd(flat)");
         }

@@ -15,15 +15,23 @@
 namespace wm {
 
 constexpr int kBlock = 256;   // 4 waves
-constexpr int kUnroll = 4;    // float4 loads in flight per thread per step
+// Streaming kernels give each thread one float4 per operand and launch a
+// grid that covers the whole tensor (kWholeGrid: the loops are still
+// grid-stride, for tensors beyond a million workgroups).  On MI355X that
+// measured 4-8 points of the HBM peak faster than a grid of 32 workgroups
+// per CU looping over 4 float4s per thread (c2 A+r forward 72 -> 78 %, a
+// same-shape backward 71 -> 79 %): short-lived workgroups keep the chip's
+// accesses inside a narrow, advancing window of the tensor.
+constexpr int kUnroll = 1;
+constexpr int kWholeGrid = 1 << 12;  // grid_for cap, in workgroups per CU
 
 // pow's forward evaluates ~40 vector instructions per element with 16
-// doubles live per float4, so it keeps half as many float4s per thread: at
-// kUnroll it needs ~150 VGPRs (3 waves per SIMD), which leaves too few
-// waves to cover the loads.
-// With that, asking for 6 workgroups of kBlock threads per CU (6 waves per
-// SIMD) caps it at 80 VGPRs, which pow(x, scalar) and pow with one exponent
-// per row meet without spills (two tensor operands would spill).
+// doubles live per float4; it is issue-bound rather than latency-bound, and
+// keeps 2 float4s per thread on a grid of 32 workgroups per CU, which
+// measured faster for it than the whole-tensor grid.  Asking for 6
+// workgroups of kBlock threads per CU (6 waves per SIMD) caps it at 80
+// VGPRs, which pow(x, scalar) and pow with one exponent per row meet without
+// spills (two tensor operands would spill).
 template <int OP>
 constexpr int fwd_unroll() {
     return OP == WM_POW || OP == WM_POWS ? 2 : kUnroll;
@@ -31,6 +39,10 @@ constexpr int fwd_unroll() {
 template <int OP>
 constexpr int fwd_min_blocks() {
     return OP == WM_POW || OP == WM_POWS ? 6 : 1;
+}
+template <int OP>
+constexpr int fwd_grid_cap() {
+    return OP == WM_POW || OP == WM_POWS ? 32 : kWholeGrid;
 }
 
 // ---------------------------------------------------------------------------
@@ -152,6 +164,10 @@ __global__ void __launch_bounds__(kBlock) fill_scalar_kernel(float* __restrict__
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) out[i] = v;
 }
 
+// NT: non-temporal loads and stores (the streaming form every hot kernel
+// uses); otherwise ordinary cached ones.  Both move the same bytes, so their
+// counter readings calibrate each kind of access.
+template <bool NT>
 __global__ void __launch_bounds__(kBlock) copy_vec_kernel(float* __restrict__ dst, const float* __restrict__ src,
                                                            int64_t n4) {
     const int64_t stride = (int64_t)gridDim.x * kBlock * kUnroll;
@@ -160,12 +176,17 @@ __global__ void __launch_bounds__(kBlock) copy_vec_kernel(float* __restrict__ ds
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) v[u] = ld_stream(src + 4 * i);
+            if (i < n4) v[u] = NT ? ld_stream(src + 4 * i) : *reinterpret_cast<const float4*>(src + 4 * i);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             int64_t i = base + (int64_t)u * kBlock;
-            if (i < n4) st_stream(dst + 4 * i, v[u]);
+            if (i < n4) {
+                if (NT)
+                    st_stream(dst + 4 * i, v[u]);
+                else
+                    *reinterpret_cast<float4*>(dst + 4 * i) = v[u];
+            }
         }
     }
 }
@@ -225,7 +246,7 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
 }
 
 // Broadcast binary op over [rows, inner]: each tile is one row segment of
-// kBlock*4*kUnroll elements; the row's operand offsets come from the outer
+// kBlock*4*fwd_unroll elements; the row's operand offsets come from the outer
 // dims once per tile.  AI/BI: stride of a/b along inner (1 = contiguous,
 // 0 = one value per row).  VEC: inner % 4 == 0 and 16-byte aligned bases.
 // SA/SB: the operand is streamed (read once: it has a row stride), else it
@@ -413,7 +434,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     // Same shape (or both fully contiguous after folding): flat float4 walk.
     if (nd == 1 && ia == 1 && ib == 1 && (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         int64_t n4 = inner / 4;
-        launch_kernel(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
+        launch_kernel(binary_flat_kernel<OP>, dim3(grid_for(n4, kBlock * fwd_unroll<OP>(), fwd_grid_cap<OP>())), dim3(kBlock), 0, s,
                            out, a, b, n4);
         return check_launch("wm_binary(flat)");
     }
@@ -429,7 +450,7 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
         int64_t tile = (vec ? 4 : 1) * kBlock * fwd_unroll<OP>();
         int64_t tiles = rows * ((inner + tile - 1) / tile);
-        dim3 grid(grid_for(tiles, 1, 32));
+        dim3 grid(grid_for(tiles, 1, fwd_grid_cap<OP>()));
         // An operand with a row stride is read once; a row vector is re-read by every row.
         int stream_a = 0, stream_b = 0;
         for (int i = 0; i < nd - 1; ++i) {
@@ -466,7 +487,7 @@ template <int OP>
 int launch_unary(float* out, const float* x, int64_t n, float p0, float p1) {
     hipStream_t s = stream();
     if (aligned16(out) && aligned16(x)) {
-        launch_kernel(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * fwd_unroll<OP>(), 32)), dim3(kBlock), 0, s,
+        launch_kernel(unary_fwd_kernel<OP>, dim3(grid_for(n / 4 + 1, kBlock * fwd_unroll<OP>(), fwd_grid_cap<OP>())), dim3(kBlock), 0, s,
                            out, x, n, p0, p1);
     } else {
         launch_kernel(unary_fwd_scalar_kernel<OP>, dim3(grid_for(n, kBlock)), dim3(kBlock), 0, s, out, x, n,
@@ -484,7 +505,7 @@ int launch_unary_bwd(const float* g, const float* x, const float* o, float* gx, 
     if (RX && !x) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward input x");
     if (RO && !o) return set_error(WM_ERR_INVALID, "wm_unary_bwd: this op needs the forward output");
     bool vec = aligned16(g) && aligned16(gx) && (!RX || aligned16(x)) && (!RO || aligned16(o));
-    dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll, 32)), grid_s(grid_for(n, kBlock));
+    dim3 grid_v(grid_for(n / 4 + 1, kBlock * kUnroll, kWholeGrid)), grid_s(grid_for(n, kBlock));
     if (vec) {
         if (acc) launch_kernel((unary_bwd_kernel<OP, true>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
         else launch_kernel((unary_bwd_kernel<OP, false>), grid_v, dim3(kBlock), 0, s, g, x, o, gx, n, p0, p1);
@@ -513,6 +534,21 @@ int64_t shape_numel(const int64_t* shape, int nd) {
 
 using namespace wm;
 
+namespace {
+template <bool NT>
+int copy_entry(float* dst, const float* src, int64_t n, const char* what) {
+    if (n < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
+    if (n == 0) return WM_OK;
+    if (!dst || !src) return set_error(WM_ERR_INVALID, std::string(what) + ": null pointer");
+    if (n % 4 || !aligned16(dst) || !aligned16(src))
+        return set_error(WM_ERR_INVALID, std::string(what) + ": needs 16-byte aligned buffers and n % 4 == 0");
+    WM_CHECK_INIT();
+    launch_kernel(copy_vec_kernel<NT>, dim3(grid_for(n / 4, kBlock * kUnroll, kWholeGrid)), dim3(kBlock), 0, stream(), dst,
+                  src, n / 4);
+    return check_launch(what);
+}
+}  // namespace
+
 extern "C" {
 
 int wm_fill(float* out, float value, int64_t n) {
@@ -529,16 +565,10 @@ int wm_fill(float* out, float value, int64_t n) {
     return check_launch("wm_fill");
 }
 
-int wm_copy_kernel(float* dst, const float* src, int64_t n) {
-    if (n < 0) return set_error(WM_ERR_INVALID, "wm_copy_kernel: negative size");
-    if (n == 0) return WM_OK;
-    if (!dst || !src) return set_error(WM_ERR_INVALID, "wm_copy_kernel: null pointer");
-    if (n % 4 || !aligned16(dst) || !aligned16(src))
-        return set_error(WM_ERR_INVALID, "wm_copy_kernel: needs 16-byte aligned buffers and n % 4 == 0");
-    WM_CHECK_INIT();
-    launch_kernel(copy_vec_kernel, dim3(grid_for(n / 4, kBlock * kUnroll, 32)), dim3(kBlock), 0, stream(), dst,
-                       src, n / 4);
-    return check_launch("wm_copy_kernel");
+int wm_copy_kernel(float* dst, const float* src, int64_t n) { return copy_entry<true>(dst, src, n, "wm_copy_kernel"); }
+
+int wm_copy_kernel_cached(float* dst, const float* src, int64_t n) {
+    return copy_entry<false>(dst, src, n, "wm_copy_kernel_cached");
 }
 
 int wm_f32_to_f16_rtz(uint16_t* out, const float* x, int64_t n) {
@@ -548,7 +578,7 @@ int wm_f32_to_f16_rtz(uint16_t* out, const float* x, int64_t n) {
     if (!aligned16(x) || ((uintptr_t)out & 7u))
         return set_error(WM_ERR_INVALID, "wm_f32_to_f16_rtz: x must be 16-byte and out 8-byte aligned");
     WM_CHECK_INIT();
-    launch_kernel(f32_to_f16_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    launch_kernel(f32_to_f16_kernel, dim3(grid_for(n / 4 + 1, kBlock, kWholeGrid)), dim3(kBlock), 0, stream(), out, x, n);
     return check_launch("wm_f32_to_f16_rtz");
 }
 
@@ -559,7 +589,7 @@ int wm_f16_to_f32(float* out, const uint16_t* x, int64_t n) {
     if (!aligned16(out) || ((uintptr_t)x & 7u))
         return set_error(WM_ERR_INVALID, "wm_f16_to_f32: out must be 16-byte and x 8-byte aligned");
     WM_CHECK_INIT();
-    launch_kernel(f16_to_f32_kernel, dim3(grid_for(n / 4 + 1, kBlock)), dim3(kBlock), 0, stream(), out, x, n);
+    launch_kernel(f16_to_f32_kernel, dim3(grid_for(n / 4 + 1, kBlock, kWholeGrid)), dim3(kBlock), 0, stream(), out, x, n);
     return check_launch("wm_f16_to_f32");
 }
 
