@@ -88,18 +88,21 @@ __global__ void __launch_bounds__(kBlock) bwd_flat_kernel(const float* __restric
 // colsum: F full [R,C], V row vector [1,C]; C % 4 == 0, 16-byte aligned
 // ---------------------------------------------------------------------------
 
-// One thread owns 4 adjacent columns of one column tile and walks the rows of
-// one row chunk.  VB: the vector operand is b (else a).
+// One thread owns 4 adjacent columns of one column tile.  Row group k
+// (blockIdx.y, of K = gridDim.y) takes rows k, k + K, k + 2K, ...: at any
+// moment the resident workgroups read a narrow band of adjacent rows that
+// advances down the matrix, which measured 4-5 points of the HBM peak faster
+// than giving each group a contiguous block of R/K rows (every group then
+// reads its own distant row).  The partial of group k is a sum in a fixed
+// order, so results stay deterministic.  VB: the vector operand is b (else a).
 template <int OP, bool VB>
 __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restrict__ g, const float* __restrict__ F,
                                                              const float* __restrict__ V, const float* __restrict__ o,
                                                              float* __restrict__ gF, int accF, float* __restrict__ part,
-                                                             int64_t R, int64_t C, int64_t rows_per_chunk) {
+                                                             int64_t R, int64_t C) {
     binary_prologue<OP>();
     const int64_t c = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 4;
     if (c >= C) return;
-    const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
-    const int64_t r1 = min(R, r0 + rows_per_chunk);
     const bool want_v = part != nullptr;
     // Which tensors the contributions read.
     const bool gF_reads_F = VB ? da_reads_a<OP>() : db_reads_b<OP>();
@@ -113,11 +116,29 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
     const float4 vv = need_V ? *reinterpret_cast<const float4*>(V + c) : z;
     float4 s = z;
-    // One row per iteration: walking rows 32 KiB apart, several rows' loads in
-    // flight per thread measured slower than one (more workgroups carry the
-    // memory-level parallelism instead).
+    // a / b with b the row vector: each column's divisor is fixed, so the
+    // gradients multiply by its reciprocal (g / b -> g * q, g a / b^2 ->
+    // g a q q; a few ulp, within the gradients' 1e-5) instead of dividing twice per
+    // element, when |b| is in [2^-62, 2^62], where neither q nor q * q can
+    // overflow or underflow.  Other divisors (zero, infinite, NaN, tiny,
+    // huge) keep the divisions.
+    float q[4] = {0.f, 0.f, 0.f, 0.f};
+    bool rcp = false;
+    if constexpr (OP == WM_DIV && VB) {
+        const float bv4[4] = {vv.x, vv.y, vv.z, vv.w};
+        rcp = true;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float m = fabsf(bv4[j]);
+            rcp = rcp && m >= 0x1p-62f && m <= 0x1p62f;
+            q[j] = 1.0f / bv4[j];
+        }
+    }
+    // One row per iteration (several rows' loads in flight per thread
+    // measured slower than one; more workgroups carry the memory-level
+    // parallelism instead).
 #pragma unroll 1
-    for (int64_t r = r0; r < r1; ++r) {
+    for (int64_t r = blockIdx.y; r < R; r += gridDim.y) {
         const int64_t off = r * C + c;
         float4 vg = ld_stream(g + off);
         float4 vf = need_F ? ld_stream(F + off) : z;
@@ -127,8 +148,16 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
         const float eg[4] = {vg.x, vg.y, vg.z, vg.w}, ea[4] = {av.x, av.y, av.z, av.w},
                     eb[4] = {bv.x, bv.y, bv.z, bv.w}, eo[4] = {vo.x, vo.y, vo.z, vo.w};
         float da[4], db[4];
-        binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, VB ? gF != nullptr : want_v, VB ? want_v : gF != nullptr, da,
-                              db);
+        if (OP == WM_DIV && VB && rcp) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                da[j] = eg[j] * q[j];
+                db[j] = -((eg[j] * ea[j]) * q[j] * q[j]);
+            }
+        } else {
+            binary_grads_n<OP, 4>(eg, ea, eb, eo, need_o, VB ? gF != nullptr : want_v, VB ? want_v : gF != nullptr,
+                                  da, db);
+        }
         const float* dF = VB ? da : db;
         const float* dV = VB ? db : da;
         if (gF) {
@@ -423,19 +452,18 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
         const bool colvec = (nd == 2 && sv[0] == 1 && sv[1] == 0) || (nd == 1 && sv[0] == 0);
         if (rowvec && C % 4 == 0 && aligned) {
             const int64_t col_tiles = (C + kBlock * 4 - 1) / (kBlock * 4);
+            // ~1024 workgroups (4 per CU), each group of at least 16 rows
             int64_t K = std::min<int64_t>((1024 + col_tiles - 1) / col_tiles, (R + 15) / 16);
             K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
-            const int64_t rpc = (R + K - 1) / K;
-            K = (R + rpc - 1) / rpc;
             Workspace ws(gV ? (size_t)(K * C) * sizeof(float) : 0);
             if (gV && !ws.p) return set_error(WM_ERR_NOMEM, "wm_binary_bwd: workspace");
             dim3 grid((unsigned)col_tiles, (unsigned)K);
             if (vb)
                 launch_kernel((bwd_colsum_kernel<OP, true>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
-                                   ws.as<float>(), R, C, rpc);
+                                   ws.as<float>(), R, C);
             else
                 launch_kernel((bwd_colsum_kernel<OP, false>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF,
-                                   ws.as<float>(), R, C, rpc);
+                                   ws.as<float>(), R, C);
             WM_TRY(check_launch("wm_binary_bwd(colsum)"));
             if (gV) {
                 launch_kernel(colsum_finalize_kernel, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st,
