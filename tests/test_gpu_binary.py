@@ -33,6 +33,12 @@ SHAPES = [
     ((5, 7, 64), (7, 1)),            # middle-dim broadcast
     ((8, 2048), (8, 2048)),
     ((5, 70000), (5, 1)),            # column vector, few long rows: split into chunks
+    ((40, 1024), (40, 1)),           # column vector, one workgroup per row (256 threads)
+    ((24, 2052), (24, 1)),           # ... 512 threads, the last float4s idle
+    ((16, 4096), (16, 1)),
+    ((8, 6000), (8, 1)),             # ... 1024 threads
+    ((40, 1), (40, 2048)),           # column vector on the left
+    ((8, 8196), (8, 1)),             # beyond one workgroup's row: the wave kernel
     ((0, 16), (16,)),                # empty
 ]
 
@@ -137,3 +143,33 @@ def test_pow_nan_grad_positions(wm):
     ra, rc = oracle.get("f64").binary_bwd("pow", G, A, c, out)
     assert np.array_equal(np.isnan(ga), np.isnan(ra))
     assert np.array_equal(np.isnan(gc), np.isnan(rc))
+
+
+def test_div_row_vector_special_divisors(wm):
+    """a / b with b a row vector: columns whose divisor is zero, infinite,
+    NaN, subnormal or outside [2^-62, 2^62] take the divisions, the others
+    one reciprocal per column; both match the reference's fp32 expressions
+    (g / b, -(g a / (b b))) to the gradient tolerance, with the same NaN and
+    infinity positions."""
+    cols = 1024
+    a = rng_normal((96, cols), 41)
+    b = rng_uniform((1, cols), 42, 0.5, 2.0)
+    special = [0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 1e-30, -1e30, 2.0 ** -62, 2.0 ** -63,
+               2.0 ** 62, 2.0 ** 63, -(2.0 ** -62) * 1.5, 3.0e18]
+    for i, v in enumerate(special):
+        col = 7 + 61 * i
+        b[0, col] = np.float32(v)
+        if 0 < abs(v) < 1e-18:
+            # keep g a / b^2 far below the float range, so that no column sum
+            # of finite terms overflows (where that happens depends on the
+            # summation order, which differs from the reference's)
+            a[:, col] *= np.float32(1e-25)
+    out = binary_fwd("div", a, b)
+    g = rng_normal(out.shape, 43)
+    ga, gb = binary_bwd("div", g, a, b, out)
+    ra, rb = oracle.get("f32").binary_bwd("div", g, a, b, out)
+    sa_, sb_ = oracle.get("abs").binary_bwd("div", g, a, b, out)
+    ok_a, wa = oracle.close_scaled(ga, ra, np.abs(sa_), RTOL)
+    ok_b, wb = oracle.close_scaled(gb, rb, np.abs(sb_), RTOL)
+    assert ok_a, f"grad a off by {wa:.3g}x tolerance"
+    assert ok_b, f"grad b off by {wb:.3g}x tolerance"
