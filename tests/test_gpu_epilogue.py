@@ -104,7 +104,7 @@ def reference_chain(h16, r16, g, dm, lo=None, hi=None):
 # (-4, 4): the bounds for which the kernels clamp with the hardware min /
 # max; a zero bound takes the compare-and-select path
 @pytest.mark.parametrize("bounds", [(-4.0, 4.0), (0.0, 4.0), (-1.5, -0.0)], ids=str)
-@pytest.mark.parametrize("shape", [(64, 4096), (37, 1000), (5, 13), (1, 8), (300, 256)])
+@pytest.mark.parametrize("shape", [(64, 4096), (37, 1000), (5, 13), (1, 8), (300, 256), (40, 1024), (24, 2056), (9, 6144), (6, 8200)])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_fused_epilogue(wm, shape, accumulate, bounds):
     lo, hi = bounds

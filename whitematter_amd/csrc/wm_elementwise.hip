@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
                                : make_float4(sb0, sb0, sb0, sb0);
                 }
             }
-            binary_fwd_v<OP, U>(vr, va, vb);
+            if constexpr (OP == WM_POW && BI == 0) pow_fwd_v_exp<U>(vr, va, sb0);  // one exponent per row
+            else binary_fwd_v<OP, U>(vr, va, vb);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;

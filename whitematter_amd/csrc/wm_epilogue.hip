@@ -136,13 +136,80 @@ __global__ void __launch_bounds__(kBlock) epilogue_fwd_kernel(uint16_t* __restri
     }
 }
 
-// Backward: a workgroup owns 8*kBlock adjacent columns and a chunk of rows.
-// With 128-bit accesses lane i of wave w handles the two 4-column groups at
-// tile + 512 w + 4 i and 256 columns further on, so every load and store
-// instruction of a wave covers one contiguous span (512 B of fp16 input, 1 KB
-// of fp32 gradient).  Each thread keeps its 8 column partials of dg in
-// registers over the chunk's rows (fixed order) and writes them to
-// part[chunk, col] for a fixed-order second pass.
+// Forward for rows of 1024 to 8192 columns (VEC): one workgroup of NT
+// threads per row, thread t taking the 8 columns at 8 (u NT + t) for u < S.
+// All of a row's loads are issued before any math and the row mean is one
+// fixed-order block sum.  A short-lived workgroup reading one contiguous row
+// measured 67.8 -> 73.1 % of the HBM peak against a wave walking each row
+// (config 5, [32768, 4096], 256 threads x 2 steps).
+template <int NT, int S, bool FC>
+__global__ void __launch_bounds__(NT) epilogue_fwd_wg_kernel(uint16_t* __restrict__ out, float* __restrict__ mean,
+                                                              const uint16_t* __restrict__ h,
+                                                              const uint16_t* __restrict__ res,
+                                                              const float* __restrict__ g, int64_t rows,
+                                                              int64_t cols, float lo, float hi) {
+    __shared__ float lds[NT / 64];
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint16_t* hr = h + r * cols;
+        const uint16_t* rr = res + r * cols;
+        uint16_t* orow = out ? out + r * cols : nullptr;
+        float4 hq[S], rq[S];
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int64_t c = ((int64_t)u * NT + threadIdx.x) * 8;
+            hq[u] = c < cols ? ld_stream(reinterpret_cast<const float*>(hr + c)) : make_float4(0.f, 0.f, 0.f, 0.f);
+            rq[u] = c < cols ? ld_stream(reinterpret_cast<const float*>(rr + c)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float s = 0.f;
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int64_t c = ((int64_t)u * NT + threadIdx.x) * 8;
+            if (c >= cols) continue;
+            const float4 g0 = *reinterpret_cast<const float4*>(g + c);
+            const float4 g1 = *reinterpret_cast<const float4*>(g + c + 4);
+            const uint32_t hw[4] = {__float_as_uint(hq[u].x), __float_as_uint(hq[u].y), __float_as_uint(hq[u].z),
+                                    __float_as_uint(hq[u].w)};
+            const uint32_t rw[4] = {__float_as_uint(rq[u].x), __float_as_uint(rq[u].y), __float_as_uint(rq[u].z),
+                                    __float_as_uint(rq[u].w)};
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            float wv[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                wv[2 * k] = chain<FC>(h2f(hw[k] & 0xFFFFu), h2f(rw[k] & 0xFFFFu), gv[2 * k], lo, hi).w;
+                wv[2 * k + 1] = chain<FC>(h2f(hw[k] >> 16), h2f(rw[k] >> 16), gv[2 * k + 1], lo, hi).w;
+            }
+            const float t = ((wv[0] + wv[1]) + (wv[2] + wv[3])) + ((wv[4] + wv[5]) + (wv[6] + wv[7]));
+            s += t;
+            uint32_t ow[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                typedef __fp16 wm_h2 __attribute__((ext_vector_type(2)));
+                ow[k] = __builtin_bit_cast(uint32_t, (wm_h2)__builtin_amdgcn_cvt_pkrtz(wv[2 * k], wv[2 * k + 1]));
+            }
+            if (__builtin_isnan(t)) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ow[k] = float2_to_half2_bits_rtz(wv[2 * k], wv[2 * k + 1]);
+            }
+            if (orow)
+                st_stream(reinterpret_cast<float*>(orow + c),
+                          make_float4(__uint_as_float(ow[0]), __uint_as_float(ow[1]), __uint_as_float(ow[2]),
+                                      __uint_as_float(ow[3])));
+        }
+        s = block_sum<NT>(s, lds);
+        if (threadIdx.x == 0) mean[r] = s / (float)cols;
+    }
+}
+
+// Backward: a workgroup owns 8*kBlock adjacent columns and row group k
+// (blockIdx.y of K = gridDim.y), the rows k, k + K, k + 2K, ...: the resident
+// workgroups then read one narrow band of rows that advances down the
+// matrix (67.6 -> 73.4 % of the HBM peak at config 5 against contiguous
+// blocks of rows / K rows).  With 128-bit accesses lane i of wave w handles
+// the two 4-column groups at tile + 512 w + 4 i and 256 columns further on,
+// so every load and store instruction of a wave covers one contiguous span
+// (512 B of fp16 input, 1 KB of fp32 gradient).  Each thread keeps its 8
+// column partials of dg in registers over its rows (fixed order) and writes
+// them to part[k, col] for a fixed-order second pass.
 typedef unsigned int wm_v2u __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void load_half4(const uint16_t* p, float* out) {
@@ -160,7 +227,7 @@ __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __res
                                                                const float* __restrict__ g, float* __restrict__ gh,
                                                                int acc_h, float* __restrict__ gres, int acc_res,
                                                                float* __restrict__ part, int64_t rows, int64_t cols,
-                                                               int64_t rows_per_chunk, float lo, float hi) {
+                                                               float lo, float hi) {
     constexpr int W = VEC ? 8 : 1;
     int64_t cg[2];  // first column of each 4-column group (VEC), or the one column
     if constexpr (VEC) {
@@ -172,8 +239,6 @@ __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __res
         cg[0] = (int64_t)blockIdx.x * kBlock + threadIdx.x;
         if (cg[0] >= cols) return;
     }
-    const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
-    const int64_t r1 = min(rows, r0 + rows_per_chunk);
     float gv[W], acc[W];
 #pragma unroll
     for (int j = 0; j < W; ++j) {
@@ -181,7 +246,7 @@ __global__ void __launch_bounds__(kBlock) epilogue_bwd_kernel(const float* __res
         acc[j] = 0.f;
     }
 #pragma unroll 2
-    for (int64_t r = r0; r < r1; ++r) {
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
         const float dw = dm[r];
         const int64_t roff = r * cols;
         float hv[W], rv[W];
@@ -299,6 +364,17 @@ int wm_epilogue_f16_fwd(uint16_t* out, float* mean, const uint16_t* h, const uin
 #define WM_EPI_FWD(V, F)                                                                                       \
     launch_kernel(epilogue_fwd_kernel<V, F>, grid, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows, cols, lo, \
                   hi)
+    if (vec && cols >= 1024 && cols <= 8192) {
+        const dim3 g1(grid_for(rows, 1, 1 << 12));
+#define WM_EPI_WG(S, F)                                                                                       \
+    launch_kernel(epilogue_fwd_wg_kernel<kBlock, S, F>, g1, dim3(kBlock), 0, stream(), out, mean, h, res, g, rows, \
+                  cols, lo, hi)
+        if (cols <= 2048) { if (fc) WM_EPI_WG(1, true); else WM_EPI_WG(1, false); }
+        else if (cols <= 4096) { if (fc) WM_EPI_WG(2, true); else WM_EPI_WG(2, false); }
+        else { if (fc) WM_EPI_WG(4, true); else WM_EPI_WG(4, false); }
+#undef WM_EPI_WG
+        return check_launch("wm_epilogue_f16_fwd");
+    }
     if (vec) { if (fc) WM_EPI_FWD(true, true); else WM_EPI_FWD(true, false); }
     else { if (fc) WM_EPI_FWD(false, true); else WM_EPI_FWD(false, false); }
 #undef WM_EPI_FWD
@@ -321,19 +397,18 @@ int wm_epilogue_f16_bwd(const float* dm, const uint16_t* h, const uint16_t* res,
                      (!gres || aligned16(gres));
     const int64_t W = vec ? 8 : 1;
     const int64_t col_tiles = (cols + kBlock * W - 1) / (kBlock * W);
-    // ~2 workgroups per CU: each thread folds its columns' dg partials over
-    // rows / K rows, and the second pass reads K partials per column
+    // ~4 workgroups per CU, each row group of at least 16 rows: each thread
+    // folds its columns' dg partials over rows / K rows, and the second pass
+    // reads K partials per column
     int64_t K = std::min<int64_t>(((int64_t)num_cus() * 4 + col_tiles - 1) / col_tiles, (rows + 15) / 16);
     K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
-    const int64_t rpc = (rows + K - 1) / K;
-    K = (rows + rpc - 1) / rpc;
     Workspace ws(gg ? (size_t)(K * cols) * sizeof(float) : 0);
     if (gg && !ws.p) return set_error(WM_ERR_NOMEM, "wm_epilogue_f16_bwd: workspace");
     dim3 grid((unsigned)col_tiles, (unsigned)K);
     const bool fc = clamp_is_minmax(lo, hi);
 #define WM_EPI_BWD(V, F)                                                                                     \
     launch_kernel(epilogue_bwd_kernel<V, F>, grid, dim3(kBlock), 0, stream(), dm, h, res, g, gh, acc_h, gres, \
-                  acc_res, ws.as<float>(), rows, cols, rpc, lo, hi)
+                  acc_res, ws.as<float>(), rows, cols, lo, hi)
     if (vec) { if (fc) WM_EPI_BWD(true, true); else WM_EPI_BWD(true, false); }
     else { if (fc) WM_EPI_BWD(false, true); else WM_EPI_BWD(false, false); }
 #undef WM_EPI_BWD

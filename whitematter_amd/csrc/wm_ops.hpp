@@ -209,14 +209,37 @@ template <int OP> constexpr bool unary_bwd_reads_out() {
     return OP == WM_SIGMOID || OP == WM_TANH || OP == WM_EXP || OP == WM_SQRT;
 }
 
-// unary_fwd over U float4s; pow(x, p0) as in binary_fwd_v.
+// pow over U float4s that share one exponent y (a per-row or scalar
+// exponent): the exponent's part of the table path and of the special-operand
+// test is computed once (pow_exponent), the rest as in binary_fwd_v; equal
+// to binary_fwd_v with b = y everywhere, bit for bit.
+template <int U>
+__device__ __forceinline__ void pow_fwd_v_exp(float4 (&r)[U], const float4 (&a)[U], float y) {
+    const PowExponent e = pow_exponent(y);
+    bool fix = false;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        r[u] = make_float4(pow_table_exp(a[u].x, e), pow_table_exp(a[u].y, e), pow_table_exp(a[u].z, e),
+                           pow_table_exp(a[u].w, e));
+        fix |= pow_needs_fix_exp(a[u].x, e) || pow_needs_fix_exp(a[u].y, e) || pow_needs_fix_exp(a[u].z, e) ||
+               pow_needs_fix_exp(a[u].w, e);
+    }
+    if (fix) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (pow_needs_fix_exp(a[u].x, e)) r[u].x = powf(a[u].x, y);
+            if (pow_needs_fix_exp(a[u].y, e)) r[u].y = powf(a[u].y, y);
+            if (pow_needs_fix_exp(a[u].z, e)) r[u].z = powf(a[u].z, y);
+            if (pow_needs_fix_exp(a[u].w, e)) r[u].w = powf(a[u].w, y);
+        }
+    }
+}
+
+// unary_fwd over U float4s; pow(x, p0) through pow_fwd_v_exp.
 template <int OP, int U>
 __device__ __forceinline__ void unary_fwd_v(float4 (&r)[U], const float4 (&x)[U], float p0, float p1) {
     if constexpr (OP == WM_POWS) {
-        float4 pe[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) pe[u] = make_float4(p0, p0, p0, p0);
-        binary_fwd_v<WM_POW, U>(r, x, pe);
+        pow_fwd_v_exp<U>(r, x, p0);
     } else {
 #pragma unroll
         for (int u = 0; u < U; ++u)
@@ -226,16 +249,13 @@ __device__ __forceinline__ void unary_fwd_v(float4 (&r)[U], const float4 (&x)[U]
 }
 
 // unary_bwd over U float4s, plus the existing gradient when ACC; pow's
-// pow(x, p0 - 1) as in binary_fwd_v.
+// pow(x, p0 - 1) through pow_fwd_v_exp.
 template <int OP, bool ACC, int U>
 __device__ __forceinline__ void unary_bwd_v(float4 (&r)[U], const float4 (&g)[U], const float4 (&x)[U],
                                             const float4 (&o)[U], const float4 (&gx)[U], float p0, float p1) {
     if constexpr (OP == WM_POWS) {
-        const float pm1 = p0 - 1.0f;
-        float4 pe[U], q[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) pe[u] = make_float4(pm1, pm1, pm1, pm1);
-        binary_fwd_v<WM_POW, U>(q, x, pe);
+        float4 q[U];
+        pow_fwd_v_exp<U>(q, x, p0 - 1.0f);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             r[u] = make_float4(g[u].x * p0 * q[u].x, g[u].y * p0 * q[u].y, g[u].z * p0 * q[u].z, g[u].w * p0 * q[u].w);

@@ -214,6 +214,36 @@ WM_HD inline float pow_table(float x, float y) {
 
 WM_HD inline bool pow_needs_fix(float x, float y) { return !powdetail::table_ok(x, y); }
 
+// The exponent's share of pow_table and pow_needs_fix, for a run of
+// elements that share one exponent (a per-row or scalar exponent): its
+// double, C pow's sign rule for a negative base (NaN unless y is an integer;
+// an odd y flips the sign bit of |x|^y) and its half of table_ok.
+struct PowExponent {
+    double yd;
+    uint32_t odd_mask;  // 0x80000000 for an odd integer y
+    bool is_int;
+    bool ok;            // finite and non-zero
+};
+
+WM_HD inline PowExponent pow_exponent(float y) {
+    const float yi = std::rint(y);
+    const bool odd = ((int)std::fmin(std::fabs(yi), 16777216.0f) & 1) != 0;
+    return {(double)y, odd ? 0x80000000u : 0u, yi == y, std::isfinite(y) && y != 0.0f};
+}
+
+// pow_table(x, y) for y described by e: the same value, bit for bit (the
+// magnitude is never NaN, so flipping its sign bit is negation).
+WM_HD inline float pow_table_exp(float x, const PowExponent& e) {
+    using namespace powdetail;
+    const float mag = exp2_to_float(e.yd * log2_normal(std::fabs(x)));
+    const float neg = e.is_int ? float_of(bits_of(mag) ^ e.odd_mask) : NAN;
+    return x < 0.0f ? neg : mag;
+}
+
+WM_HD inline bool pow_needs_fix_exp(float x, const PowExponent& e) {
+    return !(e.ok && std::isnormal(x) && std::fabs(x) != 1.0f);
+}
+
 // pow(x, y) with C semantics, within 1 ulp.
 WM_HD inline float pow_f32(float x, float y) {
     return pow_needs_fix(x, y) ? powf(x, y) : pow_table(x, y);
