@@ -210,6 +210,52 @@ def test_multi_steps_bitexact(wm, kind, hp):
                 assert oracle.bit_equal(slots[j].get(), arrs[j]), (kind, t, i, j)
 
 
+def test_multi_many_tensors_and_unscale(wm):
+    """A list long enough that the element-wise passes' chunk -> tensor lookup
+    crosses many coarse-index blocks, several of them holding dozens of small
+    tensors: AdamW bit-exact against the oracle for every tensor, then an
+    unscale whose first non-finite value sits in a late small tensor."""
+    r = rng(4242)
+    sizes = [int(v) for v in r.integers(1, 3000, 300)] + [300001, 4, 70000] + [int(v) for v in r.integers(1, 600, 200)]
+    mis = [i % 7 == 3 for i in range(len(sizes))]
+    hp = dict(lr=1e-3, a=0.9, b=0.999, c=1e-8, d=0.01)
+    mine = [[rng(5 * i).standard_normal(n).astype(np.float32), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+            for i, n in enumerate(sizes)]
+    dev = [[Slot(x, m) for x in arrs] for arrs, m in zip(mine, mis)]
+    gs = [(rng(900 + i).standard_normal(n)).astype(np.float32) for i, n in enumerate(sizes)]
+    dgs = [Slot(g, m) for g, m in zip(gs, mis)]
+    ns, _ns = W.i64_array(sizes)
+    P, _p = _ptrs([x[0] for x in dev])
+    G, _g = _ptrs(dgs)
+    S1, _s1 = _ptrs([x[1] for x in dev])
+    S2, _s2 = _ptrs([x[2] for x in dev])
+    W.call("wm_adamw_step_multi", len(sizes), P, G, S1, S2, ns, hp["lr"], hp["a"], hp["b"], hp["c"],
+           o32.bias_correction(hp["a"], 1), o32.bias_correction(hp["b"], 1), hp["d"])
+    for arrs, g in zip(mine, gs):
+        oracle_step("adamw", hp, arrs[0], g, arrs[1], arrs[2], 1)
+    for i, (arrs, slots) in enumerate(zip(mine, dev)):
+        for j in range(3):
+            assert oracle.bit_equal(slots[j].get(), arrs[j]), (i, sizes[i], j)
+    # unscale: the first non-finite product is in tensor `bad`
+    bad = len(sizes) - 40
+    gs2 = [g * np.float32(64.0) for g in gs]
+    gs2[bad][sizes[bad] // 2] = np.float32(np.inf)
+    gs2[-3][0] = np.float32(np.nan)  # later: must stay untouched
+    d2 = [Slot(g, m) for g, m in zip(gs2, mis)]
+    G2, _g2 = _ptrs(d2)
+    found = W.C.c_int(-1)
+    W.call("wm_grad_unscale", len(sizes), G2, ns, W.C.c_float(1.0 / 64.0), W.C.byref(found))
+    assert found.value == 1
+    for i, (d_, g) in enumerate(zip(d2, gs2)):
+        want = g.copy()
+        if i < bad:
+            want = want * np.float32(1.0 / 64.0)
+        elif i == bad:
+            k = sizes[bad] // 2
+            want[:k] = want[:k] * np.float32(1.0 / 64.0)
+        assert oracle.bit_equal(d_.get(), want), i
+
+
 def test_multi_norm_clip_value(wm):
     gs = [(rng(80 + i).standard_normal(n) * 3).astype(np.float32) for i, (n, _) in enumerate(MULTI_SIZES)]
     ds = [Slot(g, mis) for g, (_, mis) in zip(gs, MULTI_SIZES)]
