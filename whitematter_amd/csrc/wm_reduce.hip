@@ -647,29 +647,56 @@ __global__ void __launch_bounds__(kBlock) reduce_bwd_sum_kernel(const float* __r
 }
 
 // Vector variant: inner % 4 == 0 (4 adjacent i share o, k) or inner == 1 and
-// n % 4 == 0 (4 adjacent k share o and g).
-template <bool ACC, bool INNER1>
+// n % 4 == 0 (4 adjacent k share o and g).  kSlotsBwd float4s per thread,
+// their values gathered before any store, on a grid that covers the tensor,
+// with streaming stores: 74.7 % of the HBM peak for a [32768, 4096] mean
+// backward against 63 % with one float4 per thread (each thread then waits
+// on its g load before its only store).  IDX32: every index fits 32 bits,
+// so the position arithmetic divides in 32 bits (a 64-bit division is a
+// long instruction sequence).
+constexpr int kSlotsBwd = 4;
+template <bool ACC, bool INNER1, bool IDX32>
 __global__ void __launch_bounds__(kBlock) reduce_bwd_sum_vec_kernel(const float* __restrict__ g,
-                                                                     float4* __restrict__ gx, int64_t outer, int64_t n,
+                                                                     float* __restrict__ gx, int64_t outer, int64_t n,
                                                                      int64_t inner) {
     const int64_t total4 = outer * n * inner / 4;
     const int64_t ni = n * inner;
-    for (int64_t q = (int64_t)blockIdx.x * kBlock + threadIdx.x; q < total4; q += (int64_t)gridDim.x * kBlock) {
-        const int64_t e = q * 4;
-        float4 c;
-        if constexpr (INNER1) {
-            const float s = g[e / n];
-            c = make_float4(s, s, s, s);
-        } else {
-            const int64_t o = e / ni;
-            const int64_t i = (e - o * ni) % inner;
-            c = *reinterpret_cast<const float4*>(g + o * inner + i);
+    const int64_t step = (int64_t)gridDim.x * kBlock * kSlotsBwd;
+    for (int64_t q0 = (int64_t)blockIdx.x * kBlock * kSlotsBwd + threadIdx.x; q0 < total4; q0 += step) {
+        float4 cc[kSlotsBwd];
+#pragma unroll
+        for (int u = 0; u < kSlotsBwd; ++u) {
+            const int64_t q = q0 + (int64_t)u * kBlock;
+            const int64_t e = q * 4;
+            if (q >= total4) continue;
+            float4 c;
+            if constexpr (INNER1) {
+                const float s = g[IDX32 ? (int64_t)((uint32_t)e / (uint32_t)n) : e / n];
+                c = make_float4(s, s, s, s);
+            } else {
+                int64_t o, i;
+                if constexpr (IDX32) {
+                    const uint32_t o32 = (uint32_t)e / (uint32_t)ni;
+                    o = o32;
+                    i = ((uint32_t)e - o32 * (uint32_t)ni) % (uint32_t)inner;
+                } else {
+                    o = e / ni;
+                    i = (e - o * ni) % inner;
+                }
+                c = *reinterpret_cast<const float4*>(g + o * inner + i);
+            }
+            if (ACC) {
+                const float4 old = ld_stream(gx + e);
+                c.x += old.x; c.y += old.y; c.z += old.z; c.w += old.w;
+            }
+            cc[u] = c;
         }
-        if (ACC) {
-            float4 old = gx[q];
-            c.x += old.x; c.y += old.y; c.z += old.z; c.w += old.w;
+#pragma unroll
+        for (int u = 0; u < kSlotsBwd; ++u) {
+            const int64_t q = q0 + (int64_t)u * kBlock;
+            if (q >= total4) continue;
+            st_stream(gx + q * 4, cc[u]);
         }
-        gx[q] = c;
     }
 }
 
@@ -919,14 +946,18 @@ int wm_reduce_bwd(int op, const float* g, const int64_t* idx, int64_t outer, int
     if (op == WM_R_SUM || op == WM_R_MEAN) {
         const bool vec4 = aligned16(gx) && ((inner % 4 == 0 && aligned16(g)) || (inner == 1 && n % 4 == 0));
         if (vec4) {
-            dim3 grid(grid_for(total / 4, kBlock, 16));
+            const dim3 grid(grid_for(total / 4, kBlock * kSlotsBwd, 1 << 12));
+            const bool i32 = total < ((int64_t)1 << 32);
+#define WM_RBS(A, I1, I32) \
+    launch_kernel((reduce_bwd_sum_vec_kernel<A, I1, I32>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner)
             if (inner == 1) {
-                if (accumulate) launch_kernel((reduce_bwd_sum_vec_kernel<true, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
-                else launch_kernel((reduce_bwd_sum_vec_kernel<false, true>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                if (accumulate) { if (i32) WM_RBS(true, true, true); else WM_RBS(true, true, false); }
+                else { if (i32) WM_RBS(false, true, true); else WM_RBS(false, true, false); }
             } else {
-                if (accumulate) launch_kernel((reduce_bwd_sum_vec_kernel<true, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
-                else launch_kernel((reduce_bwd_sum_vec_kernel<false, false>), grid, dim3(kBlock), 0, st, g, reinterpret_cast<float4*>(gx), outer, n, inner);
+                if (accumulate) { if (i32) WM_RBS(true, false, true); else WM_RBS(true, false, false); }
+                else { if (i32) WM_RBS(false, false, true); else WM_RBS(false, false, false); }
             }
+#undef WM_RBS
         } else {
             dim3 grid(grid_for(total, kBlock, 16));
             if (accumulate) launch_kernel((reduce_bwd_sum_kernel<true>), grid, dim3(kBlock), 0, st, g, gx, outer, n, inner);

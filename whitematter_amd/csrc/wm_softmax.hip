@@ -161,8 +161,12 @@ int launch_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
     hipStream_t st = stream();
     TileChoice tc = choose_tile(cols);
     const bool vec = cols % 4 == 0 && aligned16(out) && aligned16(x);
-    // Several rows per CU in flight; the grid-stride loop covers the rest.
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    // Rows of up to 2048 columns: a wave per row, 32 workgroups per CU and a
+    // grid-stride loop.  Longer rows: one workgroup per row on a grid that
+    // covers them all, which measured 70.3 -> 74.5 % of the HBM peak (the
+    // backward 75 -> 76.5 %) at [8192, 32000] against 4 workgroups per CU
+    // each looping over rows.
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : (1 << 12))));
     if (tc.nt == 0) {
         launch_kernel(softmax_fwd_long_kernel<LOG>, grid, dim3(1024), 0, st, out, x, rows, cols);
         return check_launch("wm_softmax_fwd(long)");
@@ -184,7 +188,7 @@ int launch_softmax_bwd(const float* g, const float* out, float* gx, int acc, int
     hipStream_t st = stream();
     TileChoice tc = choose_tile(cols);
     const bool vec = cols % 4 == 0 && aligned16(g) && aligned16(out) && aligned16(gx);
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : (1 << 12))));
     if (tc.nt == 0) {
         launch_kernel(softmax_bwd_long_kernel<LOG>, grid, dim3(1024), 0, st, g, out, gx, acc, rows, cols);
         return check_launch("wm_softmax_bwd(long)");
