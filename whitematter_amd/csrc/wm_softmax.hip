@@ -161,12 +161,12 @@ int launch_softmax_fwd(float* out, const float* x, int64_t rows, int64_t cols) {
     hipStream_t st = stream();
     TileChoice tc = choose_tile(cols);
     const bool vec = cols % 4 == 0 && aligned16(out) && aligned16(x);
-    // Rows of up to 2048 columns: a wave per row, 32 workgroups per CU and a
-    // grid-stride loop.  Longer rows: one workgroup per row on a grid that
-    // covers them all, which measured 70.3 -> 74.5 % of the HBM peak (the
-    // backward 75 -> 76.5 %) at [8192, 32000] against 4 workgroups per CU
-    // each looping over rows.
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : (1 << 12))));
+    // One workgroup per row (a wave for rows of up to 2048 columns) on a grid
+    // that covers every row: 70.3 -> 74.5 % of the HBM peak at [8192, 32000]
+    // (backward 75 -> 76.5 %) against 4 workgroups per CU each looping over
+    // rows; the one-wave tile, in the attention softmax at 1024 columns,
+    // 68.4 -> 75.7 % against 32 workgroups per CU.
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (1 << 12)));
     if (tc.nt == 0) {
         launch_kernel(softmax_fwd_long_kernel<LOG>, grid, dim3(1024), 0, st, out, x, rows, cols);
         return check_launch("wm_softmax_fwd(long)");
@@ -188,7 +188,7 @@ int launch_softmax_bwd(const float* g, const float* out, float* gx, int acc, int
     hipStream_t st = stream();
     TileChoice tc = choose_tile(cols);
     const bool vec = cols % 4 == 0 && aligned16(g) && aligned16(out) && aligned16(gx);
-    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (tc.nt == 64 ? 32 : (1 << 12))));
+    dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * (1 << 12)));  // as in the forward
     if (tc.nt == 0) {
         launch_kernel(softmax_bwd_long_kernel<LOG>, grid, dim3(1024), 0, st, g, out, gx, acc, rows, cols);
         return check_launch("wm_softmax_bwd(long)");
