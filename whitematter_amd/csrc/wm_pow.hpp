@@ -8,10 +8,15 @@
 //            with invc ~ 1/c (20 significant bits, so z * invc is exact in
 //            double) and logc = log2(c); r = z * invc - 1 with |r| < 0.0297;
 //            log2(1 + r) by its series to r^6 (truncation < 4.2e-12).
-//   2^t:     t = kd/32 + r with |r| <= 1/64; 2^(kd/32) from a 32-entry
-//            table and an exponent shift; 2^r = e^(r ln 2) by its series to
-//            degree 3 (truncation < 5.7e-10 relative).
-// The double result is within ~6e-10 (relative) of the exact power, so its
+//   2^t:     t = kd/128 + r with |r| <= 1/256; 2^(kd/128) from a
+//            128-entry table and an exponent shift; 2^r by 1 + E1 r + E2 r^2
+//            with E1, E2 minimising the largest relative error on
+//            [-1/256, 1/256]: 8.3e-10.  (The
+//            Taylor series to degree 3 on a 32-entry table, 5.7e-10, took
+//            one more FMA per element; degree 2 on 64 entries, 6.6e-9,
+//            rounded results near ties in the subnormal range the other way
+//            from the C library noticeably more often.)
+// The double result is within ~9e-10 (relative) of the exact power, so its
 // one rounding to float is within 1 ulp.  A negative base takes C pow's sign
 // rule (NaN for a non-integer exponent, the magnitude's sign flipped for an
 // odd one) without a branch.  The operands the tables do not cover (zero,
@@ -24,7 +29,8 @@
 // hardware exp2 on a reduced argument (relative error ~2e-7).
 //
 // The file is plain C++ with explicit fma(), so the same code compiles for
-// the host and is checked there against long double powl.
+// the host and is checked there against long double powl
+// (tests/cpp/pow_table_check.cpp).
 #pragma once
 
 #include <cmath>
@@ -46,7 +52,7 @@ struct LogEntry {
 
 struct alignas(16) PowTables {
     LogEntry log[16];  // {1/c, log2(c)} for the 16 sub-intervals of z
-    double exp2[32];   // 2^(j/32), j = 0..31
+    double exp2[128];  // 2^(j/128), j = 0..127, correctly rounded
 };
 
 WM_HD inline const PowTables& pow_table_data() {
@@ -62,13 +68,38 @@ WM_HD inline const PowTables& pow_table_data() {
             {0.7664670944213867, 0.38370423872947484},  {0.7314281463623047, 0.4512119502479954},
         },
         {
-            1.0,                1.0218971486541166, 1.0442737824274138, 1.0671404006768237, 1.0905077326652577,
-            1.1143867425958924, 1.1387886347566916, 1.1637248587775775, 1.189207115002721,  1.215247359980469,
-            1.241857812073484,  1.2690509571917332, 1.2968395546510096, 1.3252366431597413, 1.3542555469368927,
-            1.383909881963832,  1.4142135623730951, 1.4451808069770467, 1.4768261459394993, 1.5091644275934228,
-            1.5422108254079407, 1.5759808451078865, 1.6104903319492543, 1.645755478153965,  1.681792830507429,
-            1.718619298122478,  1.7562521603732995, 1.7947090750031072, 1.8340080864093424, 1.8741676341103,
-            1.9152065613971474, 1.9571441241754002,
+            1.0, 1.0054299011128027, 1.0108892860517005, 1.016378314910953,
+            1.0218971486541166, 1.0274459491187637, 1.0330248790212284, 1.0386341019613787,
+            1.0442737824274138, 1.0499440858006872, 1.0556451783605572, 1.061377227289262,
+            1.0671404006768237, 1.0729348675259756, 1.0787607977571199, 1.0846183622133092,
+            1.0905077326652577, 1.0964290818163769, 1.102382583307841, 1.1083684117236787,
+            1.1143867425958924, 1.1204377524096067, 1.1265216186082418, 1.1326385195987192,
+            1.1387886347566916, 1.1449721444318042, 1.1511892299529827, 1.1574400736337511,
+            1.1637248587775775, 1.1700437696832502, 1.1763969916502812, 1.182784710984341,
+            1.189207115002721, 1.1956643920398273, 1.202156731452703, 1.2086843236265816,
+            1.215247359980469, 1.2218460329727576, 1.22848053610687, 1.2351510639369334,
+            1.241857812073484, 1.2486009771892048, 1.255380757024691, 1.2621973503942507,
+            1.2690509571917332, 1.275941778396392, 1.2828700160787783, 1.2898358734066657,
+            1.2968395546510096, 1.3038812651919358, 1.3109612115247644, 1.318079601266064,
+            1.3252366431597413, 1.3324325470831615, 1.339667524053303, 1.3469417862329458,
+            1.3542555469368927, 1.3616090206382248, 1.3690024229745905, 1.3764359707545302,
+            1.383909881963832, 1.3914243757719262, 1.3989796725383112, 1.4065759938190154,
+            1.4142135623730951, 1.4218926021691656, 1.42961333839197, 1.4373759974489824,
+            1.4451808069770467, 1.4530279958490526, 1.460917794180647, 1.4688504333369818,
+            1.4768261459394993, 1.4848451658727524, 1.4929077282912648, 1.5010140696264256,
+            1.5091644275934228, 1.5173590411982147, 1.5255981507445384, 1.533881997840956,
+            1.5422108254079407, 1.550584877685, 1.559004400237837, 1.567469639965553,
+            1.5759808451078865, 1.5845382652524937, 1.593142151342267, 1.6017927556826934,
+            1.6104903319492543, 1.6192351351948637, 1.6280274218573478, 1.6368674497669644,
+            1.645755478153965, 1.6546917676561943, 1.6636765803267364, 1.6727101796415966,
+            1.681792830507429, 1.6909247992693053, 1.7001063537185235, 1.709337763100463,
+            1.718619298122478, 1.7279512309618377, 1.7373338352737062, 1.746767386199169,
+            1.7562521603732995, 1.7657884359332727, 1.7753764925265212, 1.785016611318935,
+            1.7947090750031072, 1.804454167806624, 1.8142521755003989, 1.8241033854070534,
+            1.8340080864093424, 1.843966568958626, 1.8539791250833855, 1.864046048397789,
+            1.8741676341103, 1.8843441790323345, 1.8945759815869656, 1.9048633418176741,
+            1.9152065613971474, 1.925605943636125, 1.9360617934922943, 1.9465744175792332,
+            1.9571441241754002, 1.9677712232331759, 1.978456026387951, 1.9891988469672663,
         },
     };
     return t;
@@ -76,10 +107,11 @@ WM_HD inline const PowTables& pow_table_data() {
 
 #ifdef __HIP_DEVICE_COMPILE__
 // On the device the lookups read a copy of the tables in LDS, which every
-// kernel that evaluates pow fills first (pow_tables_to_lds).  Each table
-// entry sits in its own LDS banks, so a wave's lookups never conflict, and
-// they stay off the texture path, which per-lane gathers from global memory
-// had saturated.
+// kernel that evaluates pow fills first (pow_tables_to_lds).  Each log
+// entry sits in its own LDS banks; exp2 entries j, j + 32, j + 64 and
+// j + 96 share theirs, so a wave's exp2 lookups conflict at most four ways.  The lookups stay off
+// the texture path, which per-lane gathers from global memory had
+// saturated.
 static __shared__ PowTables wm_pow_lds;
 #endif
 
@@ -136,19 +168,21 @@ WM_HD inline double log2_normal(float ax) {
 // integer conversion is exact and the table index in range.
 WM_HD inline float exp2_to_float(double t) {
     t = std::fmax(std::fmin(t, 200.0), -200.0);
-    // kd = rint(32 t) by adding 1.5 * 2^52: the low word is then rint(32 t)
-    // in two's complement (|32 t| <= 6400).
+    // kd = rint(128 t) by adding 1.5 * 2^52: the low word is then rint(128 t)
+    // in two's complement (|128 t| <= 25600).
     const double SHIFT = 6755399441055744.0;
-    const double kds = std::fma(t, 32.0, SHIFT);
+    const double kds = std::fma(t, 128.0, SHIFT);
     const int ki = (int)low_word(kds);
     const double kd = kds - SHIFT;
-    const double r = std::fma(kd, -1.0 / 32.0, t);  // exact, |r| <= 1/64
-    // 2^r = 1 + E1 r + E2 r^2 + E3 r^3, En = (ln 2)^n / n!
-    const double E1 = 0.6931471805599453, E2 = 0.2402265069591007, E3 = 0.055504108664821576;
-    double p = std::fma(E3, r, E2);
-    p = std::fma(p, r, E1);
-    p = std::fma(p, r, 1.0);
-    return (float)std::ldexp(pow_tables().exp2[ki & 31] * p, ki >> 5);
+    const double r = std::fma(kd, -1.0 / 128.0, t);  // exact, |r| <= 1/256
+    // 2^r ~ 1 + E1 r + E2 r^2: the coefficients minimise the largest
+    // relative error on the range (8.3e-10) with the constant held at 1, so
+    // r = 0 gives exactly the table entry: an exact power of two stays
+    // exact (2^-150, a tie between 0 and the smallest subnormal, must round
+    // to even as the C library's powf does).
+    const double E1 = 0.6931478155387308, E2 = 0.24022650685171912;
+    const double p = std::fma(std::fma(E2, r, E1), r, 1.0);
+    return (float)std::ldexp(pow_tables().exp2[ki & 127] * p, ki >> 7);
 }
 
 // 2^t for values used only inside gradients: relative error ~2e-7 (the
@@ -191,13 +225,14 @@ WM_HD inline float apply_sign(float x, float y, float mag) {
 #ifdef __HIPCC__
 // Copies the pow tables into LDS.  Every kernel that evaluates pow_table,
 // pow_f32 or pow_grad_* calls this first, with all its threads (it contains
-// a barrier); blockDim.x >= 32.
+// a barrier).
 __device__ inline void pow_tables_to_lds() {
 #ifdef __HIP_DEVICE_COMPILE__
-    static_assert(sizeof(powdetail::PowTables) == 32 * 16, "pow tables are 32 x 16 bytes");
-    if (threadIdx.x < 32)
-        reinterpret_cast<uint4*>(&powdetail::wm_pow_lds)[threadIdx.x] =
-            reinterpret_cast<const uint4*>(&powdetail::pow_table_data())[threadIdx.x];
+    constexpr int kWords = (int)(sizeof(powdetail::PowTables) / 16);
+    static_assert(kWords * 16 == sizeof(powdetail::PowTables), "pow tables are whole 16-byte words");
+    for (int i = threadIdx.x; i < kWords; i += blockDim.x)
+        reinterpret_cast<uint4*>(&powdetail::wm_pow_lds)[i] =
+            reinterpret_cast<const uint4*>(&powdetail::pow_table_data())[i];
     __syncthreads();
 #endif
 }
@@ -258,7 +293,7 @@ WM_HD inline float pow_f32(float x, float y) {
 // path out carries a relative error of ~2e-7 and pbm1 ~3e-7 against the
 // exact pow(a, b - 1) (the reciprocal adds at most 1 ulp); the reference's
 // pow(a, b - 1.0f) rounds the exponent to float first, which moves it by up
-// to |ln a| 2^-24 < 5.3e-6 relative (see below).  lga is log(a) rounded once
+// to |(b - 1) ln a| 2^-24 < 5.3e-6 relative (see below).  lga is log(a) rounded once
 // from double (NaN for a < 0).  The quotient stands for pow(a, b - 1) while |b| < 2^24, pow(a, b)
 // stays in the normal range (or is the NaN of a negative base) and 1 / a
 // does too (|a| < 2^126); other lanes set `slow`, for pow_grad_fix.
@@ -284,12 +319,12 @@ WM_HD inline PowGrad pow_grad_table(float a, float b, bool want_out, bool want_p
         if (want_out) r.out = o;
         if (want_pbm1) {
             r.pbm1 = o * recip_normal(a);
-            // pow(a, b - 1.0f) takes b - 1 rounded to float.  Below |b| =
-            // 2^24 that rounding is non-zero only for |b - 1| < 2 (|b| beyond
-            // that keeps b - 1 exact) and then at most 2^-24, which changes
-            // the power by at most |ln a| 2^-24 < 5.3e-6 relative (normal a);
-            // from 2^24 up it can drop the "- 1" altogether, so those lanes
-            // are slow.  A NaN power (a < 0, b not an integer) is
+            // pow(a, b - 1.0f) takes b - 1 rounded to float, at most
+            // |b - 1| 2^-24 from the exact b - 1, which changes the power by
+            // at most |(b - 1) ln a| 2^-24 relative: below 5.3e-6 wherever
+            // the power is a normal float (|(b - 1) ln a| < 88.8).  From
+            // |b| = 2^24 up the rounding can drop the "- 1" altogether, so
+            // those lanes are slow.  A NaN power (a < 0, b not an integer) is
             // pow(a, b - 1) too unless b - 1 rounded to an integer (|b| below
             // 2^-25).
             const float bm1 = b - 1.0f;
