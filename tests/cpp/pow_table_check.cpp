@@ -9,6 +9,8 @@
 //                      of powl(a, (float)(b - 1)) (the reference rounds
 //                      b - 1 to float first, which moves its power by up to
 //                      |(b - 1) ln a| 2^-24); lga within 1 ulp of logl(a)
+//   pow_table_exp, pow_grad_table_exp (one exponent shared by many
+//                      elements) equal pow_table, pow_grad_table bit for bit
 // Prints "POW CHECK PASSED" and exits 0 when every case holds.
 #include "../../whitematter_amd/csrc/wm_pow.hpp"
 
@@ -73,6 +75,18 @@ int main(int argc, char** argv) {
         if (!rel_close(gp.pbm1, ref2, tol2)) fail("grad pbm1", x, y, gp.pbm1, ref2);
         const long double l = logl((long double)x);
         if (ulp_dist(gp.lga, l) > 1 && !(x == 1.0f && gp.lga == 0.f)) fail("grad lga", x, y, gp.lga, l);
+        // the shared-exponent forms equal the per-element ones bit for bit
+        const wm::PowExponent pe = wm::pow_exponent(y);
+        const float t1 = wm::pow_table(x, y), t2 = wm::pow_table_exp(x, pe);
+        if (std::memcmp(&t1, &t2, 4) != 0 || wm::pow_needs_fix(x, y) != wm::pow_needs_fix_exp(x, pe))
+            fail("shared exponent", x, y, t2, t1);
+        const wm::PowGradExponent pq = wm::pow_grad_exponent(y);
+        const wm::PowGrad g1 = wm::pow_grad_table(x, y, true, true, true);
+        const wm::PowGrad g2 = wm::pow_grad_table_exp(x, pq, true, true, true);
+        if (std::memcmp(&g1.out, &g2.out, 4) != 0 || std::memcmp(&g1.pbm1, &g2.pbm1, 4) != 0 ||
+            std::memcmp(&g1.lga, &g2.lga, 4) != 0 || g1.slow != g2.slow ||
+            wm::pow_grad_needs_fix(x, y, g1) != wm::pow_grad_needs_fix_exp(x, pq, g2))
+            fail("shared exponent (grad)", x, y, g2.pbm1, g1.pbm1);
     };
     std::uniform_real_distribution<float> u(-3.f, 3.f), e(-20.f, 20.f);
     std::uniform_int_distribution<uint32_t> bits;

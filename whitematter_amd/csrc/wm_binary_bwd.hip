@@ -245,6 +245,7 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
             constexpr int kSlots = OP == WM_POW ? 1 : 4;
             constexpr bool kPipe = OP == WM_POW;
             constexpr int kGroup = OP == WM_POW ? 2 : 4;
+            const PowGradExponent pq = pow_grad_exponent(OP == WM_POW && VB ? v : 0.0f);
             const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
             float4 s4 = z4;
             float4 vg[kSlots], vf[kSlots], vo[kSlots], old[kSlots];
@@ -283,8 +284,11 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
                             bh[j] = VB ? v : e[h + j];
                             oh[j] = oo[h + j];
                         }
-                        binary_grads_n<OP, kGroup>(gh, ah, bh, oh, need_o, VB ? gfr != nullptr : want_v,
-                                                   VB ? want_v : gfr != nullptr, dah, dbh);
+                        if constexpr (OP == WM_POW && VB)  // one exponent per row
+                            pow_grads_n_exp<kGroup>(gh, ah, v, pq, oh, need_o, gfr != nullptr, want_v, dah, dbh);
+                        else
+                            binary_grads_n<OP, kGroup>(gh, ah, bh, oh, need_o, VB ? gfr != nullptr : want_v,
+                                                       VB ? want_v : gfr != nullptr, dah, dbh);
 #pragma unroll
                         for (int j = 0; j < kGroup; ++j) {
                             da[h + j] = dah[j];

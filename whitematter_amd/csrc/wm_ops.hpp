@@ -128,6 +128,33 @@ __device__ __forceinline__ void binary_grads_n(const float (&g)[N], const float 
     }
 }
 
+// pow's gradients over N elements that share the exponent b (q =
+// pow_grad_exponent(b)): bit for bit binary_grads_n<WM_POW, N> with b
+// everywhere, the exponent's share computed once.
+template <int N>
+__device__ __forceinline__ void pow_grads_n_exp(const float (&g)[N], const float (&a)[N], float b,
+                                                const PowGradExponent& q, const float (&o)[N], bool have_o,
+                                                bool want_da, bool want_db, float (&da)[N], float (&db)[N]) {
+    const bool want_out = want_db && !have_o;
+    PowGrad p[N];
+    bool fix = false;
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        p[j] = pow_grad_table_exp(a[j], q, want_out, want_da, want_db);
+        fix |= pow_grad_needs_fix_exp(a[j], q, p[j]);
+    }
+    if (fix) {
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            if (pow_grad_needs_fix_exp(a[j], q, p[j])) pow_grad_fix(a[j], b, want_out, want_da, want_db, p[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        da[j] = g[j] * b * p[j].pbm1;
+        db[j] = g[j] * (have_o ? o[j] : p[j].out) * p[j].lga;
+    }
+}
+
 // binary_fwd over U float4s, with pow's table path first and one fix-up
 // branch after (as in binary_grads_n).
 template <int OP, int U>

@@ -359,6 +359,45 @@ WM_HD inline void pow_grad_fix(float a, float b, bool want_out, bool want_pbm1, 
     if (want_lga) r.lga = logf(a);
 }
 
+// The exponent's share of pow_grad_table and pow_grad_needs_fix, for
+// elements that share one exponent b (a per-row exponent): computed once,
+// the per-element work is then pow_grad_table_exp, bit for bit
+// pow_grad_table.
+struct PowGradExponent {
+    PowExponent e;  // b: its double, sign rule, finite and non-zero
+    bool ok_bm1;    // b - 1.0f finite and non-zero
+    bool bm1_int;   // b - 1.0f an integer
+    bool b_small;   // |b| < 2^24
+};
+
+WM_HD inline PowGradExponent pow_grad_exponent(float b) {
+    const float bm1 = b - 1.0f;
+    return {pow_exponent(b), std::isfinite(bm1) && bm1 != 0.0f, std::rint(bm1) == bm1, std::fabs(b) < 0x1p24f};
+}
+
+WM_HD inline PowGrad pow_grad_table_exp(float a, const PowGradExponent& q, bool want_out, bool want_pbm1,
+                                        bool want_lga) {
+    using namespace powdetail;
+    PowGrad r = {0.0f, 0.0f, 0.0f, false};
+    const double l2 = log2_normal(std::fabs(a));
+    if (want_out || want_pbm1) {
+        const float mag = exp2_grad(q.e.yd * l2);  // never NaN: flipping its sign bit is negation
+        const float o = a < 0.0f ? (q.e.is_int ? float_of(bits_of(mag) ^ q.e.odd_mask) : NAN) : mag;
+        if (want_out) r.out = o;
+        if (want_pbm1) {
+            r.pbm1 = o * recip_normal(a);
+            const bool ok = std::isnormal(o) || (std::isnan(o) && !q.bm1_int);
+            r.slow = !ok || !q.b_small || !(std::fabs(a) < 0x1p126f);
+        }
+    }
+    if (want_lga) r.lga = a > 0.0f ? (float)(l2 * 0.6931471805599453) : NAN;
+    return r;
+}
+
+WM_HD inline bool pow_grad_needs_fix_exp(float a, const PowGradExponent& q, const PowGrad& r) {
+    return r.slow || !(q.e.ok && q.ok_bm1 && std::isnormal(a) && std::fabs(a) != 1.0f);
+}
+
 WM_HD inline PowGrad pow_grad_parts(float a, float b, bool want_out, bool want_pbm1, bool want_lga) {
     PowGrad r = pow_grad_table(a, b, want_out, want_pbm1, want_lga);
     if (pow_grad_needs_fix(a, b, r)) pow_grad_fix(a, b, want_out, want_pbm1, want_lga, r);
