@@ -28,8 +28,10 @@ def binary_fwd(op, a, b):
 
 def binary_bwd(op, g, a, b, out, ga0=None, gb0=None, need_a=True, need_b=True):
     """Backward through wm_binary_bwd.  ga0/gb0: initial gradient buffers for
-    the accumulate mode (None = known-zero, overwrite mode)."""
-    dg, da, db, dout = dev(g), dev(a), dev(b), dev(out)
+    the accumulate mode (None = known-zero, overwrite mode).  out=None passes
+    no forward output (pow then recomputes it)."""
+    dg, da, db = dev(g), dev(a), dev(b)
+    dout = dev(out) if out is not None else None
     dga = (dev(ga0) if ga0 is not None else W.DeviceArray(a.shape)) if need_a else None
     dgb = (dev(gb0) if gb0 is not None else W.DeviceArray(b.shape)) if need_b else None
     if dga is not None and ga0 is None:

@@ -173,3 +173,35 @@ def test_div_row_vector_special_divisors(wm):
     ok_b, wb = oracle.close_scaled(gb, rb, np.abs(sb_), RTOL)
     assert ok_a, f"grad a off by {wa:.3g}x tolerance"
     assert ok_b, f"grad b off by {wb:.3g}x tolerance"
+
+
+@pytest.mark.parametrize("sa,sb", [((96, 1000), (96, 1)), ((40, 1), (40, 2048)), ((5, 70000), (5, 1)),
+                                   ((33, 1001), (33, 1)), ((64, 1024), (1024,))])
+@pytest.mark.parametrize("need", [(True, True), (True, False), (False, True)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_pow_backward_recomputes_output(wm, sa, sb, need, accumulate):
+    """pow's backward without the forward output (as config 2's bench step
+    calls it): the power is recomputed in the kernel; every layout and
+    gradient subset against the fp64 oracle."""
+    seed = stable_seed("pow-noout", sa, sb)
+    a, b = make_inputs("pow", sa, sb, seed)
+    out = binary_fwd("pow", a, b)
+    g = rng_normal(out.shape, seed + 7)
+    ga0 = rng_normal(sa, seed + 8) if accumulate else None
+    gb0 = rng_normal(sb, seed + 9) if accumulate else None
+    ga, gb = binary_bwd("pow", g, a, b, None, ga0, gb0, need_a=need[0], need_b=need[1])
+    ra, rb = oracle.get("f64").binary_bwd("pow", g, a, b, out)
+    sa_, sb_ = oracle.get("abs").binary_bwd("pow", g, a, b, out)
+    if accumulate:
+        ra, rb = ra + ga0, rb + gb0
+        sa_, sb_ = sa_ + np.abs(ga0), sb_ + np.abs(gb0)
+    if need[0]:
+        ok, w = oracle.close_scaled(ga, ra, sa_, RTOL)
+        assert ok, f"grad a off by {w:.3g}x tolerance"
+    else:
+        assert ga is None
+    if need[1]:
+        ok, w = oracle.close_scaled(gb, rb, sb_, RTOL)
+        assert ok, f"grad b off by {w:.3g}x tolerance"
+    else:
+        assert gb is None

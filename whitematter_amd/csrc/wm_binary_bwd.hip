@@ -203,8 +203,10 @@ __global__ void __launch_bounds__(kBlock) colsum_finalize_kernel(const float* __
 // ---------------------------------------------------------------------------
 
 // One wave per (row, chunk) item; lanes walk the chunk 4 columns at a time.
-// VEC: C % 4 == 0 and 16-byte aligned bases.
-template <int OP, bool VB, bool VEC>
+// VEC: C % 4 == 0 and 16-byte aligned bases.  FULL (pow with VB only): both
+// gradients are wanted and the forward output is recomputed (not given), so
+// the gradient code carries no runtime flags.
+template <int OP, bool VB, bool VEC, bool FULL = false>
 __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restrict__ g, const float* __restrict__ F,
                                                              const float* __restrict__ V, const float* __restrict__ o,
                                                              float* __restrict__ gF, int accF, float* __restrict__ gV,
@@ -214,15 +216,16 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
     const int lane = threadIdx.x & 63;
     const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
     const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
-    const bool want_v = gV != nullptr;
+    static_assert(!FULL || (OP == WM_POW && VB), "FULL is pow's specialisation");
+    const bool want_v = FULL || gV != nullptr;
     const bool gF_reads_F = VB ? da_reads_a<OP>() : db_reads_b<OP>();
     const bool gF_reads_V = VB ? da_reads_b<OP>() : db_reads_a<OP>();
     const bool gV_reads_F = VB ? db_reads_a<OP>() : da_reads_b<OP>();
     const bool gV_reads_V = VB ? db_reads_b<OP>() : da_reads_a<OP>();
     const bool want_o = VB ? (want_v && db_reads_out<OP>()) : (gF && db_reads_out<OP>());
-    const bool need_o = want_o && o;
-    const bool need_F = (gF && gF_reads_F) || (want_v && gV_reads_F) || (want_o && !o);
-    const bool need_V = (gF && gF_reads_V) || (want_v && gV_reads_V) || (want_o && !o);
+    const bool need_o = !FULL && want_o && o;
+    const bool need_F = FULL || (gF && gF_reads_F) || (want_v && gV_reads_F) || (want_o && !o);
+    const bool need_V = FULL || (gF && gF_reads_V) || (want_v && gV_reads_V) || (want_o && !o);
     for (int64_t item = wave; item < R * K; item += nwaves) {
         const int64_t r = item / K;
         const int64_t k = item - r * K;
@@ -232,7 +235,7 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
         const float* gr = g + r * C;
         const float* fr = F + r * C;
         const float* orow = o + r * C;
-        float* gfr = gF ? gF + r * C : nullptr;
+        float* gfr = (FULL || gF) ? gF + r * C : nullptr;
         float s = 0.f;
         if constexpr (VEC) {
             // kSlots float4 per lane per step (256 columns apart), every load
@@ -285,7 +288,8 @@ __global__ void __launch_bounds__(kBlock) bwd_rowsum_kernel(const float* __restr
                             oh[j] = oo[h + j];
                         }
                         if constexpr (OP == WM_POW && VB)  // one exponent per row
-                            pow_grads_n_exp<kGroup>(gh, ah, v, pq, oh, need_o, gfr != nullptr, want_v, dah, dbh);
+                            pow_grads_n_exp<kGroup>(gh, ah, v, pq, oh, !FULL && need_o, FULL || gfr != nullptr,
+                                                    FULL || want_v, dah, dbh);
                         else
                             binary_grads_n<OP, kGroup>(gh, ah, bh, oh, need_o, VB ? gfr != nullptr : want_v,
                                                        VB ? want_v : gfr != nullptr, dah, dbh);
@@ -591,6 +595,19 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
 #define WM_RS(VBv, VECv)                                                                                          \
     launch_kernel((bwd_rowsum_kernel<OP, VBv, VECv>), grid, dim3(kBlock), 0, st, g, F, V, o, gF, accF, gV, accV, \
                        ws.as<float>(), R, C, chunk, K)
+            if constexpr (OP == WM_POW) {
+                if (vb && vec && gF && gV && !o) {
+                    launch_kernel((bwd_rowsum_kernel<OP, true, true, true>), grid, dim3(kBlock), 0, st, g, F, V, o,
+                                  gF, accF, gV, accV, ws.as<float>(), R, C, chunk, K);
+                    WM_TRY(check_launch("wm_binary_bwd(rowsum)"));
+                    if (K > 1) {
+                        launch_kernel(rowsum_finalize_kernel, dim3(grid_for(R, 1, 8)), dim3(kBlock), 0, st,
+                                      ws.as<float>(), gV, accV, R, K);
+                        WM_TRY(check_launch("wm_binary_bwd(rowsum finalize)"));
+                    }
+                    return WM_OK;
+                }
+            }
             if (vb) { if (vec) WM_RS(true, true); else WM_RS(true, false); }
             else { if (vec) WM_RS(false, true); else WM_RS(false, false); }
 #undef WM_RS
