@@ -220,8 +220,13 @@ __global__ void __launch_bounds__(256) head_bwd_tile_kernel(const float* __restr
     const float scale = loss_grad[0] / (float)rows;
     const int64_t n4 = cols >> 2;
     const int64_t tiles = (n4 + 255) / 256;
+    // rows * tiles < 2^32 (the host falls back to the row kernel otherwise).
+    // The one-hot write (NLL, no loads) divides in 32 bits: 76.9 -> 83.7 %
+    // of the HBM peak against the 64-bit division (~130 instructions per
+    // workgroup); the modes that read the logits measured 2 points slower
+    // with it (cross entropy 78.9 -> 77 %) and keep the 64-bit one.
     for (int64_t item = blockIdx.x; item < rows * tiles; item += gridDim.x) {
-        const int64_t r = item / tiles;
+        const int64_t r = MODE == kOneHot ? (int64_t)((uint32_t)item / (uint32_t)tiles) : item / tiles;
         const int64_t q = (item - r * tiles) * 256 + threadIdx.x;
         const HeadRow h = head_row<MODE>(stats, labels[r], r, cols, scale);
         if (q >= n4) continue;
@@ -509,8 +514,8 @@ int launch_head_bwd(const float* x, const float* labels, const float* stats, con
                     int acc, int64_t rows, int64_t cols, float alpha, const char* what) {
     const bool vec = cols % 4 == 0 && aligned16(gx) && (MODE == kOneHot || aligned16(x));
     dim3 grid((unsigned)std::min<int64_t>(rows, (int64_t)num_cus() * 8));
-    if (vec) {
-        const int64_t tiles = (cols / 4 + 255) / 256;
+    const int64_t tiles = (cols / 4 + 255) / 256;
+    if (vec && rows * tiles < ((int64_t)1 << 32)) {
         launch_kernel((head_bwd_tile_kernel<MODE>), dim3(grid_for(rows * tiles, 1, 1 << 12)), dim3(256), 0,
                       stream(), x, labels, stats, loss_grad, gx, acc, rows, cols, alpha);
     } else
