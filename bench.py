@@ -645,8 +645,29 @@ def cpu_baseline_c5api(sample_rows=256, c=4096, reps=3):
                        f"the same chain, the (h, res) fp16 bits made by the reference's float_to_half", reps)
 
 
+def cpu_baseline_c5(b=32, t=1024, c=4096):
+    """Config 5 has no fused op in the reference: its CPU path is the chain
+    cpu_baseline_c5api times (HalfTensor -> add -> mul -> clamp -> tanh_ ->
+    reshape -> mean and the closures).  The chain's forward and backward
+    times are reported against the fused ops, and value is the fused step's
+    algorithmic bytes over the chain's time, so that value / value is the
+    time ratio."""
+    chain = cpu_baseline_c5api(c=c)
+    rows, N = b * t, b * t * c
+    fwd_b = N * (2 + 2 + 2) + c * F32 + rows * F32           # as c5_ops
+    bwd_b = N * (2 + 2 + 8 + 8) + c * F32 + rows * F32 + 2 * c * F32
+    per = chain["per_op_ms_full"]
+    t_fwd = sum(v for k, v in per.items() if k.endswith("fwd") or k.startswith("HalfTensor"))
+    t_bwd = sum(v for k, v in per.items() if k.endswith("bwd"))
+    return {"value": round((fwd_b + bwd_b) / ((t_fwd + t_bwd) * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "reference",
+            "sample": "the reference's chain for config 5 (no fused op there): " + chain["sample"] +
+                      "; its forward and backward times set against the fused ops",
+            "per_op_ms_full": {"epilogue fwd": round(t_fwd, 3), "epilogue bwd": round(t_bwd, 3)}}
+
+
 CPU_BASELINES = {"c1": cpu_baseline_c1, "c2": cpu_baseline_c2, "c3": cpu_baseline_c3, "c4": cpu_baseline_c4,
-                 "c5api": cpu_baseline_c5api}
+                 "c5": cpu_baseline_c5, "c5api": cpu_baseline_c5api}
 
 
 # ---------------------------------------------------------------------------
