@@ -88,6 +88,53 @@ def test_reduce_nan_and_ties(wm, op):
     assert oracle.bit_equal(val, ref) and np.array_equal(idx, ridx)
 
 
+def special_slices(outer, n, inner, seed):
+    """[outer, n, inner] quantised normals where each (outer, inner) slice is
+    one of: plain, NaN first, NaNs later, signed zeros only, all -inf, all
+    +inf, all NaN, all equal (ties)."""
+    x = quantised((outer, n, inner), seed).reshape(outer, n, inner)
+    rng = np.random.default_rng(seed)
+    kind = rng.integers(0, 8, size=(outer, inner))
+    for o, c in zip(*np.nonzero(kind)):
+        k = kind[o, c]
+        if k == 1:
+            x[o, 0, c] = np.nan
+        elif k == 2 and n > 1:
+            x[o, rng.choice(np.arange(1, n), size=min(3, n - 1), replace=False), c] = np.nan
+        elif k == 3:
+            x[o, :, c] = np.where(rng.integers(0, 2, size=n) == 1, np.float32(-0.0), np.float32(0.0))
+        elif k == 4:
+            x[o, :, c] = -np.inf
+        elif k == 5:
+            x[o, :, c] = np.inf
+        elif k == 6:
+            x[o, :, c] = np.nan
+        elif k == 7:
+            x[o, :, c] = 7.0
+    return x.reshape(-1)
+
+
+@pytest.mark.parametrize("op", ["max", "min", "argmax", "argmin"])
+@pytest.mark.parametrize("view", [
+    (1, 4096, 8),       # float4 columns, split into chunks + second pass
+    (1024, 16, 8),      # float4 columns, one workgroup per column tile
+    (1, 3000, 1024),    # several column tiles, split
+    (2, 100, 520),      # partial last tile (dead lanes), split
+    (512, 300, 1),      # rows, one wave per row
+    (2, 300000, 1),     # long rows, split + second pass
+])
+def test_reduce_special_values(wm, op, view):
+    """Bit-exact values and first-occurrence indices with NaNs, signed zeros,
+    infinities and ties mixed per slice, on every launch shape of the max
+    family: the cross-wave and cross-chunk folds see every kind of state."""
+    outer, n, inner = view
+    x = special_slices(outer, n, inner, outer * 31 + n + inner)
+    val, idx = reduce(op, x, outer, n, inner, want_idx=True)
+    ref, ridx = oracle.get("f32").reduce(op, x, outer, n, inner)
+    assert oracle.bit_equal(val, ref)
+    assert np.array_equal(idx, ridx)
+
+
 @pytest.mark.parametrize("accumulate", [False, True])
 @pytest.mark.parametrize("op", ["sum", "mean", "max", "min"])
 @pytest.mark.parametrize("view", [(1, 1000, 1), (300, 257, 1), (1, 500, 64), (7, 50, 9), (64, 1024, 1)])

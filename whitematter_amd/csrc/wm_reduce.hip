@@ -217,7 +217,7 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
 // position order; the lanes are combined with DPP / shuffles.  Every lane
 // returns the wave's state.
 template <int KIND, bool VEC, class I>
-__device__ __forceinline__ void wave_scan_row(const float* __restrict__ xr, int64_t c0, int64_t c1, int lane,
+__device__ __forceinline__ void lane_scan_row(const float* __restrict__ xr, int64_t c0, int64_t c1, int lane,
                                               float& v_out, I& pos_out) {
     constexpr bool MX = KIND == 1;
     float v = KIND == 0 ? 0.f : scan_init<MX>();
@@ -287,10 +287,32 @@ __device__ __forceinline__ void wave_scan_row(const float* __restrict__ xr, int6
     if constexpr (KIND != 0) {
         if (has0) scan_start<MX>(v, pos, x0);
     }
-    if constexpr (KIND == 0) v = wave_sum((s.x + s.y) + (s.z + s.w));
-    else wave_combine_t<MX>(v, pos);
+    if constexpr (KIND == 0) v = (s.x + s.y) + (s.z + s.w);
     v_out = v;
     pos_out = pos;
+}
+
+// The wave's state: its sum (every lane), or for the max family with 64-bit
+// positions its (value, position) through pairwise combines (every lane).
+template <int KIND, bool VEC, class I>
+__device__ __forceinline__ void wave_scan_row(const float* __restrict__ xr, int64_t c0, int64_t c1, int lane,
+                                              float& v, I& pos) {
+    lane_scan_row<KIND, VEC, I>(xr, c0, c1, lane, v, pos);
+    if constexpr (KIND == 0) v = wave_sum(v);
+    else wave_combine_t<KIND == 1>(v, pos);
+}
+
+// The max family with 32-bit positions: the wave's state as its chunk key
+// (every lane).  The key's order is combine's preference, so the fold is an
+// unsigned maximum: no branches on NaN or emptiness between lanes.
+template <int KIND, bool VEC, class I>
+__device__ __forceinline__ uint64_t wave_scan_row_key(const float* __restrict__ xr, int64_t c0, int64_t c1,
+                                                      int lane) {
+    static_assert(KIND != 0 && sizeof(I) == 4, "keys hold 32-bit positions");
+    float v;
+    I pos;
+    lane_scan_row<KIND, VEC, I>(xr, c0, c1, lane, v, pos);
+    return wave_max_u64(chunk_key<KIND == 1>(v, pos, 0u));
 }
 
 // Two shapes of launch, chosen by K (uniform):
@@ -306,26 +328,51 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __rest
                                                               uint64_t* __restrict__ pk, I* __restrict__ pi) {
     constexpr int KIND = kind_of(OP);
     constexpr bool MX = KIND == 1;
+    constexpr bool KEYED = KIND != 0 && sizeof(I) == 4;  // states fold as chunk keys
     constexpr int NW = kBlock / 64;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (K == 1) {
         const int64_t wave = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
         const int64_t nwaves = ((int64_t)gridDim.x * kBlock) >> 6;
         for (int64_t r = wave; r < rows; r += nwaves) {
+            const float* xr = x + r * n;
             float v;
             I pos;
-            wave_scan_row<KIND, VEC, I>(x + r * n, 0, n, lane, v, pos);
-            if (lane == 0) write_result<OP>(val, idx, r, v, pos, n);
+            if constexpr (KEYED) {
+                // n >= 1, so the row's key is never the empty state's 0.
+                const uint64_t key = wave_scan_row_key<KIND, VEC, I>(xr, 0, n, lane);
+                if (lane == 0) {
+                    decode_winner<MX>(key, (const I*)nullptr, 0, [&](int64_t p) { return xr[p]; }, v, pos);
+                    write_result<OP>(val, idx, r, v, pos, n);
+                }
+            } else {
+                wave_scan_row<KIND, VEC, I>(xr, 0, n, lane, v, pos);
+                if (lane == 0) write_result<OP>(val, idx, r, v, pos, n);
+            }
         }
         return;
     }
     __shared__ float lv[NW];
     __shared__ I li[NW];
+    __shared__ uint64_t lk[NW];
     for (int64_t item = blockIdx.x; item < rows * K; item += gridDim.x) {
         const int64_t r = item / K, k = item - r * K;
         const int64_t c0 = k * chunk, c1 = min(n, c0 + chunk);
         const int64_t q = chunk / NW;  // a multiple of 256
         const int64_t a0 = min(c1, c0 + w * q), a1 = min(c1, a0 + q);
+        if constexpr (KEYED) {
+            const uint64_t key = wave_scan_row_key<KIND, VEC, I>(x + r * n, a0, a1, lane);
+            if (lane == 0) lk[w] = key;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                uint64_t best = lk[0];
+#pragma unroll
+                for (int ww = 1; ww < NW; ++ww) best = lk[ww] > best ? lk[ww] : best;
+                pk[r * K + k] = best;
+            }
+            __syncthreads();  // LDS is reused by the next item
+            continue;
+        }
         float v;
         I pos;
         wave_scan_row<KIND, VEC, I>(x + r * n, a0, a1, lane, v, pos);
@@ -424,34 +471,61 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
     constexpr int W = VEC ? 4 : 1;
     constexpr int NW = kBlock / 64;
     constexpr int U = VEC ? 8 : 4;
-    __shared__ float lv[NW][64 * W];
-    __shared__ I li[KIND != 0 ? NW : 1][KIND != 0 ? 64 * W : 1];
+    constexpr bool KEYED = KIND != 0 && sizeof(I) == 4;  // states fold as chunk keys
+    __shared__ float lv[KEYED ? 1 : NW][KEYED ? 1 : 64 * W];
+    __shared__ I li[KIND != 0 && !KEYED ? NW : 1][KIND != 0 && !KEYED ? 64 * W : 1];
+    __shared__ uint64_t lk[KEYED ? NW : 1][KEYED ? W : 1][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t tile_elems = (int64_t)64 * W;
     const int64_t tiles = (inner + tile_elems - 1) / tile_elems;
     const int64_t items = outer * K * tiles;
 
     // The four wave states (v, pos) -> wave 0 lanes hold the workgroup's
-    // state of their W columns.
+    // state of their W columns (sums, and the max family with 64-bit
+    // positions).
     auto lds_combine = [&](float (&v)[W], I (&pos)[W]) {
+        if constexpr (!KEYED) {  // else lds_keys below
+            __syncthreads();  // earlier LDS reads are done
+#pragma unroll
+            for (int j = 0; j < W; ++j) {
+                lv[w][lane * W + j] = v[j];
+                if constexpr (KIND != 0) li[w][lane * W + j] = pos[j];
+            }
+            __syncthreads();
+            if (w == 0) {
+#pragma unroll
+                for (int j = 0; j < W; ++j) {
+                    if constexpr (KIND == 0) {
+                        v[j] = (lv[0][lane * W + j] + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
+                    } else {
+                        v[j] = lv[0][lane * W + j];
+                        pos[j] = li[0][lane * W + j];
+#pragma unroll
+                        for (int ww = 1; ww < NW; ++ww) combine<MX>(v[j], pos[j], lv[ww][lane * W + j], li[ww][lane * W + j]);
+                    }
+                }
+            }
+        }
+    };
+
+    // The max family with 32-bit positions: the four wave states as chunk
+    // keys, folded by an unsigned maximum (the keys' order is combine's
+    // preference) -> wave 0 lanes hold the workgroup's keys of their W
+    // columns.  Branch-free, where combine's NaN and emptiness tests cost
+    // every workgroup's last wave a few hundred instructions at the end of
+    // its item.
+    auto lds_keys = [&](const float (&v)[W], const I (&pos)[W], uint64_t (&key)[W]) {
         __syncthreads();  // earlier LDS reads are done
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
-            lv[w][lane * W + j] = v[j];
-            if constexpr (KIND != 0) li[w][lane * W + j] = pos[j];
-        }
+        for (int j = 0; j < W; ++j) lk[w][j][lane] = chunk_key<MX>(v[j], pos[j], 0u);
         __syncthreads();
         if (w == 0) {
 #pragma unroll
             for (int j = 0; j < W; ++j) {
-                if constexpr (KIND == 0) {
-                    v[j] = (lv[0][lane * W + j] + lv[1][lane * W + j]) + (lv[2][lane * W + j] + lv[3][lane * W + j]);
-                } else {
-                    v[j] = lv[0][lane * W + j];
-                    pos[j] = li[0][lane * W + j];
+                uint64_t b = lk[0][j][lane];
 #pragma unroll
-                    for (int ww = 1; ww < NW; ++ww) combine<MX>(v[j], pos[j], lv[ww][lane * W + j], li[ww][lane * W + j]);
-                }
+                for (int ww = 1; ww < NW; ++ww) b = lk[ww][j][lane] > b ? lk[ww][j][lane] : b;
+                key[j] = b;
             }
         }
     };
@@ -522,6 +596,27 @@ __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __rest
                     if (has0) scan_start<MX>(v[j], pos[j], x0[j]);
                 }
             }
+        }
+        if constexpr (KEYED) {
+            uint64_t key[W];
+            lds_keys(v, pos, key);
+            if (w == 0) {
+#pragma unroll
+                for (int j = 0; j < W; ++j) {
+                    if (i0 + j >= inner) continue;
+                    if (K == 1) {
+                        // n >= 1, so the column's key is never the empty state's 0.
+                        float rv;
+                        I rp;
+                        decode_winner<MX>(key[j], (const I*)nullptr, 0,
+                                          [&](int64_t pp) { return xp[pp * inner + j]; }, rv, rp);
+                        write_result<OP>(val, idx, o * inner + i0 + j, rv, rp, n);
+                    } else {
+                        pk[(o * K + k) * inner + i0 + j] = key[j];
+                    }
+                }
+            }
+            continue;
         }
         lds_combine(v, pos);
         if (K == 1) {
