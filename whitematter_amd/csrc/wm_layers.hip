@@ -121,8 +121,18 @@ __global__ void __launch_bounds__(NT) ln_fwd_kernel(const float* __restrict__ x,
 
 // pgamma / pbeta: [gridDim.x, n] partials of this workgroup's rows (NULL
 // when that gradient is not wanted).
+//
+// The second __launch_bounds__ argument is HIP's minimum waves per SIMD: a
+// 1024-thread workgroup puts 4 waves on each SIMD, so 8 keeps the kernel
+// within 64 VGPRs and two workgroups resident per CU (one float4 per
+// thread and row; the compiler's own choice, 66, left one: 67 -> 71 % of
+// the HBM peak at [32768, 4096]).  Two float4s per thread need more than
+// 64 without spilling.
+template <int NT, int ITEMS>
+constexpr int ln_bwd_min_waves() { return NT == 1024 && ITEMS == 1 ? 8 : 1; }
+
 template <int NT, int ITEMS, bool VEC>
-__global__ void __launch_bounds__(NT) ln_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
+__global__ void __launch_bounds__(NT, (ln_bwd_min_waves<NT, ITEMS>())) ln_bwd_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                      const float* __restrict__ gamma, const float* __restrict__ mean,
                                                      const float* __restrict__ inv_std, int64_t rows, int64_t n,
                                                      float* __restrict__ gx, int acc, float* __restrict__ pgamma,
