@@ -303,7 +303,11 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
                     v = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
                 }
                 if (P.bias) v = make_float4(v.x + bias4.x, v.y + bias4.y, v.z + bias4.z, v.w + bias4.w);
-                *reinterpret_cast<float4*>(dst) = v;
+                // C is written once: streaming stores keep it from evicting
+                // the A and B panels that the resident tiles re-read from the
+                // caches (bmm at k = 128: 0.188 -> 0.181 ms).
+                if (accum) *reinterpret_cast<float4*>(dst) = v;
+                else st_stream(dst, v);
             } else if (row < P.m) {
                 const float ve[4] = {v.x, v.y, v.z, v.w}, be[4] = {bias4.x, bias4.y, bias4.z, bias4.w};
 #pragma unroll
