@@ -368,8 +368,9 @@ __device__ __forceinline__ void bn_for_chunk(const BnGeom& gm, F&& f) {
     }
 }
 
-// Cached loads: the apply pass reads x again right after, and a tensor that
-// fits the last-level cache is then served from it.
+// Cached loads: the apply pass reads x again right after, and for a tensor
+// of a few tens of MiB part of that re-read then comes from the caches
+// (measured: a re-read of 64 MiB 2-15 % faster, of 192 MiB no faster).
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_stats_kernel(const float* __restrict__ x, BnGeom gm,
                                                         double* __restrict__ part) {
