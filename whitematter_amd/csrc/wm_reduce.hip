@@ -319,8 +319,9 @@ __device__ __forceinline__ uint64_t wave_scan_row_key(const float* __restrict__ 
 //   K == 1  one wave per row: the wave's state is the row's result;
 //   K  > 1  one workgroup per (row, chunk of `chunk` positions): the four
 //           waves take consecutive quarters of the chunk and their states
-//           are combined in wave order through LDS; the workgroup's state is
-//           the chunk's partial, which reduce_rows_finalize_kernel combines.
+//           are combined through LDS (in wave order, or as chunk keys by an
+//           unsigned maximum); the workgroup's state is the chunk's partial,
+//           which reduce_rows_finalize_kernel combines.
 template <int OP, bool VEC, class I>
 __global__ void __launch_bounds__(kBlock) reduce_rows_kernel(const float* __restrict__ x, int64_t rows, int64_t n,
                                                               int64_t chunk, int64_t K, float* __restrict__ val,
@@ -454,12 +455,15 @@ __global__ void __launch_bounds__(kBlock) reduce_rows_finalize_kernel(const floa
 // loads) of output row o, so a wave reads 64*W contiguous floats per position
 // of n.  The workgroup's 4 waves take four contiguous quarters of the chunk
 // [k0, k1) of n, each walking its quarter in increasing order with U loads
-// in flight; the four wave states are combined in wave order through LDS.
+// in flight; the four wave states are combined through LDS (sums in wave
+// order; the max family with 32-bit positions as chunk keys by an unsigned
+// maximum, with 64-bit positions by pairwise combines in wave order).
 // Items are (o, chunk, inner tile) triples, tile fastest; every thread of a
 // workgroup walks the same items, so the barriers are uniform.
 //
-// With K > 1 chunks the workgroup's state is a partial (value and I-typed
-// position per column) that reduce_cols_finalize_kernel combines.
+// With K > 1 chunks the workgroup's state is a partial per column (a sum, or
+// the chunk key plus, for 64-bit positions, the position) that
+// reduce_cols_finalize_kernel combines.
 template <int OP, bool VEC, class I>
 __global__ void __launch_bounds__(kBlock) reduce_cols_kernel(const float* __restrict__ x, int64_t outer, int64_t n,
                                                               int64_t inner, int64_t chunk, int64_t K,
