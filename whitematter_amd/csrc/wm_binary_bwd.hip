@@ -540,8 +540,12 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
         const bool colvec = (nd == 2 && sv[0] == 1 && sv[1] == 0) || (nd == 1 && sv[0] == 0);
         if (rowvec && C % 4 == 0 && aligned) {
             const int64_t col_tiles = (C + kBlock * 4 - 1) / (kBlock * 4);
-            // ~1024 workgroups (4 per CU), each group of at least 16 rows
-            int64_t K = std::min<int64_t>((1024 + col_tiles - 1) / col_tiles, (R + 15) / 16);
+            // ~1024 workgroups (4 per CU), each group of at least 4 rows (a
+            // thread walks its group's rows one at a time, so a small R needs
+            // many groups: at R = C = 1024 the column pass took 12 µs with
+            // groups of 16 rows, 6 µs with 4; a large R reaches the 1024
+            // first)
+            int64_t K = std::min<int64_t>((1024 + col_tiles - 1) / col_tiles, (R + 3) / 4);
             K = std::max<int64_t>(1, std::min<int64_t>(K, 65535));
             Workspace ws(gV ? (size_t)(K * C) * sizeof(float) : 0);
             if (gV && !ws.p) return set_error(WM_ERR_NOMEM, "wm_binary_bwd: workspace");
