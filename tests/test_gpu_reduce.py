@@ -120,6 +120,8 @@ def special_slices(outer, n, inner, seed):
     (1024, 16, 8),      # float4 columns, one workgroup per column tile
     (1, 3000, 1024),    # several column tiles, split
     (2, 100, 520),      # partial last tile (dead lanes), split
+    (64, 50, 7),        # scalar columns, one workgroup per column tile
+    (1, 3000, 7),       # scalar columns, split
     (512, 300, 1),      # rows, one wave per row
     (2, 300000, 1),     # long rows, split + second pass
 ])
