@@ -251,6 +251,15 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
 // 0 = one value per row).  VEC: inner % 4 == 0 and 16-byte aligned bases.
 // SA/SB: the operand is streamed (read once: it has a row stride), else it
 // is a row vector reused by every row and stays on cached loads.
+//
+// A matrix with a row vector (one outer dim, one operand's row stride 0,
+// rows even) takes items of kRowPair rows instead: the row vector's float4 is
+// loaded once for both rows and the item bookkeeping is shared (config 2:
+// A + r forward 77.3 -> 80.6 %, A / r 74.8 -> 81 % of the HBM peak).
+template <int OP, int AI, int BI, bool VEC>
+constexpr bool row_pairs() { return OP != WM_POW && VEC && AI == 1 && BI == 1; }
+constexpr int kRowPair = 2;
+
 template <int OP, int AI, int BI, bool VEC>
 __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
     binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b, int64_t rows,
@@ -258,6 +267,9 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
     binary_prologue<OP>();
     constexpr int U = fwd_unroll<OP>();
     constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * U;
+    const bool pairs = row_pairs<OP, AI, BI, VEC>() && d.nd == 1 && (d.sa[0] == 0 || d.sb[0] == 0) &&
+                       rows % kRowPair == 0;
+    const int64_t items_rows = pairs ? rows / kRowPair : rows;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
     // Grid-stride over (row, tile) pairs, advanced incrementally so the loop
     // itself divides nothing (a 64-bit division costs ~40 instructions).
@@ -265,9 +277,42 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
     const int64_t step_tiles = (int64_t)gridDim.x - step_rows * tiles_per_row;
     int64_t row = (int64_t)blockIdx.x / tiles_per_row;
     int64_t tile = (int64_t)blockIdx.x - row * tiles_per_row;
-    for (; row < rows; row += step_rows, tile += step_tiles) {
-        if (tile >= tiles_per_row) { tile -= tiles_per_row; ++row; if (row >= rows) break; }
+    for (; row < items_rows; row += step_rows, tile += step_tiles) {
+        if (tile >= tiles_per_row) { tile -= tiles_per_row; ++row; if (row >= items_rows) break; }
         const int64_t c0 = tile * kTile;
+        if constexpr (row_pairs<OP, AI, BI, VEC>()) {
+            if (pairs) {
+                // Rows kRowPair*row .. +kRowPair-1; v is the row vector's float4,
+                // s the streamed operand's of each row.
+                const bool a_vec = d.sa[0] == 0;
+                const float* sbase = a_vec ? b : a;
+                const int64_t sstride = a_vec ? d.sb[0] : d.sa[0];
+                float4 vr[kRowPair][U], va[kRowPair][U], vb[kRowPair][U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (c < inner) v = *reinterpret_cast<const float4*>((a_vec ? a : b) + c);
+#pragma unroll
+                    for (int q = 0; q < kRowPair; ++q) {
+                        float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (c < inner) sv = ld_stream(sbase + (row * kRowPair + q) * sstride + c);
+                        va[q][u] = a_vec ? v : sv;
+                        vb[q][u] = a_vec ? sv : v;
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < kRowPair; ++q) binary_fwd_v<OP, U>(vr[q], va[q], vb[q]);
+#pragma unroll
+                for (int q = 0; q < kRowPair; ++q)
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                        if (c < inner) st_stream(out + (row * kRowPair + q) * inner + c, vr[q][u]);
+                    }
+                continue;
+            }
+        }
         int64_t oa, ob;
         row_offsets(d, row, oa, ob);
         const float* ar = a + oa;
@@ -451,6 +496,9 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
         int64_t tile = (vec ? 4 : 1) * kBlock * fwd_unroll<OP>();
         int64_t tiles = rows * ((inner + tile - 1) / tile);
+        // Row pairs (binary_rows_kernel): half the items.
+        if (OP != WM_POW && vec && ia && ib && nd == 2 && (L.sa[0] == 0 || L.sb[0] == 0) && rows % kRowPair == 0)
+            tiles /= kRowPair;
         dim3 grid(grid_for(tiles, 1, fwd_grid_cap<OP>()));
         // An operand with a row stride is read once; a row vector is re-read by every row.
         int stream_a = 0, stream_b = 0;
