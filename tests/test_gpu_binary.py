@@ -39,6 +39,11 @@ SHAPES = [
     ((8, 6000), (8, 1)),             # ... 1024 threads
     ((40, 1), (40, 2048)),           # column vector on the left
     ((8, 8196), (8, 1)),             # beyond one workgroup's row: the wave kernel
+    ((6, 8192), (1, 8192)),          # row vector, rows of >= 8192 floats: two rows per item
+    ((4, 8196), (8196,)),            # ... with a partial last tile
+    ((1, 8192), (6, 8192)),          # ... row vector on the left
+    ((6, 1), (6, 8192)),             # ... column vector on the left
+    ((7, 8192), (1, 8192)),          # odd row count: single rows
     ((0, 16), (16,)),                # empty
 ]
 

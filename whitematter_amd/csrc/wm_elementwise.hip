@@ -252,24 +252,34 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
 // SA/SB: the operand is streamed (read once: it has a row stride), else it
 // is a row vector reused by every row and stays on cached loads.
 //
-// A matrix with a row vector (one outer dim, one operand's row stride 0,
-// rows even) takes items of kRowPair rows instead: the row vector's float4 is
-// loaded once for both rows and the item bookkeeping is shared (config 2:
-// A + r forward 77.3 -> 80.6 %, A / r 74.8 -> 81 % of the HBM peak).
+// With one outer dim, an even row count and rows of at least kPairMinInner
+// floats, a matrix with a row vector or a column vector takes items of
+// kRowPair rows instead: the item bookkeeping (row and tile indices, operand
+// offsets) is shared by both rows and a row vector's float4 is loaded once
+// for them.  Measured on 256 MiB operands: config 2 ([8192, 8192]) A + r
+// forward 77.3 -> 81 %, A / r 74.8 -> 81 %, A * c 77 -> 81 % of the HBM
+// peak, and 80.2 -> 81.9 % for a row vector at [4096, 16384]; with rows of
+// 1024-4096 floats the pairs ran 1-3 points slower than single rows, which
+// they keep.  pow keeps single rows (its own launch shape).
+//   AI = BI = 1: one operand has row stride 0 (the row vector);
+//   one of AI, BI = 0: that operand is one value per row (a column vector).
 template <int OP, int AI, int BI, bool VEC>
-constexpr bool row_pairs() { return OP != WM_POW && VEC && AI == 1 && BI == 1; }
+constexpr bool row_pairs() { return OP != WM_POW && VEC && (AI == 1 || BI == 1); }
 constexpr int kRowPair = 2;
+constexpr int64_t kPairMinInner = 8192;
 
-template <int OP, int AI, int BI, bool VEC>
+// PAIRS: the row-pair form (the host checks use_row_pairs; a separate
+// instantiation, because the pair code compiled into the single-row kernel
+// slowed its own rows: a row vector at [16384, 4096] 77.7 -> 74.5 %).
+template <int OP, int AI, int BI, bool VEC, bool PAIRS>
 __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
     binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b, int64_t rows,
                        int64_t inner, RowDims d, int stream_a, int stream_b) {
+    static_assert(!PAIRS || row_pairs<OP, AI, BI, VEC>(), "row pairs: not for this operand layout");
     binary_prologue<OP>();
     constexpr int U = fwd_unroll<OP>();
     constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * U;
-    const bool pairs = row_pairs<OP, AI, BI, VEC>() && d.nd == 1 && (d.sa[0] == 0 || d.sb[0] == 0) &&
-                       rows % kRowPair == 0;
-    const int64_t items_rows = pairs ? rows / kRowPair : rows;
+    const int64_t items_rows = PAIRS ? rows / kRowPair : rows;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
     // Grid-stride over (row, tile) pairs, advanced incrementally so the loop
     // itself divides nothing (a 64-bit division costs ~40 instructions).
@@ -280,25 +290,48 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
     for (; row < items_rows; row += step_rows, tile += step_tiles) {
         if (tile >= tiles_per_row) { tile -= tiles_per_row; ++row; if (row >= items_rows) break; }
         const int64_t c0 = tile * kTile;
-        if constexpr (row_pairs<OP, AI, BI, VEC>()) {
-            if (pairs) {
-                // Rows kRowPair*row .. +kRowPair-1; v is the row vector's float4,
-                // s the streamed operand's of each row.
-                const bool a_vec = d.sa[0] == 0;
-                const float* sbase = a_vec ? b : a;
-                const int64_t sstride = a_vec ? d.sb[0] : d.sa[0];
+        if constexpr (PAIRS) {
+            {
+                // Rows kRowPair*row .. +kRowPair-1.
                 float4 vr[kRowPair][U], va[kRowPair][U], vb[kRowPair][U];
+                if constexpr (AI == 1 && BI == 1) {
+                    // v: the row vector's float4; sv: the streamed operand's, per row
+                    const bool a_vec = d.sa[0] == 0;
+                    const float* sbase = a_vec ? b : a;
+                    const int64_t sstride = a_vec ? d.sb[0] : d.sa[0];
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
-                    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (c < inner) v = *reinterpret_cast<const float4*>((a_vec ? a : b) + c);
+                    for (int u = 0; u < U; ++u) {
+                        const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+                        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (c < inner) v = *reinterpret_cast<const float4*>((a_vec ? a : b) + c);
 #pragma unroll
-                    for (int q = 0; q < kRowPair; ++q) {
-                        float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
-                        if (c < inner) sv = ld_stream(sbase + (row * kRowPair + q) * sstride + c);
-                        va[q][u] = a_vec ? v : sv;
-                        vb[q][u] = a_vec ? sv : v;
+                        for (int q = 0; q < kRowPair; ++q) {
+                            float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+                            if (c < inner) sv = ld_stream(sbase + (row * kRowPair + q) * sstride + c);
+                            va[q][u] = a_vec ? v : sv;
+                            vb[q][u] = a_vec ? sv : v;
+                        }
+                    }
+                } else {
+                    // One operand streamed (S*), the other one value per row (C*).
+                    const float* sbase = AI ? a : b;
+                    const float* cbase = AI ? b : a;
+                    const int64_t sstride = AI ? d.sa[0] : d.sb[0];
+                    const int64_t cstride = AI ? d.sb[0] : d.sa[0];
+                    float cv[kRowPair];
+#pragma unroll
+                    for (int q = 0; q < kRowPair; ++q) cv[q] = cbase[(row * kRowPair + q) * cstride];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
+#pragma unroll
+                        for (int q = 0; q < kRowPair; ++q) {
+                            float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+                            if (c < inner) sv = ld_stream(sbase + (row * kRowPair + q) * sstride + c);
+                            const float4 v = make_float4(cv[q], cv[q], cv[q], cv[q]);
+                            va[q][u] = AI ? sv : v;
+                            vb[q][u] = AI ? v : sv;
+                        }
                     }
                 }
 #pragma unroll
@@ -310,9 +343,8 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
                         const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * 4;
                         if (c < inner) st_stream(out + (row * kRowPair + q) * inner + c, vr[q][u]);
                     }
-                continue;
             }
-        }
+        } else {
         int64_t oa, ob;
         row_offsets(d, row, oa, ob);
         const float* ar = a + oa;
@@ -347,6 +379,7 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
                 if (c < inner) orow[c] = binary_fwd<OP>(ar[AI ? c : 0], br[BI ? c : 0]);
             }
         }
+        }  // single rows
     }
 }
 
@@ -497,8 +530,9 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         int64_t tile = (vec ? 4 : 1) * kBlock * fwd_unroll<OP>();
         int64_t tiles = rows * ((inner + tile - 1) / tile);
         // Row pairs (binary_rows_kernel): half the items.
-        if (OP != WM_POW && vec && ia && ib && nd == 2 && (L.sa[0] == 0 || L.sb[0] == 0) && rows % kRowPair == 0)
-            tiles /= kRowPair;
+        const bool pairs = OP != WM_POW && vec && (ia || ib) && nd == 2 && rows % kRowPair == 0 &&
+                           inner >= kPairMinInner && (!ia || !ib || L.sa[0] == 0 || L.sb[0] == 0);
+        if (pairs) tiles /= kRowPair;
         dim3 grid(grid_for(tiles, 1, fwd_grid_cap<OP>()));
         // An operand with a row stride is read once; a row vector is re-read by every row.
         int stream_a = 0, stream_b = 0;
@@ -507,19 +541,27 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
             if (L.sb[i] != 0) stream_b = 1;
         }
         if (nd == 1) stream_a = stream_b = 1;
-#define WM_ROWS(AI, BI, V) \
-    launch_kernel((binary_rows_kernel<OP, AI, BI, V>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
+#define WM_ROWS(AI, BI, V, P) \
+    launch_kernel((binary_rows_kernel<OP, AI, BI, V, P>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
                        stream_a, stream_b)
         if (vec) {
-            if (ia && ib) WM_ROWS(1, 1, true);
-            else if (ia) WM_ROWS(1, 0, true);
-            else if (ib) WM_ROWS(0, 1, true);
-            else WM_ROWS(0, 0, true);
+            if constexpr (OP != WM_POW) {
+                if (pairs) {
+                    if (ia && ib) WM_ROWS(1, 1, true, true);
+                    else if (ia) WM_ROWS(1, 0, true, true);
+                    else WM_ROWS(0, 1, true, true);
+                    return check_launch("wm_binary(rows)");
+                }
+            }
+            if (ia && ib) WM_ROWS(1, 1, true, false);
+            else if (ia) WM_ROWS(1, 0, true, false);
+            else if (ib) WM_ROWS(0, 1, true, false);
+            else WM_ROWS(0, 0, true, false);
         } else {
-            if (ia && ib) WM_ROWS(1, 1, false);
-            else if (ia) WM_ROWS(1, 0, false);
-            else if (ib) WM_ROWS(0, 1, false);
-            else WM_ROWS(0, 0, false);
+            if (ia && ib) WM_ROWS(1, 1, false, false);
+            else if (ia) WM_ROWS(1, 0, false, false);
+            else if (ib) WM_ROWS(0, 1, false, false);
+            else WM_ROWS(0, 0, false, false);
         }
 #undef WM_ROWS
         return check_launch("wm_binary(rows)");
