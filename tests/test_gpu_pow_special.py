@@ -65,9 +65,11 @@ def test_pow_special_flat(wm, pad):
     check_fwd(binary_fwd("pow", a, b), a, b)
 
 
-@pytest.mark.parametrize("pad", [0, 1, 4052])
+@pytest.mark.parametrize("pad", [0, 1, 4052, 8148, 8152])
 def test_pow_special_column_exponent(wm, pad):
-    """b is a column vector [m, 1]: the row-broadcast kernel (cached b)."""
+    """b is a column vector [m, 1]: the row-broadcast kernel (cached b);
+    rows of 8192 and 8196 floats (an even row count) take its two-row
+    items."""
     a, b = grid(pad)
     bc = np.ascontiguousarray(b[:, :1])
     check_fwd(binary_fwd("pow", a, bc), a, bc)

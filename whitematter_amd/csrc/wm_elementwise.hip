@@ -260,24 +260,40 @@ __global__ void __launch_bounds__(kBlock) binary_flat_kernel(float* __restrict__
 // forward 77.3 -> 81 %, A / r 74.8 -> 81 %, A * c 77 -> 81 % of the HBM
 // peak, and 80.2 -> 81.9 % for a row vector at [4096, 16384]; with rows of
 // 1024-4096 floats the pairs ran 1-3 points slower than single rows, which
-// they keep.  pow keeps single rows (its own launch shape).
+// they keep.  pow pairs only with one exponent per row (A^c): one float4 per
+// row instead of its single rows' two, at 7 waves per SIMD (72 VGPRs, no
+// spills) on the same 32 workgroups per CU, 69.5 -> 72.0-72.4 % at config 2
+// (pairs at 6 waves: 71 %; caps of 16-40 workgroups per CU within the
+// spread, 64 and the whole-tensor grid 67 and 62 %).
 //   AI = BI = 1: one operand has row stride 0 (the row vector);
 //   one of AI, BI = 0: that operand is one value per row (a column vector).
 template <int OP, int AI, int BI, bool VEC>
-constexpr bool row_pairs() { return OP != WM_POW && VEC && (AI == 1 || BI == 1); }
+constexpr bool row_pairs() {
+    return VEC && (OP != WM_POW ? (AI == 1 || BI == 1) : (AI == 1 && BI == 0));
+}
 constexpr int kRowPair = 2;
 constexpr int64_t kPairMinInner = 8192;
 
-// PAIRS: the row-pair form (the host checks use_row_pairs; a separate
-// instantiation, because the pair code compiled into the single-row kernel
-// slowed its own rows: a row vector at [16384, 4096] 77.7 -> 74.5 %).
 template <int OP, int AI, int BI, bool VEC, bool PAIRS>
-__global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
+constexpr int rows_min_waves() {
+    return BI != 0 ? 1 : (PAIRS && OP == WM_POW) ? 7 : fwd_min_blocks<OP>();
+}
+// Float4s per row and thread of a tile.
+template <int OP, bool PAIRS>
+constexpr int rows_unroll() {
+    return PAIRS && OP == WM_POW ? 1 : fwd_unroll<OP>();
+}
+
+// PAIRS: the row-pair form (the host decides it, as row_pairs allows; a
+// separate instantiation, because the pair code compiled into the single-row
+// kernel slowed its own rows: a row vector at [16384, 4096] 77.7 -> 74.5 %).
+template <int OP, int AI, int BI, bool VEC, bool PAIRS>
+__global__ void __launch_bounds__(kBlock, (rows_min_waves<OP, AI, BI, VEC, PAIRS>()))
     binary_rows_kernel(float* __restrict__ out, const float* __restrict__ a, const float* __restrict__ b, int64_t rows,
                        int64_t inner, RowDims d, int stream_a, int stream_b) {
     static_assert(!PAIRS || row_pairs<OP, AI, BI, VEC>(), "row pairs: not for this operand layout");
     binary_prologue<OP>();
-    constexpr int U = fwd_unroll<OP>();
+    constexpr int U = rows_unroll<OP, PAIRS>();
     constexpr int64_t kTile = (VEC ? 4 : 1) * kBlock * U;
     const int64_t items_rows = PAIRS ? rows / kRowPair : rows;
     const int64_t tiles_per_row = (inner + kTile - 1) / kTile;
@@ -334,8 +350,13 @@ __global__ void __launch_bounds__(kBlock, BI == 0 ? fwd_min_blocks<OP>() : 1)
                         }
                     }
                 }
+                if constexpr (OP == WM_POW) {
+                    static_assert(kRowPair == 2 && U == 1, "pow pairs: one float4 of each of two rows");
+                    pow_fwd_pair(vr[0][0], vr[1][0], va[0][0], va[1][0], vb[0][0].x, vb[1][0].x);
+                } else {
 #pragma unroll
-                for (int q = 0; q < kRowPair; ++q) binary_fwd_v<OP, U>(vr[q], va[q], vb[q]);
+                    for (int q = 0; q < kRowPair; ++q) binary_fwd_v<OP, U>(vr[q], va[q], vb[q]);
+                }
 #pragma unroll
                 for (int q = 0; q < kRowPair; ++q)
 #pragma unroll
@@ -527,11 +548,12 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
         }
         // float4 path: every row start is a multiple of 4 floats when inner is.
         bool vec = (inner % 4) == 0 && aligned16(out) && aligned16(a) && aligned16(b);
-        int64_t tile = (vec ? 4 : 1) * kBlock * fwd_unroll<OP>();
-        int64_t tiles = rows * ((inner + tile - 1) / tile);
-        // Row pairs (binary_rows_kernel): half the items.
-        const bool pairs = OP != WM_POW && vec && (ia || ib) && nd == 2 && rows % kRowPair == 0 &&
+        // Row pairs (binary_rows_kernel; pow only with one exponent per row):
+        // half the items.
+        const bool pairs = vec && (OP != WM_POW ? (ia || ib) : (ia && !ib)) && nd == 2 && rows % kRowPair == 0 &&
                            inner >= kPairMinInner && (!ia || !ib || L.sa[0] == 0 || L.sb[0] == 0);
+        const int64_t tile = (vec ? 4 : 1) * kBlock * (pairs ? rows_unroll<OP, true>() : fwd_unroll<OP>());
+        int64_t tiles = rows * ((inner + tile - 1) / tile);
         if (pairs) tiles /= kRowPair;
         dim3 grid(grid_for(tiles, 1, fwd_grid_cap<OP>()));
         // An operand with a row stride is read once; a row vector is re-read by every row.
@@ -545,7 +567,12 @@ int launch_binary(float* out, const float* a, const float* b, const BcastLayout&
     launch_kernel((binary_rows_kernel<OP, AI, BI, V, P>), grid, dim3(kBlock), 0, s, out, a, b, rows, inner, d, \
                        stream_a, stream_b)
         if (vec) {
-            if constexpr (OP != WM_POW) {
+            if constexpr (OP == WM_POW) {
+                if (pairs) {
+                    WM_ROWS(1, 0, true, true);
+                    return check_launch("wm_binary(rows)");
+                }
+            } else {
                 if (pairs) {
                     if (ia && ib) WM_ROWS(1, 1, true, true);
                     else if (ia) WM_ROWS(1, 0, true, true);

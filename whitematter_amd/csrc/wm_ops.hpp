@@ -262,6 +262,32 @@ __device__ __forceinline__ void pow_fwd_v_exp(float4 (&r)[U], const float4 (&a)[
     }
 }
 
+// pow over the float4s of two rows, each row with its own exponent (y0 for
+// a0, y1 for a1): pow_fwd_v_exp<1> of each, with one special-operand branch
+// for both.  Bit for bit equal to binary_fwd_v with b = y0 / y1.
+__device__ __forceinline__ void pow_fwd_pair(float4& r0, float4& r1, const float4& a0, const float4& a1, float y0,
+                                             float y1) {
+    const PowExponent e0 = pow_exponent(y0), e1 = pow_exponent(y1);
+    r0 = make_float4(pow_table_exp(a0.x, e0), pow_table_exp(a0.y, e0), pow_table_exp(a0.z, e0),
+                     pow_table_exp(a0.w, e0));
+    r1 = make_float4(pow_table_exp(a1.x, e1), pow_table_exp(a1.y, e1), pow_table_exp(a1.z, e1),
+                     pow_table_exp(a1.w, e1));
+    const bool f0 = pow_needs_fix_exp(a0.x, e0) || pow_needs_fix_exp(a0.y, e0) || pow_needs_fix_exp(a0.z, e0) ||
+                    pow_needs_fix_exp(a0.w, e0);
+    const bool f1 = pow_needs_fix_exp(a1.x, e1) || pow_needs_fix_exp(a1.y, e1) || pow_needs_fix_exp(a1.z, e1) ||
+                    pow_needs_fix_exp(a1.w, e1);
+    if (f0 || f1) {
+        if (pow_needs_fix_exp(a0.x, e0)) r0.x = powf(a0.x, y0);
+        if (pow_needs_fix_exp(a0.y, e0)) r0.y = powf(a0.y, y0);
+        if (pow_needs_fix_exp(a0.z, e0)) r0.z = powf(a0.z, y0);
+        if (pow_needs_fix_exp(a0.w, e0)) r0.w = powf(a0.w, y0);
+        if (pow_needs_fix_exp(a1.x, e1)) r1.x = powf(a1.x, y1);
+        if (pow_needs_fix_exp(a1.y, e1)) r1.y = powf(a1.y, y1);
+        if (pow_needs_fix_exp(a1.z, e1)) r1.z = powf(a1.z, y1);
+        if (pow_needs_fix_exp(a1.w, e1)) r1.w = powf(a1.w, y1);
+    }
+}
+
 // unary_fwd over U float4s; pow(x, p0) through pow_fwd_v_exp.
 template <int OP, int U>
 __device__ __forceinline__ void unary_fwd_v(float4 (&r)[U], const float4 (&x)[U], float p0, float p1) {
