@@ -263,8 +263,8 @@ def c5api_ops(b=32, t=1024, c=4096):
     """Config 5 as a caller of the drop-in Tensor API issues it (core/amp.h
     HalfTensor, core/tensor.h ops): every op materialises its fp32 output, as
     the reference's do, and every closure is timed on its own after the
-    upstream gradient dm is injected (y->grad = dm; y->grad_fn(), SURVEY's
-    injection rule).  Intermediate gradients start known-zero each step, so
+    upstream gradient dm is injected (y->grad = dm; y->grad_fn(), which
+    equals backward() from the scalar (y * dm).sum()).  Intermediate gradients start known-zero each step, so
     each closure's first contribution is written without a read."""
     from whitematter_amd import _tensor as T
     h, res, g, dm = synth.config5(b, t, c)

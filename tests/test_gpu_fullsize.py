@@ -269,7 +269,7 @@ def test_c5_tensor_api_chain(wm):
     HalfTensor :256-286, then core/tensor.cpp add :897, mul :1063 (row
     broadcast of g), clamp :1524, tanh_ :1302, reshape :2250, mean :1709,
     reshape), at full size, forward and every closure of the backward with
-    the upstream gradient injected at the root (SURVEY's injection rule).
+    the upstream gradient injected at the root (y->grad = dm; y->grad_fn()).
     Forward: fp16 storage bit-exact, add / mul / clamp bit-exact IEEE fp32,
     tanh within 2 ulp of fp64, the mean within the sums contract; backward:
     every gradient within 1e-5 of the fp64 closed form (the mean's gradient

@@ -202,9 +202,9 @@ def test_matrix_ops_through_the_api(T):
 
 
 def test_host_pointer_contract(tmp_path):
-    """The drop-in's host-pointer contract,
-    through the reference's class API in C++: a non-const data() / begin()
-    pointer is valid until the next device operation on the vector."""
+    """The drop-in's host-pointer contract, through the reference's class
+    API in C++: a non-const data() / begin() pointer is valid until the next
+    device operation on the vector."""
     import os
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
