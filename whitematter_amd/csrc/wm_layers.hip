@@ -201,10 +201,16 @@ __global__ void __launch_bounds__(NT, (ln_bwd_min_waves<NT, ITEMS>())) ln_bwd_ke
 
 // Column sums of [parts, n] partials: out[c] (+)= sum_w part[w][c], w in
 // order.  64 columns per workgroup; the 4 waves take every 4th partial row
-// and combine in LDS.
-__global__ void __launch_bounds__(256) colsum_parts_kernel(const float* __restrict__ part, int64_t parts, int64_t n,
-                                                            float* __restrict__ out, int acc) {
+// and combine in LDS.  blockIdx.z picks one of two independent sums (the
+// weight and bias gradients share the launch).
+__global__ void __launch_bounds__(256) colsum_parts_kernel(const float* __restrict__ part0,
+                                                            const float* __restrict__ part1, int64_t parts, int64_t n,
+                                                            float* __restrict__ out0, float* __restrict__ out1,
+                                                            int acc0, int acc1) {
     __shared__ float lds[4][64];
+    const float* part = blockIdx.z ? part1 : part0;
+    float* out = blockIdx.z ? out1 : out0;
+    const int acc = blockIdx.z ? acc1 : acc0;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t c = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.f;
@@ -218,14 +224,18 @@ __global__ void __launch_bounds__(256) colsum_parts_kernel(const float* __restri
     }
 }
 
-// First stage for many partial rows: workgroup (x, y) sums partial rows
-// [y * chunk, (y + 1) * chunk) of 64 columns into out2[y][c]; each wave takes
-// every 4th row with four independent accumulators (loads in flight), the
-// waves combine in LDS in a fixed order.  colsum_parts_kernel then sums the
-// out2 rows.
-__global__ void __launch_bounds__(256) colsum_stage_kernel(const float* __restrict__ part, int64_t parts, int64_t n,
-                                                            int64_t chunk, float* __restrict__ out2) {
+// First stage for many partial rows: workgroup (x, y, z) sums partial rows
+// [y * chunk, (y + 1) * chunk) of 64 columns of sum z into out2_z[y][c]; each
+// wave takes every 4th row with four independent accumulators (loads in
+// flight), the waves combine in LDS in a fixed order.  colsum_parts_kernel
+// then sums the out2 rows.
+__global__ void __launch_bounds__(256) colsum_stage_kernel(const float* __restrict__ part0,
+                                                            const float* __restrict__ part1, int64_t parts, int64_t n,
+                                                            int64_t chunk, float* __restrict__ out2_0,
+                                                            float* __restrict__ out2_1) {
     __shared__ float lds[4][64];
+    const float* part = blockIdx.z ? part1 : part0;
+    float* out2 = blockIdx.z ? out2_1 : out2_0;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t c = (int64_t)blockIdx.x * 64 + lane;
     const int64_t p0 = (int64_t)blockIdx.y * chunk;
@@ -246,22 +256,36 @@ __global__ void __launch_bounds__(256) colsum_stage_kernel(const float* __restri
     if (w == 0 && c < n) out2[(int64_t)blockIdx.y * n + c] = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
 }
 
-// Column sums of [parts, n] partial rows into out (+= when acc): one pass
-// for up to 64 rows, else colsum_stage_kernel first.
-int colsum_parts(const float* part, int64_t parts, int64_t n, float* out, int acc, const char* what) {
+// Column sums of [parts, n] partial rows into out_g and out_b (+= when
+// acc_*; a null partial array skips its sum): one pass for up to 64 rows,
+// else colsum_stage_kernel first.  Both sums share each launch, so the
+// weight and bias gradients cost two dispatches, not four (LayerNorm
+// backward at [32768, 4096]: 283.5-284.1 -> 278.0-280.8 us).
+int colsum_parts(const float* part_g, float* out_g, int acc_g, const float* part_b, float* out_b, int acc_b,
+                 int64_t parts, int64_t n, const char* what) {
     hipStream_t st = stream();
-    const dim3 cg((unsigned)((n + 63) / 64));
+    if (!part_g) {  // the bias sum alone: slot 0
+        part_g = part_b; out_g = out_b; acc_g = acc_b;
+        part_b = nullptr;
+    }
+    if (!part_g) return WM_OK;
+    const unsigned jobs = part_b ? 2u : 1u;
+    const dim3 cg((unsigned)((n + 63) / 64), 1u, jobs);
     if (parts <= 64) {
-        launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, part, parts, n, out, acc);
+        launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, part_g, part_b, parts, n, out_g, out_b, acc_g,
+                      acc_b);
         return check_launch(what);
     }
     const int64_t chunk = 64, parts2 = (parts + chunk - 1) / chunk;
-    Workspace w2((size_t)(parts2 * n) * sizeof(float));
+    Workspace w2((size_t)(jobs * parts2 * n) * sizeof(float));
     if (!w2.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
-    launch_kernel(colsum_stage_kernel, dim3(cg.x, (unsigned)parts2), dim3(256), 0, st, part, parts, n, chunk,
-                       w2.as<float>());
+    float* s0 = w2.as<float>();
+    float* s1 = jobs == 2 ? s0 + parts2 * n : nullptr;
+    launch_kernel(colsum_stage_kernel, dim3(cg.x, (unsigned)parts2, jobs), dim3(256), 0, st, part_g, part_b, parts,
+                  n, chunk, s0, s1);
     WM_TRY(check_launch(what));
-    launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, w2.as<float>(), parts2, n, out, acc);
+    launch_kernel(colsum_parts_kernel, cg, dim3(256), 0, st, (const float*)s0, (const float*)s1, parts2, n, out_g,
+                  out_b, acc_g, acc_b);
     return check_launch(what);
 }
 
@@ -812,9 +836,8 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
         launch_kernel(ln_param_parts_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)chunks), dim3(256), 0,
                            st, g, x, mean, inv, rows, n, rpc, wg.as<float>(), wb.as<float>());
         WM_TRY(check_launch("wm_layernorm_bwd(params)"));
-        if (dgamma) WM_TRY(colsum_parts(wg.as<float>(), chunks, n, dgamma, acc_g, "wm_layernorm_bwd(colsum)"));
-        if (dbeta) WM_TRY(colsum_parts(wb.as<float>(), chunks, n, dbeta, acc_b, "wm_layernorm_bwd(colsum)"));
-        return WM_OK;
+        return colsum_parts(dgamma ? wg.as<float>() : nullptr, dgamma, acc_g, dbeta ? wb.as<float>() : nullptr,
+                            dbeta, acc_b, chunks, n, "wm_layernorm_bwd(colsum)");
     }
     // Fused path: G workgroups, each leaving one [n] partial per parameter
     // gradient.  G also bounds the partial traffic: at least 32 rows each.
@@ -840,9 +863,8 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
 #undef WM_LNB
     if (!launched) return set_error(WM_ERR_INVALID, "wm_layernorm_bwd: no tile");
     WM_TRY(check_launch("wm_layernorm_bwd"));
-    if (dgamma) WM_TRY(colsum_parts(wg.as<float>(), G, n, dgamma, acc_g, "wm_layernorm_bwd(colsum)"));
-    if (dbeta) WM_TRY(colsum_parts(wb.as<float>(), G, n, dbeta, acc_b, "wm_layernorm_bwd(colsum)"));
-    return WM_OK;
+    return colsum_parts(dgamma ? wg.as<float>() : nullptr, dgamma, acc_g, dbeta ? wb.as<float>() : nullptr, dbeta,
+                        acc_b, G, n, "wm_layernorm_bwd(colsum)");
 }
 
 BnGeom bn_geom(int64_t B, int64_t C, int64_t S, bool vec) {
