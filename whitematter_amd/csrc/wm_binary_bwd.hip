@@ -170,32 +170,53 @@ __global__ void __launch_bounds__(kBlock) bwd_colsum_kernel(const float* __restr
     if (want_v) *reinterpret_cast<float4*>(part + (int64_t)blockIdx.y * C + c) = s;
 }
 
-// out[c] (+)= sum_k part[k, c], k in 0..K-1.  A workgroup owns 64 adjacent
-// columns; its 4 waves take k = w, w+4, w+8, ... (8 interleaved accumulators
-// each), and the 4 wave sums are added in wave order through LDS.
+// out[c] (+)= sum_k part[k, c], k in 0..K-1.  A workgroup owns S adjacent
+// columns and its threads form G = 256 / S groups: group g folds partial
+// rows k = g, g + G, g + 2G, ... (8 interleaved accumulators, combined in a
+// fixed order), and the G group sums are added in group order through LDS.
+// S is chosen so the grid has ~256 workgroups or more: with few columns
+// and many partial rows (a Linear bias gradient, 1024 columns over 1024
+// row groups) 64-column workgroups left 16 workgroups each walking 256
+// rows per wave (13.6 us).
+template <int S>
 __global__ void __launch_bounds__(kBlock) colsum_finalize_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                                   int acc, int64_t K, int64_t C) {
-    __shared__ float lds[4][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    for (int64_t c0 = (int64_t)blockIdx.x * 64; c0 < C; c0 += (int64_t)gridDim.x * 64) {
-        const int64_t c = c0 + lane;
+    constexpr int G = kBlock / S;
+    __shared__ float lds[G][S];
+    const int cl = threadIdx.x % S, g = threadIdx.x / S;
+    for (int64_t c0 = (int64_t)blockIdx.x * S; c0 < C; c0 += (int64_t)gridDim.x * S) {
+        const int64_t c = c0 + cl;
         float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (c < C) {
-            int64_t k = w;
-            for (; k + 28 < K; k += 32) {
+            int64_t k = g;
+            for (; k + 7 * G < K; k += 8 * G) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) s[j] += part[(k + 4 * j) * C + c];
+                for (int j = 0; j < 8; ++j) s[j] += part[(k + j * G) * C + c];
             }
-            for (int j = 0; k < K; k += 4, ++j) s[j & 7] += part[k * C + c];
+            for (int j = 0; k < K; k += G, ++j) s[j & 7] += part[k * C + c];
         }
-        lds[w][lane] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+        lds[g][cl] = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
         __syncthreads();
-        if (w == 0 && c < C) {
-            float t = (lds[0][lane] + lds[1][lane]) + (lds[2][lane] + lds[3][lane]);
+        if (g == 0 && c < C) {
+            float t = lds[0][cl];
+#pragma unroll
+            for (int gg = 1; gg < G; ++gg) t += lds[gg][cl];
             out[c] = acc ? out[c] + t : t;
         }
         __syncthreads();
     }
+}
+
+// colsum_finalize_kernel with its column slot width chosen for C.
+int launch_colsum_finalize(const float* part, float* out, int acc, int64_t K, int64_t C, hipStream_t st) {
+    const int64_t want = (int64_t)num_cus();
+    if (C >= 64 * want)
+        launch_kernel(colsum_finalize_kernel<64>, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st, part, out, acc, K, C);
+    else if (C >= 16 * want)
+        launch_kernel(colsum_finalize_kernel<16>, dim3(grid_for(C, 16, 8)), dim3(kBlock), 0, st, part, out, acc, K, C);
+    else
+        launch_kernel(colsum_finalize_kernel<4>, dim3(grid_for(C, 4, 8)), dim3(kBlock), 0, st, part, out, acc, K, C);
+    return check_launch("wm_binary_bwd(colsum finalize)");
 }
 
 // ---------------------------------------------------------------------------
@@ -558,9 +579,7 @@ int launch_binary_bwd(const float* g, const float* a, const float* b, const floa
                                    ws.as<float>(), R, C);
             WM_TRY(check_launch("wm_binary_bwd(colsum)"));
             if (gV) {
-                launch_kernel(colsum_finalize_kernel, dim3(grid_for(C, 64, 8)), dim3(kBlock), 0, st,
-                                   ws.as<float>(), gV, accV, K, C);
-                WM_TRY(check_launch("wm_binary_bwd(colsum finalize)"));
+                WM_TRY(launch_colsum_finalize(ws.as<float>(), gV, accV, K, C, st));
             }
             return WM_OK;
         }
