@@ -65,9 +65,14 @@ def test_layernorm_backward(wm, shape, accumulate):
         close(got[k], r, s)
 
 
-@pytest.mark.parametrize("want", [(True, False, False), (False, True, True), (False, True, False)])
-def test_layernorm_backward_subsets(wm, want):
-    x, gamma, beta = ln_inputs(64, 768, 3)
+@pytest.mark.parametrize("rows,n", [(64, 768), (4096, 256), (130, 9000)])
+@pytest.mark.parametrize("want", [(True, False, False), (False, True, True), (False, True, False),
+                                  (False, False, True), (True, False, True)])
+def test_layernorm_backward_subsets(wm, want, rows, n):
+    """Each subset of (dx, dgamma, dbeta); [4096, 256] takes the two-stage
+    parameter column sum (more than 64 partial rows), [130, 9000] the
+    long-row kernels."""
+    x, gamma, beta = ln_inputs(rows, n, 3)
     g = rng_normal(x.shape, 9)
     _, mean, inv = layernorm_fwd(x, gamma, beta)
     got = layernorm_bwd(g, x, gamma, mean, inv, want=want)
