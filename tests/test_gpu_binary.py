@@ -44,6 +44,8 @@ SHAPES = [
     ((1, 8192), (6, 8192)),          # ... row vector on the left
     ((6, 1), (6, 8192)),             # ... column vector on the left
     ((7, 8192), (1, 8192)),          # odd row count: single rows
+    ((3, 16384), (16384,)),          # row vector's gradient: 64-column slots in the second pass
+    ((4, 16388), (16388,)),          # ... with a partial last slot
     ((6, 8192), (6, 1)),             # column vector, rows of >= 8192 floats: two rows per item (pow too)
     ((4, 8196), (4, 1)),             # ... with a partial last tile
     ((7, 8192), (7, 1)),             # ... odd row count: single rows
