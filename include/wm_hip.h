@@ -104,17 +104,24 @@ int wm_device_cus(int* cus);
 /* Events on the library stream bracketing enqueued work. */
 int wm_timer_start(void);
 int wm_timer_stop(float* elapsed_ms);
-/* Kernel timing: between wm_span_begin and wm_span_end, each kernel the
-   library launches (up to 64) carries a start and a stop event bound to its
-   own dispatch.  wm_span_end waits for the last one and gives the sum of the
-   kernels' durations (*kernel_ms: what a kernel trace shows, without the
-   marker packets wm_timer_* put around the work) and, if span_ms is not
-   null, the time from the first kernel's start to the last one's end.
-   It fails if no kernel ran. */
+/* Per-launch event pairs: between wm_span_begin and wm_span_end, each
+   kernel the library launches (up to 64) is launched with its own start and
+   stop event (hipExtLaunchKernelGGL).  wm_span_end waits for the last one
+   and gives the sum of the pairs' elapsed times (*kernel_ms) and, if span_ms
+   is not null, the time from the first start event to the last stop event.
+   The events are marker packets on either side of the dispatch, so each
+   pair reads a few microseconds longer than the dispatch's own duration in a
+   kernel trace.  It fails if no kernel ran.  Spans are single-threaded: a
+   launch from another host thread while a span is open takes one of its
+   event pairs. */
 int wm_span_begin(void);
 int wm_span_end(float* kernel_ms, float* span_ms, int* kernels);
 /* Duration of the i-th kernel (0-based) of the last span wm_span_end closed. */
 int wm_span_kernel(int i, float* ms);
+/* Kernels the library has launched since the process started (every
+   thread): the difference across a call is the number of dispatches it
+   issued itself (copies the HIP runtime runs as kernels are not counted). */
+int wm_launch_count(int64_t* count);
 /* Device blocks the library's pool has handed out so far (wm_alloc and
    internal workspace); a test of an entry point that allocates nothing. */
 int wm_pool_handouts(int64_t* count);

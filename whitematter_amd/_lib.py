@@ -54,6 +54,7 @@ _SIGS = {
     "wm_span_begin": [],
     "wm_span_end": [C.POINTER(C.c_float), C.POINTER(C.c_float), C.POINTER(C.c_int)],
     "wm_span_kernel": [C.c_int, C.POINTER(C.c_float)],
+    "wm_launch_count": [C.POINTER(C.c_int64)],
     "wm_pool_handouts": [C.POINTER(C.c_int64)],
     "wm_copy_kernel": [_vp, _vp, C.c_int64],
     "wm_copy_kernel_cached": [_vp, _vp, C.c_int64],

@@ -47,9 +47,9 @@ int upload_async(void* dev_dst, const void* host_src, size_t bytes);
 // Check the launch that was just enqueued.
 int check_launch(const char* what);
 
-// Events for the next launch: both null unless a kernel span is open
-// (wm_span_begin); then the span's first launch gets the start event and
-// every launch the stop event.
+// Called once per launch: counts it, and gives the events for it -- both
+// null unless a kernel span is open (wm_span_begin); then each launch of
+// the span gets its own (start, stop) pair.  Spans are single-threaded.
 void span_events(hipEvent_t* start, hipEvent_t* stop);
 
 // Every kernel of the library is launched through here: a plain launch, or

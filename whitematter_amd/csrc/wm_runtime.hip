@@ -9,6 +9,7 @@
 #include "wm_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstring>
 #include <mutex>
 #include <map>
@@ -27,7 +28,8 @@ struct DeviceState {
 };
 
 // An open kernel span (wm_span_begin .. wm_span_end): one (start, stop)
-// event pair per launch, bound to that launch's own dispatch.
+// event pair per launch, passed to hipExtLaunchKernelGGL with that launch.
+// Used from one host thread (span_events does not lock).
 constexpr int kSpanMax = 64;
 struct Span {
     bool open = false;
@@ -158,7 +160,10 @@ void* ws_alloc(size_t bytes) { return pool_alloc(bytes); }
 void ws_free(void* p) { (void)pool_free(p); }
 
 
+std::atomic<int64_t> g_launches{0};
+
 void span_events(hipEvent_t* start, hipEvent_t* stop) {
+    g_launches.fetch_add(1, std::memory_order_relaxed);
     if (!g_span.open) {
         *start = *stop = nullptr;
         return;
@@ -376,6 +381,12 @@ int wm_span_end(float* kernel_ms, float* span_ms, int* kernels) {
     if (e == hipSuccess && span_ms) e = hipEventElapsedTime(span_ms, g_span.start[0], g_span.stop[n - 1]);
     if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string("wm_span_end: ") + hipGetErrorString(e));
     *kernel_ms = total;
+    return WM_OK;
+}
+
+int wm_launch_count(int64_t* count) {
+    if (!count) return set_error(WM_ERR_INVALID, "wm_launch_count: null pointer");
+    *count = g_launches.load(std::memory_order_relaxed);
     return WM_OK;
 }
 
