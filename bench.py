@@ -15,10 +15,14 @@ Each op is timed twice per step, in separate launches:
                 the numbers a rocprofv3 --kernel-trace of the same run
                 shows.  Every GB/s and roofline fraction is computed from
                 this basis (median of K steps; an op's time is the sum of
-                its dispatches).  Where the tracer cannot register (the
-                process already runs under a profiler), the per-launch
-                event pairs of wm_span_* stand in ("basis": "span"); they
-                read ~4 us longer per dispatch than the trace.
+                its dispatches).  Where the process already runs under a
+                profiler (rocprofv3), the tracer cannot register: the
+                kernels are then launched exactly as on the trace basis and
+                the profiler's trace is the measurement ("basis":
+                "external"; bench's own figures fall back to the event
+                basis).  If it cannot register for any other reason, the
+                per-launch event pairs of wm_span_* stand in ("basis":
+                "span"); they read ~4 us longer per dispatch.
   event basis   events recorded on the library stream before and after the
                 op (wm_timer_*): launch gaps and marker latency included;
                 reported beside as value_event.
@@ -119,6 +123,17 @@ class KTrace:
             self.ok = True
         else:
             self.err = L.wm_ktrace_error().decode(errors="replace")
+
+    @property
+    def basis(self):
+        """trace: this library's dispatch timestamps; external: another tool
+        (rocprofv3) already traces the process, so kernels are launched
+        plainly, exactly as on the trace basis, and that tool's trace is the
+        kernel measurement (bench's own figures fall back to the event basis);
+        span: per-launch event pairs, when the tracer cannot register at all."""
+        if self.ok:
+            return "trace"
+        return "external" if "already configured" in self.err else "span"
 
     def begin(self):
         if self.L.wm_ktrace_begin() != 0:
@@ -515,7 +530,8 @@ def _timed(fn):
 
 
 def host_llc_bytes():
-    """The largest cache of host core 0 (sysfs), 0 if unknown."""
+    """The last-level cache one host core sees (its L3 instance): sysfs for
+    core 0, else the C library's sysconf; 0 if neither says."""
     base = "/sys/devices/system/cpu/cpu0/cache"
     best = 0
     try:
@@ -526,7 +542,30 @@ def host_llc_bytes():
             best = max(best, int(v.rstrip("KMG")) * mult)
     except (OSError, ValueError):
         pass
-    return best
+    if not best:
+        # lscpu -B: "L3 cache: <bytes> (<n> instances)" -> one instance
+        try:
+            import subprocess
+            out = subprocess.run(["lscpu", "-B"], capture_output=True, text=True, timeout=10).stdout
+            for line in out.splitlines():
+                if line.startswith("L3 cache:") or (line.startswith("L2 cache:") and not best):
+                    f = line.split(":", 1)[1].split()
+                    n = int(f[1].strip("(")) if len(f) > 1 else 1
+                    best = max(best, int(f[0]) // max(n, 1))
+        except (OSError, ValueError, IndexError, subprocess.SubprocessError):
+            pass
+    return max(best, 0)
+
+
+def host_cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def _cpu_record(samples, ncpus, sample, reps, sample_bytes=None):
@@ -545,6 +584,7 @@ def _cpu_record(samples, ncpus, sample, reps, sample_bytes=None):
                      f"workload; single-threaded on 1 of {ncpus} host cores",
            "per_op_ms_full": per_ms, "per_op_GBps": per_gbps}
     llc = host_llc_bytes()
+    rec["host_cpu"] = host_cpu_model()
     if sample_bytes is not None:
         rec["sample_MiB"] = round(sample_bytes / 2 ** 20, 1)
         rec["host_llc_MiB"] = round(llc / 2 ** 20, 1) if llc else None
@@ -905,8 +945,8 @@ def c4_sample(sample_rows):
     return L, G
 
 
-def cpu_baseline_c4(sample_rows=64, jac_rows=4, cols=32000, reps=3):
-    """softmax / log_softmax forward and log_softmax backward on 64 rows; the
+def cpu_baseline_c4(sample_rows=512, jac_rows=4, cols=32000, reps=3):
+    """softmax / log_softmax forward and log_softmax backward on 512 rows; the
     softmax backward (the reference's explicit Jacobian, O(cols^2) per row)
     on jac_rows rows, each timed on its own (the spread shows the rows cost
     the same), extrapolated by rows."""
@@ -1008,7 +1048,7 @@ def parity_c4(ctx, outs):
 _C5_CHAIN = {}
 
 
-def _c5_chain_baseline(sample_rows=256, c=4096, reps=3):
+def _c5_chain_baseline(sample_rows=2048, c=4096, reps=3):
     """The config-5 chain through the reference's Tensor API on the first
     sample_rows rows (t = 0 .. sample_rows - 1 of batch 0); timed once per
     process, shared by the c5 and c5api records."""
@@ -1067,7 +1107,7 @@ def _c5_chain_baseline(sample_rows=256, c=4096, reps=3):
     return rec, outs
 
 
-def cpu_baseline_c5api(sample_rows=256, c=4096, reps=3):
+def cpu_baseline_c5api(sample_rows=2048, c=4096, reps=3):
     return _c5_chain_baseline(sample_rows, c, reps)
 
 
@@ -1480,10 +1520,18 @@ TARGET_FRAC = 0.70
 def _launch(op, basis, flush, kt):
     """One launch of op after the 512 MiB flush fill, timed in `basis`."""
     flush.fill(1.0)
-    if basis in ("trace", "span") and getattr(op, "host_io", False):
+    if basis in ("trace", "span", "external") and getattr(op, "host_io", False):
         return  # host-driven copies: timed on the event basis only
     if basis is None:
         op.launch()
+    elif basis == "external":
+        # another tool (rocprofv3) traces this process: launch exactly as the
+        # trace basis does (no event markers), counting the dispatches
+        c0, c1 = ctypes.c_int64(), ctypes.c_int64()
+        W.call("wm_launch_count", ctypes.byref(c0))
+        op.launch()
+        W.call("wm_launch_count", ctypes.byref(c1))
+        op.ndisp = c1.value - c0.value
     elif basis == "trace":
         c0, c1 = ctypes.c_int64(), ctypes.c_int64()
         W.call("wm_launch_count", ctypes.byref(c0))
@@ -1530,7 +1578,7 @@ def run_config(name, args, flush, want_cpu, kt):
     span events -- and event basis, one flush before every launch), check
     parity on the recipe's bytes, and return (compact record, detail record)."""
     ops, ctx, workload = CONFIGS[name]()
-    basis = "trace" if kt.ok else "span"
+    basis = kt.basis
 
     for _ in range(args.warmup):
         for op in ops:
@@ -1571,6 +1619,8 @@ def run_config(name, args, flush, want_cpu, kt):
         d = {"ms": round(km, 4), "ms_event_median": round(statistics.median(op.ms), 4), "GBps": round(gbps, 1),
              "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "Gelem_per_s": round(op.elems / (km * 1e-3) / 1e9, 2),
              "bytes": op.bytes}
+        if getattr(op, "ndisp", None) is not None:
+            d["dispatches"] = op.ndisp
         if op.kms:
             nk = len(op.kparts[0])
             d["dispatches"] = nk
@@ -1736,8 +1786,8 @@ def copy_calibration(flush, kt):
     for entry in ("wm_copy_kernel", "wm_copy_kernel_cached"):
         op = Op(entry, lambda e=entry: W.call(e, dst.vp, src.vp, n_copy), 2 * n_copy * F32, entry, n_copy)
         for _ in range(3):
-            _launch(op, "trace" if kt.ok else "span", flush, kt)
-        out[entry] = round(op.bytes / (statistics.median(op.kms) * 1e-3) / 1e9, 1)
+            _launch(op, kt.basis if kt.basis != "external" else "event", flush, kt)
+        out[entry] = round(op.bytes / (statistics.median(op.kms or op.ms) * 1e-3) / 1e9, 1)
     src.free()
     dst.free()
     return out
@@ -1761,7 +1811,7 @@ def main():
 
     kt = KTrace()  # before the first HIP call of the process
     if not kt.ok:
-        print("bench.py: dispatch tracer not registered (%s); timing on per-launch event pairs" % kt.err,
+        print("bench.py: dispatch tracer not registered (%s); basis %s" % (kt.err, kt.basis),
               file=sys.stderr, flush=True)
     W.call("wm_init", 0)
     cus = W.device_cus()
@@ -1774,7 +1824,7 @@ def main():
         print(f"bench.py: {nm} done: {recs[nm]['value']} {recs[nm]['unit']}, parity "
               f"{recs[nm].get('parity', {}).get('pass', 'n/a')}", file=sys.stderr, flush=True)
     copies = copy_calibration(flush, kt)
-    basis = "trace" if kt.ok else "span"
+    basis = kt.basis
     detail_line = json.dumps({"copy_kernel_GBps": copies, "basis": basis, "configs": details})
     print("bench.py detail: " + detail_line, file=sys.stderr, flush=True)
     if args.detail:

@@ -200,15 +200,18 @@ int wm_reduce(int op, const float* x, int64_t outer, int64_t n, int64_t inner,
               float* val, int64_t* idx);
 
 /* wm_reduce without allocating: no counterpart in the reference; for callers
- * that cannot allocate device memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
+ * that cannot allocate device memory (tight serving loops, harnesses that
+ * forbid hipMalloc).  It launches on the library's own stream, like every
+ * entry point, so it is not meant for capture into a caller's graph.  Same
+ * arguments, results
  * and errors as wm_reduce, and the same kernels; the chunk partials of a
  * split reduction live in a fixed 8 MiB device array per GPU (held until the
  * process ends) instead of the library's pool, so no device memory is taken
  * from the pool or the driver.  A reduction whose partials exceed 8 MiB
  * fails with WM_ERR_UNSUPPORTED (wm_reduce handles it).  Every call on one
  * GPU shares the array: this library orders its calls on its one stream, and
- * work that overlaps a call on another stream (a replayed graph) races on it.
+ * calls that overlap on one GPU (from another process or library instance)
+ * race on it.
  * Call wm_init first: the first call on a device looks up the array's
  * address (no allocation). */
 int wm_reduce_noalloc(int op, const float* x, int64_t outer, int64_t n, int64_t inner,

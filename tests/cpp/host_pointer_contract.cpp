@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <vector>
 
+#include "amp.h"
 #include "optimizer.h"
 #include "tensor.h"
 
@@ -50,6 +51,15 @@ int main() {
     for (float v : cd) s += v;
     auto u = prm->mul(1.0f);
     check(s > 243.19f && s < 243.21f && u->data[5] == 0.95f, "const reads leave the device copy current");
+    // 7. HalfVector(n) holds n zeros, as std::vector<uint16_t>(n) does, on the host and on the device
+    wm::HalfVector hv(1001);
+    bool zeros = hv.size() == 1001;
+    for (uint16_t v : hv) zeros = zeros && v == 0;
+    auto hf = HalfTensor(Tensor::create(std::vector<float>(8, 2.0f), {8}, false));
+    hf.data = wm::HalfVector(8);
+    auto back = hf.to_float();
+    for (float v : back->data) zeros = zeros && v == 0.0f;
+    check(zeros, "HalfVector(n) is n zeros (host reads and a device conversion)");
     std::printf("%s\n", fails ? "CONTRACT BROKEN" : "CONTRACT HOLDS");
     return fails ? 1 : 0;
 }

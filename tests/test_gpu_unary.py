@@ -116,3 +116,34 @@ def test_calibration_copies_are_copies(wm, entry):
     W.call(entry, dst.vp, src.vp, n)
     assert oracle.bit_equal(dst.to_host(), x)
     assert getattr(W.lib(), entry)(dst.vp, src.vp, n - 1) != 0
+
+
+def subnormal_result_inputs(op, n=20000):
+    """Inputs whose exact results lie below fp32's normal range (including
+    zero-crossing neighbours), for the ulp check in the subnormal range."""
+    u = rng_uniform((n,), 77, 0.0, 1.0).astype(np.float64)
+    if op in ("exp", "sigmoid"):
+        x = -87.3 - 16.6 * u                           # exp(x) in [1.4e-45, 1.2e-38]
+    elif op == "pows":
+        x = 10.0 ** (-15.2 - 2.4 * u)                  # x^2.5 in [~1e-44, 1.6e-38]
+    elif op == "tanh":
+        x = np.copysign(10.0 ** (-44.8 - 7.0 * u), u - 0.5) * 1e7   # tanh(x) = x: subnormal in, subnormal out
+    else:
+        raise ValueError(op)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("op", ["exp", "sigmoid", "pows", "tanh"])
+def test_unary_subnormal_results(wm, op):
+    """Results in fp32's subnormal range are within 2 ulp of fp64 there too
+    (the ulp below 2^-126 is 2^-149).  The reference's own build runs with
+    flush-to-zero (S16) and returns 0 for these; the GPU path keeps fp32's
+    gradual underflow, so its results stay within the contract's 2 ulp."""
+    p0, p1 = ULP[op]
+    x = subnormal_result_inputs(op)
+    got = unary_fwd(op, x, p0, p1)
+    ref = oracle.get("f64").unary(op, x, p0, p1)
+    sub = np.isfinite(ref) & (np.abs(ref) < 1.1754944e-38) & (ref != 0)
+    assert sub.sum() > 1000, "the inputs must produce subnormal results"
+    u = oracle.ulp_vs_f64(got, ref)
+    assert u[sub].max() <= 2.0, f"{op}: max ulp {u[sub].max()} on subnormal results"

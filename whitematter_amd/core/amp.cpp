@@ -64,7 +64,7 @@ bool GradScaler::unscale(Optimizer* optimizer) {
 // core/amp.h:263-267
 HalfTensor::HalfTensor(const TensorPtr& tensor) : shape(tensor->shape) {
     const size_t n = tensor->data.size();
-    data = wm::HalfVector(n);
+    data = wm::HalfVector::uninitialized(n);  // every element is written below
     if (n == 0) return;
     check(wm_f32_to_f16_rtz(data.dev_write(), tensor->data.dev(), (int64_t)n), "HalfTensor");
 }

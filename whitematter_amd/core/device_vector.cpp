@@ -268,11 +268,17 @@ bool DeviceVector::operator==(const DeviceVector& o) const {
 
 // ---- HalfVector -----------------------------------------------------------
 
-HalfVector::HalfVector(size_type n) : n_(n) {
-    if (n_ == 0) return;
-    ensure_dev_alloc();
-    host_valid_ = false;  // neither copy holds values until the first write
-    dev_valid_ = true;
+// Zeros in the host mirror, uploaded when the device first needs them.
+HalfVector::HalfVector(size_type n) : n_(n), h_(n, 0) { dev_valid_ = n_ == 0; }
+
+HalfVector HalfVector::uninitialized(size_type n) {
+    HalfVector v;
+    v.n_ = n;
+    if (n == 0) return v;
+    v.ensure_dev_alloc();
+    v.host_valid_ = false;  // neither copy holds values until the caller's write
+    v.dev_valid_ = true;
+    return v;
 }
 
 HalfVector::HalfVector(const std::vector<uint16_t>& v) : n_(v.size()), h_(v) { dev_valid_ = n_ == 0; }

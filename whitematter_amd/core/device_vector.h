@@ -120,7 +120,11 @@ public:
     using const_iterator = const uint16_t*;
 
     HalfVector() = default;
-    explicit HalfVector(size_type n);  // device storage of n elements, contents unset until written
+    explicit HalfVector(size_type n);  // n zeros, as std::vector<uint16_t>(n)
+    // Device storage of n elements whose contents are unset until the caller
+    // overwrites all of them through dev_write() (HalfTensor's converting
+    // constructor does, at once).
+    static HalfVector uninitialized(size_type n);
     HalfVector(const std::vector<uint16_t>& v);  // NOLINT: implicit, like a vector copy
     HalfVector(const HalfVector& o);
     HalfVector(HalfVector&& o) noexcept;

@@ -9,10 +9,10 @@
 // softmax ops and their backward closures run as HIP kernels through the
 // C ABI in include/wm_hip.h; they never touch host memory.
 //
-// Ops outside that path (matmul, bmm, conv, pools, concat/stack, transpose,
-// slice, permute, augmentation) are declared for source compatibility and
-// throw std::logic_error: this build covers the elementwise / broadcast /
-// reduction path only.
+// matmul, bmm and transpose run on the device too (fp32 on the matrix cores,
+// include/wm_gemm.h).  The ops outside the path -- conv2d / conv_transpose2d,
+// the pools, concat / stack, slice, permute and the augmentation helpers --
+// are declared for source compatibility and throw std::logic_error.
 //
 // The include guard is the reference header's own (TENSOR_H): this header
 // replaces that one, and the two must never both be active in a translation

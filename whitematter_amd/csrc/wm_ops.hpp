@@ -189,7 +189,15 @@ __device__ __forceinline__ void binary_fwd_v(float4 (&r)[U], const float4 (&a)[U
 template <int OP>
 __device__ __forceinline__ float unary_fwd(float x, float p0, float p1) {
     if constexpr (OP == WM_RELU) return x > 0.0f ? x : 0.0f;            // simd_relu :139-158
-    else if constexpr (OP == WM_SIGMOID) return 1.0f / (1.0f + expf(-x)); // :1286
+    else if constexpr (OP == WM_SIGMOID) {                              // :1286
+        // Below -80, 1 + exp(-x) rounds past FLT_MAX to inf (from -88.7) and
+        // sigmoid(x) = exp(x) / (1 + exp(x)) is exp(x) to within 2e-35
+        // relative: exp(x) keeps the results that fall in fp32's subnormal
+        // range within the 2-ulp contract (the quotient gives 0 there).
+        const bool far = x < -80.0f;
+        const float e = expf(far ? x : -x);
+        return far ? e : 1.0f / (1.0f + e);
+    }
     else if constexpr (OP == WM_TANH) return tanh_fast(x);              // :1307
     else if constexpr (OP == WM_LOG)                                    // :1328
         // The +1e-8f is the reference's fp32 add; the log itself is taken in

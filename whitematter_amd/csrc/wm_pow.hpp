@@ -28,6 +28,18 @@
 // gradients, so it shares one log2|a| and takes the powers of two from the
 // hardware exp2 on a reduced argument (relative error ~2e-7).
 //
+// The method is the published table-driven one: P. T. P. Tang,
+// "Table-driven implementation of the exponential function in IEEE
+// floating-point arithmetic", ACM TOMS 15(2), 1989, and "... of the
+// logarithm function ...", ACM TOMS 16(4), 1990, in the double-precision
+// arrangement for powf of the ARM Optimized Routines (Szabolcs Nagy, 2018;
+// the same scheme is in musl and in glibc's powf since 2.28): log2 of the
+// reduced argument from a 16-entry table of (1/c, log2 c) and a polynomial
+// in r = z/c - 1, the product with y in double, then 2^t from a table of
+// 2^(j/N) and a short polynomial.  The table sizes (N = 128 here), the
+// polynomial degrees and the coefficients are this file's own, generated and
+// fitted for this build.
+//
 // The file is plain C++ with explicit fma(), so the same code compiles for
 // the host and is checked there against long double powl
 // (tests/cpp/pow_table_check.cpp).
