@@ -124,6 +124,8 @@ def special_slices(outer, n, inner, seed):
     (1, 3000, 7),       # scalar columns, split
     (512, 300, 1),      # rows, one wave per row
     (2, 300000, 1),     # long rows, split + second pass
+    (9000, 5, 256),     # float4 columns: 9000 items on an 8192-workgroup grid (some workgroups take two)
+    (9000, 3, 63),      # scalar columns, the same with a partial tile
 ])
 def test_reduce_special_values(wm, op, view):
     """Bit-exact values and first-occurrence indices with NaNs, signed zeros,
