@@ -127,6 +127,58 @@ int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, 
                                   float max_norm);
 int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float clip_value);
 
+/* ---- deferred gradient scaling -------------------------------------------
+ * GradScaler::unscale (core/amp.h:125-147) and clip_grad_norm_
+ * (core/optimizer.cpp:155-164) multiply every gradient in place; done eagerly
+ * that is a read and a write of each gradient after the pass that decides the
+ * factor (the first non-finite position, the norm).  The drop-in records the
+ * multiplication with the gradient instead and lets the next pass over the
+ * gradients apply it as it reads them -- the optimizer step, a norm, a
+ * finiteness search -- or writes it once (wm_grad_scale_apply_multi) before
+ * any other use.  A gradient's stored values g and its wm_grad_scale give its
+ * values as the reference holds them:
+ *   v = g[i];
+ *   if (i < unscale_count) v = v * unscale;           (unscale's prefix)
+ *   if (clip_sumsq) { c = clip_max_norm / (sqrt(*clip_sumsq) + 1e-6f);
+ *                     if (c < 1) v = v * c; }         (clip_grad_norm_)
+ * each product rounded to fp32 as the reference's in-place multiply is, so
+ * every result below equals the eager passes' bit for bit.  clip_sumsq is a
+ * device float (the norm's sum of squares), read when the scaling is
+ * applied.  No counterpart in the reference (its multiplications are
+ * eager); these entry points take one wm_grad_scale per list entry.        */
+typedef struct wm_grad_scale {
+    float unscale;           /* factor of the elements [0, unscale_count) */
+    int64_t unscale_count;   /* 0: no deferred unscale; at most the tensor's size */
+    const float* clip_sumsq; /* NULL: no deferred clip */
+    float clip_max_norm;
+} wm_grad_scale;
+
+/* Write each gradient's deferred scaling into it (g[i] = v).                */
+int wm_grad_scale_apply_multi(int count, float* const* g, const wm_grad_scale* gs, const int64_t* n);
+/* The optimizer steps above on the gradients' values v (their stored values
+ * and deferred scalings, gs may be NULL: none).                             */
+int wm_sgd_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                         float* const* velocity, const int64_t* n, float lr, float momentum);
+int wm_adam_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                          float* const* m, float* const* v, const int64_t* n, float lr, float beta1, float beta2,
+                          float eps, float bias_correction1, float bias_correction2);
+int wm_adamw_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                           float* const* m, float* const* v, const int64_t* n, float lr, float beta1, float beta2,
+                           float eps, float bias_correction1, float bias_correction2, float weight_decay);
+int wm_rmsprop_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                             float* const* v, float* const* buffer, const int64_t* n, float lr, float alpha,
+                             float eps, float momentum, float weight_decay);
+/* *total (device) = sum over the list of (v * mul)^2 (get_grad_norm,
+ * clip_grad_norm_amp).                                                      */
+int wm_grad_sumsq_multi_gs(int count, const float* const* g, const wm_grad_scale* gs, const int64_t* n, float mul,
+                           float* total);
+/* where[0], where[1] (host) = list position and element of the first value
+ * v with v * scale not finite, in list order, or (count, 0): unscale's stop
+ * (scale = 1 / loss scale) and check_gradients_finite (scale = 1).  Read-only;
+ * synchronises for the answer.                                              */
+int wm_grad_first_bad_multi_gs(int count, const float* const* g, const wm_grad_scale* gs, const int64_t* n,
+                               float scale, int64_t* where);
+
 #ifdef __cplusplus
 }
 #endif

@@ -343,3 +343,114 @@ def test_multi_duplicated_gradient_clip_and_unscale(wm):
     W.call("wm_grad_unscale", 2, G, ns, float(inv), C.byref(found))
     assert found.value == 0
     assert oracle.bit_equal(d.get(), (mine * inv) * inv)
+
+
+# ---- deferred scalings (wm_grad_scale) ---------------------------------------
+
+def _eager(g, gsv, sumsq):
+    """The reference's in-place multiplications on a copy of g: unscale's
+    prefix (core/amp.h:131-142), then clip_grad_norm_'s coefficient
+    (core/optimizer.cpp:155-164), each product rounded to fp32."""
+    v = g.copy()
+    k = gsv.unscale_count
+    v[:k] = v[:k] * np.float32(gsv.unscale)
+    if gsv.clip_sumsq:
+        c = np.float32(gsv.clip_max_norm) / (np.sqrt(np.float32(sumsq)) + np.float32(1e-6))
+        if c < 1:
+            v = v * c
+    return v
+
+
+@pytest.mark.parametrize("kind,hp", CONFIGS, ids=lambda v: v if isinstance(v, str) else "-".join(map(str, v.values())))
+def test_multi_steps_with_deferred_scaling(wm, kind, hp):
+    """The *_multi_gs steps read each gradient through its pending unscale
+    prefix and clip coefficient: bit-exact against the oracle's steps on the
+    eagerly multiplied gradients, per-entry scalings differing (full, partial
+    and no unscale; clip or none), the clip's sum of squares a device float
+    written by wm_grad_sumsq_multi_gs over the unscaled values."""
+    lr, a, b, c, d = hp["lr"], hp.get("a", 0.0), hp.get("b", 0.0), hp.get("c", 0.0), hp.get("d", 0.0)
+    sizes = [n for n, _ in MULTI_SIZES]
+    mine, dev = [], []
+    for i, (n, mis) in enumerate(MULTI_SIZES):
+        arrs = [rng(17 * i).standard_normal(n).astype(np.float32), np.zeros(n, np.float32), np.zeros(n, np.float32)]
+        mine.append(arrs)
+        dev.append([Slot(x, mis) for x in arrs])
+    ns, _ns = W.i64_array(sizes)
+    inv = float(np.float32(1.0) / np.float32(1024.0))
+    counts = [n if i % 3 != 2 else n // 3 for i, n in enumerate(sizes)]
+    counts[3] = 0
+    total = W.DeviceArray((1,))
+    for t in range(1, 4):
+        gs = [(rng(300 * t + i).standard_normal(n) * 1024.0).astype(np.float32) for i, n in enumerate(sizes)]
+        dgs = [Slot(g, mis) for g, (_, mis) in zip(gs, MULTI_SIZES)]
+        G, _g = _ptrs(dgs)
+        unscale = [W.GradScale(inv, k, None, 0.0) for k in counts]
+        GS, _gs = W.grad_scale_array(unscale)
+        W.call("wm_grad_sumsq_multi_gs", len(sizes), G, GS, ns, 1.0, total.vp)
+        sumsq = np.float32(total.to_host()[0])
+        entries = [W.GradScale(inv, k, None if i == 5 else total.ptr, 1.0) for i, k in enumerate(counts)]
+        GS, _gs = W.grad_scale_array(entries)
+        P, _p = _ptrs([x[0] for x in dev])
+        S1, _s1 = _ptrs([x[1] for x in dev])
+        S2, _s2 = _ptrs([x[2] for x in dev])
+        cnt = len(sizes)
+        if kind == "sgd":
+            W.call("wm_sgd_step_multi_gs", cnt, P, G, GS, S1 if a > 0 else None, ns, lr, a)
+        elif kind == "adam":
+            W.call("wm_adam_step_multi_gs", cnt, P, G, GS, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t))
+        elif kind == "adamw":
+            W.call("wm_adamw_step_multi_gs", cnt, P, G, GS, S1, S2, ns, lr, a, b, c, o32.bias_correction(a, t),
+                   o32.bias_correction(b, t), d)
+        else:
+            W.call("wm_rmsprop_step_multi_gs", cnt, P, G, GS, S1, S2 if c > 0 else None, ns, lr, a, b, c, d)
+        eager = [_eager(g, e, sumsq) for g, e in zip(gs, entries)]
+        for arrs, v in zip(mine, eager):
+            oracle_step(kind, hp, arrs[0], v, arrs[1], arrs[2], t)
+        for i, (arrs, slots) in enumerate(zip(mine, dev)):
+            for j in range(3):
+                assert oracle.bit_equal(slots[j].get(), arrs[j]), (kind, t, i, j)
+        for dg, g in zip(dgs, gs):                       # the steps only read the gradients
+            assert oracle.bit_equal(dg.get(), g)
+
+
+def test_deferred_scaling_norm_search_and_apply(wm):
+    """wm_grad_sumsq_multi_gs equals wm_grad_sumsq_multi over the eagerly
+    multiplied gradients bit for bit (same reduction order); the finiteness
+    search finds the first non-finite v * scale; wm_grad_scale_apply_multi
+    writes exactly the eager products."""
+    sizes = [n for n, _ in MULTI_SIZES]
+    ns, _ns = W.i64_array(sizes)
+    gs = [(rng(500 + i).standard_normal(n) * 300.0).astype(np.float32) for i, n in enumerate(sizes)]
+    counts = [n // 2 if i % 2 else n for i, n in enumerate(sizes)]
+    clip_total = W.DeviceArray.from_host(np.float32([2.5e9]))
+    entries = [W.GradScale(0.125, k, clip_total.ptr if i != 1 else None, 3000.0) for i, k in enumerate(counts)]
+    GS, _gs = W.grad_scale_array(entries)
+    eager = [_eager(g, e, np.float32(2.5e9)) for g, e in zip(gs, entries)]
+    dgs = [Slot(g, mis) for g, (_, mis) in zip(gs, MULTI_SIZES)]
+    des = [Slot(v, mis) for v, (_, mis) in zip(eager, MULTI_SIZES)]
+    G, _g = _ptrs(dgs)
+    E, _e = _ptrs(des)
+    t_gs, t_eager = W.DeviceArray((1,)), W.DeviceArray((1,))
+    W.call("wm_grad_sumsq_multi_gs", len(sizes), G, GS, ns, 1.0, t_gs.vp)
+    W.call("wm_grad_sumsq_multi", len(sizes), E, ns, t_eager.vp)
+    assert oracle.bit_equal(t_gs.to_host(), t_eager.to_host())
+    W.call("wm_grad_sumsq_multi_gs", len(sizes), G, GS, ns, 0.5, t_gs.vp)
+    W.call("wm_grad_sumsq_scaled_multi", len(sizes), E, ns, 0.5, t_eager.vp)
+    assert oracle.bit_equal(t_gs.to_host(), t_eager.to_host())
+    where = (C.c_int64 * 2)(-1, -1)
+    W.call("wm_grad_first_bad_multi_gs", len(sizes), G, GS, ns, 1.0, C.cast(where, C.c_void_p))
+    assert list(where) == [len(sizes), 0]
+    # a value finite as stored but not once multiplied: the search sees v
+    big = np.float32(3e38)
+    gs[5][77] = big
+    dgs[5] = Slot(gs[5], MULTI_SIZES[5][1])
+    G, _g = _ptrs(dgs)
+    ent = list(entries)
+    ent[5] = W.GradScale(4.0, 100, None, 0.0)
+    GS, _gs = W.grad_scale_array(ent)
+    W.call("wm_grad_first_bad_multi_gs", len(sizes), G, GS, ns, 1.0, C.cast(where, C.c_void_p))
+    assert list(where) == [5, 77]
+    W.call("wm_grad_scale_apply_multi", len(sizes), G, GS, ns)
+    for dg, g, e in zip(dgs, gs, ent):
+        assert oracle.bit_equal(dg.get(), _eager(g, e, np.float32(2.5e9)))

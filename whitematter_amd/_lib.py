@@ -95,6 +95,13 @@ _SIGS = {
     "wm_grads_finite_multi": [C.c_int, _vp, _vp, C.POINTER(C.c_int)],
     "wm_clip_grad_norm_scale_multi": [C.c_int, _vp, _vp, _vp, C.c_float],
     "wm_clip_grad_value_multi": [C.c_int, _vp, _vp, C.c_float],
+    "wm_grad_scale_apply_multi": [C.c_int, _vp, _vp, _vp],
+    "wm_sgd_step_multi_gs": [C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_float, C.c_float],
+    "wm_adam_step_multi_gs": [C.c_int] + [_vp] * 6 + [C.c_float] * 6,
+    "wm_adamw_step_multi_gs": [C.c_int] + [_vp] * 6 + [C.c_float] * 7,
+    "wm_rmsprop_step_multi_gs": [C.c_int] + [_vp] * 6 + [C.c_float] * 5,
+    "wm_grad_sumsq_multi_gs": [C.c_int, _vp, _vp, _vp, C.c_float, _vp],
+    "wm_grad_first_bad_multi_gs": [C.c_int, _vp, _vp, _vp, C.c_float, _vp],
     # include/wm_loss.h
     "wm_cross_entropy_fwd": [_vp, _vp, C.c_int64, C.c_int64, _vp, _vp],
     "wm_cross_entropy_bwd": [_vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int64, C.c_int64],
@@ -139,6 +146,20 @@ def ptr_array(ptrs):
     """A host array of device pointers (None -> NULL) for the multi-tensor
     entry points, as a void*."""
     arr = (C.c_void_p * max(1, len(ptrs)))(*[(p.value if isinstance(p, C.c_void_p) else p) for p in ptrs])
+    return C.cast(arr, C.c_void_p), arr
+
+
+class GradScale(C.Structure):
+    """struct wm_grad_scale (include/wm_optim.h): a gradient's pending
+    multiplications -- the first unscale_count elements by unscale, then,
+    when clip_sumsq is set, every element by the clip coefficient."""
+    _fields_ = [("unscale", C.c_float), ("unscale_count", C.c_int64), ("clip_sumsq", C.c_void_p),
+                ("clip_max_norm", C.c_float)]
+
+
+def grad_scale_array(entries):
+    """A host array of wm_grad_scale, one per list position, as a void*."""
+    arr = (GradScale * max(1, len(entries)))(*entries)
     return C.cast(arr, C.c_void_p), arr
 
 

@@ -6,6 +6,7 @@
 
 #include <cmath>
 #include <limits>
+#include <memory>
 #include <stdexcept>
 #include <string>
 
@@ -18,15 +19,19 @@ void check(int rc, const char* what) {
     if (rc != WM_OK) throw std::runtime_error(std::string("whitematter_amd ") + what + ": " + wm_last_error());
 }
 
-// The gradients that hold values: a gradient that is empty or known to be
-// all zeros is skipped (scaling zeros by a finite factor leaves zeros, and
-// zeros are finite).  `write` hands out pointers for in-place updates (the
-// host mirrors go stale), otherwise read-only ones.
-void live_grads(const std::vector<TensorPtr>& params, std::vector<float*>& ptrs, std::vector<int64_t>& sizes,
-                bool write = true) {
+// The gradients that hold values, with their deferred scalings: a gradient
+// that is empty or known to be all zeros is skipped (scaling zeros by a
+// finite factor leaves zeros, and zeros are finite).  `vecs` gets the
+// storage of each; the pointers are for read-only passes that apply the
+// deferred scalings as they read.
+void live_grads_deferred(const std::vector<TensorPtr>& params, std::vector<wm::DeviceVector*>& vecs,
+                         std::vector<const float*>& ptrs, std::vector<wm_grad_scale>& gs,
+                         std::vector<int64_t>& sizes) {
     for (const auto& p : params) {
         if (!p || p->grad.empty() || p->grad.known_zero()) continue;
-        ptrs.push_back(write ? p->grad.dev_rw() : const_cast<float*>(p->grad.dev()));
+        vecs.push_back(&p->grad);
+        gs.emplace_back();
+        ptrs.push_back(p->grad.dev_deferred(&gs.back()));
         sizes.push_back((int64_t)p->grad.size());
     }
 }
@@ -52,12 +57,38 @@ bool GradScaler::unscale(Optimizer* optimizer) {
         found_inf_or_nan_ = any_grad(optimizer->params);
         return !found_inf_or_nan_;
     }
-    std::vector<float*> ptrs;
+    std::vector<wm::DeviceVector*> vecs;
+    std::vector<const float*> ptrs;
+    std::vector<wm_grad_scale> gs;
     std::vector<int64_t> sizes;
-    live_grads(optimizer->params, ptrs, sizes);
-    int found = 0;
-    check(wm_grad_unscale((int)ptrs.size(), ptrs.data(), sizes.data(), inv_scale, &found), "GradScaler::unscale");
-    found_inf_or_nan_ = found != 0;
+    live_grads_deferred(optimizer->params, vecs, ptrs, gs, sizes);
+    bool listed_twice = false;
+    for (size_t i = 0; i < vecs.size() && !listed_twice; ++i)
+        for (size_t j = i + 1; j < vecs.size(); ++j)
+            if (vecs[i] == vecs[j]) { listed_twice = true; break; }
+    if (listed_twice) {
+        // A gradient listed twice is scaled twice, the second pass searching
+        // the first pass's products: the eager search-and-scale runs per list
+        // position in order (wm_grad_unscale).
+        std::vector<float*> rw;
+        for (auto* v : vecs) rw.push_back(v->dev_rw());
+        int found = 0;
+        check(wm_grad_unscale((int)rw.size(), rw.data(), sizes.data(), inv_scale, &found), "GradScaler::unscale");
+        found_inf_or_nan_ = found != 0;
+        return !found_inf_or_nan_;
+    }
+    // One read of every gradient finds the stop; the products themselves are
+    // deferred (DeviceVector::defer_unscale) to the pass that reads the
+    // gradients next -- normally the optimizer step.
+    int64_t where[2] = {0, 0};
+    check(wm_grad_first_bad_multi_gs((int)ptrs.size(), ptrs.data(), gs.data(), sizes.data(), inv_scale, where),
+          "GradScaler::unscale");
+    const int64_t stop = where[0];
+    for (size_t k = 0; k < vecs.size(); ++k) {
+        const int64_t cnt = (int64_t)k < stop ? sizes[k] : ((int64_t)k == stop ? where[1] : 0);
+        vecs[k]->defer_unscale(inv_scale, cnt);
+    }
+    found_inf_or_nan_ = stop < (int64_t)vecs.size();
     return !found_inf_or_nan_;
 }
 
@@ -80,13 +111,15 @@ TensorPtr HalfTensor::to_float(bool requires_grad) const {
 
 // core/amp.h:293-300: every element finite; a read-only device search.
 bool check_gradients_finite(const std::vector<TensorPtr>& params) {
-    std::vector<float*> ptrs;
+    std::vector<wm::DeviceVector*> vecs;
+    std::vector<const float*> ptrs;
+    std::vector<wm_grad_scale> gs;
     std::vector<int64_t> sizes;
-    live_grads(params, ptrs, sizes, false);
-    int all = 1;
-    check(wm_grads_finite_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()), sizes.data(), &all),
+    live_grads_deferred(params, vecs, ptrs, gs, sizes);
+    int64_t where[2] = {0, 0};
+    check(wm_grad_first_bad_multi_gs((int)ptrs.size(), ptrs.data(), gs.data(), sizes.data(), 1.0f, where),
           "check_gradients_finite");
-    return all != 0;
+    return where[0] >= (int64_t)ptrs.size();
 }
 
 // core/amp.h:303-327: norm of g / scale over all gradients; when
@@ -94,20 +127,18 @@ bool check_gradients_finite(const std::vector<TensorPtr>& params) {
 // by that coefficient.
 float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, float scale) {
     const float inv_scale = 1.0f / scale;
-    std::vector<float*> ptrs;
+    std::vector<wm::DeviceVector*> vecs;
+    std::vector<const float*> ptrs;
+    std::vector<wm_grad_scale> gs;
     std::vector<int64_t> sizes;
-    live_grads(params, ptrs, sizes);
+    live_grads_deferred(params, vecs, ptrs, gs, sizes);
     float sumsq = 0.0f;
+    auto total = std::make_shared<wm::DeviceVector>(1, 0.0f);
     if (!ptrs.empty()) {
-        void* d = nullptr;
-        check(wm_alloc(&d, sizeof(float)), "clip_grad_norm_amp");
-        int rc = wm_fill(static_cast<float*>(d), 0.0f, 1);
-        if (rc == WM_OK)
-            rc = wm_grad_sumsq_scaled_multi((int)ptrs.size(), const_cast<const float* const*>(ptrs.data()),
-                                            sizes.data(), inv_scale, static_cast<float*>(d));
-        if (rc == WM_OK) rc = wm_d2h(&sumsq, d, sizeof(float));
-        wm_free(d);
-        check(rc, "clip_grad_norm_amp");
+        check(wm_grad_sumsq_multi_gs((int)ptrs.size(), ptrs.data(), gs.data(), sizes.data(), inv_scale,
+                                     total->dev_rw()),
+              "clip_grad_norm_amp");
+        sumsq = (*total)[0];
     }
     // Known-zero gradients were skipped; with a non-finite inv_scale their
     // zeros would add 0 * inf (or 0 * NaN) = NaN to the reference's sum.
@@ -117,8 +148,9 @@ float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, f
     // each element scaled before it is squared, as the reference does
     const float total_norm = std::sqrt(sumsq);
     const float clip_coef = max_norm / (total_norm + 1e-6f);
+    // Deferred like clip_grad_norm_'s: the device recomputes this coefficient
+    // from the same sum of squares, bit for bit, when the products are taken.
     if (clip_coef < 1.0f)
-        for (size_t k = 0; k < ptrs.size(); ++k)
-            check(wm_unary(WM_SCALE, ptrs[k], ptrs[k], sizes[k], clip_coef, 0.0f), "clip_grad_norm_amp");
+        for (auto* v : vecs) v->defer_clip(total, max_norm);
     return total_norm;
 }

@@ -41,6 +41,11 @@ DeviceVector::DeviceVector(const DeviceVector& o) : n_(o.n_) {
         ck(wm_d2d(d_, o.d_, n_ * sizeof(float)), "DeviceVector copy");
         dev_valid_ = true;
         host_valid_ = false;
+        // the copy holds the same stored values: it takes the same scaling
+        def_unscale_ = o.def_unscale_;
+        def_count_ = o.def_count_;
+        def_sumsq_ = o.def_sumsq_;
+        def_max_norm_ = o.def_max_norm_;
     } else {
         h_ = o.h_;
         host_valid_ = true;
@@ -49,11 +54,14 @@ DeviceVector::DeviceVector(const DeviceVector& o) : n_(o.n_) {
 }
 
 DeviceVector::DeviceVector(DeviceVector&& o) noexcept
-    : n_(o.n_), d_(o.d_), h_(std::move(o.h_)), host_valid_(o.host_valid_), dev_valid_(o.dev_valid_), zero_(o.zero_) {
+    : n_(o.n_), d_(o.d_), h_(std::move(o.h_)), host_valid_(o.host_valid_), dev_valid_(o.dev_valid_), zero_(o.zero_),
+      def_unscale_(o.def_unscale_), def_count_(o.def_count_), def_sumsq_(std::move(o.def_sumsq_)),
+      def_max_norm_(o.def_max_norm_) {
     o.n_ = 0;
     o.d_ = nullptr;
     o.host_valid_ = o.dev_valid_ = true;
     o.zero_ = false;
+    o.drop_deferred();
 }
 
 DeviceVector::~DeviceVector() { release(); }
@@ -74,15 +82,21 @@ DeviceVector& DeviceVector::operator=(DeviceVector&& o) noexcept {
     host_valid_ = o.host_valid_;
     dev_valid_ = o.dev_valid_;
     zero_ = o.zero_;
+    def_unscale_ = o.def_unscale_;
+    def_count_ = o.def_count_;
+    def_sumsq_ = std::move(o.def_sumsq_);
+    def_max_norm_ = o.def_max_norm_;
     o.n_ = 0;
     o.d_ = nullptr;
     o.host_valid_ = o.dev_valid_ = true;
     o.zero_ = false;
+    o.drop_deferred();
     return *this;
 }
 
 DeviceVector& DeviceVector::operator=(const std::vector<float>& v) {
     release();
+    drop_deferred();
     n_ = v.size();
     h_ = v;
     host_valid_ = true;
@@ -110,6 +124,7 @@ void DeviceVector::ensure_dev_alloc() const {
 void DeviceVector::sync_host() const {
     if (n_ == 0) return;
     if (host_valid_) return;
+    apply_deferred();
     if (zero_) {
         h_.assign(n_, 0.0f);
     } else {
@@ -147,6 +162,11 @@ const float& DeviceVector::at(size_type i) const {
 
 const float* DeviceVector::dev() const {
     if (n_ == 0) return nullptr;
+    apply_deferred();
+    return dev_stored();
+}
+
+const float* DeviceVector::dev_stored() const {
     ensure_dev_alloc();
     if (!dev_valid_) {
         if (zero_) {
@@ -161,6 +181,7 @@ const float* DeviceVector::dev() const {
 
 float* DeviceVector::dev_write() {
     if (n_ == 0) return nullptr;
+    drop_deferred();
     ensure_dev_alloc();
     zero_ = false;
     dev_valid_ = true;
@@ -186,6 +207,7 @@ float* DeviceVector::dev_accum(int* accumulate) {
 }
 
 void DeviceVector::set_zero() {
+    drop_deferred();
     zero_ = n_ > 0;
     host_valid_ = n_ == 0;
     dev_valid_ = n_ == 0;
@@ -197,6 +219,7 @@ void DeviceVector::fill(float value) {
         set_zero();
         return;
     }
+    drop_deferred();
     ensure_dev_alloc();
     ck(wm_fill(d_, value, (int64_t)n_), "DeviceVector fill");
     zero_ = false;
@@ -208,6 +231,7 @@ void DeviceVector::resize(size_type n, float value) {
     if (n == n_) return;
     if (n_ == 0 || (zero_ && value == 0.0f && !std::signbit(value))) {
         release();
+        drop_deferred();
         h_.clear();
         n_ = n;
         if (value == 0.0f && !std::signbit(value)) set_zero();
@@ -225,6 +249,7 @@ void DeviceVector::resize(size_type n, float value) {
 
 void DeviceVector::assign(size_type n, float value) {
     release();
+    drop_deferred();
     h_.clear();
     n_ = n;
     zero_ = false;
@@ -236,6 +261,7 @@ void DeviceVector::assign(size_type n, float value) {
 
 void DeviceVector::clear() {
     release();
+    drop_deferred();
     h_.clear();
     n_ = 0;
     zero_ = false;
@@ -264,6 +290,57 @@ bool DeviceVector::operator==(const DeviceVector& o) const {
     const float* a = data();
     const float* b = o.data();
     return std::equal(a, a + n_, b);
+}
+
+// ---- deferred scaling --------------------------------------------------------
+
+void DeviceVector::drop_deferred() const {
+    def_unscale_ = 1.0f;
+    def_count_ = 0;
+    def_sumsq_.reset();
+    def_max_norm_ = 0.0f;
+}
+
+void DeviceVector::apply_deferred() const {
+    if (!deferred()) return;
+    // Hold the sum of squares until the kernel that reads it is enqueued: the
+    // call allocates its descriptor table from the pool, which must not hand
+    // out the sum's block before that.
+    const std::shared_ptr<const DeviceVector> keep = def_sumsq_;
+    wm_grad_scale gs{def_unscale_, def_count_, keep ? keep->dev() : nullptr, def_max_norm_};
+    float* p = d_;
+    const int64_t n = (int64_t)n_;
+    drop_deferred();
+    ck(wm_grad_scale_apply_multi(1, &p, &gs, &n), "deferred gradient scaling");
+}
+
+void DeviceVector::defer_unscale(float factor, int64_t count) {
+    if (n_ == 0 || count <= 0 || zero_) return;  // zeros times a finite factor stay zeros
+    if (count > (int64_t)n_) count = (int64_t)n_;
+    if (deferred()) apply_deferred();
+    dev_stored();
+    host_valid_ = false;
+    def_unscale_ = factor;
+    def_count_ = count;
+}
+
+void DeviceVector::defer_clip(std::shared_ptr<const DeviceVector> sumsq, float max_norm) {
+    if (n_ == 0 || zero_ || !sumsq) return;  // zeros times a finite coefficient stay zeros
+    if (def_sumsq_) apply_deferred();
+    dev_stored();  // an unscale deferred before stays: the clip follows it
+    host_valid_ = false;
+    def_sumsq_ = std::move(sumsq);
+    def_max_norm_ = max_norm;
+}
+
+const float* DeviceVector::dev_deferred(wm_grad_scale* gs) const {
+    wm_grad_scale none{1.0f, 0, nullptr, 0.0f};
+    if (!deferred()) {
+        *gs = none;
+        return dev();
+    }
+    *gs = wm_grad_scale{def_unscale_, def_count_, def_sumsq_ ? def_sumsq_->dev() : nullptr, def_max_norm_};
+    return d_;  // valid: a scaling is only deferred on a current device copy
 }
 
 // ---- HalfVector -----------------------------------------------------------

@@ -17,6 +17,15 @@
 //                 only a flag: nothing is allocated or filled until someone
 //                 needs the values, and the first backward contribution can
 //                 overwrite instead of read-modify-write (dev_accum()).
+//   deferred scaling  GradScaler::unscale and clip_grad_norm_ multiply a
+//                 gradient in place; the drop-in records the multiplication
+//                 instead (defer_unscale / defer_clip, include/wm_optim.h's
+//                 wm_grad_scale) and the next pass over the gradient applies
+//                 it as it reads: the optimizer step, a norm or a finiteness
+//                 search take dev_deferred().  Every other access sees the
+//                 scaled values: host access, dev(), dev_rw() and dev_accum()
+//                 first write the scaling into the device copy (one pass);
+//                 a full overwrite, set_zero() or fill() drop it.
 //
 // Not thread-safe, like the reference Tensor.
 #pragma once
@@ -24,7 +33,10 @@
 #include <cstddef>
 #include <cstdint>
 #include <initializer_list>
+#include <memory>
 #include <vector>
+
+#include "wm_optim.h"
 
 namespace wm {
 
@@ -95,10 +107,28 @@ public:
     // Fill with a constant on the device.
     void fill(float value);
 
+    // ---- deferred scaling (gradients) ------------------------------------
+    // Record v[i] *= factor for i < count (GradScaler::unscale's prefix).  An
+    // earlier deferred scaling is written first.
+    void defer_unscale(float factor, int64_t count);
+    // Record clip_grad_norm_'s v[i] *= c, c = max_norm / (sqrt(*sumsq) + 1e-6f),
+    // applied when c < 1; sumsq is a one-element device vector kept alive
+    // until the scaling is applied.  An earlier deferred clip is written
+    // first (an unscale may stay: the clip follows it).
+    void defer_clip(std::shared_ptr<const DeviceVector> sumsq, float max_norm);
+    bool deferred() const { return def_count_ > 0 || def_sumsq_ != nullptr; }
+    // Device pointer to the stored values and, in *gs, the scaling that gives
+    // the current values from them (none: unscale_count 0, clip_sumsq NULL).
+    const float* dev_deferred(wm_grad_scale* gs) const;
+    // Write a deferred scaling into the device copy.
+    void apply_deferred() const;
+
 private:
     void ensure_dev_alloc() const;
     void sync_host() const;   // make the host mirror current
     void release();
+    void drop_deferred() const;
+    const float* dev_stored() const;  // current device copy of the stored values (no deferred scaling applied)
 
     size_type n_ = 0;
     mutable float* d_ = nullptr;           // device buffer (capacity n_), lazily allocated
@@ -106,6 +136,11 @@ private:
     mutable bool host_valid_ = true;       // h_ holds the current values
     mutable bool dev_valid_ = true;        // d_ holds the current values
     bool zero_ = false;                    // logically all zeros (neither copy needs to be valid)
+    // deferred scaling of the device copy (the host mirror is stale while one is set)
+    mutable float def_unscale_ = 1.0f;
+    mutable int64_t def_count_ = 0;
+    mutable std::shared_ptr<const DeviceVector> def_sumsq_;
+    mutable float def_max_norm_ = 0.0f;
 };
 
 // fp16 bit patterns (uint16_t) with std::vector<uint16_t>'s API and the

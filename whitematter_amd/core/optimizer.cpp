@@ -4,6 +4,7 @@
 // host arithmetic (:179-259).
 #include "optimizer.h"
 
+#include <memory>
 #include <stdexcept>
 #include <string>
 
@@ -46,17 +47,19 @@ namespace {
 struct Lists {
     std::vector<float*> p, s1, s2;
     std::vector<const float*> g;
+    std::vector<wm_grad_scale> gs;  // each gradient's deferred scaling (unscale, clip)
     std::vector<int64_t> n;
 };
 
 Lists param_lists(std::vector<TensorPtr>& params, std::vector<wm::DeviceVector>* s1,
                   std::vector<wm::DeviceVector>* s2) {
     Lists l;
+    l.gs.resize(params.size());
     for (size_t i = 0; i < params.size(); ++i) {
         auto& p = params[i];
         l.n.push_back(numel(p));
         l.p.push_back(p->data.dev_rw());
-        l.g.push_back(p->grad.dev());
+        l.g.push_back(p->grad.dev_deferred(&l.gs[i]));
         l.s1.push_back(s1 ? (*s1)[i].dev_rw() : nullptr);
         l.s2.push_back(s2 ? (*s2)[i].dev_rw() : nullptr);
     }
@@ -73,8 +76,8 @@ SGD::SGD(const std::vector<TensorPtr>& params, float lr, float momentum) : Optim
 void SGD::step() {
     if (params.empty()) return;
     Lists l = param_lists(params, momentum > 0.0f ? &velocity : nullptr, nullptr);
-    check(wm_sgd_step_multi((int)params.size(), l.p.data(), l.g.data(), momentum > 0.0f ? l.s1.data() : nullptr,
-                            l.n.data(), lr, momentum),
+    check(wm_sgd_step_multi_gs((int)params.size(), l.p.data(), l.g.data(), l.gs.data(),
+                               momentum > 0.0f ? l.s1.data() : nullptr, l.n.data(), lr, momentum),
           "SGD::step");
 }
 
@@ -86,8 +89,9 @@ void Adam::step() {
     ++t;
     if (params.empty()) return;
     Lists l = param_lists(params, &m, &v);
-    check(wm_adam_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(), l.s2.data(), l.n.data(), lr,
-                             beta1, beta2, eps, bias_correction(beta1, t), bias_correction(beta2, t)),
+    check(wm_adam_step_multi_gs((int)params.size(), l.p.data(), l.g.data(), l.gs.data(), l.s1.data(), l.s2.data(),
+                                l.n.data(), lr, beta1, beta2, eps, bias_correction(beta1, t),
+                                bias_correction(beta2, t)),
           "Adam::step");
 }
 
@@ -99,8 +103,9 @@ void AdamW::step() {
     ++t;
     if (params.empty()) return;
     Lists l = param_lists(params, &m, &v);
-    check(wm_adamw_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(), l.s2.data(), l.n.data(), lr,
-                              beta1, beta2, eps, bias_correction(beta1, t), bias_correction(beta2, t), weight_decay),
+    check(wm_adamw_step_multi_gs((int)params.size(), l.p.data(), l.g.data(), l.gs.data(), l.s1.data(), l.s2.data(),
+                                 l.n.data(), lr, beta1, beta2, eps, bias_correction(beta1, t),
+                                 bias_correction(beta2, t), weight_decay),
           "AdamW::step");
 }
 
@@ -114,9 +119,9 @@ RMSprop::RMSprop(const std::vector<TensorPtr>& params, float lr, float alpha, fl
 void RMSprop::step() {
     if (params.empty()) return;
     Lists l = param_lists(params, &v, momentum > 0.0f ? &buffer : nullptr);
-    check(wm_rmsprop_step_multi((int)params.size(), l.p.data(), l.g.data(), l.s1.data(),
-                                momentum > 0.0f ? l.s2.data() : nullptr, l.n.data(), lr, alpha, eps, momentum,
-                                weight_decay),
+    check(wm_rmsprop_step_multi_gs((int)params.size(), l.p.data(), l.g.data(), l.gs.data(), l.s1.data(),
+                                   momentum > 0.0f ? l.s2.data() : nullptr, l.n.data(), lr, alpha, eps, momentum,
+                                   weight_decay),
           "RMSprop::step");
 }
 
@@ -143,31 +148,42 @@ GradList grad_list(const std::vector<TensorPtr>& params, bool write) {
 }
 
 // get_grad_norm's sum of squares (core/optimizer.cpp:145-153) into a
-// one-element device buffer.
-wm::DeviceVector grad_sumsq(const std::vector<TensorPtr>& params) {
-    wm::DeviceVector total(1, 0.0f);
-    GradList l = grad_list(params, false);
-    float* t = total.dev_rw();
-    if (!l.g.empty())
-        check(wm_grad_sumsq_multi((int)l.g.size(), l.g.data(), l.n.data(), t), "get_grad_norm");
+// one-element device buffer, over the gradients' current values (their
+// deferred scalings applied as they are read).
+std::shared_ptr<wm::DeviceVector> grad_sumsq(const std::vector<TensorPtr>& params) {
+    auto total = std::make_shared<wm::DeviceVector>(1, 0.0f);
+    std::vector<const float*> g;
+    std::vector<wm_grad_scale> gs;
+    std::vector<int64_t> n;
+    for (const auto& p : params) {
+        if (p->grad.empty()) continue;
+        gs.emplace_back();
+        g.push_back(p->grad.dev_deferred(&gs.back()));
+        n.push_back((int64_t)p->grad.size());
+    }
+    float* t = total->dev_rw();
+    if (!g.empty())
+        check(wm_grad_sumsq_multi_gs((int)g.size(), g.data(), gs.data(), n.data(), 1.0f, t), "get_grad_norm");
     return total;
 }
 
 }  // namespace
 
 float get_grad_norm(const std::vector<TensorPtr>& params) {
-    const wm::DeviceVector total = grad_sumsq(params);
-    return std::sqrt(total[0]);
+    const auto total = grad_sumsq(params);
+    return std::sqrt((*total)[0]);
 }
 
-// The clip coefficient is computed on the device from the device-side norm,
-// so clipping never waits for the host.
+// The norm is one read of every gradient; the multiplication by the clip
+// coefficient is deferred (DeviceVector::defer_clip): the coefficient is
+// computed on the device from the device-side norm when the scaling is
+// applied -- by the optimizer step that reads the gradients next, or one
+// pass before any other use -- so clipping never waits for the host and
+// costs no second pass over the gradients before a step.
 void clip_grad_norm_(std::vector<TensorPtr>& params, float max_norm) {
-    const wm::DeviceVector total = grad_sumsq(params);
-    GradList l = grad_list(params, true);
-    if (!l.g.empty())
-        check(wm_clip_grad_norm_scale_multi((int)l.g.size(), l.g.data(), l.n.data(), total.dev(), max_norm),
-              "clip_grad_norm_");
+    const auto total = grad_sumsq(params);
+    for (auto& p : params)
+        if (!p->grad.empty()) p->grad.defer_clip(total, max_norm);
 }
 
 void clip_grad_value_(std::vector<TensorPtr>& params, float clip_value) {

@@ -287,7 +287,36 @@ struct MultiEntry {
     int64_t chunk0;    // global index of the tensor's first kChunk chunk
     int64_t chunk0s;   // ... of its first kChunkS chunk
     int vec;           // every array of the tensor is 16-byte aligned
+    float gs_unscale;  // the gradient's deferred scaling (wm_grad_scale): elements
+    int64_t gs_count;  //   [0, gs_count) times gs_unscale, then every element times
+    const float* gs_sumsq;  // clip_grad_norm_'s coefficient from *gs_sumsq when < 1
+    float gs_max_norm;
     int pad;
+};
+
+// The deferred scaling of an entry's gradient (the g array of an update, the
+// p array of the gradient passes), as the eager passes would have left it in
+// memory: the unscale's product, then the clip's, each rounded to fp32
+// (__fmul_rn: never fused into a neighbouring add).  coef() is read once per
+// chunk.
+struct GradScaleApply {
+    float unscale, coef;
+    int64_t count;
+    bool clip;
+    __device__ __forceinline__ explicit GradScaleApply(const MultiEntry& e)
+        : unscale(e.gs_unscale), coef(1.0f), count(e.gs_count), clip(false) {
+        if (e.gs_sumsq) {
+#pragma clang fp contract(off)
+            const float c = e.gs_max_norm / (sqrtf(*e.gs_sumsq) + 1e-6f);  // core/optimizer.cpp:157
+            clip = c < 1.0f;
+            coef = c;
+        }
+    }
+    __device__ __forceinline__ float operator()(float g, int64_t i) const {
+        if (i < count) g = __fmul_rn(g, unscale);
+        if (clip) g = __fmul_rn(g, coef);
+        return g;
+    }
 };
 
 // Largest k with tab[k].chunk0 <= c.
@@ -327,6 +356,7 @@ __global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* 
     constexpr int NS = U::NS;
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const MultiEntry e = tab[find_entry_s(tab, count, chunks, c)];
+        const GradScaleApply gs(e);
         const int64_t start = (c - e.chunk0s) * kChunkS;
         const int64_t end = min(e.n, start + kChunkS);
         int64_t tail = start;
@@ -337,10 +367,10 @@ __global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* 
                 const float4 vg = ld_stream(e.g + i);
                 float4 v1 = NS > 0 ? ld_stream(e.s1 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
                 float4 v2 = NS > 1 ? ld_stream(e.s2 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-                upd(vp.x, vg.x, v1.x, v2.x);
-                upd(vp.y, vg.y, v1.y, v2.y);
-                upd(vp.z, vg.z, v1.z, v2.z);
-                upd(vp.w, vg.w, v1.w, v2.w);
+                upd(vp.x, gs(vg.x, i), v1.x, v2.x);
+                upd(vp.y, gs(vg.y, i + 1), v1.y, v2.y);
+                upd(vp.z, gs(vg.z, i + 2), v1.z, v2.z);
+                upd(vp.w, gs(vg.w, i + 3), v1.w, v2.w);
                 st_stream(e.p + i, vp);
                 if (NS > 0) st_stream(e.s1 + i, v1);
                 if (NS > 1) st_stream(e.s2 + i, v2);
@@ -351,7 +381,7 @@ __global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* 
             float vp = e.p[i];
             float v1 = NS > 0 ? e.s1[i] : 0.f;
             float v2 = NS > 1 ? e.s2[i] : 0.f;
-            upd(vp, e.g[i], v1, v2);
+            upd(vp, gs(e.g[i], i), v1, v2);
             e.p[i] = vp;
             if (NS > 0) e.s1[i] = v1;
             if (NS > 1) e.s2[i] = v2;
@@ -359,10 +389,12 @@ __global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* 
     }
 }
 
-// In-place per-element maps on the p arrays: kind 0 scales by clip_grad_norm_'s
+// In-place per-element maps on the p arrays, each element first taken through
+// its entry's deferred scaling: kind 0 scales by clip_grad_norm_'s
 // coefficient when it is < 1 (read from *total on the device), kind 1 clips to
 // [-a, a], kind 2 multiplies by a every element before the cutoff (table row
-// cut_tensor, element cut_index) in parameter order.
+// cut_tensor, element cut_index) in parameter order, kind 3 only writes the
+// deferred scaling into the array.
 __global__ void __launch_bounds__(kBlock) multi_map_kernel(const MultiEntry* __restrict__ tab, int count,
                                                             int64_t chunks, int kind, const float* __restrict__ total,
                                                             float a, int cut_tensor, int64_t cut_index) {
@@ -374,28 +406,31 @@ __global__ void __launch_bounds__(kBlock) multi_map_kernel(const MultiEntry* __r
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const int k = find_entry_s(tab, count, chunks, c);
         const MultiEntry e = tab[k];
+        const GradScaleApply gs(e);
         const int64_t start = (c - e.chunk0s) * kChunkS;
         int64_t end = min(e.n, start + kChunkS);
         if (kind == 2) {
             if (k > cut_tensor) continue;
             if (k == cut_tensor) end = min(end, cut_index);
         }
-        auto map1 = [&](float v) {
+        auto map1 = [&](float v, int64_t i) {
+            v = gs(v, i);
             if (kind == 0) return v * coef;
             if (kind == 1) return v > a ? a : (v < -a ? -a : v);
-            return v * a;
+            if (kind == 2) return v * a;
+            return v;
         };
         int64_t tail = start;
         if (e.vec && end > start) {
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
             for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
                 float4 v = ld_stream(e.p + i);
-                v.x = map1(v.x); v.y = map1(v.y); v.z = map1(v.z); v.w = map1(v.w);
+                v.x = map1(v.x, i); v.y = map1(v.y, i + 1); v.z = map1(v.z, i + 2); v.w = map1(v.w, i + 3);
                 st_stream(e.p + i, v);
             }
             tail = end4;
         }
-        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) e.p[i] = map1(e.p[i]);
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) e.p[i] = map1(e.p[i], i);
     }
 }
 
@@ -406,6 +441,7 @@ __global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* _
     __shared__ float lds[kBlock / 64];
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const MultiEntry e = tab[find_entry(tab, count, c)];
+        const GradScaleApply gs(e);
         const int64_t start = (c - e.chunk0) * kChunk;
         const int64_t end = min(e.n, start + kChunk);
         float s = 0.f;
@@ -414,13 +450,14 @@ __global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* _
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
             for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
                 const float4 v = ld_stream(e.p + i);
-                const float a = v.x * mul, b = v.y * mul, c2 = v.z * mul, d = v.w * mul;
+                const float a = gs(v.x, i) * mul, b = gs(v.y, i + 1) * mul, c2 = gs(v.z, i + 2) * mul,
+                            d = gs(v.w, i + 3) * mul;
                 s += a * a + b * b + c2 * c2 + d * d;
             }
             tail = end4;
         }
         for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) {
-            const float a = e.p[i] * mul;
+            const float a = gs(e.p[i], i) * mul;
             s += a * a;
         }
         s = block_sum<kBlock>(s, lds);
@@ -447,6 +484,7 @@ __global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntr
     __shared__ int64_t lds[kBlock];
     for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
         const MultiEntry e = tab[find_entry(tab, count, c)];
+        const GradScaleApply gs(e);
         const int64_t start = (c - e.chunk0) * kChunk;
         const int64_t end = min(e.n, start + kChunk);
         int64_t f = e.n;
@@ -455,8 +493,9 @@ __global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntr
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
             for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
                 const float4 v = ld_stream(e.p + i);
-                const bool b0 = !__builtin_isfinite(v.x * scale), b1 = !__builtin_isfinite(v.y * scale),
-                           b2 = !__builtin_isfinite(v.z * scale), b3 = !__builtin_isfinite(v.w * scale);
+                const bool b0 = !__builtin_isfinite(gs(v.x, i) * scale), b1 = !__builtin_isfinite(gs(v.y, i + 1) * scale),
+                           b2 = !__builtin_isfinite(gs(v.z, i + 2) * scale),
+                           b3 = !__builtin_isfinite(gs(v.w, i + 3) * scale);
                 if (b0 || b1 || b2 || b3) {
                     f = i + (b0 ? 0 : b1 ? 1 : b2 ? 2 : 3);
                     break;
@@ -466,7 +505,7 @@ __global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntr
         }
         if (f == e.n)
             for (int64_t i = tail + threadIdx.x; i < end; i += kBlock)
-                if (!__builtin_isfinite(e.p[i] * scale)) { f = i; break; }
+                if (!__builtin_isfinite(gs(e.p[i], i) * scale)) { f = i; break; }
         lds[threadIdx.x] = f;
         __syncthreads();
         for (int w = kBlock / 2; w > 0; w >>= 1) {
@@ -518,7 +557,7 @@ struct MultiTable {
     ~MultiTable() { delete dev; }
 
     int build(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
-              const int64_t* n, int ns, const char* what) {
+              const int64_t* n, int ns, const char* what, const wm_grad_scale* gscale = nullptr) {
         for (int k = 0; k < count; ++k) {
             if (n[k] < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
             if (n[k] == 0) continue;
@@ -534,6 +573,16 @@ struct MultiTable {
             e.chunk0s = chunks_s;
             e.vec = aligned16(e.p) && (!e.g || aligned16(e.g)) && (!e.s1 || aligned16(e.s1)) &&
                     (!e.s2 || aligned16(e.s2));
+            e.gs_unscale = 1.0f;
+            if (gscale) {
+                const wm_grad_scale& q = gscale[k];
+                if (q.unscale_count < 0 || q.unscale_count > n[k])
+                    return set_error(WM_ERR_INVALID, std::string(what) + ": unscale_count outside the tensor");
+                e.gs_unscale = q.unscale;
+                e.gs_count = q.unscale_count;
+                e.gs_sumsq = q.clip_sumsq;
+                e.gs_max_norm = q.clip_max_norm;
+            }
             chunks += (n[k] + kChunk - 1) / kChunk;
             chunks_s += (n[k] + kChunkS - 1) / kChunkS;
             host.push_back(e);
@@ -617,7 +666,7 @@ std::vector<std::pair<int, int>> independent_runs(int count, float* const* p, co
 
 template <class U>
 int launch_multi(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
-                 const int64_t* n, const U& upd, const char* what) {
+                 const int64_t* n, const U& upd, const char* what, const wm_grad_scale* gs = nullptr) {
     if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
     if (count == 0) return WM_OK;
     if (!p || !g || !n || (U::NS > 0 && !s1) || (U::NS > 1 && !s2))
@@ -627,7 +676,7 @@ int launch_multi(int count, float* const* p, const float* const* g, float* const
         const int b = run.first;
         MultiTable t;
         WM_TRY(t.build(run.second - b, p + b, g + b, s1 ? s1 + b : nullptr, s2 ? s2 + b : nullptr, n + b, U::NS,
-                       what));
+                       what, gs ? gs + b : nullptr));
         if (t.chunks == 0) continue;
         launch_kernel(multi_update_kernel<U>, dim3(t.grid_s()), dim3(kBlock), 0, stream(), t.table(), t.count(),
                       t.chunks_s, upd);
@@ -777,51 +826,96 @@ int wm_grad_unscale(int count, float* const* grads, const int64_t* sizes, float 
 
 // ---- multi-tensor variants ---------------------------------------------------
 
+static int sgd_multi(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                     float* const* velocity, const int64_t* n, float lr, float momentum, const char* what) {
+    const SgdArgs a{lr, momentum};
+    if (momentum > 0.0f) return launch_multi(count, p, g, velocity, nullptr, n, Upd<0, true, false>{a}, what, gs);
+    return launch_multi(count, p, g, nullptr, nullptr, n, Upd<0, false, false>{a}, what, gs);
+}
+
+static int adam_multi(bool decoupled, int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                      float* const* m, float* const* v, const int64_t* n, float lr, float beta1, float beta2,
+                      float eps, float bc1, float bc2, float wd, const char* what) {
+    const AdamArgs a{lr, beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bc1, bc2, wd};
+    if (decoupled) return launch_multi(count, p, g, m, v, n, Upd<1, true, false>{a}, what, gs);
+    return launch_multi(count, p, g, m, v, n, Upd<1, false, false>{a}, what, gs);
+}
+
+static int rmsprop_multi(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                         float* const* v, float* const* buffer, const int64_t* n, float lr, float alpha, float eps,
+                         float momentum, float weight_decay, const char* what) {
+    const RmsArgs a{lr, alpha, 1.0f - alpha, eps, momentum, weight_decay};
+    const bool mom = momentum > 0.0f, wd = weight_decay != 0.0f;
+    if (wd && mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, true, true>{a}, what, gs);
+    if (wd) return launch_multi(count, p, g, v, nullptr, n, Upd<2, true, false>{a}, what, gs);
+    if (mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, false, true>{a}, what, gs);
+    return launch_multi(count, p, g, v, nullptr, n, Upd<2, false, false>{a}, what, gs);
+}
+
 int wm_sgd_step_multi(int count, float* const* p, const float* const* g, float* const* velocity, const int64_t* n,
                       float lr, float momentum) {
-    const SgdArgs a{lr, momentum};
-    if (momentum > 0.0f)
-        return launch_multi(count, p, g, velocity, nullptr, n, Upd<0, true, false>{a}, "wm_sgd_step_multi");
-    return launch_multi(count, p, g, nullptr, nullptr, n, Upd<0, false, false>{a}, "wm_sgd_step_multi");
+    return sgd_multi(count, p, g, nullptr, velocity, n, lr, momentum, "wm_sgd_step_multi");
 }
 
 int wm_adam_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
                        const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
                        float bias_correction2) {
-    const AdamArgs a{lr, beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bias_correction1, bias_correction2, 0.0f};
-    return launch_multi(count, p, g, m, v, n, Upd<1, false, false>{a}, "wm_adam_step_multi");
+    return adam_multi(false, count, p, g, nullptr, m, v, n, lr, beta1, beta2, eps, bias_correction1,
+                      bias_correction2, 0.0f, "wm_adam_step_multi");
 }
 
 int wm_adamw_step_multi(int count, float* const* p, const float* const* g, float* const* m, float* const* v,
                         const int64_t* n, float lr, float beta1, float beta2, float eps, float bias_correction1,
                         float bias_correction2, float weight_decay) {
-    const AdamArgs a{lr,  beta1, beta2, 1.0f - beta1, 1.0f - beta2, eps, bias_correction1, bias_correction2,
-                     weight_decay};
-    return launch_multi(count, p, g, m, v, n, Upd<1, true, false>{a}, "wm_adamw_step_multi");
+    return adam_multi(true, count, p, g, nullptr, m, v, n, lr, beta1, beta2, eps, bias_correction1, bias_correction2,
+                      weight_decay, "wm_adamw_step_multi");
 }
 
 int wm_rmsprop_step_multi(int count, float* const* p, const float* const* g, float* const* v, float* const* buffer,
                           const int64_t* n, float lr, float alpha, float eps, float momentum, float weight_decay) {
-    const RmsArgs a{lr, alpha, 1.0f - alpha, eps, momentum, weight_decay};
-    const bool mom = momentum > 0.0f, wd = weight_decay != 0.0f;
-    const char* what = "wm_rmsprop_step_multi";
-    if (wd && mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, true, true>{a}, what);
-    if (wd) return launch_multi(count, p, g, v, nullptr, n, Upd<2, true, false>{a}, what);
-    if (mom) return launch_multi(count, p, g, v, buffer, n, Upd<2, false, true>{a}, what);
-    return launch_multi(count, p, g, v, nullptr, n, Upd<2, false, false>{a}, what);
+    return rmsprop_multi(count, p, g, nullptr, v, buffer, n, lr, alpha, eps, momentum, weight_decay,
+                         "wm_rmsprop_step_multi");
 }
 
-static int multi_grads(int count, const float* const* g, const int64_t* n, MultiTable& t, const char* what) {
+int wm_sgd_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                         float* const* velocity, const int64_t* n, float lr, float momentum) {
+    return sgd_multi(count, p, g, gs, velocity, n, lr, momentum, "wm_sgd_step_multi_gs");
+}
+
+int wm_adam_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                          float* const* m, float* const* v, const int64_t* n, float lr, float beta1, float beta2,
+                          float eps, float bias_correction1, float bias_correction2) {
+    return adam_multi(false, count, p, g, gs, m, v, n, lr, beta1, beta2, eps, bias_correction1, bias_correction2,
+                      0.0f, "wm_adam_step_multi_gs");
+}
+
+int wm_adamw_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                           float* const* m, float* const* v, const int64_t* n, float lr, float beta1, float beta2,
+                           float eps, float bias_correction1, float bias_correction2, float weight_decay) {
+    return adam_multi(true, count, p, g, gs, m, v, n, lr, beta1, beta2, eps, bias_correction1, bias_correction2,
+                      weight_decay, "wm_adamw_step_multi_gs");
+}
+
+int wm_rmsprop_step_multi_gs(int count, float* const* p, const float* const* g, const wm_grad_scale* gs,
+                             float* const* v, float* const* buffer, const int64_t* n, float lr, float alpha,
+                             float eps, float momentum, float weight_decay) {
+    return rmsprop_multi(count, p, g, gs, v, buffer, n, lr, alpha, eps, momentum, weight_decay,
+                         "wm_rmsprop_step_multi_gs");
+}
+
+static int multi_grads(int count, const float* const* g, const int64_t* n, MultiTable& t, const char* what,
+                       const wm_grad_scale* gs = nullptr) {
     if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
     if (count > 0 && (!g || !n)) return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
     WM_CHECK_INIT();
-    return t.build(count, const_cast<float* const*>(g), nullptr, nullptr, nullptr, n, 0, what);
+    return t.build(count, const_cast<float* const*>(g), nullptr, nullptr, nullptr, n, 0, what, gs);
 }
 
-static int sumsq_multi(int count, const float* const* g, const int64_t* n, float mul, float* total, const char* what) {
+static int sumsq_multi(int count, const float* const* g, const int64_t* n, float mul, float* total, const char* what,
+                       const wm_grad_scale* gs = nullptr) {
     if (!total) return set_error(WM_ERR_INVALID, std::string(what) + ": null total");
     MultiTable t;
-    WM_TRY(multi_grads(count, g, n, t, what));
+    WM_TRY(multi_grads(count, g, n, t, what, gs));
     if (t.chunks == 0) return wm_fill(total, 0.0f, 1);
     Workspace part((size_t)t.chunks * sizeof(float));
     if (!part.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
@@ -840,30 +934,57 @@ int wm_grad_sumsq_scaled_multi(int count, const float* const* g, const int64_t* 
     return sumsq_multi(count, g, n, mul, total, "wm_grad_sumsq_scaled_multi");
 }
 
+// (list position, element) of the first element whose value times `scale`
+// is not finite, in list order, or (count, 0); one search launch and its
+// finalize, then one synchronisation for the answer.
+static int first_bad_multi(int count, const float* const* g, const wm_grad_scale* gs, const int64_t* n, float scale,
+                           int64_t* where_out, const char* what) {
+    where_out[0] = count;
+    where_out[1] = 0;
+    MultiTable t;
+    WM_TRY(multi_grads(count, g, n, t, what, gs));
+    if (t.chunks == 0) return WM_OK;
+    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
+    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
+    launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
+                  scale, first.as<int64_t>());
+    WM_TRY(check_launch(what));
+    launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
+                  t.chunks, first.as<int64_t>(), where.as<int64_t>());
+    WM_TRY(check_launch(what));
+    int64_t cut[2] = {0, 0};
+    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
+    if (cut[0] < t.count()) {  // table row -> list position
+        where_out[0] = t.index[(size_t)cut[0]];
+        where_out[1] = cut[1];
+    }
+    return WM_OK;
+}
+
 int wm_grads_finite_multi(int count, const float* const* g, const int64_t* n, int* all_finite) {
     if (!all_finite) return set_error(WM_ERR_INVALID, "wm_grads_finite_multi: null all_finite");
     *all_finite = 1;
-    MultiTable t;
-    WM_TRY(multi_grads(count, g, n, t, "wm_grads_finite_multi"));
-    if (t.chunks == 0) return WM_OK;
-    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
-    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, "wm_grads_finite_multi: workspace");
-    launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
-                  1.0f, first.as<int64_t>());
-    WM_TRY(check_launch("wm_grads_finite_multi"));
-    launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                  t.chunks, first.as<int64_t>(), where.as<int64_t>());
-    WM_TRY(check_launch("wm_grads_finite_multi(finalize)"));
-    int64_t cut[2] = {0, 0};
-    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
-    *all_finite = cut[0] < t.count() ? 0 : 1;
+    int64_t where[2];
+    WM_TRY(first_bad_multi(count, g, nullptr, n, 1.0f, where, "wm_grads_finite_multi"));
+    *all_finite = where[0] < count ? 0 : 1;
     return WM_OK;
+}
+
+int wm_grad_first_bad_multi_gs(int count, const float* const* g, const wm_grad_scale* gs, const int64_t* n,
+                               float scale, int64_t* where) {
+    if (!where) return set_error(WM_ERR_INVALID, "wm_grad_first_bad_multi_gs: null where");
+    return first_bad_multi(count, g, gs, n, scale, where, "wm_grad_first_bad_multi_gs");
+}
+
+int wm_grad_sumsq_multi_gs(int count, const float* const* g, const wm_grad_scale* gs, const int64_t* n, float mul,
+                           float* total) {
+    return sumsq_multi(count, g, n, mul, total, "wm_grad_sumsq_multi_gs", gs);
 }
 
 // An in-place map over a gradient list, one launch per run of gradients that
 // do not overlap (a gradient listed twice is mapped twice, in list order).
 static int map_grads(int count, float* const* g, const int64_t* n, int mode, const float* total, float arg,
-                     const char* what) {
+                     const char* what, const wm_grad_scale* gs = nullptr) {
     if (count < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative count");
     if (count > 0 && (!g || !n)) return set_error(WM_ERR_INVALID, std::string(what) + ": null array");
     if (count == 0) return WM_OK;
@@ -871,7 +992,7 @@ static int map_grads(int count, float* const* g, const int64_t* n, int mode, con
     for (const auto& run : independent_runs(count, g, nullptr, nullptr, nullptr, n, 0)) {
         const int b = run.first;
         MultiTable t;
-        WM_TRY(t.build(run.second - b, g + b, nullptr, nullptr, nullptr, n + b, 0, what));
+        WM_TRY(t.build(run.second - b, g + b, nullptr, nullptr, nullptr, n + b, 0, what, gs ? gs + b : nullptr));
         if (t.chunks == 0) continue;
         launch_kernel(multi_map_kernel, dim3(t.grid_s()), dim3(kBlock), 0, stream(), t.table(), t.count(),
                       t.chunks_s, mode, total, arg, 0, (int64_t)0);
@@ -888,6 +1009,11 @@ int wm_clip_grad_norm_scale_multi(int count, float* const* g, const int64_t* n, 
 
 int wm_clip_grad_value_multi(int count, float* const* g, const int64_t* n, float clip_value) {
     return map_grads(count, g, n, 1, nullptr, clip_value, "wm_clip_grad_value_multi");
+}
+
+int wm_grad_scale_apply_multi(int count, float* const* g, const wm_grad_scale* gs, const int64_t* n) {
+    if (count > 0 && !gs) return set_error(WM_ERR_INVALID, "wm_grad_scale_apply_multi: null scales");
+    return map_grads(count, g, n, 3, nullptr, 0.0f, "wm_grad_scale_apply_multi", gs);
 }
 
 }  // extern "C"
