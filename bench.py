@@ -96,6 +96,7 @@ class Op:
         self.kms = []  # kernel basis: the op's dispatch durations summed (trace, or span events)
         self.kparts = []  # the same, dispatch by dispatch
         self.knames = None  # the dispatches' kernel names (trace basis)
+        self.prepare = None  # untimed work before each launch (e.g. refilling gradients)
 
 
 class KTrace:
@@ -436,10 +437,6 @@ def opt_ops():
         S2.append(W.DeviceArray((n,))); S2[-1].fill(0.0)
     N = sum(int(np.prod(s)) for s in shapes)
     sizes = [int(np.prod(s)) for s in shapes]
-    total = W.DeviceArray((1,))
-    gptrs = (W.C.c_void_p * len(G))(*[g.ptr for g in G])
-    gsizes = (W.C.c_int64 * len(G))(*sizes)
-    found = W.C.c_int()
     L = W.lib()
     t = [0]
 
@@ -462,30 +459,52 @@ def opt_ops():
     def rms():
         W.check(L.wm_rmsprop_step_multi(cnt, pP, pG, pS2, None, pN, 1e-4, 0.99, 1e-8, 0.0, 0.0))
 
-    def clip():
-        W.check(L.wm_grad_sumsq_multi(cnt, pG, pN, total.vp))
-        # max_norm 0 clips on every call (coefficient 0 < 1), so the timed pass
-        # always reads and writes every gradient
-        W.check(L.wm_clip_grad_norm_scale_multi(cnt, pG, pN, total.vp, 0.0))
+    # clip_grad_norm_ / GradScaler::unscale followed by the step, through the
+    # drop-in API (core/optimizer.h, core/amp.h) on a second copy of the list:
+    # the norm (or the unscale's finiteness search) reads every gradient once,
+    # its multiplication is deferred into the step, which reads the gradients
+    # once more -- 4 + 28 bytes per element, the eager in-place multiplication's
+    # read + write of every gradient gone.  Before each launch (untimed) the
+    # gradients are refilled from their source copy, as a backward pass would
+    # rewrite them, so no deferred scaling carries over between launches.
+    from whitematter_amd import _tensor as T
+    tp, tsrc = [], []
+    for i, s in enumerate(shapes):
+        n = int(np.prod(s))
+        tp.append(T.Tensor.from_array((rng.standard_normal(n) * 0.02).astype(np.float32), list(s), True))
+        # mul(1.0): an exact device copy, so the refills are device-to-device
+        tsrc.append(T.Tensor.from_array((rng.standard_normal(n) * 1e-3).astype(np.float32), list(s)).mul(1.0))
+    topt = T.AdamW(tp, 1e-4, 0.9, 0.999, 1e-8, 0.01)
+    scaler = T.GradScaler(1024.0, 2.0, 0.5, 2000)
 
-    def unscale():
-        W.check(L.wm_grad_unscale(len(G), W.C.cast(gptrs, W.C.c_void_p), W.C.cast(gsizes, W.C.c_void_p), 1.0,
-                                  W.C.byref(found)))
+    def refill():
+        for p_, s_ in zip(tp, tsrc):
+            p_.set_grad_from(s_)
+
+    def clip_step():
+        T.clip_grad_norm_(tp, 1.0)  # norm ~11: clips on every call
+        topt.step()
+
+    def unscale_step():
+        if not scaler.unscale(topt):
+            raise RuntimeError("opt: unscale found a non-finite gradient")
+        scaler.step(topt, True)
 
     ops = [
         Op("AdamW step", adam, N * 28, "multi_update_kernel<wm::Upd<1, true", N),
         Op("SGD momentum step", sgd, N * 20, "multi_update_kernel<wm::Upd<0, true", N),
         Op("RMSprop step", rms, N * 20, "multi_update_kernel<wm::Upd<2, false, false", N),
-        # algorithmic bytes: every gradient read once and written once (8 per
-        # element); both ops read the gradients twice (the norm, or the first
-        # non-finite position, must be known before any write), so they move 12
-        Op("clip_grad_norm_", clip, N * 8, "multi_sumsq_kernel", N),
-        Op("GradScaler unscale", unscale, N * 8, "multi_first_bad_kernel", N),
+        Op("clip_grad_norm_ + AdamW step", clip_step, N * 32, "multi_update_kernel<wm::Upd<1, true", N),
+        Op("GradScaler unscale + AdamW step", unscale_step, N * 32, "multi_update_kernel<wm::Upd<1, true", N),
     ]
-    return ops, P + G + S1 + S2 + [total], {
+    for op in ops[3:]:
+        op.prepare = refill
+    return ops, P + G + S1 + S2 + [tp, tsrc, topt, scaler], {
         "workload": "opt: %d parameter tensors, %d parameters (GPT-2-small shapes), fp32 params / grads / "
-                    "state; one AdamW, SGD-momentum and RMSprop step, clip_grad_norm_ and GradScaler unscale, "
-                    "each one multi-tensor launch (pair) over the list" % (len(shapes), N), "elements": N}
+                    "state; one AdamW, SGD-momentum and RMSprop step (one multi-tensor launch each), and "
+                    "clip_grad_norm_ + AdamW step, GradScaler unscale + AdamW step through the drop-in "
+                    "optimizer / GradScaler (the gradients refilled, untimed, before each launch)"
+                    % (len(shapes), N), "elements": N}
 
 
 
@@ -1518,7 +1537,11 @@ TARGET_FRAC = 0.70
 
 
 def _launch(op, basis, flush, kt):
-    """One launch of op after the 512 MiB flush fill, timed in `basis`."""
+    """One launch of op after the 512 MiB flush fill (and the op's untimed
+    preparation, if it has one), timed in `basis`."""
+    if op.prepare is not None:
+        op.prepare()
+        W.sync()  # its copies dispatched and done before the timed window opens
     flush.fill(1.0)
     if basis in ("trace", "span", "external") and getattr(op, "host_io", False):
         return  # host-driven copies: timed on the event basis only

@@ -136,7 +136,7 @@ float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, f
     auto total = std::make_shared<wm::DeviceVector>(1, 0.0f);
     if (!ptrs.empty()) {
         check(wm_grad_sumsq_multi_gs((int)ptrs.size(), ptrs.data(), gs.data(), sizes.data(), inv_scale,
-                                     total->dev_rw()),
+                                     total->dev_write()),
               "clip_grad_norm_amp");
         sumsq = (*total)[0];
     }

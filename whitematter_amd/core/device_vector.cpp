@@ -68,6 +68,19 @@ DeviceVector::~DeviceVector() { release(); }
 
 DeviceVector& DeviceVector::operator=(const DeviceVector& o) {
     if (this == &o) return *this;
+    if (o.n_ == n_ && n_ > 0 && d_ && !o.zero_ && o.dev_valid_) {
+        // same size: copy into this buffer, as std::vector's copy assignment
+        // reuses its storage (a gradient assigned every step keeps its address)
+        ck(wm_d2d(d_, o.d_, n_ * sizeof(float)), "DeviceVector copy");
+        dev_valid_ = true;
+        host_valid_ = false;
+        zero_ = false;
+        def_unscale_ = o.def_unscale_;
+        def_count_ = o.def_count_;
+        def_sumsq_ = o.def_sumsq_;
+        def_max_norm_ = o.def_max_norm_;
+        return *this;
+    }
     DeviceVector tmp(o);
     *this = std::move(tmp);
     return *this;

@@ -161,9 +161,9 @@ std::shared_ptr<wm::DeviceVector> grad_sumsq(const std::vector<TensorPtr>& param
         g.push_back(p->grad.dev_deferred(&gs.back()));
         n.push_back((int64_t)p->grad.size());
     }
-    float* t = total->dev_rw();
-    if (!g.empty())
-        check(wm_grad_sumsq_multi_gs((int)g.size(), g.data(), gs.data(), n.data(), 1.0f, t), "get_grad_norm");
+    if (g.empty()) return total;  // known zero
+    check(wm_grad_sumsq_multi_gs((int)g.size(), g.data(), gs.data(), n.data(), 1.0f, total->dev_write()),
+          "get_grad_norm");
     return total;
 }
 

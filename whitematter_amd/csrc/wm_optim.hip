@@ -19,6 +19,8 @@
 
 #include <algorithm>
 #include <cstring>
+#include <memory>
+#include <mutex>
 #include <vector>
 
 namespace wm {
@@ -276,7 +278,13 @@ __global__ void __launch_bounds__(kBlock) scale_prefix_kernel(float* __restrict_
 // ---------------------------------------------------------------------------
 
 constexpr int64_t kChunk = 65536;              // reductions: elements per chunk
-constexpr int64_t kChunkS = 4 * (int64_t)kBlock;  // element-wise passes
+constexpr int kUpdU = 4;                         // float4 per thread per element-wise chunk
+constexpr int64_t kChunkS = 4 * (int64_t)kBlock * kUpdU;  // element-wise passes
+// The reductions' sweep issues kRedU float4 loads per thread before using
+// any: one load in flight per wave left the sum of squares at 80 % and the
+// finiteness search at 60 % of the HBM peak (GPT-2-small list).
+constexpr int kRedU = 4;
+constexpr int64_t kRedStride = 4 * (int64_t)kBlock;
 
 struct MultiEntry {
     float* p;          // updated array (params; gradients for clipping / unscaling)
@@ -359,6 +367,30 @@ __global__ void __launch_bounds__(kBlock) multi_update_kernel(const MultiEntry* 
         const GradScaleApply gs(e);
         const int64_t start = (c - e.chunk0s) * kChunkS;
         const int64_t end = min(e.n, start + kChunkS);
+        if (e.vec && end - start == kChunkS) {
+            // a whole chunk: every load issued before the first update
+            float4 vp[kUpdU], vg[kUpdU], v1[kUpdU], v2[kUpdU];
+#pragma unroll
+            for (int u = 0; u < kUpdU; ++u) {
+                const int64_t i = start + 4 * (int64_t)threadIdx.x + u * kRedStride;
+                vp[u] = ld_stream(e.p + i);
+                vg[u] = ld_stream(e.g + i);
+                v1[u] = NS > 0 ? ld_stream(e.s1 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                v2[u] = NS > 1 ? ld_stream(e.s2 + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kUpdU; ++u) {
+                const int64_t i = start + 4 * (int64_t)threadIdx.x + u * kRedStride;
+                upd(vp[u].x, gs(vg[u].x, i), v1[u].x, v2[u].x);
+                upd(vp[u].y, gs(vg[u].y, i + 1), v1[u].y, v2[u].y);
+                upd(vp[u].z, gs(vg[u].z, i + 2), v1[u].z, v2[u].z);
+                upd(vp[u].w, gs(vg[u].w, i + 3), v1[u].w, v2[u].w);
+                st_stream(e.p + i, vp[u]);
+                if (NS > 0) st_stream(e.s1 + i, v1[u]);
+                if (NS > 1) st_stream(e.s2 + i, v2[u]);
+            }
+            continue;
+        }
         int64_t tail = start;
         if (e.vec) {
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
@@ -448,12 +480,20 @@ __global__ void __launch_bounds__(kBlock) multi_sumsq_kernel(const MultiEntry* _
         int64_t tail = start;
         if (e.vec) {
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
-            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
-                const float4 v = ld_stream(e.p + i);
+            auto acc = [&](const float4 v, int64_t i) {
                 const float a = gs(v.x, i) * mul, b = gs(v.y, i + 1) * mul, c2 = gs(v.z, i + 2) * mul,
                             d = gs(v.w, i + 3) * mul;
                 s += a * a + b * b + c2 * c2 + d * d;
+            };
+            int64_t i = start + 4 * (int64_t)threadIdx.x;
+            for (; i + (kRedU - 1) * kRedStride < end4; i += kRedU * kRedStride) {
+                float4 v[kRedU];
+#pragma unroll
+                for (int u = 0; u < kRedU; ++u) v[u] = ld_stream(e.p + i + u * kRedStride);
+#pragma unroll
+                for (int u = 0; u < kRedU; ++u) acc(v[u], i + u * kRedStride);
             }
+            for (; i < end4; i += kRedStride) acc(ld_stream(e.p + i), i);
             tail = end4;
         }
         for (int64_t i = tail + threadIdx.x; i < end; i += kBlock) {
@@ -477,7 +517,9 @@ __global__ void __launch_bounds__(kBlock) multi_sum_finalize_kernel(const float*
 }
 
 // first[c] = smallest in-tensor index of chunk c whose scaled value is not
-// finite, or -1.
+// finite, or -1.  The scan has no early exit (each thread keeps its first
+// non-finite index), so its loads pipeline like the sum of squares'; the
+// block's minimum is only formed when some thread found one.
 __global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntry* __restrict__ tab, int count,
                                                                   int64_t chunks, float scale,
                                                                   int64_t* __restrict__ first) {
@@ -491,29 +533,37 @@ __global__ void __launch_bounds__(kBlock) multi_first_bad_kernel(const MultiEntr
         int64_t tail = start;
         if (e.vec) {
             const int64_t end4 = start + ((end - start) & ~int64_t(3));
-            for (int64_t i = start + 4 * (int64_t)threadIdx.x; i < end4; i += 4 * kBlock) {
-                const float4 v = ld_stream(e.p + i);
+            auto scan = [&](const float4 v, int64_t i) {
                 const bool b0 = !__builtin_isfinite(gs(v.x, i) * scale), b1 = !__builtin_isfinite(gs(v.y, i + 1) * scale),
                            b2 = !__builtin_isfinite(gs(v.z, i + 2) * scale),
                            b3 = !__builtin_isfinite(gs(v.w, i + 3) * scale);
-                if (b0 || b1 || b2 || b3) {
-                    f = i + (b0 ? 0 : b1 ? 1 : b2 ? 2 : 3);
-                    break;
-                }
+                if ((b0 || b1 || b2 || b3) && f == e.n) f = i + (b0 ? 0 : b1 ? 1 : b2 ? 2 : 3);
+            };
+            int64_t i = start + 4 * (int64_t)threadIdx.x;
+            for (; i + (kRedU - 1) * kRedStride < end4; i += kRedU * kRedStride) {
+                float4 v[kRedU];
+#pragma unroll
+                for (int u = 0; u < kRedU; ++u) v[u] = ld_stream(e.p + i + u * kRedStride);
+#pragma unroll
+                for (int u = 0; u < kRedU; ++u) scan(v[u], i + u * kRedStride);
             }
+            for (; i < end4; i += kRedStride) scan(ld_stream(e.p + i), i);
             tail = end4;
         }
-        if (f == e.n)
-            for (int64_t i = tail + threadIdx.x; i < end; i += kBlock)
-                if (!__builtin_isfinite(gs(e.p[i], i) * scale)) { f = i; break; }
-        lds[threadIdx.x] = f;
-        __syncthreads();
-        for (int w = kBlock / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+        for (int64_t i = tail + threadIdx.x; i < end; i += kBlock)
+            if (!__builtin_isfinite(gs(e.p[i], i) * scale) && f == e.n) f = i;
+        if (__syncthreads_or(f < e.n)) {
+            lds[threadIdx.x] = f;
             __syncthreads();
+            for (int w = kBlock / 2; w > 0; w >>= 1) {
+                if ((int)threadIdx.x < w) lds[threadIdx.x] = min_i64(lds[threadIdx.x], lds[threadIdx.x + w]);
+                __syncthreads();
+            }
+            if (threadIdx.x == 0) first[c] = lds[0];
+            __syncthreads();
+        } else if (threadIdx.x == 0) {
+            first[c] = -1;
         }
-        if (threadIdx.x == 0) first[c] = lds[0] < e.n ? lds[0] : -1;
-        __syncthreads();
     }
 }
 
@@ -546,6 +596,68 @@ __global__ void __launch_bounds__(kBlock) multi_first_bad_finalize_kernel(const 
     }
 }
 
+// A descriptor table's device copy; returned to the pool when the last
+// holder lets go (the pool's reuse is ordered on the library stream, after
+// the launches that read it).
+struct DevTable {
+    void* p = nullptr;
+    explicit DevTable(size_t bytes) : p(ws_alloc(bytes)) {}
+    ~DevTable() { if (p) ws_free(p); }
+    DevTable(const DevTable&) = delete;
+    DevTable& operator=(const DevTable&) = delete;
+};
+
+// Device copies of the last kTableSlots descriptor tables.  A training loop
+// passes the same lists every step, so a table equal byte for byte to a
+// cached one is used again instead of uploaded: the upload is a copy
+// dispatch on the stream (~4 us) and may wait for the staging buffer.
+// Tables are read-only on the device; each launch holds its table until the
+// launch is enqueued, so an eviction by another thread cannot recycle it
+// under a pending launch.
+class TableCache {
+    static constexpr size_t kTableSlots = 16;
+    struct Slot {
+        std::vector<unsigned char> bytes;
+        std::shared_ptr<DevTable> dev;
+        uint64_t used = 0;
+    };
+    std::mutex mu_;
+    std::vector<Slot> slots_;
+    uint64_t clock_ = 0;
+
+public:
+    int get(const std::vector<unsigned char>& bytes, std::shared_ptr<DevTable>* out, const char* what) {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (auto& s : slots_)
+            if (s.bytes == bytes) {
+                s.used = ++clock_;
+                *out = s.dev;
+                return WM_OK;
+            }
+        auto dev = std::make_shared<DevTable>(bytes.size());
+        if (!dev->p) return set_error(WM_ERR_NOMEM, std::string(what) + ": descriptor table");
+        WM_TRY(upload_async(dev->p, bytes.data(), bytes.size()));
+        Slot* s = nullptr;
+        if (slots_.size() < kTableSlots) {
+            slots_.emplace_back();
+            s = &slots_.back();
+        } else {
+            s = &*std::min_element(slots_.begin(), slots_.end(),
+                                   [](const Slot& a, const Slot& b) { return a.used < b.used; });
+        }
+        s->bytes = bytes;
+        s->dev = dev;
+        s->used = ++clock_;
+        *out = std::move(dev);
+        return WM_OK;
+    }
+};
+// Never destroyed: a static destructor could run after the pool's.
+TableCache& tables() {
+    static TableCache* t = new TableCache;
+    return *t;
+}
+
 // Descriptor table of a parameter list on the device (entries with n == 0 or
 // a null array are dropped; `index` maps table rows back to list positions).
 struct MultiTable {
@@ -553,15 +665,15 @@ struct MultiTable {
     std::vector<int> index;
     int64_t chunks = 0;    // kChunk chunks (reductions)
     int64_t chunks_s = 0;  // kChunkS chunks (element-wise passes)
-    Workspace* dev = nullptr;
-    ~MultiTable() { delete dev; }
+    std::shared_ptr<DevTable> dev;
 
     int build(int count, float* const* p, const float* const* g, float* const* s1, float* const* s2,
               const int64_t* n, int ns, const char* what, const wm_grad_scale* gscale = nullptr) {
         for (int k = 0; k < count; ++k) {
             if (n[k] < 0) return set_error(WM_ERR_INVALID, std::string(what) + ": negative size");
             if (n[k] == 0) continue;
-            MultiEntry e{};
+            MultiEntry e;
+            std::memset(&e, 0, sizeof e);  // padding included: tables are compared byte for byte
             e.p = p[k];
             e.g = g ? g[k] : nullptr;
             e.s1 = ns > 0 && s1 ? s1[k] : nullptr;
@@ -601,11 +713,9 @@ struct MultiTable {
             while (k + 1 < host.size() && host[k + 1].chunk0s <= c) ++k;
             coarse[j] = (int)k;
         }
-        dev = new Workspace(buf.size());
-        if (!dev->p) return set_error(WM_ERR_NOMEM, std::string(what) + ": descriptor table");
-        return upload_async(dev->p, buf.data(), buf.size());
+        return tables().get(buf, &dev, what);
     }
-    const MultiEntry* table() const { return dev->as<MultiEntry>(); }
+    const MultiEntry* table() const { return static_cast<const MultiEntry*>(dev->p); }
     int count() const { return (int)host.size(); }
     unsigned grid() const { return grid_for(chunks, 1, 8); }
     unsigned grid_s() const { return grid_for(chunks_s, 1, 1 << 12); }
@@ -944,16 +1054,35 @@ static int first_bad_multi(int count, const float* const* g, const wm_grad_scale
     MultiTable t;
     WM_TRY(multi_grads(count, g, n, t, what, gs));
     if (t.chunks == 0) return WM_OK;
-    Workspace first((size_t)t.chunks * sizeof(int64_t)), where(2 * sizeof(int64_t));
-    if (!first.p || !where.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
+    Workspace first((size_t)t.chunks * sizeof(int64_t));
+    if (!first.p) return set_error(WM_ERR_NOMEM, std::string(what) + ": workspace");
+    // The answer goes straight to pinned host memory (no copy dispatch after
+    // the finalize kernel); one buffer per process, held across the wait.
+    static std::mutex mu;
+    static int64_t* host_where = nullptr;
+    static int64_t* dev_where = nullptr;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!host_where) {
+        void* h = nullptr;
+        void* d = nullptr;
+        hipError_t e = hipHostMalloc(&h, 2 * sizeof(int64_t), hipHostMallocMapped | hipHostMallocCoherent);
+        if (e == hipSuccess) e = hipHostGetDevicePointer(&d, h, 0);
+        if (e != hipSuccess) {
+            if (h) (void)hipHostFree(h);
+            return set_error(WM_ERR_HIP, std::string(what) + ": pinned result: " + hipGetErrorString(e));
+        }
+        host_where = static_cast<int64_t*>(h);
+        dev_where = static_cast<int64_t*>(d);
+    }
     launch_kernel(multi_first_bad_kernel, dim3(t.grid()), dim3(kBlock), 0, stream(), t.table(), t.count(), t.chunks,
                   scale, first.as<int64_t>());
     WM_TRY(check_launch(what));
     launch_kernel(multi_first_bad_finalize_kernel, dim3(1), dim3(kBlock), 0, stream(), t.table(), t.count(),
-                  t.chunks, first.as<int64_t>(), where.as<int64_t>());
+                  t.chunks, first.as<int64_t>(), dev_where);
     WM_TRY(check_launch(what));
-    int64_t cut[2] = {0, 0};
-    WM_TRY(wm_d2h(cut, where.p, sizeof(cut)));
+    const hipError_t e = hipStreamSynchronize(stream());
+    if (e != hipSuccess) return set_error(WM_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    const int64_t cut[2] = {host_where[0], host_where[1]};
     if (cut[0] < t.count()) {  // table row -> list position
         where_out[0] = t.index[(size_t)cut[0]];
         where_out[1] = cut[1];
