@@ -114,6 +114,36 @@ def test_batchnorm_forward(wm, shape, training):
         assert oracle.bit_equal(rm1, rm) and oracle.bit_equal(rv1, rv)
 
 
+# Larger tensors: several workgroups per channel (the statistics from chunk
+# partials, combined by every workgroup of the second pass itself), channel
+# counts below and above the grid's rows, odd plane sizes.
+BN_LARGE_SHAPES = [(64, 64, 32, 32), (256, 24, 28, 28), (20, 300, 28, 28), (128, 3, 112, 112), (4, 1100, 32, 32),
+                   (64, 256, 56, 56), (16, 40, 33, 35)]
+
+
+@pytest.mark.parametrize("shape", BN_LARGE_SHAPES)
+def test_batchnorm_large(wm, shape):
+    x, gamma, beta, rm, rv = bn_inputs(shape, 20)
+    y, mean, inv, rm1, rv1 = batchnorm_fwd(x, gamma, beta, rm, rv, True)
+    y64, m64, i64, rm64, rv64 = o64.batchnorm2d(x, gamma, beta, rm, rv, training=True)
+    close(y, y64, oab.batchnorm2d(x, gamma, beta, rm, rv, training=True)[0])
+    xs = np.abs(x)
+    close(mean, m64, o64.batchnorm2d(xs, gamma, beta, np.abs(rm), rv, training=True)[1])
+    close(inv, i64, i64)
+    close(rm1, rm64, 0.9 * np.abs(rm) + 0.1 * np.abs(xs).mean((0, 2, 3)))
+    close(rv1, rv64, rv64)
+    # a second launch gives the same bits (fixed-order combines)
+    y2, mean2, inv2, rm2, rv2 = batchnorm_fwd(x, gamma, beta, rm, rv, True)
+    for a, b in ((y, y2), (mean, mean2), (inv, inv2), (rm1, rm2), (rv1, rv2)):
+        assert oracle.bit_equal(a, b)
+    g = rng_normal(shape, 21)
+    got = batchnorm_bwd(g, x, gamma, mean, inv)
+    ref = o64.batchnorm2d_bwd(g, x, gamma, mean, inv)
+    scale = oab.batchnorm2d_bwd(g, x, gamma, mean, inv)
+    for k in range(3):
+        close(got[k], ref[k], scale[k])
+
+
 @pytest.mark.parametrize("accumulate", [False, True])
 @pytest.mark.parametrize("shape", BN_SHAPES)
 def test_batchnorm_backward(wm, shape, accumulate):

@@ -440,45 +440,68 @@ __global__ void __launch_bounds__(256) bn_stats_kernel(const float* __restrict__
     }
 }
 
-// One lane per channel: combine the chunk partials in order, then the
-// reference's float arithmetic for the running statistics and 1/std.
-__global__ void __launch_bounds__(256) bn_stats_finalize_kernel(const double* __restrict__ part, int64_t C,
-                                                                 int64_t chunks, int64_t n, float eps, float momentum,
-                                                                 int training, float* __restrict__ running_mean,
-                                                                 float* __restrict__ running_var,
-                                                                 float* __restrict__ mean_out,
-                                                                 float* __restrict__ inv_out) {
+// Channel c's statistics: the chunk partials combined in order, then the
+// reference's float arithmetic for the running statistics and 1/std.  With
+// `update`, the running statistics and the saved mean / 1/std are written.
+struct BnStats {
+    const double* part;
+    int64_t chunks;
+    int64_t n;
+    float eps, momentum;
+    int training;
+    float* running_mean;
+    float* running_var;
+    float* mean_out;
+    float* inv_out;
+};
+
+__device__ __forceinline__ float2 bn_channel_stats(const BnStats& a, int64_t c, bool update) {
 #pragma clang fp contract(off)
-    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < C; c += (int64_t)gridDim.x * 256) {
-        float mean, var;
-        if (training) {
-            double s = 0.0, q = 0.0;
-            for (int64_t k = 0; k < chunks; ++k) {
-                s += part[(c * chunks + k) * 2];
-                q += part[(c * chunks + k) * 2 + 1];
-            }
-            const double md = s / (double)n;
-            const double m2 = q - s * md;
-            mean = (float)md;
-            var = (float)((m2 > 0.0 ? m2 : 0.0) / (double)n);
-            running_mean[c] = (1.0f - momentum) * running_mean[c] + momentum * mean;
-            running_var[c] = (1.0f - momentum) * running_var[c] + momentum * var;
-        } else {
-            mean = running_mean[c];
-            var = running_var[c];
+    float mean, var;
+    if (a.training) {
+        double s = 0.0, q = 0.0;
+        for (int64_t k = 0; k < a.chunks; ++k) {
+            s += a.part[(c * a.chunks + k) * 2];
+            q += a.part[(c * a.chunks + k) * 2 + 1];
         }
-        mean_out[c] = mean;
-        inv_out[c] = 1.0f / sqrtf(var + eps);
+        const double md = s / (double)a.n;
+        const double m2 = q - s * md;
+        mean = (float)md;
+        var = (float)((m2 > 0.0 ? m2 : 0.0) / (double)a.n);
+        if (update) {
+            a.running_mean[c] = (1.0f - a.momentum) * a.running_mean[c] + a.momentum * mean;
+            a.running_var[c] = (1.0f - a.momentum) * a.running_var[c] + a.momentum * var;
+        }
+    } else {
+        mean = a.running_mean[c];
+        var = a.running_var[c];
     }
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    if (update) {
+        a.mean_out[c] = mean;
+        a.inv_out[c] = inv;
+    }
+    return make_float2(mean, inv);
 }
 
+// One lane per channel (the statistics alone, when no output is wanted).
+__global__ void __launch_bounds__(256) bn_stats_finalize_kernel(BnStats a, int64_t C) {
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < C; c += (int64_t)gridDim.x * 256)
+        (void)bn_channel_stats(a, c, true);
+}
+
+// Each workgroup combines its channel's partials itself (chunk 0's also
+// writes the running and saved statistics): no finalize launch between the
+// two passes.
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_apply_kernel(const float* __restrict__ x, const float* __restrict__ gamma,
-                                                        const float* __restrict__ beta, const float* __restrict__ mean,
-                                                        const float* __restrict__ inv_std, BnGeom gm,
+                                                        const float* __restrict__ beta, BnStats sa, BnGeom gm,
                                                         float* __restrict__ y) {
     const int64_t c = blockIdx.y;
-    const float gc = gamma[c], bc = beta[c], mc = mean[c], ic = inv_std[c];
+    __shared__ float2 s_mi;
+    if (threadIdx.x == 0) s_mi = bn_channel_stats(sa, c, blockIdx.x == 0);
+    __syncthreads();
+    const float gc = gamma[c], bc = beta[c], mc = s_mi.x, ic = s_mi.y;
     auto nrm = [&](float v) { return gc * ((v - mc) * ic) + bc; };
     bn_for_chunk<VEC>(gm, [&](int64_t base, int64_t u0) {
         if (VEC) {
@@ -555,48 +578,62 @@ __global__ void __launch_bounds__(256) bn_bwd_sums_kernel(const float* __restric
     }
 }
 
-// One lane per channel: dgamma, dbeta (accumulated as requested) and the
-// closure's dvar, dmean (coef[c] = {dvar, dmean}) from the chunk sums.
-__global__ void __launch_bounds__(256) bn_bwd_finalize_kernel(const double* __restrict__ part, int64_t C,
-                                                               int64_t chunks, int64_t n,
-                                                               const float* __restrict__ gamma,
-                                                               const float* __restrict__ inv_std,
-                                                               float* __restrict__ dgamma, int acc_gamma,
-                                                               float* __restrict__ dbeta, int acc_beta,
-                                                               float2* __restrict__ coef) {
-    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < C; c += (int64_t)gridDim.x * 256) {
-        double s1 = 0.0, s2 = 0.0, s3 = 0.0;
-        for (int64_t k = 0; k < chunks; ++k) {
-            const double* p = part + (c * chunks + k) * 3;
-            s1 += p[0];
-            s2 += p[1];
-            s3 += p[2];
-        }
-        const double iv = inv_std[c], gm = gamma[c];
-        if (dgamma) {
-            const float dg = (float)(s2 * iv);
-            dgamma[c] = acc_gamma ? dgamma[c] + dg : dg;
-        }
-        if (dbeta) {
-            const float db = (float)s1;
-            dbeta[c] = acc_beta ? dbeta[c] + db : db;
-        }
-        const float dvar = (float)(gm * s2 * -0.5 * iv * iv * iv);
-        const float dmean = (float)(-gm * iv * s1 + (double)dvar * (-2.0 * s3) / (double)n);
-        coef[c] = make_float2(dvar, dmean);
+// Channel c's backward coefficients from the chunk sums: the closure's
+// dvar, dmean; with `update`, dgamma and dbeta (accumulated as requested).
+struct BnBwdCoef {
+    const double* part;
+    int64_t chunks;
+    int64_t n;
+    const float* gamma;
+    const float* inv_std;
+    float* dgamma;
+    int acc_gamma;
+    float* dbeta;
+    int acc_beta;
+};
+
+__device__ __forceinline__ float2 bn_channel_coef(const BnBwdCoef& a, int64_t c, bool update) {
+    double s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    for (int64_t k = 0; k < a.chunks; ++k) {
+        const double* p = a.part + (c * a.chunks + k) * 3;
+        s1 += p[0];
+        s2 += p[1];
+        s3 += p[2];
     }
+    const double iv = a.inv_std[c], gm = a.gamma[c];
+    if (update && a.dgamma) {
+        const float dg = (float)(s2 * iv);
+        a.dgamma[c] = a.acc_gamma ? a.dgamma[c] + dg : dg;
+    }
+    if (update && a.dbeta) {
+        const float db = (float)s1;
+        a.dbeta[c] = a.acc_beta ? a.dbeta[c] + db : db;
+    }
+    const float dvar = (float)(gm * s2 * -0.5 * iv * iv * iv);
+    const float dmean = (float)(-gm * iv * s1 + (double)dvar * (-2.0 * s3) / (double)a.n);
+    return make_float2(dvar, dmean);
 }
 
+// One lane per channel: dgamma, dbeta when no input gradient is wanted.
+__global__ void __launch_bounds__(256) bn_bwd_finalize_kernel(BnBwdCoef a, int64_t C) {
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < C; c += (int64_t)gridDim.x * 256)
+        (void)bn_channel_coef(a, c, true);
+}
+
+// Each workgroup combines its channel's sums itself (chunk 0's also writes
+// dgamma / dbeta): no finalize launch between the two passes.
 template <bool VEC>
 __global__ void __launch_bounds__(256) bn_bwd_apply_kernel(const float* __restrict__ g, const float* __restrict__ x,
                                                             const float* __restrict__ gamma,
                                                             const float* __restrict__ mean,
-                                                            const float* __restrict__ inv_std,
-                                                            const float2* __restrict__ coef, BnGeom gm, float nf,
-                                                            float* __restrict__ gx, int acc) {
+                                                            const float* __restrict__ inv_std, BnBwdCoef ca,
+                                                            BnGeom gm, float nf, float* __restrict__ gx, int acc) {
     const int64_t c = blockIdx.y;
+    __shared__ float2 s_cf;
+    if (threadIdx.x == 0) s_cf = bn_channel_coef(ca, c, blockIdx.x == 0);
+    __syncthreads();
     const float gc = gamma[c], mc = mean[c], ic = inv_std[c];
-    const float2 cf = coef[c];
+    const float2 cf = s_cf;
     const float dm = cf.y / nf;
     auto dx = [&](float gv, float xv) { return gv * gc * ic + cf.x * 2.0f * (xv - mc) / nf + dm; };
     bn_for_chunk<VEC>(gm, [&](int64_t base, int64_t u0) {
@@ -867,14 +904,27 @@ int launch_ln_bwd(const float* g, const float* x, const float* gamma, const floa
                         acc_b, G, n, "wm_layernorm_bwd(colsum)");
 }
 
-BnGeom bn_geom(int64_t B, int64_t C, int64_t S, bool vec) {
+// Workgroups per CU for a pass of two kernels: as many as both keep
+// resident, at most 8, so the grid runs in one round (the backward's
+// kernels hold 7 per CU: a grid of 8 per CU ran as 7 plus a one-per-CU
+// tail, 178.7 against 164.2 us at [64, 256, 56, 56]).
+template <class K1, class K2>
+int bn_per_cu(K1 k1, K2 k2) {
+    int a = 0, b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k1, 256, 0) != hipSuccess || a < 1) a = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k2, 256, 0) != hipSuccess || b < 1) b = 1;
+    return std::min(8, std::min(a, b));
+}
+
+// per_cu: workgroups per CU the grid aims at.
+BnGeom bn_geom(int64_t B, int64_t C, int64_t S, bool vec, int per_cu) {
     BnGeom gm;
     gm.C = C;
     gm.S = S;
     gm.units = vec ? S / 4 : S;
     gm.spp = (gm.units + kSeg - 1) / kSeg;
     gm.nseg = B * gm.spp;
-    const int64_t target = (int64_t)num_cus() * 8;
+    const int64_t target = (int64_t)num_cus() * per_cu;
     gm.chunks = std::max<int64_t>(1, std::min<int64_t>(gm.nseg, (target + C - 1) / C));
     return gm;
 }
@@ -931,22 +981,31 @@ int wm_batchnorm2d_fwd(const float* x, const float* gamma, const float* beta, fl
     WM_CHECK_INIT();
     hipStream_t st = stream();
     const bool vec = spatial % 4 == 0 && aligned16(x) && aligned16(y);
-    const BnGeom gm = bn_geom(batch, channels, spatial, vec);
+    const BnGeom gm = bn_geom(batch, channels, spatial, vec,
+                              vec ? bn_per_cu(bn_stats_kernel<true>, bn_apply_kernel<true>)
+                                  : bn_per_cu(bn_stats_kernel<false>, bn_apply_kernel<false>));
     Workspace part(training ? (size_t)(channels * gm.chunks) * 2 * sizeof(double) : 0);
     if (training && !part.p) return set_error(WM_ERR_NOMEM, "wm_batchnorm2d_fwd: workspace");
+    const BnStats sa{part.as<double>(), gm.chunks, n, eps, momentum, training, running_mean, running_var, mean,
+                     inv_std};
+    if (n == 0) {  // no elements: the statistics of empty sums (the reference's 0 / 0)
+        if (training) {
+            launch_kernel(bn_stats_kernel<false>, dim3((unsigned)gm.chunks, (unsigned)channels), dim3(256), 0, st, x,
+                          gm, part.as<double>());
+            WM_TRY(check_launch("wm_batchnorm2d_fwd(stats)"));
+        }
+        launch_kernel(bn_stats_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st, sa,
+                      channels);
+        return check_launch("wm_batchnorm2d_fwd(finalize)");
+    }
     const dim3 grid((unsigned)gm.chunks, (unsigned)channels);
     if (training) {
         if (vec) launch_kernel(bn_stats_kernel<true>, grid, dim3(256), 0, st, x, gm, part.as<double>());
         else launch_kernel(bn_stats_kernel<false>, grid, dim3(256), 0, st, x, gm, part.as<double>());
         WM_TRY(check_launch("wm_batchnorm2d_fwd(stats)"));
     }
-    launch_kernel(bn_stats_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
-                       part.as<double>(), channels, gm.chunks, n, eps, momentum, training, running_mean, running_var,
-                       mean, inv_std);
-    WM_TRY(check_launch("wm_batchnorm2d_fwd(finalize)"));
-    if (n == 0) return WM_OK;
-    if (vec) launch_kernel(bn_apply_kernel<true>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
-    else launch_kernel(bn_apply_kernel<false>, grid, dim3(256), 0, st, x, gamma, beta, mean, inv_std, gm, y);
+    if (vec) launch_kernel(bn_apply_kernel<true>, grid, dim3(256), 0, st, x, gamma, beta, sa, gm, y);
+    else launch_kernel(bn_apply_kernel<false>, grid, dim3(256), 0, st, x, gamma, beta, sa, gm, y);
     return check_launch("wm_batchnorm2d_fwd(apply)");
 }
 
@@ -961,26 +1020,28 @@ int wm_batchnorm2d_bwd(const float* g, const float* x, const float* gamma, const
     WM_CHECK_INIT();
     hipStream_t st = stream();
     const bool vec = spatial % 4 == 0 && aligned16(g) && aligned16(x) && (!gx || aligned16(gx));
-    const BnGeom gm = bn_geom(batch, channels, spatial, vec);
+    const BnGeom gm = bn_geom(batch, channels, spatial, vec,
+                              vec ? bn_per_cu(bn_bwd_sums_kernel<true>, bn_bwd_apply_kernel<true>)
+                                  : bn_per_cu(bn_bwd_sums_kernel<false>, bn_bwd_apply_kernel<false>));
     Workspace part((size_t)(channels * gm.chunks) * 3 * sizeof(double));
-    Workspace coef((size_t)channels * sizeof(float2));
-    if (!part.p || !coef.p) return set_error(WM_ERR_NOMEM, "wm_batchnorm2d_bwd: workspace");
+    if (!part.p) return set_error(WM_ERR_NOMEM, "wm_batchnorm2d_bwd: workspace");
+    const BnBwdCoef ca{part.as<double>(), gm.chunks, n, gamma, inv_std, dgamma, acc_gamma, dbeta, acc_beta};
+    const float nf = (float)n;
     const dim3 grid((unsigned)gm.chunks, (unsigned)channels);
     if (vec) launch_kernel(bn_bwd_sums_kernel<true>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
     else launch_kernel(bn_bwd_sums_kernel<false>, grid, dim3(256), 0, st, g, x, mean, gm, part.as<double>());
     WM_TRY(check_launch("wm_batchnorm2d_bwd(sums)"));
-    launch_kernel(bn_bwd_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st,
-                       part.as<double>(), channels, gm.chunks, n, gamma, inv_std, dgamma, acc_gamma, dbeta, acc_beta,
-                       coef.as<float2>());
-    WM_TRY(check_launch("wm_batchnorm2d_bwd(finalize)"));
-    if (!gx || n == 0) return WM_OK;
-    const float nf = (float)n;
+    if (!gx || n == 0) {  // the parameter gradients alone
+        launch_kernel(bn_bwd_finalize_kernel, dim3((unsigned)((channels + 255) / 256)), dim3(256), 0, st, ca,
+                      channels);
+        return check_launch("wm_batchnorm2d_bwd(finalize)");
+    }
     if (vec)
-        launch_kernel(bn_bwd_apply_kernel<true>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
-                           coef.as<float2>(), gm, nf, gx, acc_x);
+        launch_kernel(bn_bwd_apply_kernel<true>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std, ca, gm, nf, gx,
+                      acc_x);
     else
-        launch_kernel(bn_bwd_apply_kernel<false>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std,
-                           coef.as<float2>(), gm, nf, gx, acc_x);
+        launch_kernel(bn_bwd_apply_kernel<false>, grid, dim3(256), 0, st, g, x, gamma, mean, inv_std, ca, gm, nf, gx,
+                      acc_x);
     return check_launch("wm_batchnorm2d_bwd(apply)");
 }
 
