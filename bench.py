@@ -1642,6 +1642,8 @@ def run_config(name, args, flush, want_cpu, kt):
         d = {"ms": round(km, 4), "ms_event_median": round(statistics.median(op.ms), 4), "GBps": round(gbps, 1),
              "pct_peak": round(100 * gbps / PEAK_GBPS, 1), "Gelem_per_s": round(op.elems / (km * 1e-3) / 1e9, 2),
              "bytes": op.bytes}
+        if op.prepare is not None:
+            d["prepared"] = True  # untimed work before each launch (its dispatches precede the flush)
         if getattr(op, "ndisp", None) is not None:
             d["dispatches"] = op.ndisp
         if op.kms:
