@@ -219,3 +219,84 @@ def test_overflowing_unscale_and_finite_check(T):
     want[:stop] = prod[:stop]
     assert T.check_gradients_finite(ps) == bool(np.isfinite(want).all())
     assert oracle.bit_equal(np.asarray(ps[0].grad), want)
+
+
+@pytest.mark.parametrize("max_norm", [-0.5, 0.0])
+def test_clip_with_negative_or_zero_max_norm_and_a_zero_gradient(T, max_norm):
+    """A coefficient that is negative or zero still multiplies every element
+    (it is < 1), a known-zero gradient included: zeros become -0.0 under a
+    negative coefficient, negative values -0.0 under a zero one, as the
+    reference's float products give."""
+    grads = [rng(800 + i).standard_normal(s).astype(np.float32) for i, s in enumerate(SHAPES)]
+    ps = make(T, grads)
+    ps[2].zero_grad()
+    assert ps[2].grad_known_zero
+    grads[2] = np.zeros(SHAPES[2], np.float32)
+    norm = T.get_grad_norm(ps)
+    T.clip_grad_norm_(ps, max_norm)
+    coef = np.float32(max_norm) / (np.float32(norm) + np.float32(1e-6))
+    for p, g in zip(ps, grads):
+        assert oracle.bit_equal(np.asarray(p.grad), g * coef)
+
+
+def test_clip_grad_norm_amp_defers_onto_scaled_gradients(T):
+    """clip_grad_norm_amp measures the norm of g / scale and, when it clips,
+    multiplies the still-scaled gradients by the coefficient (core/amp.h:
+    303-327); the step reads them through that deferred multiplication."""
+    scale = np.float32(512.0)
+    grads = [(rng(900 + i).standard_normal(s) * 3).astype(np.float32) * scale for i, s in enumerate(SHAPES)]
+    ps = make(T, grads)
+    opt = optimizer(T, "sgd", ps)
+    mine = [np.asarray(p.data).ravel().copy() for p in ps]
+    s1 = [np.zeros_like(m) for m in mine]
+    norm = T.clip_grad_norm_amp(ps, 1.0, float(scale))
+    inv = np.float32(1.0) / scale
+    ref_norm = np.sqrt(np.float32(sum(float(np.sum((g.astype(np.float64) * inv) ** 2)) for g in grads)))
+    assert abs(norm - ref_norm) <= 1e-5 * ref_norm
+    coef = np.float32(1.0) / (np.float32(norm) + np.float32(1e-6))
+    assert coef < 1
+    opt.step()
+    for k, g in enumerate(grads):
+        step_ref("sgd", mine[k], (g * coef).ravel(), s1[k], None, 1)
+        assert oracle.bit_equal(np.asarray(ps[k].data).ravel(), mine[k]), k
+    for p, g in zip(ps, grads):
+        assert oracle.bit_equal(np.asarray(p.grad), g * coef)
+
+
+def test_skipped_step_after_overflow_keeps_parameters(T):
+    """GradScaler::step after an unscale that found an overflow leaves every
+    parameter as it was; update() backs the scale off; zero_grad clears the
+    partly unscaled gradients."""
+    grads = [rng(1000 + i).standard_normal(s).astype(np.float32) for i, s in enumerate(SHAPES)]
+    grads[3][17] = np.nan
+    ps = make(T, grads)
+    before = [np.asarray(p.data).copy() for p in ps]
+    opt = optimizer(T, "adamw", ps)
+    scaler = T.GradScaler(256.0, 2.0, 0.5, 1000)
+    scaler.step(opt)
+    for p, b in zip(ps, before):
+        assert oracle.bit_equal(np.asarray(p.data), b)
+    scaler.update()
+    assert scaler.get_scale() == 128.0
+    inv = np.float32(1.0) / np.float32(256.0)
+    assert oracle.bit_equal(np.asarray(ps[0].grad), grads[0] * inv)
+    want3 = grads[3].copy()
+    want3[:17] = want3[:17] * inv
+    assert oracle.bit_equal(np.asarray(ps[3].grad), want3)
+    opt.zero_grad()
+    assert all(p.grad_known_zero for p in ps)
+
+
+def test_negative_loss_scale_flips_zero_gradients(T):
+    """A negative loss scale: 1 / scale < 0 multiplies known-zero gradients
+    too (+0 becomes -0), as the reference's loop over every element does."""
+    grads = [rng(1100 + i).standard_normal(s).astype(np.float32) for i, s in enumerate(SHAPES)]
+    ps = make(T, grads)
+    ps[1].zero_grad()
+    grads[1] = np.zeros(SHAPES[1], np.float32)
+    opt = T.SGD(ps, 0.1)
+    scaler = T.GradScaler(-2.0, 2.0, 0.5, 1000)
+    assert scaler.unscale(opt)
+    inv = np.float32(1.0) / np.float32(-2.0)
+    for p, g in zip(ps, grads):
+        assert oracle.bit_equal(np.asarray(p.grad), g * inv)

@@ -20,15 +20,16 @@ void check(int rc, const char* what) {
 }
 
 // The gradients that hold values, with their deferred scalings: a gradient
-// that is empty or known to be all zeros is skipped (scaling zeros by a
-// finite factor leaves zeros, and zeros are finite).  `vecs` gets the
-// storage of each; the pointers are for read-only passes that apply the
-// deferred scalings as they read.
+// that is empty is skipped, and one known to be all zeros unless `zeros`
+// (scaling +0 by a positive finite factor leaves +0, and zeros are finite;
+// a negative factor would make them -0).  `vecs` gets the storage of each;
+// the pointers are for read-only passes that apply the deferred scalings as
+// they read.
 void live_grads_deferred(const std::vector<TensorPtr>& params, std::vector<wm::DeviceVector*>& vecs,
                          std::vector<const float*>& ptrs, std::vector<wm_grad_scale>& gs,
-                         std::vector<int64_t>& sizes) {
+                         std::vector<int64_t>& sizes, bool zeros = false) {
     for (const auto& p : params) {
-        if (!p || p->grad.empty() || p->grad.known_zero()) continue;
+        if (!p || p->grad.empty() || (!zeros && p->grad.known_zero())) continue;
         vecs.push_back(&p->grad);
         gs.emplace_back();
         ptrs.push_back(p->grad.dev_deferred(&gs.back()));
@@ -61,7 +62,7 @@ bool GradScaler::unscale(Optimizer* optimizer) {
     std::vector<const float*> ptrs;
     std::vector<wm_grad_scale> gs;
     std::vector<int64_t> sizes;
-    live_grads_deferred(optimizer->params, vecs, ptrs, gs, sizes);
+    live_grads_deferred(optimizer->params, vecs, ptrs, gs, sizes, inv_scale < 0.0f);
     bool listed_twice = false;
     for (size_t i = 0; i < vecs.size() && !listed_twice; ++i)
         for (size_t j = i + 1; j < vecs.size(); ++j)
@@ -150,7 +151,8 @@ float clip_grad_norm_amp(const std::vector<TensorPtr>& params, float max_norm, f
     const float clip_coef = max_norm / (total_norm + 1e-6f);
     // Deferred like clip_grad_norm_'s: the device recomputes this coefficient
     // from the same sum of squares, bit for bit, when the products are taken.
-    if (clip_coef < 1.0f)
-        for (auto* v : vecs) v->defer_clip(total, max_norm);
+    if (clip_coef < 1.0f)  // every listing of every gradient, as the reference's loop (known-zero ones too)
+        for (const auto& p : params)
+            if (p && !p->grad.empty()) p->grad.defer_clip(total, max_norm);
     return total_norm;
 }

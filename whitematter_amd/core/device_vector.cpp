@@ -328,19 +328,27 @@ void DeviceVector::apply_deferred() const {
 }
 
 void DeviceVector::defer_unscale(float factor, int64_t count) {
-    if (n_ == 0 || count <= 0 || zero_) return;  // zeros times a finite factor stay zeros
+    if (n_ == 0 || count <= 0) return;
+    // zeros times a positive finite factor stay +0; any other factor makes
+    // them -0 or NaN, so the zeros are written out first
+    if (zero_ && factor > 0.0f && std::isfinite(factor)) return;
     if (count > (int64_t)n_) count = (int64_t)n_;
     if (deferred()) apply_deferred();
     dev_stored();
+    zero_ = false;
     host_valid_ = false;
     def_unscale_ = factor;
     def_count_ = count;
 }
 
 void DeviceVector::defer_clip(std::shared_ptr<const DeviceVector> sumsq, float max_norm) {
-    if (n_ == 0 || zero_ || !sumsq) return;  // zeros times a finite coefficient stay zeros
+    if (n_ == 0 || !sumsq) return;
+    // a max_norm >= 0 gives a coefficient >= 0 (or NaN, not applied): zeros
+    // stay +0; a negative or infinite one makes them -0 or NaN
+    if (zero_ && max_norm >= 0.0f && std::isfinite(max_norm)) return;
     if (def_sumsq_) apply_deferred();
     dev_stored();  // an unscale deferred before stays: the clip follows it
+    zero_ = false;
     host_valid_ = false;
     def_sumsq_ = std::move(sumsq);
     def_max_norm_ = max_norm;
