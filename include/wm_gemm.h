@@ -11,15 +11,17 @@
  * `accumulate` flag (1 = "+=", 0 = overwrite) and may be NULL when that
  * input does not require grad.
  *
- * Arithmetic: products and sums in fp32 on v_mfma_f32_32x32x2_f32 (no
- * reduced-precision inputs).  The reference adds each product to its fp32
+ * Arithmetic: products and sums in fp32 on the matrix cores (no
+ * reduced-precision inputs): this library's v_mfma_f32_32x32x2_f32 kernel,
+ * or, for the plain large products (wm_gemm_library), rocBLAS's fp32
+ * kernels with atomics off.  The reference adds each product to its fp32
  * accumulator in k order; the matrix cores add them in another order (and a
  * product with fewer output tiles than CUs and a long k adds the partial
  * products of its k slices in a second pass, in fixed slice order), so the
  * results agree with the reference within fp32 summation error (tested
  * against an fp64 restatement relative to sum_k |a_ik * b_kj|), not bit for
- * bit.  Products of small integers, whose partial sums are exact in fp32,
- * are bit-exact.
+ * bit; each route gives the same bits on every run.  Products of small
+ * integers, whose partial sums are exact in fp32, are bit-exact.
  */
 #ifndef WM_GEMM_H
 #define WM_GEMM_H
@@ -51,6 +53,16 @@ extern "C" {
 int wm_gemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, const float* a, int64_t lda,
             const float* b, int64_t ldb, float* c, int64_t ldc, int accumulate, const float* bias, int64_t batch,
             int64_t batch_inner, const int64_t* strides);
+
+/* The route of the plain large products (unbatched, m, n >= 128, k >= 256,
+ * not both bias and accumulate): 1 (default) = rocBLAS's tuned fp32
+ * kernels, which are faster there; 0 = this library's MFMA kernel for every
+ * product.  mode 0 or 1 sets it, any other value only queries; returns the
+ * route now in force.  The results agree with the reference within the same
+ * fp32 summation error either way (both deterministic run to run).  No
+ * counterpart in the reference (a routing switch, for tests and
+ * measurements of each kernel).                                              */
+int wm_gemm_library(int mode);
 
 /* Tensor::matmul, core/tensor.cpp:783-795: c[m, n] = a[m, k] @ b[k, n]. */
 int wm_matmul(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c);

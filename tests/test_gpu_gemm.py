@@ -25,6 +25,18 @@ def close(got, ref, scale, rtol=1e-5):
     assert ok, f"{worst:.3g}x tolerance"
 
 
+@pytest.fixture(autouse=True, params=[1, 0], ids=["route-default", "route-mfma-kernel"])
+def route(request, wm):
+    """Every test under both routes of the plain large products
+    (wm_gemm_library): rocBLAS where it is faster, and this library's MFMA
+    kernel for everything."""
+    from whitematter_amd import _lib as W
+    before = W.lib().wm_gemm_library(-1)
+    W.lib().wm_gemm_library(request.param)
+    yield request.param
+    W.lib().wm_gemm_library(before)
+
+
 SHAPES = [(1, 1, 1), (2, 3, 2), (3, 5, 7), (33, 65, 17), (64, 31, 129), (5, 1, 4), (7, 40, 1), (128, 32, 128),
           (128, 64, 256), (129, 33, 127), (256, 100, 200), (300, 513, 257)]
 

@@ -37,7 +37,11 @@
 
 #include "../../include/wm_gemm.h"
 
+#include <rocblas/rocblas.h>
+
 #include <algorithm>
+#include <climits>
+#include <mutex>
 
 namespace wm {
 namespace {
@@ -429,6 +433,101 @@ int64_t choose_kslices(int64_t work, int64_t k) {
     return std::min<int64_t>(s, k / kMinSlice);
 }
 
+// ---- rocBLAS for the plain large products ----------------------------------
+//
+// The vendor library's tuned fp32 kernels beat this file's on large, plain
+// products (measured on MI355X, % of the fp32 matrix peak, library / this
+// kernel: 8192^3 92.9-97.8 / 83-84; the [8192, 1024] x [1024, 1024]
+// projections and their weight and input gradients 88.9-90.3 / 65-70),
+// tie on k = 128 (62 / 61) and lose on the attention's per-head products
+// (k = 64 scores 19.7 / 46, n = 64 contexts 45.7 / 64: two-level batches
+// the library can only take as one call per outer batch).  Unbatched
+// products with m, n >= 128 and k >= 256 go to rocBLAS (atomics off: the
+// same bits on every run); batched ones, the rest, and every product while
+// the library route is switched off (wm_gemm_library), to gemm_kernel.  A
+// bias is written into C first and the library adds the product to it.
+int g_library = 1;  // wm_gemm_library
+
+struct Blas {
+    std::mutex mu;
+    rocblas_handle h = nullptr;
+    bool failed = false;
+};
+
+Blas& blas() {
+    static Blas* b = new Blas;  // never destroyed: no teardown ordering with the runtime
+    return *b;
+}
+
+// C rows = bias (one float4 per thread when n, ldc and the stride are
+// multiples of 4 and C is aligned; one float otherwise), on a grid covering
+// C: the library then adds the product to it (beta = 1).
+template <bool VEC>
+__global__ void __launch_bounds__(256) bias_rows_kernel(float* __restrict__ c, int64_t m, int64_t n, int64_t ldc,
+                                                        int64_t batch, int64_t sc, const float* __restrict__ bias) {
+    constexpr int W = VEC ? 4 : 1;
+    const int64_t nw = n / W, rows = batch * m;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * nw) return;
+    const int64_t row = i / nw, j = (i - row * nw) * W;
+    const int64_t p = row / m, r = row - p * m;
+    float* dst = c + p * sc + r * ldc + j;
+    if constexpr (VEC) *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(bias + j);
+    else *dst = bias[j];
+}
+
+bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
+
+// The library route for P, or 1 when it does not take P (the caller then
+// launches gemm_kernel); WM_OK or an error status when it ran.
+int try_library(bool ta, bool tb, const GemmParams& P) {
+    if (!g_library || P.kslices > 1) return 1;
+    if (P.m < 128 || P.n < 128 || P.k < 256) return 1;
+    if (P.bias && P.accumulate) return 1;
+    if (P.batch != 1) return 1;  // batched: measured no faster (bmm's gradients at [64, 1024, 128]: slower)
+    if (!fits_int(P.m) || !fits_int(P.n) || !fits_int(P.k) || !fits_int(P.lda) || !fits_int(P.ldb) ||
+        !fits_int(P.ldc) || !fits_int(P.batch))
+        return 1;
+    const int64_t sc = 0;
+    Blas& B = blas();
+    std::lock_guard<std::mutex> lk(B.mu);
+    if (B.failed) return 1;
+    if (!B.h) {
+        if (rocblas_create_handle(&B.h) != rocblas_status_success ||
+            rocblas_set_atomics_mode(B.h, rocblas_atomics_not_allowed) != rocblas_status_success ||
+            rocblas_set_pointer_mode(B.h, rocblas_pointer_mode_host) != rocblas_status_success) {
+            B.failed = true;  // the product still runs, on gemm_kernel
+            return 1;
+        }
+    }
+    if (rocblas_set_stream(B.h, stream()) != rocblas_status_success)
+        return set_error(WM_ERR_HIP, "wm_gemm: rocblas_set_stream failed");
+    float beta = P.accumulate ? 1.0f : 0.0f;
+    if (P.bias) {
+        const bool vec = P.n % 4 == 0 && P.ldc % 4 == 0 && (P.batch == 1 || sc % 4 == 0) && aligned16(P.c) &&
+                         aligned16(P.bias);
+        const int64_t items = P.batch * P.m * (vec ? P.n / 4 : P.n);
+        const dim3 grid((unsigned)((items + 255) / 256));
+        if (vec) launch_kernel(bias_rows_kernel<true>, grid, dim3(256), 0, stream(), P.c, P.m, P.n, P.ldc, P.batch, sc,
+                               P.bias);
+        else launch_kernel(bias_rows_kernel<false>, grid, dim3(256), 0, stream(), P.c, P.m, P.n, P.ldc, P.batch, sc,
+                           P.bias);
+        WM_TRY(check_launch("wm_gemm(bias)"));
+        beta = 1.0f;
+    }
+    // Row-major C = op(A) op(B) is column-major C^T = op(B)^T op(A)^T: the
+    // row-major buffers read as their column-major transposes.
+    const rocblas_operation oa = ta ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation ob = tb ? rocblas_operation_transpose : rocblas_operation_none;
+    const float alpha = P.alpha;
+    const rocblas_status st = rocblas_sgemm(B.h, ob, oa, (rocblas_int)P.n, (rocblas_int)P.m, (rocblas_int)P.k, &alpha,
+                                            P.b, (rocblas_int)P.ldb, P.a, (rocblas_int)P.lda, &beta, P.c,
+                                            (rocblas_int)P.ldc);
+    if (st != rocblas_status_success)
+        return set_error(WM_ERR_HIP, std::string("wm_gemm: rocBLAS: ") + rocblas_status_to_string(st));
+    return WM_OK;
+}
+
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
     // 64-wide column tiles for narrow products (attention's per-head products
@@ -444,6 +543,9 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
                      (P.batch == 1 || (P.sa0 % 4 == 0 && P.sa1 % 4 == 0 && P.sb0 % 4 == 0 && P.sb1 % 4 == 0));
     P.c_aligned = aligned16(P.c) && (P.batch == 1 || (P.sc0 % 4 == 0 && P.sc1 % 4 == 0)) ? 1 : 0;
     hipStream_t s = stream();
+    P.kslices = 1;
+    const int lib = try_library(ta, tb, P);
+    if (lib != 1) return lib;
 
     // Split k: the partial products go to a workspace [batch][kslices][m][n]
     // (unscaled, overwritten), and a second pass adds them into C.
@@ -543,6 +645,11 @@ int wm_gemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alp
     P.alpha = alpha;
     P.accumulate = accumulate ? 1 : 0;
     return launch_gemm(trans_a != 0, trans_b != 0, P);
+}
+
+int wm_gemm_library(int mode) {
+    if (mode == 0 || mode == 1) g_library = mode;
+    return g_library;
 }
 
 int wm_matmul(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c) {
