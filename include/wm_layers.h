@@ -100,8 +100,12 @@ int wm_dropout_mask(float* mask, int64_t n, float p, uint64_t seed);
  * [mask_batches, 1, Sq, Sk] with mask_batches 1 or B.  Writes out [B, Sq, E]
  * and the values the reference's closure captures: Q [B, Sq, E], K, V
  * [B, Sk, E], attn [B, H, Sq, Sk] (the module's attn_weights), ctx
- * [B, Sq, E].  Products on the matrix cores (include/wm_gemm.h), the mask
- * and softmax by wm_attention_softmax_fwd.                                   */
+ * [B, Sq, E].  Products on the matrix cores (include/wm_gemm.h).  For
+ * Sk <= 1024 and hd <= 128 with hd and E multiples of 4 (16-byte aligned
+ * operands) the score product, mask and softmax are one kernel that writes
+ * only attn (the scores stay in registers; the softmax's arithmetic is
+ * wm_attention_softmax_fwd's, its sums in another order); otherwise the
+ * scores go to a buffer and wm_attention_softmax_fwd takes them.           */
 int wm_mha_fwd(const float* q, const float* k, const float* v, const float* mask, int64_t mask_batches,
                const float* Wq, const float* Wk, const float* Wv, const float* Wo, const float* bq, const float* bk,
                const float* bv, const float* bo, int64_t batch, int64_t seq_q, int64_t seq_k, int64_t embed,
@@ -112,12 +116,24 @@ int wm_mha_fwd(const float* q, const float* k, const float* v, const float* mask
  * reference's loops do; the eight parameter gradients are always written
  * (the reference does not test their requires_grad); gq, gk, gv may be NULL
  * (that input does not require grad) and may be the same buffer (self
- * attention: the V, K and Q projections add into it in that order).         */
+ * attention: the V, K and Q projections add into it in that order).  On the
+ * fused route (the forward's conditions) dattn = dctx_h V_h^T and the
+ * softmax backward are one kernel, whose row dot sum_j attn_ij dattn_ij is
+ * taken as dctx_i . ctx_i over the head's columns -- the same value in exact
+ * arithmetic since ctx_h = attn_h V_h, so ctx must be the forward's.        */
 int wm_mha_bwd(const float* dout, const float* q, const float* k, const float* v, const float* Wq, const float* Wk,
                const float* Wv, const float* Wo, const float* Q, const float* K, const float* V, const float* attn,
                const float* ctx, int64_t batch, int64_t seq_q, int64_t seq_k, int64_t embed, int64_t heads,
                float* gWq, float* gWk, float* gWv, float* gWo, float* gbq, float* gbk, float* gbv, float* gbo,
                float* gq, float* gk, float* gv);
+
+/* The route of the attention's per-head score products: 1 (default) = the
+ * fused kernels above where the shape fits; 0 = always the two-pass route
+ * (wm_gemm's product into a scores buffer, then the attention-softmax
+ * kernels).  mode 0 or 1 sets it, any other value only queries; returns the
+ * route now in force.  No counterpart in the reference (a routing switch,
+ * for tests and measurements of each route).                               */
+int wm_mha_fused(int mode);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,19 @@ pytestmark = pytest.mark.gpu
 o64, oab = oracle.get("f64"), oracle.get("abs")
 
 
+@pytest.fixture(autouse=True, params=[1, 0], ids=["route-fused", "route-two-pass"])
+def route(request, wm):
+    """Every test under both routes of the per-head score products
+    (wm_mha_fused): the fused score / softmax kernels where the shape fits
+    (keys <= 1024, head width <= 128 and a multiple of 4), and the two-pass
+    route (product into a scores buffer, then the attention softmax)."""
+    from whitematter_amd import _lib as W
+    before = W.lib().wm_mha_fused(-1)
+    W.lib().wm_mha_fused(request.param)
+    yield request.param
+    W.lib().wm_mha_fused(before)
+
+
 def close(got, ref, scale, rtol=1e-5, atol=1e-30):
     ok, worst = oracle.close_scaled(got, ref, scale, rtol, atol)
     assert ok, f"{worst:.3g}x tolerance"
@@ -37,7 +50,12 @@ CASES = [(2, 5, 5, 8, 2, None), (1, 4, 6, 12, 3, "batch"), (2, 6, 6, 16, 4, "cau
          (1, 200, 130, 64, 2, None), (2, 256, 256, 256, 8, "causal"),
          # ragged query blocks against longer key rows (softmax tiles of 2, 4
          # and more than 8 float4 per thread)
-         (1, 37, 300, 32, 1, "causal"), (2, 40, 700, 64, 2, "batch"), (1, 20, 1100, 32, 2, None)]
+         (1, 37, 300, 32, 1, "causal"), (2, 40, 700, 64, 2, "batch"), (1, 20, 1100, 32, 2, None),
+         # the fused kernels' edges: 1024 keys (eight 128-key chunks) at head
+         # width 64; widths 128 (four k stages), 100 (zero-filled k) and 36;
+         # past the fused limits (1025 keys, width 132: the two-pass route)
+         (2, 70, 1024, 128, 2, "causal"), (1, 50, 257, 256, 2, "batch"), (1, 33, 129, 200, 2, None),
+         (1, 40, 90, 72, 2, "batch"), (2, 96, 1025, 64, 1, "causal"), (1, 17, 64, 264, 2, None)]
 
 
 def case_inputs(case, seed):
@@ -111,3 +129,48 @@ def test_mha_backward_without_some_input_gradients(wm, need):
             assert name not in got
         else:
             close(got[name], ref[name], scale[name])
+
+
+@pytest.mark.parametrize("Sk", [7, 300])
+def test_mha_fully_masked_rows(wm, Sk):
+    """A row whose mask is -inf everywhere: the reference's max stays at
+    -FLT_MAX, every exp is 0 and the row becomes 0 / 0 = NaN (core/layer.cpp:
+    1213-1236); the other rows are unaffected."""
+    B, Sq, E, H = 1, 5, 16, 2
+    q, k, v = rng_normal((B, Sq, E), 60), rng_normal((B, Sk, E), 61), rng_normal((B, Sk, E), 62)
+    m = np.zeros((1, 1, Sq, Sk), np.float32)
+    m[0, 0, 2, :] = -np.inf
+    params = params_for(E, 63)
+    got = mha_fwd(q, k, v, params, H, m)
+    assert np.all(np.isnan(got["attn"][:, :, 2, :]))
+    rest = np.delete(got["attn"], 2, axis=2)
+    assert np.all(np.isfinite(rest))
+    assert np.allclose(rest.astype(np.float64).sum(-1), 1.0, atol=1e-5)
+
+
+def test_mha_routes_agree_at_width_64(wm):
+    """The fused kernels against the two-pass route at the bench's head width
+    and key length (16 heads of 64, 1024 keys, causal): the same products in
+    the same k order, so the weights differ only by the softmax sums' order
+    and the score gradients by the row dot's form."""
+    from whitematter_amd import _lib as W
+    B, Sq, Sk, E, H = 1, 64, 1024, 1024, 16
+    q, k, v = rng_normal((B, Sq, E), 70), rng_normal((B, Sk, E), 71), rng_normal((B, Sk, E), 72)
+    m = np.where(np.triu(np.ones((Sq, Sk)), 1) > 0, -1e9, 0).astype(np.float32)[None, None]
+    params = params_for(E, 73)
+    dout = rng_normal(q.shape, 74)
+    res = {}
+    for mode in (1, 0):
+        W.lib().wm_mha_fused(mode)
+        saved = mha_fwd(q, k, v, params, H, m)
+        res[mode] = (saved, mha_bwd(dout, q, k, v, params, H, saved))
+    (f1, g1), (f0, g0) = res[1], res[0]
+    for name in ("Q", "K", "V"):
+        assert np.array_equal(f1[name], f0[name])
+    ref = o64.mha_forward(q, k, v, params, H, m)
+    sc = mha_forward_scales(q, k, v, params, H, ref)
+    for name in ("attn", "ctx", "out"):
+        close(f1[name], f0[name], sc[name])
+    scale = oab.mha_backward(dout, q, k, v, params, H, f0)
+    for name in g0:
+        close(g1[name], g0[name], scale[name])

@@ -58,6 +58,7 @@ _SIGS = {
     "wm_pool_handouts": [C.POINTER(C.c_int64)],
     "wm_copy_kernel": [_vp, _vp, C.c_int64],
     "wm_gemm_library": [C.c_int],
+    "wm_mha_fused": [C.c_int],
     "wm_copy_kernel_cached": [_vp, _vp, C.c_int64],
     "wm_fill": [_vp, C.c_float, C.c_int64],
     "wm_f32_to_f16_rtz": [_vp, _vp, C.c_int64],
