@@ -1417,7 +1417,8 @@ def mha_ops(B=8, S=1024, E=1024, H=16):
     transformer shape: self attention over [B, S, E] with H heads and a
     causal mask.  flops = the products (projections 4 * 2 B S E^2, scores and
     attn V 2 * 2 B H S^2 hd; the closure twice that); the attention softmax
-    and the bias column sums ride along in the same time."""
+    and the bias column sums ride along in the same time (the score product, mask
+    and softmax run as one kernel)."""
     hd = E // H
     x = W.DeviceArray.from_host(synth.normal((B, S, E), synth.seed_for(13, 0)))
     params = [W.DeviceArray.from_host(synth.normal((E, E), synth.seed_for(13, 1 + i), 0.0, E ** -0.5))
@@ -1445,8 +1446,9 @@ def mha_ops(B=8, S=1024, E=1024, H=16):
     fwd()
     f_fl = 4 * 2 * B * S * E * E + 2 * 2 * B * H * S * S * hd
     att = B * H * S * S * F32
-    ops = [Op("mha fwd", fwd, 4 * B * S * E * F32 + 3 * att, "gemm_kernel", B * S * E, f_fl),
-           Op("mha bwd", bwd, 6 * B * S * E * F32 + 4 * att, "gemm_kernel", B * S * E, 2 * f_fl)]
+    kn = "rocBLAS sgemm + head_rows_kernel + gemm_kernel"
+    ops = [Op("mha fwd", fwd, 4 * B * S * E * F32 + 3 * att, kn, B * S * E, f_fl),
+           Op("mha bwd", bwd, 6 * B * S * E * F32 + 4 * att, kn, B * S * E, 2 * f_fl)]
     keep = [x, mask, out, ctx, Q, K, V, attn, dout, gx] + params + grads
     return ops, keep, {"workload": "mha: MultiHeadAttention self attention x[%d,%d,%d], %d heads (hd %d), causal "
                                    "mask; forward and closure (parameter gradients accumulated, one input gradient "
