@@ -55,7 +55,11 @@ CASES = [(2, 5, 5, 8, 2, None), (1, 4, 6, 12, 3, "batch"), (2, 6, 6, 16, 4, "cau
          # width 64; widths 128 (four k stages), 100 (zero-filled k) and 36;
          # past the fused limits (1025 keys, width 132: the two-pass route)
          (2, 70, 1024, 128, 2, "causal"), (1, 50, 257, 256, 2, "batch"), (1, 33, 129, 200, 2, None),
-         (1, 40, 90, 72, 2, "batch"), (2, 96, 1025, 64, 1, "causal"), (1, 17, 64, 264, 2, None)]
+         (1, 40, 90, 72, 2, "batch"), (2, 96, 1025, 64, 1, "causal"), (1, 17, 64, 264, 2, None),
+         # one key, one query row, width 128 at E = 1024, and workgroup counts
+         # that are (16, 72) and are not (1, 4, 6, 27) multiples of the 8 XCDs
+         (3, 1, 1, 8, 2, None), (1, 2, 1, 4, 1, "batch"), (1, 1, 300, 64, 4, "causal"),
+         (1, 40, 70, 1024, 8, "causal"), (3, 70, 200, 96, 8, "batch"), (3, 65, 128, 48, 3, None)]
 
 
 def case_inputs(case, seed):
