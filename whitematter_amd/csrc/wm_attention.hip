@@ -43,9 +43,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (backward) and B = K or V.  Each row of S stays whole in the accumulators:
 // wave w holds the columns 128 j + 32 w .. + 31 for j < NB as one 32 x 32
 // v_mfma_f32_32x32x2_f32 block per j.  B's rows pass through LDS in chunks
-// of 128 (two buffers: the next chunk's loads are in flight while the matrix
-// cores work on the current one, one barrier per chunk); A's fragments are
-// loaded once into registers.  The k order is wm_gemm's (stages of 32, the
+// of 128 (two buffers, one barrier per chunk; the next chunk's loads -- the
+// backward's, two chunks ahead -- are in flight while the matrix cores work
+// on the current one); A's 32 rows are loaded once and kept in LDS, from
+// which each chunk reads its fragments.  The k order is wm_gemm's (stages of 32, the
 // half-wave h taking k = 16 h .. 16 h + 15 of each, four k per fragment), so
 // S is bit for bit the product wm_gemm writes for the same operands.
 //   forward:  attn_i = softmax(S_i * scale + mask_i), with the arithmetic of
