@@ -482,9 +482,17 @@ bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
 // launches gemm_kernel); WM_OK or an error status when it ran.
 int try_library(bool ta, bool tb, const GemmParams& P) {
     if (!g_library || P.kslices > 1) return 1;
-    if (P.m < 128 || P.n < 128 || P.k < 256) return 1;
+    if (P.m < 128 || P.n < 128) return 1;
     if (P.bias && P.accumulate) return 1;
-    if (P.batch != 1) return 1;  // batched: measured no faster (bmm's gradients at [64, 1024, 128]: slower)
+    if (P.batch != 1) {
+        // One-level batches of untransposed small-k products (bmm's forward);
+        // their gradients and the attention's two-level per-head products
+        // measured slower on the library and stay on gemm_kernel.
+        if (P.batch_inner != 1 || ta || tb || P.k > 256 || P.bias) return 1;
+        if (P.sc0 < P.m * P.ldc) return 1;  // problems sharing output rows stay on gemm_kernel
+    } else if (P.k < 256) {
+        return 1;
+    }
     if (!fits_int(P.m) || !fits_int(P.n) || !fits_int(P.k) || !fits_int(P.lda) || !fits_int(P.ldb) ||
         !fits_int(P.ldc) || !fits_int(P.batch))
         return 1;
@@ -520,9 +528,13 @@ int try_library(bool ta, bool tb, const GemmParams& P) {
     const rocblas_operation oa = ta ? rocblas_operation_transpose : rocblas_operation_none;
     const rocblas_operation ob = tb ? rocblas_operation_transpose : rocblas_operation_none;
     const float alpha = P.alpha;
-    const rocblas_status st = rocblas_sgemm(B.h, ob, oa, (rocblas_int)P.n, (rocblas_int)P.m, (rocblas_int)P.k, &alpha,
-                                            P.b, (rocblas_int)P.ldb, P.a, (rocblas_int)P.lda, &beta, P.c,
-                                            (rocblas_int)P.ldc);
+    const rocblas_status st =
+        P.batch == 1
+            ? rocblas_sgemm(B.h, ob, oa, (rocblas_int)P.n, (rocblas_int)P.m, (rocblas_int)P.k, &alpha, P.b,
+                            (rocblas_int)P.ldb, P.a, (rocblas_int)P.lda, &beta, P.c, (rocblas_int)P.ldc)
+            : rocblas_sgemm_strided_batched(B.h, ob, oa, (rocblas_int)P.n, (rocblas_int)P.m, (rocblas_int)P.k,
+                                            &alpha, P.b, (rocblas_int)P.ldb, P.sb0, P.a, (rocblas_int)P.lda, P.sa0,
+                                            &beta, P.c, (rocblas_int)P.ldc, P.sc0, (rocblas_int)P.batch);
     if (st != rocblas_status_success)
         return set_error(WM_ERR_HIP, std::string("wm_gemm: rocBLAS: ") + rocblas_status_to_string(st));
     return WM_OK;
