@@ -117,7 +117,8 @@ int wm_mha_fwd(const float* q, const float* k, const float* v, const float* mask
  * (the reference does not test their requires_grad); gq, gk, gv may be NULL
  * (that input does not require grad) and may be the same buffer (self
  * attention: the V, K and Q projections add into it in that order).  On the
- * fused route (the forward's conditions) dattn = dctx_h V_h^T and the
+ * fused route (hd <= 128 with hd and E multiples of 4, 16-byte aligned
+ * operands; any key length) dattn = dctx_h V_h^T and the
  * softmax backward are one kernel, whose row dot sum_j attn_ij dattn_ij is
  * taken as dctx_i . ctx_i over the head's columns -- the same value in exact
  * arithmetic since ctx_h = attn_h V_h, so ctx must be the forward's.        */

@@ -59,7 +59,10 @@ CASES = [(2, 5, 5, 8, 2, None), (1, 4, 6, 12, 3, "batch"), (2, 6, 6, 16, 4, "cau
          # one key, one query row, width 128 at E = 1024, and workgroup counts
          # that are (16, 72) and are not (1, 4, 6, 27) multiples of the 8 XCDs
          (3, 1, 1, 8, 2, None), (1, 2, 1, 4, 1, "batch"), (1, 1, 300, 64, 4, "causal"),
-         (1, 40, 70, 1024, 8, "causal"), (3, 70, 200, 96, 8, "batch"), (3, 65, 128, 48, 3, None)]
+         (1, 40, 70, 1024, 8, "causal"), (3, 70, 200, 96, 8, "batch"), (3, 65, 128, 48, 3, None),
+         # past 1024 keys: the two-pass forward with the fused backward, whose
+         # chunk loop has no key limit
+         (1, 33, 2100, 64, 2, "batch"), (2, 40, 1500, 96, 3, "causal")]
 
 
 def case_inputs(case, seed):

@@ -9,8 +9,9 @@
 // a workgroup holds 32 whole rows of a head's scores in its accumulators and
 // writes only the attention weights, so the [B, H, Sq, Sk] scores never go to
 // HBM and back.  Its backward twin computes dattn = dctx_h V_h^T the same way
-// and writes d_scores = attn * (dattn - dot) directly.  Both cover keys up to
-// 1024 and head widths up to 128 (multiples of 4); other shapes, and every
+// and writes d_scores = attn * (dattn - dot) directly.  Both take head
+// widths up to 128 (multiples of 4); the forward up to 1024 keys (its rows
+// live in registers), the backward any number.  Other shapes, and every
 // shape when wm_mha_fused(0) is set, take the two-pass route: wm_gemm's
 // per-head product into a scores buffer, then the attention-softmax kernels.
 #include "wm_common.hpp"
@@ -22,6 +23,7 @@
 #include <climits>
 #include <cmath>
 #include <initializer_list>
+#include <type_traits>
 
 namespace wm {
 namespace {
@@ -306,14 +308,14 @@ __global__ void __launch_bounds__(256) head_rows_kernel(HeadRows P) {
         for (int g = 0; g < 4; ++g) dt[g] = red[0][0][8 * g + 4 * half + qb];
     }
 
-    // Block j's vector work once its products are done.
-    auto finish_block = [&](int j) {
-        f32x16& a = acc[BWD ? (j & 1) : j];
+    // Block j's vector work once its products (in a) are done; sv4 holds its
+    // mask or attn values.
+    auto finish_block = [&](int j, f32x16& a, const float4 (&sv4)[4]) {
         const int64_t c0 = cl + (int64_t)j * kHChunk;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             float4 x = quad_transpose(f4_of(a, g));
-            const float4 sv = sd[j & 1][g];
+            const float4 sv = sv4[g];
             if constexpr (BWD) {
                 // d_scores = attn * (dattn - dot)
                 store_out(j, g, make_float4(sv.x * (x.x - dt[g]), sv.y * (x.y - dt[g]), sv.z * (x.z - dt[g]),
@@ -331,42 +333,66 @@ __global__ void __launch_bounds__(256) head_rows_kernel(HeadRows P) {
         }
     };
 
+    // One chunk's products into a, from LDS buffer buf.
+    auto mma = [&](f32x16& a, const float* buf) {
 #pragma unroll
-    for (int c = 0; c < NB; ++c) {
-        if (c < P.nch) {
-            const bool more = c + 1 < P.nch;
-            if constexpr (BWD) {
-                if (c + 2 < P.nch) kc[c & 1].load(rB, boff, P.E, c + 2);
-            } else {
-                if (more) kc[0].load(rB, boff, P.E, c + 1);
+        for (int q = 0; q < 16; ++q) a[q] = 0.0f;
+        const float* As = alds + r * PK + 16 * half;
+        const float* Bs = buf + (32 * w + r) * PK + 16 * half;
+#pragma unroll
+        for (int st = 0; st < KS; ++st)
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) {
+                const float4 av = *reinterpret_cast<const float4*>(As + 32 * st + 4 * kq);
+                const float4 bv = *reinterpret_cast<const float4*>(Bs + 32 * st + 4 * kq);
+                a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, a, 0, 0, 0);
+                a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, a, 0, 0, 0);
             }
-            // block c's mask or attn values, added or used once its products
-            // are done (in the next chunk)
-            if (side) load_side(c, sd[c & 1]);
+    };
+
+    if constexpr (BWD) {
+        // Any number of chunks: two blocks live, the step for chunk c
+        // specialised on c's parity (the accumulator, side slot, register
+        // set and LDS buffer it uses).
+        auto step = [&](auto parity, int c) {
+            constexpr int S = decltype(parity)::value;
+            const bool more = c + 1 < P.nch;
+            if (c + 2 < P.nch) kc[S].load(rB, boff, P.E, c + 2);
+            // block c's attn values, used once its products are done (in
+            // the next chunk)
+            load_side(c, sd[S]);
             __builtin_amdgcn_sched_barrier(0);  // the loads go out before the products
-            f32x16& a = acc[BWD ? (c & 1) : c];
-#pragma unroll
-            for (int q = 0; q < 16; ++q) a[q] = 0.0f;
-            const float* As = alds + r * PK + 16 * half;
-            const float* Bs = lds[c & 1] + (32 * w + r) * PK + 16 * half;
-#pragma unroll
-            for (int st = 0; st < KS; ++st)
-#pragma unroll
-                for (int kq = 0; kq < 4; ++kq) {
-                    const float4 av = *reinterpret_cast<const float4*>(As + 32 * st + 4 * kq);
-                    const float4 bv = *reinterpret_cast<const float4*>(Bs + 32 * st + 4 * kq);
-                    a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, a, 0, 0, 0);
-                    a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, a, 0, 0, 0);
-                    a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, a, 0, 0, 0);
-                    a = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, a, 0, 0, 0);
-                }
-            if (c > 0) finish_block(c - 1);
-            if (!more) finish_block(c);
-            if (more) kc[BWD ? ((c + 1) & 1) : 0].store(lds[(c + 1) & 1], bkin);
+            mma(acc[S], lds[S]);
+            if (c > 0) finish_block(c - 1, acc[S ^ 1], sd[S ^ 1]);
+            if (!more) finish_block(c, acc[S], sd[S]);
+            if (more) kc[S ^ 1].store(lds[S ^ 1], bkin);
             __syncthreads();
+        };
+        for (int c = 0; c < P.nch; c += 2) {
+            step(std::integral_constant<int, 0>{}, c);
+            if (c + 1 < P.nch) step(std::integral_constant<int, 1>{}, c + 1);
+        }
+        return;
+    } else {
+#pragma unroll
+        for (int c = 0; c < NB; ++c) {
+            if (c < P.nch) {
+                const bool more = c + 1 < P.nch;
+                if (more) kc[0].load(rB, boff, P.E, c + 1);
+                // block c's mask values, added once its products are done
+                // (in the next chunk)
+                if (side) load_side(c, sd[c & 1]);
+                __builtin_amdgcn_sched_barrier(0);  // the loads go out before the products
+                mma(acc[c], lds[c & 1]);
+                if (c > 0) finish_block(c - 1, acc[c - 1], sd[(c - 1) & 1]);
+                if (!more) finish_block(c, acc[c], sd[c & 1]);
+                if (more) kc[0].store(lds[(c + 1) & 1], bkin);
+                __syncthreads();
+            }
         }
     }
-    if constexpr (BWD) return;
 
     // Forward: the row maxima, the exponentials and their sums, the weights.
 #pragma unroll
@@ -420,14 +446,14 @@ __global__ void __launch_bounds__(256) head_rows_kernel(HeadRows P) {
 
 // Whether the fused kernels take this shape: keys and head width within
 // the register tile, float4 operand rows, every operand 16-byte aligned.
-bool head_rows_fit(const MhaDims& d, std::initializer_list<const void*> ptrs) {
-    if (!g_fused || d.Sk < 1 || d.Sk > kHMaxKeys || d.hd < 1 || d.hd > kHMaxWidth || d.hd % 4 != 0 || d.E % 4 != 0)
+bool head_rows_fit(const MhaDims& d, int64_t max_keys, std::initializer_list<const void*> ptrs) {
+    if (!g_fused || d.Sk < 1 || d.Sk > max_keys || d.hd < 1 || d.hd > kHMaxWidth || d.hd % 4 != 0 || d.E % 4 != 0)
         return false;
     const int64_t tiles = (d.Sq + kHRows - 1) / kHRows * d.B * d.H;
     if (tiles > INT_MAX) return false;
     // 32-bit byte offsets into a head's key rows (every chunk, padding
     // included) and into a row tile's [32, Sk] slab
-    if ((d.Sk + kHChunk) * d.E * 4 > INT_MAX) return false;
+    if ((d.Sk + kHChunk) * d.E * 4 > INT_MAX || (int64_t)kHRows * d.Sk * 4 > INT_MAX) return false;
     for (const void* p : ptrs)
         if (!aligned16(p)) return false;
     return true;
@@ -439,18 +465,22 @@ int launch_head_rows(HeadRows P, int64_t BH, const char* who) {
     P.row_tiles = (int)((P.Sq + kHRows - 1) / kHRows);
     P.tiles = (int)(P.row_tiles * BH);
     P.nch = (int)((P.Sk + kHChunk - 1) / kHChunk);
-    const int nb = P.nch <= 1 ? 1 : P.nch <= 2 ? 2 : P.nch <= 4 ? 4 : 8;
+    // the forward's accumulators hold whole rows (NB chunks); the backward
+    // loops over any number of chunks
+    const int nb = BWD || P.nch <= 1 ? 1 : P.nch <= 2 ? 2 : P.nch <= 4 ? 4 : 8;
     const int ks = P.hd <= 32 ? 1 : P.hd <= 64 ? 2 : 4;
     const dim3 grid((unsigned)P.tiles), block(256);
     hipStream_t st = stream();
     const bool vec = P.Sk % 4 == 0 && aligned16(P.out) && aligned16(BWD ? P.attn : P.mask);
-#define WM_HR(NBv, KSv)                                                                      \
-    if (nb == NBv && ks == KSv) {                                                            \
-        if (vec)                                                                             \
-            launch_kernel((head_rows_kernel<NBv, KSv, BWD, true>), grid, block, 0, st, P);   \
-        else                                                                                 \
-            launch_kernel((head_rows_kernel<NBv, KSv, BWD, false>), grid, block, 0, st, P);  \
-        return check_launch(who);                                                            \
+#define WM_HR(NBv, KSv)                                                                          \
+    if constexpr (!BWD || NBv == 1) {                                                            \
+        if (nb == NBv && ks == KSv) {                                                            \
+            if (vec)                                                                             \
+                launch_kernel((head_rows_kernel<NBv, KSv, BWD, true>), grid, block, 0, st, P);   \
+            else                                                                                 \
+                launch_kernel((head_rows_kernel<NBv, KSv, BWD, false>), grid, block, 0, st, P);  \
+            return check_launch(who);                                                            \
+        }                                                                                        \
     }
     WM_HR(1, 1) WM_HR(1, 2) WM_HR(1, 4) WM_HR(2, 1) WM_HR(2, 2) WM_HR(2, 4)
     WM_HR(4, 1) WM_HR(4, 2) WM_HR(4, 4) WM_HR(8, 1) WM_HR(8, 2) WM_HR(8, 4)
@@ -498,7 +528,7 @@ int wm_mha_fwd(const float* q, const float* k, const float* v, const float* mask
     WM_TRY(project(q, Wq, bq, d.B * d.Sq, d.E, Q));
     WM_TRY(project(k, Wk, bk, d.B * d.Sk, d.E, K));
     WM_TRY(project(v, Wv, bv, d.B * d.Sk, d.E, V));
-    if (d.Sk > 0 && head_rows_fit(d, {Q, K, V})) {
+    if (d.Sk > 0 && head_rows_fit(d, kHMaxKeys, {Q, K, V})) {
         // attn[b, h] = softmax(Q_h K_h^T * scale + mask) in one pass
         HeadRows P{};
         P.a = Q;
@@ -554,7 +584,7 @@ int wm_mha_bwd(const float* dout, const float* q, const float* k, const float* v
         const int64_t s2[6] = {d.H * d.Sq * d.Sk, d.Sq * d.Sk, d.Sq * E, d.hd, d.Sk * E, d.hd};
         WM_TRY(wm_gemm(1, 0, d.Sk, d.hd, d.Sq, 1.0f, attn, d.Sk, dctx.as<float>(), E, dV.as<float>(), E, 0, nullptr,
                        d.B * d.H, d.H, s2));
-        if (head_rows_fit(d, {dctx.p, V, ctx})) {
+        if (head_rows_fit(d, INT64_MAX, {dctx.p, V, ctx})) {
             // dattn and the softmax's backward (:1341-1360) in one pass
             HeadRows P{};
             P.a = dctx.as<float>();
