@@ -146,6 +146,45 @@ def test_gemm_k_zero_and_empty(wm):
     assert matmul(np.zeros((0, 5), np.float32), rng_normal((5, 3), 42)).shape == (0, 3)
 
 
+@pytest.mark.parametrize("mnk", [(128, 128, 1), (130, 140, 100), (200, 129, 256), (128, 256, 257)], ids=str)
+def test_gemm_one_level_batch_padded_alpha_accumulate(wm, mnk):
+    """One-level batches of untransposed products with padded rows and
+    problem strides, alpha and accumulation (the shapes up to k = 256 with
+    m, n >= 128 take rocBLAS's strided-batched route by default, k = 257
+    this library's kernel); the padding of C stays untouched."""
+    m, n, k = mnk
+    P, pad, gap = 3, 3, 11
+    lda, ldb, ldc = k + pad, n + pad, n + pad
+    sa, sb, sc = m * lda + gap, k * ldb + gap, m * ldc + gap
+    A, B = rng_normal((P, m, k), 45), rng_normal((P, k, n), 46)
+    C0 = rng_normal((P, m, n), 47)
+    a = np.zeros(P * sa, np.float32)
+    b = np.zeros(P * sb, np.float32)
+    c0 = np.full(P * sc, 7.0, np.float32)
+    for p in range(P):
+        a[p * sa:p * sa + m * lda].reshape(m, lda)[:, :k] = A[p]
+        b[p * sb:p * sb + k * ldb].reshape(k, ldb)[:, :n] = B[p]
+        c0[p * sc:p * sc + m * ldc].reshape(m, ldc)[:, :n] = C0[p]
+    alpha = 0.625
+    got = gemm(0, 0, m, n, k, alpha, a, lda, b, ldb, c0, ldc, True, None, P, 1, (sa, 0, sb, 0, sc, 0))
+    for p in range(P):
+        gp = got[p * sc:p * sc + m * ldc].reshape(m, ldc)
+        close(gp[:, :n], alpha * o64.matmul(A[p], B[p]) + C0[p], alpha * oab.matmul(A[p], B[p]) + np.abs(C0[p]))
+        assert np.all(gp[:, n:] == 7.0)
+        if p + 1 < P:
+            assert np.all(got[p * sc + m * ldc:(p + 1) * sc] == 7.0)  # the gap between problems
+
+
+def test_gemm_batch_sharing_one_output(wm):
+    """A batch whose problems all write one C (stride 0) overwrites it with
+    one problem's product, whichever route: every problem here is the same
+    product, so the result is that product."""
+    m, n, k, P = 128, 128, 64, 4
+    A, B = rng_normal((m, k), 48), rng_normal((k, n), 49)
+    got = gemm(0, 0, m, n, k, 1.0, A, k, B, n, np.zeros((m, n), np.float32), n, False, None, P, 1, (0, 0, 0, 0, 0, 0))
+    close(got, o64.matmul(A, B), oab.matmul(A, B))
+
+
 def test_gemm_two_level_batch_per_head_slices(wm):
     """scores[b, h] = Q[b, :, h] @ K[b, :, h]^T * alpha on [B, S, H * hd]
     activations, as MultiHeadAttention slices its heads."""
