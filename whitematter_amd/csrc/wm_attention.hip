@@ -19,6 +19,7 @@
 #include "../../include/wm_gemm.h"
 #include "../../include/wm_layers.h"
 
+#include <atomic>
 #include <cfloat>
 #include <climits>
 #include <cmath>
@@ -32,7 +33,7 @@ struct MhaDims {
     int64_t B, Sq, Sk, E, H, hd;
 };
 
-int g_fused = 1;  // wm_mha_fused
+std::atomic<int> g_fused{1};  // wm_mha_fused (read once per wm_mha_fwd / wm_mha_bwd call)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -447,7 +448,8 @@ __global__ void __launch_bounds__(256) head_rows_kernel(HeadRows P) {
 // Whether the fused kernels take this shape: keys and head width within
 // the register tile, float4 operand rows, every operand 16-byte aligned.
 bool head_rows_fit(const MhaDims& d, int64_t max_keys, std::initializer_list<const void*> ptrs) {
-    if (!g_fused || d.Sk < 1 || d.Sk > max_keys || d.hd < 1 || d.hd > kHMaxWidth || d.hd % 4 != 0 || d.E % 4 != 0)
+    if (!g_fused.load(std::memory_order_relaxed)) return false;
+    if (d.Sk < 1 || d.Sk > max_keys || d.hd < 1 || d.hd > kHMaxWidth || d.hd % 4 != 0 || d.E % 4 != 0)
         return false;
     const int64_t tiles = (d.Sq + kHRows - 1) / kHRows * d.B * d.H;
     if (tiles > INT_MAX) return false;
@@ -635,6 +637,6 @@ int wm_mha_bwd(const float* dout, const float* q, const float* k, const float* v
 }
 
 int wm_mha_fused(int mode) {
-    if (mode == 0 || mode == 1) g_fused = mode;
-    return g_fused;
+    if (mode == 0 || mode == 1) g_fused.store(mode, std::memory_order_relaxed);
+    return g_fused.load(std::memory_order_relaxed);
 }

@@ -40,6 +40,7 @@
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <mutex>
 
@@ -439,14 +440,18 @@ int64_t choose_kslices(int64_t work, int64_t k) {
 // products (measured on MI355X, % of the fp32 matrix peak, library / this
 // kernel: 8192^3 92.9-97.8 / 83-84; the [8192, 1024] x [1024, 1024]
 // projections and their weight and input gradients 88.9-90.3 / 65-70),
-// tie on k = 128 (62 / 61) and lose on the attention's per-head products
-// (k = 64 scores 19.7 / 46, n = 64 contexts 45.7 / 64: two-level batches
-// the library can only take as one call per outer batch).  Unbatched
-// products with m, n >= 128 and k >= 256 go to rocBLAS (atomics off: the
-// same bits on every run); batched ones, the rest, and every product while
-// the library route is switched off (wm_gemm_library), to gemm_kernel.  A
-// bias is written into C first and the library adds the product to it.
-int g_library = 1;  // wm_gemm_library
+// edge ahead on bmm's k = 128 forward (62.2 / 59.7-60.8) and lose on its
+// gradients (71 / 74-76) and on the attention's per-head products (k = 64
+// scores 19.7 / 46, n = 64 contexts 45.7 / 64: two-level batches the
+// library can only take as one call per outer batch).  Unbatched products
+// with m, n >= 128 and k >= 256, and one-level batches of untransposed
+// products with m, n >= 128, k <= 256, no bias and disjoint outputs, go to
+// rocBLAS (atomics off: the same bits on every run); the rest, and every
+// product while the library route is switched off (wm_gemm_library), to
+// gemm_kernel.  A bias is written into C first and the library adds the
+// product to it.  The switch is read once per product; a product racing a
+// switch takes one route or the other, whole.
+std::atomic<int> g_library{1};  // wm_gemm_library
 
 struct Blas {
     std::mutex mu;
@@ -481,7 +486,7 @@ bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
 // The library route for P, or 1 when it does not take P (the caller then
 // launches gemm_kernel); WM_OK or an error status when it ran.
 int try_library(bool ta, bool tb, const GemmParams& P) {
-    if (!g_library || P.kslices > 1) return 1;
+    if (!g_library.load(std::memory_order_relaxed) || P.kslices > 1) return 1;
     if (P.m < 128 || P.n < 128) return 1;
     if (P.bias && P.accumulate) return 1;
     if (P.batch != 1) {
@@ -660,8 +665,8 @@ int wm_gemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alp
 }
 
 int wm_gemm_library(int mode) {
-    if (mode == 0 || mode == 1) g_library = mode;
-    return g_library;
+    if (mode == 0 || mode == 1) g_library.store(mode, std::memory_order_relaxed);
+    return g_library.load(std::memory_order_relaxed);
 }
 
 int wm_matmul(const float* a, const float* b, int64_t m, int64_t k, int64_t n, float* c) {
