@@ -175,6 +175,68 @@ def test_gemm_one_level_batch_padded_alpha_accumulate(wm, mnk):
             assert np.all(got[p * sc + m * ldc:(p + 1) * sc] == 7.0)  # the gap between problems
 
 
+@pytest.mark.parametrize("case", [(2, 128, 128, 64, False), (5, 256, 384, 192, True), (3, 384, 128, 1024, False),
+                                  (17, 1024, 1024, 64, True), (16, 1024, 512, 128, False)], ids=str)
+def test_gemm_dma_batches(wm, case):
+    """Untransposed one-level batches whose tiles are all interior (m, n
+    multiples of 128, k of 64, 16-byte rows) run on the direct-to-LDS kernel:
+    k = 64 and 192 (one and three rounds of its four stage buffers), 1024;
+    17 problems of 64 tiles take two problems per workgroup with a last
+    workgroup of one; padded rows (pad 4 keeps the rows 16-byte aligned) and
+    gaps between problems stay untouched; alpha, accumulation and a bias."""
+    P, m, n, k, with_bias = case
+    pad, gap = 4, 8
+    lda, ldb, ldc = k + pad, n + pad, n + pad
+    sa, sb, sc = m * lda + gap, k * ldb + gap, m * ldc + gap
+    A, B = rng_normal((P, m, k), 80), rng_uniform((P, k, n), 81, -1.0, 1.0)
+    C0 = rng_normal((P, m, n), 82)
+    bias = rng_normal((n,), 83) if with_bias else None
+    a = np.zeros(P * sa, np.float32)
+    b = np.zeros(P * sb, np.float32)
+    c0 = np.full(P * sc, 7.0, np.float32)
+    for q in range(P):
+        a[q * sa:q * sa + m * lda].reshape(m, lda)[:, :k] = A[q]
+        b[q * sb:q * sb + k * ldb].reshape(k, ldb)[:, :n] = B[q]
+        c0[q * sc:q * sc + m * ldc].reshape(m, ldc)[:, :n] = C0[q]
+    alpha = 0.625
+    got = gemm(0, 0, m, n, k, alpha, a, lda, b, ldb, c0, ldc, True, bias, P, 1, (sa, 0, sb, 0, sc, 0))
+    bias64 = np.zeros(n) if bias is None else bias.astype(np.float64)
+    for q in range(P):
+        gq = got[q * sc:q * sc + m * ldc].reshape(m, ldc)
+        a64, b64 = A[q].astype(np.float64), B[q].astype(np.float64)
+        ref = alpha * (a64 @ b64) + C0[q] + bias64
+        scale = alpha * (np.abs(a64) @ np.abs(b64)) + np.abs(C0[q]) + np.abs(bias64)
+        close(gq[:, :n], ref, scale)
+        assert np.all(gq[:, n:] == 7.0)
+        if q + 1 < P:
+            assert np.all(got[q * sc + m * ldc:(q + 1) * sc] == 7.0)
+
+
+@pytest.mark.parametrize("mnk_lda", [(128, 128, 96, 96), (130, 128, 64, 64), (128, 128, 64, 66)], ids=str)
+def test_gemm_dma_near_misses(wm, mnk_lda):
+    """Shapes one step outside the direct-to-LDS kernel's conditions (k not a
+    multiple of 64, a partial row tile, rows of A not 16-byte aligned) take
+    the other kernels with the same results."""
+    m, n, k, lda = mnk_lda
+    P = 3
+    A, B = rng_normal((P, m, k), 84), rng_normal((P, k, n), 85)
+    a = np.zeros((P, m, lda), np.float32)
+    a[:, :, :k] = A
+    got = gemm(0, 0, m, n, k, 1.0, a.ravel(), lda, B.ravel(), n, np.zeros(P * m * n, np.float32), n, False, None, P,
+               1, (m * lda, 0, k * n, 0, m * n, 0)).reshape(P, m, n)
+    close(got, o64.bmm(A, B), oab.bmm(A, B))
+
+
+def test_bmm_dma_consecutive_calls(wm):
+    """Two products in a row on the direct-to-LDS kernel, the first with two
+    problems per workgroup, the second smaller (one problem per workgroup):
+    each equals its float64 product."""
+    for P, m, n, k, seed in ((20, 1024, 1024, 128, 86), (2, 128, 256, 64, 88)):
+        a, b = rng_normal((P, m, k), seed), rng_normal((P, k, n), seed + 1)
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        close(matmul(a, b), a64 @ b64, np.abs(a64) @ np.abs(b64))
+
+
 def test_gemm_batch_sharing_one_output(wm):
     """A batch whose problems all write one C (stride 0) overwrites it with
     one problem's product, whichever route: every problem here is the same

@@ -32,6 +32,15 @@
 // each slice's product goes to a workspace and a second pass adds the slices
 // in fixed order, scales and accumulates into C.
 //
+// Untransposed products whose tiles are all interior (m, n multiples of 128,
+// k of 64, 16-byte rows; one batch level) take gemm_dma_kernel instead: the
+// operands go from global memory straight into LDS (no registers held for
+// them), in stages of 16 k over four LDS buffers with three stages in flight,
+// and a workgroup runs the same tile of two consecutive problems, moving the
+// second problem's first stages while the first one's C is written.  At
+// k = 128 a tile's stages are too few for one stage of look-ahead to hide
+// the loads, which bounds gemm_kernel there (see the kernel's comment).
+//
 // Sums are fp32 in the matrix cores' order (see include/wm_gemm.h).
 #include "wm_common.hpp"
 
@@ -76,6 +85,7 @@ struct GemmParams {
     // (a multiple of kBK); slice s writes its own C at + s * sck.
     int kslices;
     int64_t ksplit, sck;
+    int group;  // gemm_dma_kernel: consecutive problems per workgroup
 };
 
 // One operand's R x 32 tile per stage (R = 128 or 64 rows of op(A), or
@@ -329,6 +339,216 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
     }
 }
 
+// ---- untransposed interior products: operands straight into LDS --------
+//
+// gemm_dma_kernel computes the same 128 x 128 C tiles as gemm_kernel, with the
+// same waves, MFMA blocks and LDS-staged epilogue, for products whose tiles
+// are all interior (checked on the host).  What changes is how the operands
+// reach LDS:
+//   - global_load_lds_dwordx4 moves 16 bytes per lane from global memory to
+//     LDS at M0 + 16 * lane, so no registers hold the next stages;
+//   - k advances in stages of 16 over four LDS buffers with three stages in
+//     flight (48 k ahead of the matrix cores), where one stage of 32 in
+//     registers could not hide the loads behind a small-k tile's few stages;
+//   - a workgroup takes the same tile of `group` consecutive problems, and
+//     starts the next problem's first two stages as soon as the last stage's
+//     barrier frees the buffers, while the epilogue writes C through the
+//     other two.
+// Per stage each wave moves two 1 KB blocks of A and two of B:
+//   A block i (i = 2 wave + u): tile rows 16 i .. 16 i + 15 at 64 bytes each;
+//     lane l fills row 16 i + l / 4, 16-byte slot l % 4, with k chunk
+//     slot ^ swz(row), swz(row) = ((row >> 1) ^ (row >> 2)) & 3, so the
+//     fragment reads (one row per lane, one chunk) fall on distinct banks for
+//     32 and for 64 banks of LDS;
+//   B block i: k rows 2 i and 2 i + 1 at 512 bytes each; lane l fills k row
+//     2 i + l / 32, columns 4 (l % 32) .. + 3.
+// Half-wave h takes k = 8 h .. 8 h + 7 of a stage (A chunks 2 h and 2 h + 1).
+//
+// The transfers are issued from inline asm: the compiler cannot tell which
+// buffer a transfer writes, and for builtin transfers it waits for all of
+// them before every LDS read.  The kernel orders them itself: before stage s
+// each wave waits until at most the transfers of stages s + 1 and s + 2 are
+// outstanding (vector memory operations complete in issue order, C's stores
+// included), then a barrier makes every wave's transfers visible; a buffer
+// is refilled only after the barrier that follows its last reads.  An
+// opaque transfer can only make the compiler's own waits stricter.
+constexpr int kDK = 16;                              // k per stage
+constexpr int kDStageFloats = 2 * kTile * kDK;       // A [128][16] + B [16][128]
+constexpr int kDEp = 64 + 4;                         // epilogue row pitch (floats)
+constexpr int kDBufFloats = kDStageFloats > 64 * kDEp ? kDStageFloats : 64 * kDEp;
+
+__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Wait until at most `outstanding` (0, 4 or 8) vector memory operations of
+// this wave are in flight.
+__device__ __forceinline__ void vm_wait_upto(int outstanding) {
+    if (outstanding >= 8) __builtin_amdgcn_s_waitcnt(0x0F78);
+    else if (outstanding >= 4) __builtin_amdgcn_s_waitcnt(0x0F74);
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// 16 bytes per lane from g to LDS byte address lds + 16 * lane (lds
+// wave-uniform, in M0).  M0 is declared clobbered; the compiler warns that
+// it reserves M0, and gemm_dma_kernel's code has no other use of it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_barrier with the compiler kept from moving memory accesses across it.
+__device__ __forceinline__ void wg_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
+    // Four stage buffers; each also holds one wave's half epilogue quarter.
+    __shared__ __attribute__((aligned(16))) float lds0[kDBufFloats];
+    __shared__ __attribute__((aligned(16))) float lds1[kDBufFloats];
+    __shared__ __attribute__((aligned(16))) float lds2[kDBufFloats];
+    __shared__ __attribute__((aligned(16))) float lds3[kDBufFloats];
+    auto bufp = [&](int bi) -> float* { return bi == 0 ? lds0 : bi == 1 ? lds1 : bi == 2 ? lds2 : lds3; };
+    auto lds_addr = [&](int bi) -> uint32_t {
+        return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)bufp(bi);
+    };
+
+    const int ntiles = P.tiles_m * P.tiles_n;
+    int t = (int)blockIdx.x;
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    int tm, tn;
+    tile_of(t, P.tiles_m, P.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * kTile;
+    const int lane = (int)threadIdx.x & 63;
+    const int wave = (int)threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, r = lane & 31;
+
+    int64_t aoff[2], boff[2];  // this lane's sources at k = 0 (see above)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = 2 * wave + u;
+        const int row = 16 * i + lane / 4;
+        aoff[u] = (m0 + row) * P.lda + 4 * ((lane & 3) ^ (((row >> 1) ^ (row >> 2)) & 3));
+        boff[u] = (int64_t)(2 * i + lane / 32) * P.ldb + n0 + 4 * (lane & 31);
+    }
+    const int nk = (int)(P.k / kDK);
+    const uint32_t wofs = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 2048u;  // the wave's two blocks
+    auto issue = [&](int64_t pp, int st, int bi) {  // stage st of problem pp into buffer bi
+        const float* Ab = P.a + pp * P.sa0;
+        const float* Bb = P.b + pp * P.sb0;
+        const int64_t k0 = (int64_t)st * kDK;
+        const uint32_t la = lds_addr(bi) + wofs;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) lds_dma16(Ab + aoff[u] + k0, la + 1024u * u);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) lds_dma16(Bb + boff[u] + k0 * P.ldb, la + 4u * kTile * kDK + 1024u * u);
+    };
+
+    int64_t p = (int64_t)blockIdx.y * P.group;
+    const int64_t pend = min(P.batch, p + (int64_t)P.group);
+    issue(p, 0, 0);
+    issue(p, 1, 1);
+    issue(p, 2, 2);
+    for (; p < pend; ++p) {
+        float* C = P.c + p * P.sc0;
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+        // nk is a multiple of 4: unrolled over the buffers, so every LDS
+        // address below is a constant offset.
+        for (int s0 = 0; s0 < nk; s0 += 4) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int s = s0 + b;
+                vm_wait_upto(4 * min(nk - 1 - s, 2));
+                lgkm_wait0();
+                wg_barrier();
+                if (s + 3 < nk) issue(p, s + 3, (b + 3) & 3);
+                const float* As = bufp(b);
+                const float* Bs = As + kTile * kDK;
+#pragma unroll
+                for (int kq = 0; kq < 2; ++kq) {
+                    const int c = 2 * half + kq;
+                    const int kr = 8 * half + 4 * kq;
+                    float4 av[2], bv[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const int R = wm * 64 + i * 32 + r;
+                        av[i] = *reinterpret_cast<const float4*>(As + R * kDK + 4 * (c ^ (((R >> 1) ^ (R >> 2)) & 3)));
+                    }
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int Cc = wn * 64 + j * 32 + r;
+                        bv[j] = make_float4(Bs[kr * kTile + Cc], Bs[(kr + 1) * kTile + Cc],
+                                            Bs[(kr + 2) * kTile + Cc], Bs[(kr + 3) * kTile + Cc]);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0);
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0);
+                        }
+                }
+            }
+        }
+        lgkm_wait0();
+        wg_barrier();  // every wave is done with the stage buffers
+        const bool more = p + 1 < pend;
+        if (more) {
+            issue(p + 1, 0, 0);
+            issue(p + 1, 1, 1);
+        }
+        // Epilogue through buffers 2 and 3: each wave parks half of its
+        // 64 x 64 quarter at a time (accumulator element q of a 32 x 32 block
+        // at row 8 (q / 4) + 4 half + q % 4, column r), then writes it as
+        // float4 rows, 16 lanes per 256-byte row segment.
+        float* ep = bufp(2 + (wave >> 1)) + (wave & 1) * 32 * kDEp;
+        const float alpha = P.alpha;
+        const bool accum = P.accumulate != 0;
+        const int cq = (lane % 16) * 4;
+        const int64_t col = n0 + wn * 64 + cq;
+        float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (P.bias) bias4 = *reinterpret_cast<const float4*>(P.bias + col);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (i) lgkm_wait0();  // this wave's reads of the first half are done
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    ep[(8 * (q >> 2) + 4 * half + (q & 3)) * kDEp + j * 32 + r] = acc[i][j][q];
+#pragma unroll 4
+            for (int s4 = 0; s4 < 8; ++s4) {
+                const int rq = lane / 16 + 4 * s4;
+                const int64_t row = m0 + wm * 64 + i * 32 + rq;
+                const float4 a4 = *reinterpret_cast<const float4*>(ep + rq * kDEp + cq);
+                float4 v = make_float4(alpha * a4.x, alpha * a4.y, alpha * a4.z, alpha * a4.w);
+                float* dst = C + row * P.ldc + col;
+                if (accum) {
+                    const float4 old = *reinterpret_cast<const float4*>(dst);
+                    v = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+                }
+                if (P.bias) v = make_float4(v.x + bias4.x, v.y + bias4.y, v.z + bias4.z, v.w + bias4.w);
+                if (accum) *reinterpret_cast<float4*>(dst) = v;
+                else st_stream(dst, v);
+            }
+        }
+        lgkm_wait0();
+        wg_barrier();  // every wave is done with buffers 2 and 3
+        if (more) issue(p + 1, 2, 2);
+    }
+}
+
 // out[c][r] (+)= x[r][c] for x [rows, cols]: 64 x 64 tiles through LDS (65-
 // float pitch, so the column reads hit 64 different banks), 256 threads,
 // each moving 16 elements; reads and writes run along rows.
@@ -545,6 +765,29 @@ int try_library(bool ta, bool tb, const GemmParams& P) {
     return WM_OK;
 }
 
+// Whether gemm_dma_kernel takes P: untransposed, one batch level, every tile
+// interior (m, n multiples of 128, k of 64), 16-byte rows, and no k split
+// (gemm_kernel splits k when few tiles meet a long k).
+bool dma_fits(bool ta, bool tb, bool vec, const GemmParams& P, int64_t tiles) {
+    return !ta && !tb && vec && P.batch_inner == 1 && P.m % kTile == 0 && P.n % kTile == 0 && P.k > 0 &&
+           P.k % (4 * kDK) == 0 && P.c_aligned && P.ldc % 4 == 0 && (!P.bias || aligned16(P.bias)) &&
+           choose_kslices(tiles * P.batch, P.k) == 1;
+}
+
+// gemm_dma_kernel for P, or 1 when the grid would not fit (the caller then
+// takes the other routes).
+int launch_dma(GemmParams P, int64_t tiles) {
+    // Two problems per workgroup while that still leaves two workgroups per CU.
+    P.group = P.batch >= 2 && tiles * (P.batch / 2) >= 2 * num_cus() ? 2 : 1;
+    const int64_t gy = (P.batch + P.group - 1) / P.group;
+    if (gy > 65535) return 1;
+    P.kslices = 1;
+    P.ksplit = P.k;
+    P.sck = 0;
+    launch_kernel(gemm_dma_kernel, dim3((unsigned)tiles, (unsigned)gy), dim3(kThreads), 0, stream(), P);
+    return check_launch("wm_gemm(dma)");
+}
+
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
     // 64-wide column tiles for narrow products (attention's per-head products
@@ -561,6 +804,14 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     P.c_aligned = aligned16(P.c) && (P.batch == 1 || (P.sc0 % 4 == 0 && P.sc1 % 4 == 0)) ? 1 : 0;
     hipStream_t s = stream();
     P.kslices = 1;
+    P.group = 1;
+    // Batched products that fit gemm_dma_kernel run there (faster than the
+    // library's strided-batched kernels on them); plain ones keep the library
+    // unless its route is switched off.
+    if (dma_fits(ta, tb, vec, P, tm * tn) && (P.batch > 1 || !g_library.load(std::memory_order_relaxed))) {
+        const int r = launch_dma(P, tm * tn);
+        if (r != 1) return r;
+    }
     const int lib = try_library(ta, tb, P);
     if (lib != 1) return lib;
 
