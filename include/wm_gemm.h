@@ -12,8 +12,9 @@
  * input does not require grad.
  *
  * Arithmetic: products and sums in fp32 on the matrix cores (no
- * reduced-precision inputs): this library's v_mfma_f32_32x32x2_f32 kernel,
- * or, for the plain large products and bmm's forward (wm_gemm_library),
+ * reduced-precision inputs): this library's v_mfma_f32_32x32x2_f32 kernels
+ * (one for untransposed products whose 128 x 128 tiles are all interior,
+ * one for the rest), or, for the plain large products (wm_gemm_library),
  * rocBLAS's fp32 kernels with atomics off.  The reference adds each product to its fp32
  * accumulator in k order; the matrix cores add them in another order (and a
  * product with fewer output tiles than CUs and a long k adds the partial
@@ -55,11 +56,12 @@ int wm_gemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alp
             int64_t batch_inner, const int64_t* strides);
 
 /* The route of the plain large products (unbatched, m, n >= 128, k >= 256,
- * not both bias and accumulate) and of one-level batches of untransposed
- * products with m, n >= 128, k <= 256 and no bias (bmm's forward): 1
- * (default) = rocBLAS's tuned fp32 kernels (sgemm / sgemm_strided_batched,
- * atomics off), which are faster there; 0 = this library's MFMA kernel for
- * every product.  mode 0 or 1 sets it, any other value only queries; returns the
+ * not both bias and accumulate) and of the one-level batches of
+ * untransposed products with m, n >= 128, k <= 256 and no bias that this
+ * library's interior-tile kernel does not take (m or n not a multiple of
+ * 128, k not of 64, rows not 16-byte aligned): 1 (default) = rocBLAS's
+ * tuned fp32 kernels (sgemm / sgemm_strided_batched, atomics off), which
+ * are faster there; 0 = this library's MFMA kernels for every product.  mode 0 or 1 sets it, any other value only queries; returns the
  * route now in force.  The results agree with the reference within the same
  * fp32 summation error either way (both deterministic run to run).  No
  * counterpart in the reference (a routing switch, for tests and

@@ -29,7 +29,7 @@ def close(got, ref, scale, rtol=1e-5):
 def route(request, wm):
     """Every test under both routes of the plain large products
     (wm_gemm_library): rocBLAS where it is faster, and this library's MFMA
-    kernel for everything."""
+    kernels for everything."""
     from whitematter_amd import _lib as W
     before = W.lib().wm_gemm_library(-1)
     W.lib().wm_gemm_library(request.param)

@@ -3,8 +3,8 @@
 // (core/tensor.cpp:783-895), and the strided product the drop-in Linear and
 // MultiHeadAttention modules use.
 //
-// One kernel covers every case.  A workgroup of 4 waves computes a 128 x 128
-// tile of C; each wave a 64 x 64 quarter as 2 x 2 blocks of
+// gemm_kernel covers every case (gemm_dma_kernel, below, takes a subset
+// faster).  A workgroup of 4 waves computes a 128 x 128 tile of C; each wave a 64 x 64 quarter as 2 x 2 blocks of
 // v_mfma_f32_32x32x2_f32.  k advances in stages of 32: the next stage's tiles
 // of op(A) and op(B) are loaded from HBM into registers while the matrix
 // cores work on the current ones from LDS (two LDS buffers, one barrier per
@@ -657,18 +657,20 @@ int64_t choose_kslices(int64_t work, int64_t k) {
 // ---- rocBLAS for the plain large products ----------------------------------
 //
 // The vendor library's tuned fp32 kernels beat this file's on large, plain
-// products (measured on MI355X, % of the fp32 matrix peak, library / this
-// kernel: 8192^3 92.9-97.8 / 83-84; the [8192, 1024] x [1024, 1024]
-// projections and their weight and input gradients 88.9-90.3 / 65-70),
-// edge ahead on bmm's k = 128 forward (62.2 / 59.7-60.8) and lose on its
-// gradients (71 / 74-76) and on the attention's per-head products (k = 64
-// scores 19.7 / 46, n = 64 contexts 45.7 / 64: two-level batches the
-// library can only take as one call per outer batch).  Unbatched products
-// with m, n >= 128 and k >= 256, and one-level batches of untransposed
-// products with m, n >= 128, k <= 256, no bias and disjoint outputs, go to
-// rocBLAS (atomics off: the same bits on every run); the rest, and every
-// product while the library route is switched off (wm_gemm_library), to
-// gemm_kernel.  A bias is written into C first and the library adds the
+// products (measured on MI355X, % of the fp32 matrix peak, library /
+// gemm_kernel / gemm_dma_kernel: 8192^3 92.9-97.8 / 83-84 / 87-90; the
+// [8192, 1024] x [1024, 1024] projections and their weight and input
+// gradients 88.9-90.3 / 65-70 / -), lose on bmm's k = 128 forward
+// (62.2 / 59.7-63.2 / 64.6-70.0), on its gradients (71 / 74-76 / -) and on
+// the attention's per-head products (k = 64 scores 19.7 / 46, n = 64
+// contexts 45.7 / 64: two-level batches the library can only take as one
+// call per outer batch).  Batched products that gemm_dma_kernel takes run
+// there first (launch_gemm).  Unbatched products with m, n >= 128 and
+// k >= 256, and the other one-level batches of untransposed products with
+// m, n >= 128, k <= 256, no bias and disjoint outputs, go to rocBLAS
+// (atomics off: the same bits on every run); the rest to gemm_kernel, and
+// while the library route is switched off (wm_gemm_library) every product
+// to this file's kernels.  A bias is written into C first and the library adds the
 // product to it.  The switch is read once per product; a product racing a
 // switch takes one route or the other, whole.
 std::atomic<int> g_library{1};  // wm_gemm_library
