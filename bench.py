@@ -1403,7 +1403,7 @@ def gemm_ops(n=8192, batch=64, t=1024, hd=128):
         Op("bmm fwd", lambda: W.call("wm_bmm", qa.vp, kb.vp, batch, t, hd, t, sc.vp),
            (2 * batch * t * hd + batch * t * t) * F32, "gemm_dma_kernel", batch * t * t, bm),
         Op("bmm bwd", lambda: W.call("wm_bmm_bwd", sg.vp, qa.vp, kb.vp, batch, t, hd, t, gq.vp, 0, gk.vp, 0),
-           (batch * t * t * 2 + 4 * batch * t * hd) * F32, "gemm_kernel", 2 * batch * t * hd, 2 * bm),
+           (batch * t * t * 2 + 4 * batch * t * hd) * F32, "gemm_dma_kernel", 2 * batch * t * hd, 2 * bm),
     ]
     keep = [a, b, g, c, ga, gb, qa, kb, sg, sc, gq, gk]
     return ops, keep, {"workload": "gemm: Tensor::matmul [%d,%d]@[%d,%d] and Tensor::bmm [%d,%d,%d]@[%d,%d,%d], fp32 "

@@ -178,8 +178,8 @@ def test_gemm_one_level_batch_padded_alpha_accumulate(wm, mnk):
 @pytest.mark.parametrize("case", [(2, 128, 128, 64, False), (5, 256, 384, 192, True), (3, 384, 128, 1024, False),
                                   (17, 1024, 1024, 64, True), (16, 1024, 512, 128, False)], ids=str)
 def test_gemm_dma_batches(wm, case):
-    """Untransposed one-level batches whose tiles are all interior (m, n
-    multiples of 128, k of 64, 16-byte rows) run on the direct-to-LDS kernel:
+    """One-level batches whose tiles are all interior (m, n multiples of 128,
+    k of 64, 16-byte rows) run on the direct-to-LDS kernel (untransposed here):
     k = 64 and 192 (one and three rounds of its four stage buffers), 1024;
     17 problems of 64 tiles take two problems per workgroup with a last
     workgroup of one; padded rows (pad 4 keeps the rows 16-byte aligned) and
@@ -210,6 +210,64 @@ def test_gemm_dma_batches(wm, case):
         assert np.all(gq[:, n:] == 7.0)
         if q + 1 < P:
             assert np.all(got[q * sc + m * ldc:(q + 1) * sc] == 7.0)
+
+
+@pytest.mark.parametrize("trans", [(0, 1), (1, 0), (1, 1)], ids=lambda t: "NT"[t[0]] + "NT"[t[1]])
+@pytest.mark.parametrize("case", [(3, 128, 256, 64), (2, 256, 128, 192), (3, 1024, 128, 1024), (17, 1024, 1024, 64)],
+                         ids=str)
+def test_gemm_dma_transposed(wm, trans, case):
+    """The direct-to-LDS kernel with transposed operands (A stored k x m,
+    B stored n x k): the k-contiguous and row-contiguous stagings swap sides.
+    Padded leading dimensions and gaps between problems, alpha, accumulation
+    and a bias; 17 problems of 64 tiles take two problems per workgroup."""
+    ta, tb = trans
+    P, m, n, k = case
+    pad, gap = 4, 8
+    ar, ac = (k, m) if ta else (m, k)
+    br, bc = (n, k) if tb else (k, n)
+    lda, ldb, ldc = ac + pad, bc + pad, n + pad
+    sa, sb, sc = ar * lda + gap, br * ldb + gap, m * ldc + gap
+    A, B = rng_normal((P, ar, ac), 90), rng_uniform((P, br, bc), 91, -1.0, 1.0)
+    C0 = rng_normal((P, m, n), 92)
+    bias = rng_normal((n,), 93)
+    a = np.zeros(P * sa, np.float32)
+    b = np.zeros(P * sb, np.float32)
+    c0 = np.full(P * sc, 7.0, np.float32)
+    for q in range(P):
+        a[q * sa:q * sa + ar * lda].reshape(ar, lda)[:, :ac] = A[q]
+        b[q * sb:q * sb + br * ldb].reshape(br, ldb)[:, :bc] = B[q]
+        c0[q * sc:q * sc + m * ldc].reshape(m, ldc)[:, :n] = C0[q]
+    alpha = -1.25
+    got = gemm(ta, tb, m, n, k, alpha, a, lda, b, ldb, c0, ldc, True, bias, P, 1, (sa, 0, sb, 0, sc, 0))
+    b64 = bias.astype(np.float64)
+    for q in range(P):
+        gq = got[q * sc:q * sc + m * ldc].reshape(m, ldc)
+        oa = (A[q].T if ta else A[q]).astype(np.float64)
+        ob = (B[q].T if tb else B[q]).astype(np.float64)
+        ref = alpha * (oa @ ob) + C0[q] + b64
+        scale = abs(alpha) * (np.abs(oa) @ np.abs(ob)) + np.abs(C0[q]) + np.abs(b64)
+        close(gq[:, :n], ref, scale)
+        assert np.all(gq[:, n:] == 7.0)
+        if q + 1 < P:
+            assert np.all(got[q * sc + m * ldc:(q + 1) * sc] == 7.0)
+
+
+@pytest.mark.parametrize("shape", [(4, 1024, 128, 1024), (64, 256, 128, 256)], ids=str)
+def test_bmm_backward_on_dma_kernel(wm, shape):
+    """bmm's closure at attention-like shapes: its two products (g b^T and
+    a^T g) run on the direct-to-LDS kernel; both gradients, overwritten and
+    accumulated."""
+    P, t, hd, t2 = shape
+    a, b = rng_normal((P, t, hd), 94), rng_normal((P, hd, t2), 95)
+    g = rng_normal((P, t, t2), 96)
+    a64, b64, g64 = a.astype(np.float64), b.astype(np.float64), g.astype(np.float64)
+    ga, gb = matmul_bwd(g, a, b)
+    close(ga, g64 @ np.swapaxes(b64, 1, 2), np.abs(g64) @ np.abs(np.swapaxes(b64, 1, 2)))
+    close(gb, np.swapaxes(a64, 1, 2) @ g64, np.abs(np.swapaxes(a64, 1, 2)) @ np.abs(g64))
+    ga0, gb0 = rng_normal((P, t, hd), 97), rng_normal((P, hd, t2), 98)
+    ga, gb = matmul_bwd(g, a, b, ga0, gb0)
+    close(ga, ga0 + g64 @ np.swapaxes(b64, 1, 2), np.abs(ga0) + np.abs(g64) @ np.abs(np.swapaxes(b64, 1, 2)))
+    close(gb, gb0 + np.swapaxes(a64, 1, 2) @ g64, np.abs(gb0) + np.abs(np.swapaxes(a64, 1, 2)) @ np.abs(g64))
 
 
 @pytest.mark.parametrize("mnk_lda", [(128, 128, 96, 96), (130, 128, 64, 64), (128, 128, 64, 66)], ids=str)

@@ -32,8 +32,8 @@
 // each slice's product goes to a workspace and a second pass adds the slices
 // in fixed order, scales and accumulates into C.
 //
-// Untransposed products whose tiles are all interior (m, n multiples of 128,
-// k of 64, 16-byte rows; one batch level) take gemm_dma_kernel instead: the
+// Products whose tiles are all interior (m, n multiples of 128, k of 64,
+// 16-byte rows; one batch level) take gemm_dma_kernel instead: the
 // operands go from global memory straight into LDS (no registers held for
 // them), in stages of 16 k over four LDS buffers with three stages in flight,
 // and a workgroup runs the same tile of two consecutive problems, moving the
@@ -339,7 +339,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
     }
 }
 
-// ---- untransposed interior products: operands straight into LDS --------
+// ---- interior products: operands straight into LDS -----------------------
 //
 // gemm_dma_kernel computes the same 128 x 128 C tiles as gemm_kernel, with the
 // same waves, MFMA blocks and LDS-staged epilogue, for products whose tiles
@@ -354,15 +354,17 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
 //     starts the next problem's first two stages as soon as the last stage's
 //     barrier frees the buffers, while the epilogue writes C through the
 //     other two.
-// Per stage each wave moves two 1 KB blocks of A and two of B:
-//   A block i (i = 2 wave + u): tile rows 16 i .. 16 i + 15 at 64 bytes each;
-//     lane l fills row 16 i + l / 4, 16-byte slot l % 4, with k chunk
-//     slot ^ swz(row), swz(row) = ((row >> 1) ^ (row >> 2)) & 3, so the
-//     fragment reads (one row per lane, one chunk) fall on distinct banks for
-//     32 and for 64 banks of LDS;
-//   B block i: k rows 2 i and 2 i + 1 at 512 bytes each; lane l fills k row
-//     2 i + l / 32, columns 4 (l % 32) .. + 3.
-// Half-wave h takes k = 8 h .. 8 h + 7 of a stage (A chunks 2 h and 2 h + 1).
+// Per stage each wave moves two 1 KB blocks of each operand (block
+// i = 2 wave + u), by the operand's layout in memory (DmaOperand):
+//   k-contiguous (A untransposed, B transposed): tile rows 16 i .. 16 i + 15
+//     at 64 bytes each; lane l fills row 16 i + l / 4, 16-byte slot l % 4,
+//     with k chunk slot ^ swz(row), swz(row) = ((row >> 1) ^ (row >> 2)) & 3,
+//     so the fragment reads (one row per lane, one chunk) fall on distinct
+//     banks for 32 and for 64 banks of LDS;
+//   row-contiguous (A transposed, B untransposed): k rows 2 i and 2 i + 1 at
+//     512 bytes each; lane l fills k row 2 i + l / 32, tile rows
+//     4 (l % 32) .. + 3.
+// Half-wave h takes k = 8 h .. 8 h + 7 of a stage (chunks 2 h and 2 h + 1).
 //
 // The transfers are issued from inline asm: the compiler cannot tell which
 // buffer a transfer writes, and for builtin transfers it waits for all of
@@ -404,7 +406,40 @@ __device__ __forceinline__ void wg_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// One operand's staging in gemm_dma_kernel.  KC: element (row, k) at
+// base[row * ld + k] (A untransposed, B transposed), staged as rows of 16 k
+// in swizzled 16-byte chunks; else at base[k * ld + row] (A transposed, B
+// untransposed), staged as k rows of 128.
+template <bool KC>
+struct DmaOperand {
+    // This lane's source for transfer u (block i = 2 wave + u) at k = 0.
+    __device__ __forceinline__ static int64_t src(int64_t ld, int64_t r0, int wave, int lane, int u) {
+        const int i = 2 * wave + u;
+        if constexpr (KC) {
+            const int row = 16 * i + lane / 4;
+            return (r0 + row) * ld + 4 * ((lane & 3) ^ (((row >> 1) ^ (row >> 2)) & 3));
+        } else {
+            return (int64_t)(2 * i + lane / 32) * ld + r0 + 4 * (lane & 31);
+        }
+    }
+    __device__ __forceinline__ static int64_t k_step(int64_t k0, int64_t ld) { return KC ? k0 : k0 * ld; }
+    // Fragment of tile row R: k = 8 half + 4 kq .. + 3 of the stage.
+    __device__ __forceinline__ static float4 frag(const float* T, int R, int half, int kq) {
+        if constexpr (KC) {
+            const int c = 2 * half + kq;
+            return *reinterpret_cast<const float4*>(T + R * kDK + 4 * (c ^ (((R >> 1) ^ (R >> 2)) & 3)));
+        } else {
+            const int kr = 8 * half + 4 * kq;
+            return make_float4(T[kr * kTile + R], T[(kr + 1) * kTile + R], T[(kr + 2) * kTile + R],
+                               T[(kr + 3) * kTile + R]);
+        }
+    }
+};
+
+template <bool TA, bool TB>
 __global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
+    using OpA = DmaOperand<!TA>;
+    using OpB = DmaOperand<TB>;
     // Four stage buffers; each also holds one wave's half epilogue quarter.
     __shared__ __attribute__((aligned(16))) float lds0[kDBufFloats];
     __shared__ __attribute__((aligned(16))) float lds1[kDBufFloats];
@@ -426,13 +461,11 @@ __global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
     const int wm = wave >> 1, wn = wave & 1;
     const int half = lane >> 5, r = lane & 31;
 
-    int64_t aoff[2], boff[2];  // this lane's sources at k = 0 (see above)
+    int64_t aoff[2], boff[2];  // this lane's sources at k = 0
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-        const int i = 2 * wave + u;
-        const int row = 16 * i + lane / 4;
-        aoff[u] = (m0 + row) * P.lda + 4 * ((lane & 3) ^ (((row >> 1) ^ (row >> 2)) & 3));
-        boff[u] = (int64_t)(2 * i + lane / 32) * P.ldb + n0 + 4 * (lane & 31);
+        aoff[u] = OpA::src(P.lda, m0, wave, lane, u);
+        boff[u] = OpB::src(P.ldb, n0, wave, lane, u);
     }
     const int nk = (int)(P.k / kDK);
     const uint32_t wofs = (uint32_t)__builtin_amdgcn_readfirstlane(wave) * 2048u;  // the wave's two blocks
@@ -442,9 +475,10 @@ __global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
         const int64_t k0 = (int64_t)st * kDK;
         const uint32_t la = lds_addr(bi) + wofs;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) lds_dma16(Ab + aoff[u] + k0, la + 1024u * u);
+        for (int u = 0; u < 2; ++u) lds_dma16(Ab + aoff[u] + OpA::k_step(k0, P.lda), la + 1024u * u);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) lds_dma16(Bb + boff[u] + k0 * P.ldb, la + 4u * kTile * kDK + 1024u * u);
+        for (int u = 0; u < 2; ++u)
+            lds_dma16(Bb + boff[u] + OpB::k_step(k0, P.ldb), la + 4u * kTile * kDK + 1024u * u);
     };
 
     int64_t p = (int64_t)blockIdx.y * P.group;
@@ -475,20 +509,11 @@ __global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
                 const float* Bs = As + kTile * kDK;
 #pragma unroll
                 for (int kq = 0; kq < 2; ++kq) {
-                    const int c = 2 * half + kq;
-                    const int kr = 8 * half + 4 * kq;
                     float4 av[2], bv[2];
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const int R = wm * 64 + i * 32 + r;
-                        av[i] = *reinterpret_cast<const float4*>(As + R * kDK + 4 * (c ^ (((R >> 1) ^ (R >> 2)) & 3)));
-                    }
+                    for (int i = 0; i < 2; ++i) av[i] = OpA::frag(As, wm * 64 + i * 32 + r, half, kq);
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int Cc = wn * 64 + j * 32 + r;
-                        bv[j] = make_float4(Bs[kr * kTile + Cc], Bs[(kr + 1) * kTile + Cc],
-                                            Bs[(kr + 2) * kTile + Cc], Bs[(kr + 3) * kTile + Cc]);
-                    }
+                    for (int j = 0; j < 2; ++j) bv[j] = OpB::frag(Bs, wn * 64 + j * 32 + r, half, kq);
 #pragma unroll
                     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -767,18 +792,18 @@ int try_library(bool ta, bool tb, const GemmParams& P) {
     return WM_OK;
 }
 
-// Whether gemm_dma_kernel takes P: untransposed, one batch level, every tile
-// interior (m, n multiples of 128, k of 64), 16-byte rows, and no k split
-// (gemm_kernel splits k when few tiles meet a long k).
-bool dma_fits(bool ta, bool tb, bool vec, const GemmParams& P, int64_t tiles) {
-    return !ta && !tb && vec && P.batch_inner == 1 && P.m % kTile == 0 && P.n % kTile == 0 && P.k > 0 &&
+// Whether gemm_dma_kernel takes P: one batch level, every tile interior (m,
+// n multiples of 128, k of 64), 16-byte rows, and no k split (gemm_kernel
+// splits k when few tiles meet a long k).
+bool dma_fits(bool vec, const GemmParams& P, int64_t tiles) {
+    return vec && P.batch_inner == 1 && P.m % kTile == 0 && P.n % kTile == 0 && P.k > 0 &&
            P.k % (4 * kDK) == 0 && P.c_aligned && P.ldc % 4 == 0 && (!P.bias || aligned16(P.bias)) &&
            choose_kslices(tiles * P.batch, P.k) == 1;
 }
 
 // gemm_dma_kernel for P, or 1 when the grid would not fit (the caller then
 // takes the other routes).
-int launch_dma(GemmParams P, int64_t tiles) {
+int launch_dma(bool ta, bool tb, GemmParams P, int64_t tiles) {
     // Two problems per workgroup while that still leaves two workgroups per CU.
     P.group = P.batch >= 2 && tiles * (P.batch / 2) >= 2 * num_cus() ? 2 : 1;
     const int64_t gy = (P.batch + P.group - 1) / P.group;
@@ -786,7 +811,11 @@ int launch_dma(GemmParams P, int64_t tiles) {
     P.kslices = 1;
     P.ksplit = P.k;
     P.sck = 0;
-    launch_kernel(gemm_dma_kernel, dim3((unsigned)tiles, (unsigned)gy), dim3(kThreads), 0, stream(), P);
+    const dim3 grid((unsigned)tiles, (unsigned)gy);
+    if (!ta && !tb) launch_kernel((gemm_dma_kernel<false, false>), grid, dim3(kThreads), 0, stream(), P);
+    else if (!ta && tb) launch_kernel((gemm_dma_kernel<false, true>), grid, dim3(kThreads), 0, stream(), P);
+    else if (ta && !tb) launch_kernel((gemm_dma_kernel<true, false>), grid, dim3(kThreads), 0, stream(), P);
+    else launch_kernel((gemm_dma_kernel<true, true>), grid, dim3(kThreads), 0, stream(), P);
     return check_launch("wm_gemm(dma)");
 }
 
@@ -810,8 +839,8 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     // Batched products that fit gemm_dma_kernel run there (faster than the
     // library's strided-batched kernels on them); plain ones keep the library
     // unless its route is switched off.
-    if (dma_fits(ta, tb, vec, P, tm * tn) && (P.batch > 1 || !g_library.load(std::memory_order_relaxed))) {
-        const int r = launch_dma(P, tm * tn);
+    if (dma_fits(vec, P, tm * tn) && (P.batch > 1 || !g_library.load(std::memory_order_relaxed))) {
+        const int r = launch_dma(ta, tb, P, tm * tn);
         if (r != 1) return r;
     }
     const int lib = try_library(ta, tb, P);
