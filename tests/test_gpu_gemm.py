@@ -270,6 +270,37 @@ def test_bmm_backward_on_dma_kernel(wm, shape):
     close(gb, gb0 + np.swapaxes(a64, 1, 2) @ g64, np.abs(gb0) + np.abs(np.swapaxes(a64, 1, 2)) @ np.abs(g64))
 
 
+@pytest.mark.parametrize("kind", ["ctx", "dv", "scores"])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_gemm_two_level_per_head_interior(wm, kind, hd):
+    """Per-head products of [B, S, H * hd] activations as MultiHeadAttention
+    issues them (two-level batches, which gemm_kernel takes) at sizes whose
+    tiles are all interior: ctx = attn V (NN), dV = attn^T dctx (TN),
+    scores = alpha Q K^T (NT), for 64- and 128-wide heads."""
+    B, S, H = 2, 256, 4
+    E = H * hd
+    attn = rng_normal((B * H, S, S), 100)
+    X, Y = rng_normal((B, S, E), 101), rng_normal((B, S, E), 102)
+    heads = lambda Z: Z.reshape(B, S, H, hd).transpose(0, 2, 1, 3).reshape(B * H, S, hd).astype(np.float64)
+    a64 = attn.astype(np.float64)
+    if kind == "scores":
+        alpha = 0.125
+        out = np.full((B, H, S, S), np.nan, np.float32)
+        got = gemm(0, 1, S, S, hd, alpha, X, E, Y, E, out, S, False, None, B * H, H,
+                   (S * E, hd, S * E, hd, H * S * S, S * S)).reshape(B * H, S, S)
+        ref = alpha * (heads(X) @ np.swapaxes(heads(Y), 1, 2))
+        scale = alpha * (np.abs(heads(X)) @ np.abs(np.swapaxes(heads(Y), 1, 2)))
+        close(got, ref, scale)
+        return
+    ta = 1 if kind == "dv" else 0
+    out = np.full((B, S, E), np.nan, np.float32)
+    got = gemm(ta, 0, S, hd, S, 1.0, attn, S, X, E, out, E, False, None, B * H, H,
+               (H * S * S, S * S, S * E, hd, S * E, hd))
+    oa = np.swapaxes(a64, 1, 2) if ta else a64
+    ref, scale = oa @ heads(X), np.abs(oa) @ np.abs(heads(X))
+    close(heads(got), ref, scale)
+
+
 @pytest.mark.parametrize("mnk_lda", [(128, 128, 96, 96), (130, 128, 64, 64), (128, 128, 64, 66)], ids=str)
 def test_gemm_dma_near_misses(wm, mnk_lda):
     """Shapes one step outside the direct-to-LDS kernel's conditions (k not a
