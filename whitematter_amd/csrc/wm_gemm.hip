@@ -369,11 +369,13 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(GemmParams P) {
 // The transfers are issued from inline asm: the compiler cannot tell which
 // buffer a transfer writes, and for builtin transfers it waits for all of
 // them before every LDS read.  The kernel orders them itself: before stage s
-// each wave waits until at most the transfers of stages s + 1 and s + 2 are
-// outstanding (vector memory operations complete in issue order, C's stores
-// included), then a barrier makes every wave's transfers visible; a buffer
-// is refilled only after the barrier that follows its last reads.  An
-// opaque transfer can only make the compiler's own waits stricter.
+// each wave waits until at most as many vector memory operations are in
+// flight as it issued transfers after stage s's (those of stages s + 1 and
+// s + 2), then a barrier makes every wave's transfers visible; a buffer is
+// refilled only after the barrier that follows its last reads.  Transfers
+// are loads and complete in issue order; C's stores from the previous
+// problem, counted by the same counter, can only make such a wait stricter.
+// An opaque transfer can only make the compiler's own waits stricter too.
 constexpr int kDK = 16;                              // k per stage
 constexpr int kDStageFloats = 2 * kTile * kDK;       // A [128][16] + B [16][128]
 constexpr int kDEp = 64 + 4;                         // epilogue row pitch (floats)
