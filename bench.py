@@ -1446,7 +1446,7 @@ def mha_ops(B=8, S=1024, E=1024, H=16):
     fwd()
     f_fl = 4 * 2 * B * S * E * E + 2 * 2 * B * H * S * S * hd
     att = B * H * S * S * F32
-    kn = "rocBLAS sgemm + head_rows_kernel + gemm_kernel"
+    kn = "rocBLAS sgemm + head_rows_kernel + gemm_kernel + gemm_dma32_kernel"
     ops = [Op("mha fwd", fwd, 4 * B * S * E * F32 + 3 * att, kn, B * S * E, f_fl),
            Op("mha bwd", bwd, 6 * B * S * E * F32 + 4 * att, kn, B * S * E, 2 * f_fl)]
     keep = [x, mask, out, ctx, Q, K, V, attn, dout, gx] + params + grads

@@ -274,9 +274,10 @@ def test_bmm_backward_on_dma_kernel(wm, shape):
 @pytest.mark.parametrize("hd", [64, 128])
 def test_gemm_two_level_per_head_interior(wm, kind, hd):
     """Per-head products of [B, S, H * hd] activations as MultiHeadAttention
-    issues them (two-level batches, which gemm_kernel takes) at sizes whose
-    tiles are all interior: ctx = attn V (NN), dV = attn^T dctx (TN),
-    scores = alpha Q K^T (NT), for 64- and 128-wide heads."""
+    issues them (two-level batches) at sizes whose tiles are all interior:
+    ctx = attn V (NN), dV = attn^T dctx (TN; with 64-wide heads on the
+    32-k direct-to-LDS kernel), scores = alpha Q K^T (NT), for 64- and
+    128-wide heads."""
     B, S, H = 2, 256, 4
     E = H * hd
     attn = rng_normal((B * H, S, S), 100)
@@ -299,6 +300,40 @@ def test_gemm_two_level_per_head_interior(wm, kind, hd):
     oa = np.swapaxes(a64, 1, 2) if ta else a64
     ref, scale = oa @ heads(X), np.abs(oa) @ np.abs(heads(X))
     close(heads(got), ref, scale)
+
+
+@pytest.mark.parametrize("case", [(129, 1024, 32), (5, 256, 96), (3, 384, 1024)], ids=str)
+def test_gemm_dma32_transposed_a(wm, case):
+    """op(A) = A^T with n = 64 (the attention backward's dV and dK) on the
+    32-k direct-to-LDS kernel: one stage (k = 32), three stages rotating over
+    the three buffers (k = 96), k = 1024; 129 problems of 8 tiles take two
+    problems per workgroup with a last one of one; padded rows, gaps between
+    problems, alpha, accumulation and a bias."""
+    P, m, k = case
+    n, pad, gap = 64, 4, 8
+    lda, ldb, ldc = m + pad, n + pad, n + pad
+    sa, sb, sc = k * lda + gap, k * ldb + gap, m * ldc + gap
+    A, B = rng_normal((P, k, m), 110), rng_uniform((P, k, n), 111, -1.0, 1.0)
+    C0 = rng_normal((P, m, n), 112)
+    bias = rng_normal((n,), 113)
+    a = np.zeros(P * sa, np.float32)
+    b = np.zeros(P * sb, np.float32)
+    c0 = np.full(P * sc, 7.0, np.float32)
+    for q in range(P):
+        a[q * sa:q * sa + k * lda].reshape(k, lda)[:, :m] = A[q]
+        b[q * sb:q * sb + k * ldb].reshape(k, ldb)[:, :n] = B[q]
+        c0[q * sc:q * sc + m * ldc].reshape(m, ldc)[:, :n] = C0[q]
+    alpha = 0.75
+    got = gemm(1, 0, m, n, k, alpha, a, lda, b, ldb, c0, ldc, True, bias, P, 1, (sa, 0, sb, 0, sc, 0))
+    b64 = bias.astype(np.float64)
+    for q in range(P):
+        gq = got[q * sc:q * sc + m * ldc].reshape(m, ldc)
+        oa, ob = A[q].T.astype(np.float64), B[q].astype(np.float64)
+        close(gq[:, :n], alpha * (oa @ ob) + C0[q] + b64,
+              alpha * (np.abs(oa) @ np.abs(ob)) + np.abs(C0[q]) + np.abs(b64))
+        assert np.all(gq[:, n:] == 7.0)
+        if q + 1 < P:
+            assert np.all(got[q * sc + m * ldc:(q + 1) * sc] == 7.0)
 
 
 @pytest.mark.parametrize("mnk_lda", [(128, 128, 96, 96), (130, 128, 64, 64), (128, 128, 64, 66)], ids=str)

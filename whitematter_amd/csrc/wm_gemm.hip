@@ -576,6 +576,192 @@ __global__ void __launch_bounds__(kThreads) gemm_dma_kernel(GemmParams P) {
     }
 }
 
+// ---- narrow interior products (n = 64): 32-k stages straight into LDS ----
+//
+// gemm_dma32_kernel is gemm_dma_kernel's staging for 128 x 64 C tiles (the
+// attention's per-head products with 64-wide heads, two-level batches
+// included): with 64-wide tiles a 16-k stage gives each wave too little
+// matrix work against its waits and barrier, so k advances in stages of 32
+// over three LDS buffers (24 KB each), two stages in flight.  Each wave
+// computes a 64 x 32 quarter as 2 blocks of v_mfma_f32_32x32x2_f32 and moves
+// per stage four 1 KB blocks of op(A) and two of op(B):
+//   k-contiguous operand: rows of 32 k (128 bytes), 8 rows per block; lane l
+//     fills row 8 i + l / 8, 16-byte slot l % 8, with k chunk
+//     slot ^ swz8(row), swz8(row) = (row ^ (row >> 3)) & 7, which keeps the
+//     fragment reads on distinct banks for 32 and for 64 banks;
+//   row-contiguous operand: k rows of R floats, 256 / R of them per block.
+// Half-wave h takes k = 16 h .. 16 h + 15 of a stage (chunks 4 h .. 4 h + 3).
+// Transfers, waits and barriers as in gemm_dma_kernel; the buffer index is a
+// runtime value here (the transfers are opaque to the compiler, so nothing
+// needs its offsets to be constants).  Launched for products with a
+// transposed A only (the attention backward's dV = attn^T dctx and
+// dK = ds^T Q: 160.5 -> 146.7 us each against gemm_kernel); with A
+// untransposed (attn V, ds K) it measured slower than gemm_kernel's 64-wide
+// tiles (164.5 -> 178.0 us).
+constexpr int kNK = 32;                                // k per stage
+constexpr int kNStageFloats = kTile * kNK + kNK * 64;  // A [128][32] + B [32][64]
+constexpr int kNEp = 32 + 4;                           // epilogue row pitch (floats)
+
+__device__ __forceinline__ int swz8(int row) { return (row ^ (row >> 3)) & 7; }
+
+template <bool KC, int R>
+struct Dma32Operand {
+    static constexpr int NBLK = R * kNK * 4 / 1024 / 4;  // 1 KB blocks per wave per stage
+    static constexpr int KPB = 256 / R;                  // row-contiguous: k rows per block
+    static constexpr int LPK = R / 4;                    // row-contiguous: lanes per k row
+    __device__ __forceinline__ static int64_t src(int64_t ld, int64_t r0, int wave, int lane, int u) {
+        const int i = NBLK * wave + u;
+        if constexpr (KC) {
+            const int row = 8 * i + lane / 8;
+            return (r0 + row) * ld + 4 * ((lane & 7) ^ swz8(row));
+        } else {
+            return (int64_t)(KPB * i + lane / LPK) * ld + r0 + 4 * (lane % LPK);
+        }
+    }
+    __device__ __forceinline__ static int64_t k_step(int64_t k0, int64_t ld) { return KC ? k0 : k0 * ld; }
+    // Fragment of tile row `row`: k = 16 half + 4 kq .. + 3 of the stage.
+    __device__ __forceinline__ static float4 frag(const float* T, int row, int half, int kq) {
+        if constexpr (KC) {
+            const int c = 4 * half + kq;
+            return *reinterpret_cast<const float4*>(T + row * kNK + 4 * (c ^ swz8(row)));
+        } else {
+            const int kr = 16 * half + 4 * kq;
+            return make_float4(T[kr * R + row], T[(kr + 1) * R + row], T[(kr + 2) * R + row], T[(kr + 3) * R + row]);
+        }
+    }
+};
+
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(kThreads) gemm_dma32_kernel(GemmParams P) {
+    using OpA = Dma32Operand<!TA, kTile>;
+    using OpB = Dma32Operand<TB, 64>;
+    constexpr int XFER = OpA::NBLK + OpB::NBLK;  // transfers per wave per stage
+    __shared__ __attribute__((aligned(16))) float lds[3 * kNStageFloats];
+
+    const int ntiles = P.tiles_m * P.tiles_n;
+    int t = (int)blockIdx.x;
+    if ((ntiles & 7) == 0) t = (t & 7) * (ntiles >> 3) + (t >> 3);
+    int tm, tn;
+    tile_of(t, P.tiles_m, P.tiles_n, tm, tn);
+    const int64_t m0 = (int64_t)tm * kTile, n0 = (int64_t)tn * 64;
+    const int lane = (int)threadIdx.x & 63;
+    const int wave = (int)threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int half = lane >> 5, r = lane & 31;
+
+    int64_t aoff[OpA::NBLK], boff[OpB::NBLK];  // this lane's sources at k = 0
+#pragma unroll
+    for (int u = 0; u < OpA::NBLK; ++u) aoff[u] = OpA::src(P.lda, m0, wave, lane, u);
+#pragma unroll
+    for (int u = 0; u < OpB::NBLK; ++u) boff[u] = OpB::src(P.ldb, n0, wave, lane, u);
+    const int nk = (int)(P.k / kNK);
+    const uint32_t wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)lds;
+    // Operand and output starts of problem pp = (o, i): o = pp / batch_inner.
+    struct Bases {
+        const float* a;
+        const float* b;
+        float* c;
+    };
+    auto bases = [&](int64_t pp) -> Bases {
+        int64_t po = pp, pi = 0;
+        if (P.batch_inner != 1) {
+            po = (int64_t)((uint32_t)pp / (uint32_t)P.batch_inner);  // batch <= INT_MAX (host)
+            pi = pp - po * P.batch_inner;
+        }
+        return {P.a + po * P.sa0 + pi * P.sa1, P.b + po * P.sb0 + pi * P.sb1, P.c + po * P.sc0 + pi * P.sc1};
+    };
+    auto issue = [&](const Bases& q, int st, int bi) {  // stage st into buffer bi
+        const int64_t k0 = (int64_t)st * kNK;
+        const uint32_t la = lds0 + 4u * (uint32_t)(bi * kNStageFloats);
+#pragma unroll
+        for (int u = 0; u < OpA::NBLK; ++u)
+            lds_dma16(q.a + aoff[u] + OpA::k_step(k0, P.lda), la + 1024u * (OpA::NBLK * wv + u));
+#pragma unroll
+        for (int u = 0; u < OpB::NBLK; ++u)
+            lds_dma16(q.b + boff[u] + OpB::k_step(k0, P.ldb), la + 4u * kTile * kNK + 1024u * (OpB::NBLK * wv + u));
+    };
+
+    int64_t p = (int64_t)blockIdx.y * P.group;
+    const int64_t pend = min(P.batch, p + (int64_t)P.group);
+    Bases cur = bases(p);
+    issue(cur, 0, 0);
+    if (nk > 1) issue(cur, 1, 1);
+    for (; p < pend; ++p) {
+        f32x16 acc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][q] = 0.0f;
+        for (int s = 0; s < nk; ++s) {
+            // at most stage s + 1's transfers in flight (see gemm_dma_kernel)
+            if (s + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0F70 | XFER);
+            else __builtin_amdgcn_s_waitcnt(0x0F70);
+            lgkm_wait0();
+            wg_barrier();
+            if (s + 2 < nk) issue(cur, s + 2, (s + 2) % 3);
+            const float* As = lds + (s % 3) * kNStageFloats;
+            const float* Bs = As + kTile * kNK;
+#pragma unroll
+            for (int kq = 0; kq < 4; ++kq) {
+                float4 av[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) av[i] = OpA::frag(As, wm * 64 + i * 32 + r, half, kq);
+                const float4 bv = OpB::frag(Bs, wn * 32 + r, half, kq);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv.x, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv.y, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv.z, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv.w, acc[i], 0, 0, 0);
+                }
+            }
+        }
+        lgkm_wait0();
+        wg_barrier();  // every wave is done with the stage buffers
+        float* C = cur.c;
+        const bool more = p + 1 < pend;
+        if (more) {
+            cur = bases(p + 1);
+            issue(cur, 0, 0);
+            if (nk > 1) issue(cur, 1, 1);
+        }
+        // Epilogue through buffer 2: each wave parks half of its 64 x 32
+        // quarter at a time, then writes it as float4 rows, 8 lanes per
+        // 128-byte row segment.
+        float* ep = lds + 2 * kNStageFloats + wave * 32 * kNEp;
+        const float alpha = P.alpha;
+        const bool accum = P.accumulate != 0;
+        const int cq = (lane % 8) * 4;
+        const int64_t col = n0 + wn * 32 + cq;
+        float4 bias4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (P.bias) bias4 = *reinterpret_cast<const float4*>(P.bias + col);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (i) lgkm_wait0();  // this wave's reads of the first half are done
+#pragma unroll
+            for (int q = 0; q < 16; ++q) ep[(8 * (q >> 2) + 4 * half + (q & 3)) * kNEp + r] = acc[i][q];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int rq = lane / 8 + 8 * s4;
+                const int64_t row = m0 + wm * 64 + i * 32 + rq;
+                const float4 a4 = *reinterpret_cast<const float4*>(ep + rq * kNEp + cq);
+                float4 v = make_float4(alpha * a4.x, alpha * a4.y, alpha * a4.z, alpha * a4.w);
+                float* dst = C + row * P.ldc + col;
+                if (accum) {
+                    const float4 old = *reinterpret_cast<const float4*>(dst);
+                    v = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+                }
+                if (P.bias) v = make_float4(v.x + bias4.x, v.y + bias4.y, v.z + bias4.z, v.w + bias4.w);
+                if (accum) *reinterpret_cast<float4*>(dst) = v;
+                else st_stream(dst, v);
+            }
+        }
+        lgkm_wait0();
+        wg_barrier();  // every wave is done with buffer 2
+    }
+}
+
 // out[c][r] (+)= x[r][c] for x [rows, cols]: 64 x 64 tiles through LDS (65-
 // float pitch, so the column reads hit 64 different banks), 256 threads,
 // each moving 16 elements; reads and writes run along rows.
@@ -821,6 +1007,27 @@ int launch_dma(bool ta, bool tb, GemmParams P, int64_t tiles) {
     return check_launch("wm_gemm(dma)");
 }
 
+// Whether gemm_dma32_kernel takes P: A transposed, B not, n = 64 (one
+// 64-wide tile), m a multiple of 128, k of 32, 16-byte rows, no k split;
+// two batch levels allowed.
+bool dma32_fits(bool ta, bool tb, bool vec, const GemmParams& P, int64_t tiles) {
+    return ta && !tb && vec && P.batch <= INT_MAX && P.m % kTile == 0 && P.n == 64 && P.k > 0 && P.k % kNK == 0 &&
+           P.c_aligned && P.ldc % 4 == 0 && (!P.bias || aligned16(P.bias)) &&
+           choose_kslices(tiles * P.batch, P.k) == 1;
+}
+
+int launch_dma32(GemmParams P, int64_t tiles) {
+    P.group = P.batch >= 2 && tiles * (P.batch / 2) >= 2 * num_cus() ? 2 : 1;
+    const int64_t gy = (P.batch + P.group - 1) / P.group;
+    if (gy > 65535) return 1;
+    P.kslices = 1;
+    P.ksplit = P.k;
+    P.sck = 0;
+    const dim3 grid((unsigned)tiles, (unsigned)gy);
+    launch_kernel((gemm_dma32_kernel<true, false>), grid, dim3(kThreads), 0, stream(), P);
+    return check_launch("wm_gemm(dma32)");
+}
+
 int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     GemmParams P = P0;
     // 64-wide column tiles for narrow products (attention's per-head products
@@ -843,6 +1050,11 @@ int launch_gemm(bool ta, bool tb, const GemmParams& P0) {
     // unless its route is switched off.
     if (dma_fits(vec, P, tm * tn) && (P.batch > 1 || !g_library.load(std::memory_order_relaxed))) {
         const int r = launch_dma(ta, tb, P, tm * tn);
+        if (r != 1) return r;
+    }
+    if (narrow && dma32_fits(ta, tb, vec, P, tm * tn) &&
+        (P.batch > 1 || !g_library.load(std::memory_order_relaxed))) {
+        const int r = launch_dma32(P, tm * tn);
         if (r != 1) return r;
     }
     const int lib = try_library(ta, tb, P);
