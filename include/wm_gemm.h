@@ -16,8 +16,9 @@
  * (for products whose tiles are all interior, operands staged straight
  * into LDS; for the rest, through registers), or, for the plain large
  * products (wm_gemm_library), rocBLAS's fp32 kernels with atomics off.  The
- * reference adds each product to its fp32 accumulator in k order; the matrix cores add them in another order (and a
- * product with fewer output tiles than CUs and a long k adds the partial
+ * reference adds each product to its fp32 accumulator in k order; the
+ * matrix cores add them in another order (and a product with fewer output
+ * tiles than CUs and a long k adds the partial
  * products of its k slices in a second pass, in fixed slice order), so the
  * results agree with the reference within fp32 summation error (tested
  * against an fp64 restatement relative to sum_k |a_ik * b_kj|), not bit for
