@@ -1401,7 +1401,7 @@ def gemm_ops(n=8192, batch=64, t=1024, hd=128):
         Op("matmul bwd", lambda: W.call("wm_matmul_bwd", g.vp, a.vp, b.vp, n, n, n, ga.vp, 0, gb.vp, 0),
            6 * n * n * F32, "rocBLAS sgemm", 2 * n * n, 2 * mm),
         Op("bmm fwd", lambda: W.call("wm_bmm", qa.vp, kb.vp, batch, t, hd, t, sc.vp),
-           (2 * batch * t * hd + batch * t * t) * F32, "gemm_dma_kernel", batch * t * t, bm),
+           (2 * batch * t * hd + batch * t * t) * F32, "gemm_dma3_kernel", batch * t * t, bm),
         Op("bmm bwd", lambda: W.call("wm_bmm_bwd", sg.vp, qa.vp, kb.vp, batch, t, hd, t, gq.vp, 0, gk.vp, 0),
            (batch * t * t * 2 + 4 * batch * t * hd) * F32, "gemm_dma_kernel", 2 * batch * t * hd, 2 * bm),
     ]

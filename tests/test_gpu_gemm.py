@@ -213,11 +213,12 @@ def test_gemm_dma_batches(wm, case):
 
 
 @pytest.mark.parametrize("trans", [(0, 1), (1, 0), (1, 1)], ids=lambda t: "NT"[t[0]] + "NT"[t[1]])
-@pytest.mark.parametrize("case", [(3, 128, 256, 64), (2, 256, 128, 192), (3, 1024, 128, 1024), (17, 1024, 1024, 64)],
-                         ids=str)
+@pytest.mark.parametrize("case", [(3, 128, 256, 64), (2, 256, 128, 192), (4, 256, 256, 384), (3, 1024, 128, 1024),
+                                  (17, 1024, 1024, 64)], ids=str)
 def test_gemm_dma_transposed(wm, trans, case):
-    """The direct-to-LDS kernel with transposed operands (A stored k x m,
-    B stored n x k): the k-contiguous and row-contiguous stagings swap sides.
+    """The direct-to-LDS kernels with transposed operands (A stored k x m,
+    B stored n x k): the k-contiguous and row-contiguous stagings swap sides;
+    k <= 256 on the three-buffer kernel, k = 384 on the four-buffer one.
     Padded leading dimensions and gaps between problems, alpha, accumulation
     and a bias; 17 problems of 64 tiles take two problems per workgroup."""
     ta, tb = trans
@@ -252,7 +253,7 @@ def test_gemm_dma_transposed(wm, trans, case):
             assert np.all(got[q * sc + m * ldc:(q + 1) * sc] == 7.0)
 
 
-@pytest.mark.parametrize("shape", [(4, 1024, 128, 1024), (64, 256, 128, 256)], ids=str)
+@pytest.mark.parametrize("shape", [(4, 1024, 128, 1024), (64, 256, 128, 256), (8, 512, 128, 512)], ids=str)
 def test_bmm_backward_on_dma_kernel(wm, shape):
     """bmm's closure at attention-like shapes: its two products (g b^T and
     a^T g) run on the direct-to-LDS kernel; both gradients, overwritten and
