@@ -1012,7 +1012,7 @@ int64_t choose_kslices(int64_t work, int64_t k) {
 // gemm_kernel / gemm_dma_kernel: 8192^3 92.9-97.8 / 83-84 / 87-90; the
 // [8192, 1024] x [1024, 1024] projections and their weight and input
 // gradients 88.9-90.3 / 65-70 / -), lose on bmm's k = 128 forward
-// (62.2 / 59.7-63.2 / 64.1-70.0), on its gradients (71 / 74-76 / 80.1) and on
+// (62.2 / 59.7-63.2 / 72.6 on gemm_dma3_kernel), on its gradients (71 / 74-76 / 80.1) and on
 // the attention's per-head products (k = 64 scores 19.7 / 46, n = 64
 // contexts 45.7 / 64: two-level batches the library can only take as one
 // call per outer batch).  Batched products that gemm_dma_kernel takes run
